@@ -1,0 +1,121 @@
+/*
+ * rk.h — C-ABI of the MI355X (gfx950) backend for rakkan-mesh's quantized
+ * matrix-vector hot path: librkhip.so.
+ *
+ * The entry points replace the bodies of the Go API in internal/gpu (the
+ * Vulkan backend) one for one; each declaration cites the Go interface it
+ * stands in for (paths relative to the rakkan-mesh repository). A cgo shim in
+ * internal/gpu keeps the exported Go names and signatures and calls these.
+ *
+ * Conventions:
+ *   - Every function returns an int status (RK_OK or a negative RK_ERR_*),
+ *     except the few documented getters. Nothing aborts the process; the text
+ *     of the last error on a device is rk_last_error(dev).
+ *   - Host buffers are owned by the caller and only read or written during
+ *     the call. Handles are opaque; the caller frees them, before
+ *     rk_device_close (as internal/gpu/device.go:344-378 requires).
+ *   - A device is safe for concurrent use; calls that touch it run one at a
+ *     time (internal/gpu/device.go:202-203), on one HIP stream.
+ *   - Results are bit-identical to the reference's CPU path (internal/num):
+ *     integer block sums, then the fixed-order float32 combine of
+ *     internal/num/quant.go:14-19, 158-164.
+ */
+#ifndef RK_H
+#define RK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    RK_OK = 0,
+    RK_ERR_ARGS = -1,        /* bad handle, shape, type or offset */
+    RK_ERR_OOM = -2,         /* device memory exhausted */
+    RK_ERR_HIP = -3,         /* a HIP runtime call failed */
+    RK_ERR_UNSUPPORTED = -4, /* a format this build does not run */
+    RK_ERR_NO_DEVICE = -5,   /* no usable GPU */
+};
+
+/* Matrix storage formats (internal/gpu/device.go:562-585 Format). */
+enum {
+    RK_F32 = 0,
+    RK_BF16 = 1,
+    RK_Q8 = 2, /* int8 codes [rows][cols], float32 scales [rows][cols/32] */
+    RK_Q4 = 3, /* nibbles [rows][cols/2] (low: j, high: j+16 of a block), scales as Q8 */
+};
+
+typedef struct rk_device rk_device;
+typedef struct rk_matrix rk_matrix;
+
+typedef struct {
+    int32_t index;
+    char name[64];
+    char arch[32];       /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int64_t memory;      /* device-local bytes */
+    int32_t compute_units;
+    int32_t exact;       /* 1: IEEE f32 with denormals kept, round to nearest even */
+} rk_device_info;
+
+/* internal/gpu/device.go:125-183 Devices (count, then rk_device_info per index). */
+int rk_device_count(int32_t *count);
+int rk_device_info_get(int32_t index, rk_device_info *info);
+
+/* internal/gpu/device.go:238-279 Open; :344-378 Close. */
+int rk_device_open(int32_t index, rk_device **out);
+int rk_device_close(rk_device *dev);
+
+/* internal/gpu/device.go Device.Used: bytes of matrices, vectors and arenas
+ * held. Returns -1 for a null device. */
+int64_t rk_used_bytes(rk_device *dev);
+
+/* Text of the last error on dev (or of the last failed open when dev is
+ * NULL); valid until the next call on the device. */
+const char *rk_last_error(rk_device *dev);
+
+/* internal/gpu/device.go:587-700 Upload. w: F32 float[rows*cols], BF16
+ * uint16[rows*cols], Q8 int8[rows*cols], Q4 uint8[rows*cols/2]; scales:
+ * float[rows*cols/32] for Q8/Q4, NULL otherwise. Shape limits as the
+ * reference: cols <= 2^18, rows <= 2^24, cols % 32 == 0 for Q8/Q4. The
+ * device layout is this build's own (the reference layout is repacked). */
+int rk_matrix_upload(rk_device *dev, int32_t kind, int64_t rows, int64_t cols, const void *w, const float *scales,
+                     rk_matrix **out);
+
+/* internal/gpu/device.go:733-738 Matrix.Free. */
+int rk_matrix_free(rk_matrix *m);
+
+/* internal/gpu/device.go:727 Matrix.Bytes (-1 for NULL). */
+int64_t rk_matrix_bytes(const rk_matrix *m);
+
+/* internal/gpu/device.go:769-793 MulVecs: outs[i] = ms[i]·x for n matrices
+ * on one device sharing cols; x (cols floats) and outs are host buffers. The
+ * input is quantized once for the Q8/Q4 matrices (internal/gpu/batch.go:214-269).
+ * Blocking, like the reference's submit-and-wait. */
+int rk_matvecs(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols);
+
+/* The same products with device-resident x and outputs, enqueued on the
+ * HIP stream `stream` (NULL: the device's own) without waiting. For callers
+ * that keep activations in HBM (a stage executor, benchmarks). */
+int rk_matvecs_device(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *d_outs, const float *d_x,
+                      int64_t cols, void *stream);
+
+/* internal/gpu/profile.go:82-109 StartProfile / StopProfile. While a
+ * profile is active, every kernel the library launches is bracketed by HIP
+ * events on the stream it runs on; stop waits for them and returns, per
+ * kernel, the launches and their summed duration, the slowest first (at most
+ * cap entries written, *n = entries available). */
+typedef struct {
+    char kernel[48];
+    int64_t calls;
+    double ms;
+} rk_profile_entry;
+
+int rk_profile_start(rk_device *dev);
+int rk_profile_stop(rk_device *dev, rk_profile_entry *out, int32_t cap, int32_t *n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,85 @@
+// rk_runtime.h — internal object model of librkhip (the C-ABI is rk.h).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/rk.h"
+#include "rk_kernels.h"
+
+// The widest input and output of one product (internal/gpu/device.go:197-200).
+constexpr int64_t kMaxCols = (int64_t)1 << 18;
+constexpr int64_t kMaxRows = (int64_t)1 << 20;
+
+// internal/gpu/device.go:204-236 Device.
+struct rk_device {
+    int index = 0;
+    int cu = 0;
+    rk_device_info info{};
+    hipStream_t stream = nullptr;
+    std::mutex mu;  // held for the duration of every call on the device
+    int64_t used = 0;
+    std::string err;
+    // Scratch of the standalone products (the reference's host arena):
+    // input, its Q8 form, outputs, and pinned staging for the copies.
+    float *x = nullptr;
+    int8_t *qx = nullptr;
+    float *xs = nullptr;
+    int32_t *xsum = nullptr;
+    float *out = nullptr;
+    float *h_stage = nullptr;
+    hipEvent_t scratch_free = nullptr;
+    // Kernel timing (rk_profile_*): one event pair per launch while active.
+    struct ProfRec {
+        const char *kernel;
+        hipEvent_t a, b;
+    };
+    bool profiling = false;
+    std::vector<ProfRec> prof;
+    std::vector<hipEvent_t> event_pool;
+};
+
+// internal/gpu/device.go:543-552 Matrix.
+struct rk_matrix {
+    rk_device *d = nullptr;
+    int32_t kind = 0;
+    int64_t rows = 0, cols = 0;
+    uint8_t *w = nullptr;    // codes, [rows][row bytes]
+    float *scales = nullptr; // [rows][cols/32]
+    int64_t bytes = 0;
+};
+
+namespace rk {
+int fail(rk_device *d, int code, const char *fmt, ...);
+int hip_fail(rk_device *d, hipError_t e, const char *what);
+int dev_alloc(rk_device *d, void **p, size_t bytes, const char *what);
+int scratch_acquire(rk_device *d, hipStream_t s);
+int scratch_release(rk_device *d, hipStream_t s);
+int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
+                    hipStream_t s);
+
+// Brackets one kernel launch with events when the device is profiling.
+class ProfScope {
+  public:
+    ProfScope(rk_device *d, hipStream_t s, const char *kernel);
+    ~ProfScope();
+    ProfScope(const ProfScope &) = delete;
+    ProfScope &operator=(const ProfScope &) = delete;
+
+  private:
+    rk_device *d_;
+    hipStream_t s_;
+    int idx_ = -1;
+};
+}  // namespace rk
+
+#define HIP_TRY(d, expr, what)                          \
+    do {                                                \
+        hipError_t e_ = (expr);                         \
+        if (e_ != hipSuccess) {                         \
+            (void)hipGetLastError();                    \
+            return ::rk::hip_fail((d), e_, (what));     \
+        }                                               \
+    } while (0)

@@ -1,0 +1,396 @@
+// rk_runtime.hip — host side of librkhip: devices, matrices and the C-ABI
+// entry points of include/rk.h for them. The object model mirrors
+// internal/gpu (Device, Matrix, MulVecs); each C entry point cites the Go
+// function whose body it replaces.
+#include "rk_runtime.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <algorithm>
+#include <vector>
+
+namespace rk {
+
+thread_local std::string g_open_error;
+
+int fail(rk_device *d, int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (d)
+        d->err = buf;
+    else
+        g_open_error = buf;
+    return code;
+}
+
+int hip_fail(rk_device *d, hipError_t e, const char *what) {
+    return fail(d, e == hipErrorOutOfMemory ? RK_ERR_OOM : RK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int dev_alloc(rk_device *d, void **p, size_t bytes, const char *what) {
+    hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return hip_fail(d, e, what);
+    }
+    return RK_OK;
+}
+
+// Serialise use of the device's shared scratch across streams: work that
+// uses it waits for the previous user's work, then marks its own end.
+int scratch_acquire(rk_device *d, hipStream_t s) {
+    HIP_TRY(d, hipStreamWaitEvent(s, d->scratch_free, 0), "scratch wait");
+    return RK_OK;
+}
+int scratch_release(rk_device *d, hipStream_t s) {
+    HIP_TRY(d, hipEventRecord(d->scratch_free, s), "scratch record");
+    return RK_OK;
+}
+
+static hipEvent_t take_event(rk_device *d) {
+    if (!d->event_pool.empty()) {
+        hipEvent_t e = d->event_pool.back();
+        d->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return e;
+}
+
+ProfScope::ProfScope(rk_device *d, hipStream_t s, const char *kernel) : d_(d), s_(s) {
+    if (!d->profiling) return;
+    hipEvent_t a = take_event(d), b = take_event(d);
+    if (!a || !b) return;
+    if (hipEventRecord(a, s) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    idx_ = (int)d->prof.size();
+    d->prof.push_back({kernel, a, b});
+}
+
+ProfScope::~ProfScope() {
+    if (idx_ >= 0 && hipEventRecord(d_->prof[idx_].b, s_) != hipSuccess) (void)hipGetLastError();
+}
+
+// Enqueue ms[i]·x into outs[i]: x (cols floats) on the device; one quantize
+// of x into the device scratch, then one launch per run of up to kMaxSegs
+// matrices of one kind.
+int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
+                    hipStream_t s) {
+    bool quantized = false;
+    for (int i = 0; i < n; i++)
+        if (ms[i]->kind == RK_Q8 || ms[i]->kind == RK_Q4) quantized = true;
+    if (quantized) {
+        ProfScope p(d, s, "quantize_acts");
+        launch_quantize_acts(x, cols, d->qx, d->xs, d->xsum, s);
+    }
+    for (int kind : {RK_Q8, RK_Q4}) {
+        MatvecArgs a{};
+        a.cols = (int32_t)cols;
+        a.qx = d->qx;
+        a.xs = d->xs;
+        a.xsum = d->xsum;
+        auto flush = [&]() {
+            if (a.nseg == 0) return;
+            ProfScope p(d, s, kind == RK_Q8 ? "matvec_q8" : "matvec_q4");
+            if (kind == RK_Q8)
+                launch_matvec_q8(a, d->cu, s);
+            else
+                launch_matvec_q4(a, d->cu, s);
+            a.nseg = 0;
+            a.total_rows = 0;
+        };
+        for (int i = 0; i < n; i++) {
+            if (ms[i]->kind != kind) continue;
+            a.seg[a.nseg] = MatSeg{ms[i]->w, ms[i]->scales, outs[i], ms[i]->rows};
+            a.total_rows += ms[i]->rows;
+            if (++a.nseg == kMaxSegs) flush();
+        }
+        flush();
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(d, e, "matvec launch");
+    return RK_OK;
+}
+
+int check_products(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, int64_t *total) {
+    if (!d || n < 0 || (n > 0 && !ms)) return fail(d, RK_ERR_ARGS, "rk_matvecs: bad arguments");
+    *total = 0;
+    for (int i = 0; i < n; i++) {
+        rk_matrix *m = ms[i];
+        if (!m || m->d != d) return fail(d, RK_ERR_ARGS, "rk_matvecs: matrix %d is on another device", i);
+        if (m->cols != cols)
+            return fail(d, RK_ERR_ARGS, "gpu: %lld×%lld matrix times %lld", (long long)m->rows, (long long)m->cols,
+                        (long long)cols);
+        if (m->kind != RK_Q8 && m->kind != RK_Q4)
+            return fail(d, RK_ERR_UNSUPPORTED, "rk_matvecs: format %d has no kernel in this build", m->kind);
+        *total += m->rows;
+    }
+    return RK_OK;
+}
+
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" {
+
+int rk_device_count(int32_t *count) {
+    if (!count) return RK_ERR_ARGS;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *count = 0;
+        return RK_OK;  // no runtime devices: an empty list, as Devices()
+    }
+    *count = n;
+    return RK_OK;
+}
+
+int rk_device_info_get(int32_t index, rk_device_info *info) {
+    if (!info) return RK_ERR_ARGS;
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, index);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(nullptr, RK_ERR_NO_DEVICE, "device %d: %s", index, hipGetErrorString(e));
+    }
+    memset(info, 0, sizeof *info);
+    info->index = index;
+    snprintf(info->name, sizeof info->name, "%s", p.name);
+    snprintf(info->arch, sizeof info->arch, "%s", p.gcnArchName);
+    info->memory = (int64_t)p.totalGlobalMem;
+    info->compute_units = p.multiProcessorCount;
+    // The kernels are built for gfx950 with f32 denormals kept and
+    // round-to-nearest-even: exact there, and nowhere else.
+    info->exact = strncmp(p.gcnArchName, "gfx950", 6) == 0;
+    return RK_OK;
+}
+
+int rk_device_open(int32_t index, rk_device **out) {
+    if (!out) return RK_ERR_ARGS;
+    *out = nullptr;
+    rk_device_info info;
+    int rc = rk_device_info_get(index, &info);
+    if (rc != RK_OK) return rc;
+    if (!info.exact)
+        return fail(nullptr, RK_ERR_NO_DEVICE, "device %d is %s; this build runs on gfx950 only", index, info.arch);
+    hipError_t e = hipSetDevice(index);
+    if (e != hipSuccess) return hip_fail(nullptr, e, "hipSetDevice");
+    rk_device *d = new rk_device();
+    d->index = index;
+    d->cu = info.compute_units;
+    d->info = info;
+    auto bail = [&](int code) {
+        if (!d->err.empty()) g_open_error = d->err;
+        rk_device_close(d);
+        return code;
+    };
+    if ((e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking)) != hipSuccess)
+        return bail(hip_fail(d, e, "stream"));
+    if ((e = hipEventCreateWithFlags(&d->scratch_free, hipEventDisableTiming)) != hipSuccess)
+        return bail(hip_fail(d, e, "event"));
+    if ((rc = dev_alloc(d, (void **)&d->x, 4 * kMaxCols, "scratch")) ||
+        (rc = dev_alloc(d, (void **)&d->qx, kMaxCols, "scratch")) ||
+        (rc = dev_alloc(d, (void **)&d->xs, 4 * (kMaxCols / 32), "scratch")) ||
+        (rc = dev_alloc(d, (void **)&d->xsum, 4 * (kMaxCols / 32), "scratch")) ||
+        (rc = dev_alloc(d, (void **)&d->out, 4 * kMaxRows, "scratch")))
+        return bail(rc);
+    if ((e = hipHostMalloc((void **)&d->h_stage, 4 * (kMaxCols + kMaxRows), hipHostMallocDefault)) != hipSuccess)
+        return bail(hip_fail(d, e, "pinned staging"));
+    *out = d;
+    return RK_OK;
+}
+
+int rk_device_close(rk_device *d) {
+    if (!d) return RK_ERR_ARGS;
+    (void)hipSetDevice(d->index);
+    if (d->stream) (void)hipStreamSynchronize(d->stream);
+    (void)hipFree(d->x);
+    (void)hipFree(d->qx);
+    (void)hipFree(d->xs);
+    (void)hipFree(d->xsum);
+    (void)hipFree(d->out);
+    if (d->h_stage) (void)hipHostFree(d->h_stage);
+    if (d->scratch_free) (void)hipEventDestroy(d->scratch_free);
+    for (auto &r : d->prof) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    for (hipEvent_t e : d->event_pool) (void)hipEventDestroy(e);
+    if (d->stream) (void)hipStreamDestroy(d->stream);
+    (void)hipGetLastError();
+    delete d;
+    return RK_OK;
+}
+
+int64_t rk_used_bytes(rk_device *d) {
+    if (!d) return -1;
+    std::lock_guard<std::mutex> g(d->mu);
+    return d->used;
+}
+
+const char *rk_last_error(rk_device *d) { return d ? d->err.c_str() : g_open_error.c_str(); }
+
+int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, const void *w, const float *scales,
+                     rk_matrix **out) {
+    if (!d || !out || !w) return fail(d, RK_ERR_ARGS, "rk_matrix_upload: null argument");
+    *out = nullptr;
+    // internal/gpu/device.go:619-624 shape checks.
+    if (rows <= 0 || cols <= 0 || cols > kMaxCols || rows > (int64_t)1 << 24)
+        return fail(d, RK_ERR_ARGS, "gpu: matrix %lld×%lld out of range", (long long)rows, (long long)cols);
+    int64_t wbytes = 0;
+    switch (kind) {
+    case RK_Q8: wbytes = rows * cols; break;
+    case RK_Q4: wbytes = rows * cols / 2; break;
+    case RK_F32:
+    case RK_BF16: return fail(d, RK_ERR_UNSUPPORTED, "rk_matrix_upload: format %d has no kernel in this build", kind);
+    default: return fail(d, RK_ERR_ARGS, "rk_matrix_upload: unknown format %d", kind);
+    }
+    if (cols % 32 != 0 || !scales) return fail(d, RK_ERR_ARGS, "gpu: quantized matrix of the wrong shape");
+    const int64_t sbytes = rows * (cols / 32) * 4;
+    std::lock_guard<std::mutex> g(d->mu);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    rk_matrix *m = new rk_matrix();
+    m->d = d;
+    m->kind = kind;
+    m->rows = rows;
+    m->cols = cols;
+    int rc;
+    if ((rc = dev_alloc(d, (void **)&m->w, (size_t)wbytes, "matrix")) ||
+        (rc = dev_alloc(d, (void **)&m->scales, (size_t)sbytes, "matrix scales"))) {
+        (void)hipFree(m->w);
+        delete m;
+        return rc;
+    }
+    hipError_t e = hipMemcpyAsync(m->w, w, (size_t)wbytes, hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->scales, scales, (size_t)sbytes, hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(m->w);
+        (void)hipFree(m->scales);
+        delete m;
+        return hip_fail(d, e, "matrix upload");
+    }
+    m->bytes = wbytes + sbytes;
+    d->used += m->bytes;
+    *out = m;
+    return RK_OK;
+}
+
+int rk_matrix_free(rk_matrix *m) {
+    if (!m) return RK_ERR_ARGS;
+    rk_device *d = m->d;
+    std::lock_guard<std::mutex> g(d->mu);
+    (void)hipSetDevice(d->index);
+    (void)hipStreamSynchronize(d->stream);
+    (void)hipFree(m->w);
+    (void)hipFree(m->scales);
+    d->used -= m->bytes;
+    delete m;
+    return RK_OK;
+}
+
+int64_t rk_matrix_bytes(const rk_matrix *m) { return m ? m->bytes : -1; }
+
+int rk_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols) {
+    int64_t total;
+    int rc = check_products(d, n, ms, cols, &total);
+    if (rc) return rc;
+    if (n == 0) return RK_OK;
+    if (!x || !outs) return fail(d, RK_ERR_ARGS, "rk_matvecs: null buffer");
+    if (total > kMaxRows) return fail(d, RK_ERR_ARGS, "gpu: products too large for one submission");
+    std::lock_guard<std::mutex> g(d->mu);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipStream_t s = d->stream;
+    float *hx = d->h_stage, *hout = d->h_stage + kMaxCols;
+    memcpy(hx, x, (size_t)cols * 4);
+    if ((rc = scratch_acquire(d, s))) return rc;
+    HIP_TRY(d, hipMemcpyAsync(d->x, hx, (size_t)cols * 4, hipMemcpyHostToDevice, s), "input copy");
+    std::vector<float *> douts(n);
+    int64_t at = 0;
+    for (int i = 0; i < n; i++) {
+        douts[i] = d->out + at;
+        at += ms[i]->rows;
+    }
+    if ((rc = enqueue_matvecs(d, n, ms, douts.data(), d->x, cols, s))) return rc;
+    HIP_TRY(d, hipMemcpyAsync(hout, d->out, (size_t)total * 4, hipMemcpyDeviceToHost, s), "output copy");
+    if ((rc = scratch_release(d, s))) return rc;
+    HIP_TRY(d, hipStreamSynchronize(s), "submit");
+    at = 0;
+    for (int i = 0; i < n; i++) {
+        memcpy(outs[i], hout + at, (size_t)ms[i]->rows * 4);
+        at += ms[i]->rows;
+    }
+    return RK_OK;
+}
+
+int rk_matvecs_device(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *d_outs, const float *d_x,
+                      int64_t cols, void *stream) {
+    int64_t total;
+    int rc = check_products(d, n, ms, cols, &total);
+    if (rc) return rc;
+    if (n == 0) return RK_OK;
+    if (!d_x || !d_outs) return fail(d, RK_ERR_ARGS, "rk_matvecs_device: null buffer");
+    for (int i = 0; i < n; i++)
+        if (!d_outs[i]) return fail(d, RK_ERR_ARGS, "rk_matvecs_device: null output %d", i);
+    std::lock_guard<std::mutex> g(d->mu);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipStream_t s = stream ? (hipStream_t)stream : d->stream;
+    if ((rc = scratch_acquire(d, s))) return rc;
+    if ((rc = enqueue_matvecs(d, n, ms, d_outs, d_x, cols, s))) return rc;
+    return scratch_release(d, s);
+}
+
+int rk_profile_start(rk_device *d) {
+    if (!d) return RK_ERR_ARGS;
+    std::lock_guard<std::mutex> g(d->mu);
+    d->profiling = true;
+    return RK_OK;
+}
+
+int rk_profile_stop(rk_device *d, rk_profile_entry *out, int32_t cap, int32_t *n) {
+    if (!d || !n || (cap > 0 && !out)) return RK_ERR_ARGS;
+    std::lock_guard<std::mutex> g(d->mu);
+    d->profiling = false;
+    std::vector<rk_profile_entry> agg;
+    int rc = RK_OK;
+    for (auto &r : d->prof) {
+        float ms = 0;
+        hipError_t e = hipEventSynchronize(r.b);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a, r.b);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            rc = hip_fail(d, e, "profile event");
+        }
+        size_t i = 0;
+        while (i < agg.size() && strcmp(agg[i].kernel, r.kernel) != 0) i++;
+        if (i == agg.size()) {
+            rk_profile_entry z{};
+            snprintf(z.kernel, sizeof z.kernel, "%s", r.kernel);
+            agg.push_back(z);
+        }
+        agg[i].calls++;
+        agg[i].ms += ms;
+        d->event_pool.push_back(r.a);
+        d->event_pool.push_back(r.b);
+    }
+    d->prof.clear();
+    std::sort(agg.begin(), agg.end(), [](const rk_profile_entry &x, const rk_profile_entry &y) { return x.ms > y.ms; });
+    *n = (int32_t)agg.size();
+    for (int32_t i = 0; i < cap && i < (int32_t)agg.size(); i++) out[i] = agg[i];
+    return rc;
+}
+
+}  // extern "C"

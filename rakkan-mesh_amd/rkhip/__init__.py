@@ -1,0 +1,179 @@
+"""Python bindings of librkhip (include/rk.h) over ctypes.
+
+This is host plumbing for tests and benchmarks: every computation runs in
+librkhip.so's HIP kernels. Loading fails loudly when the library is not
+built; there is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "librkhip.so")
+HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "rk.h")
+
+RK_OK, RK_ERR_ARGS, RK_ERR_OOM, RK_ERR_HIP, RK_ERR_UNSUPPORTED, RK_ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5
+F32, BF16, Q8, Q4 = 0, 1, 2, 3
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+F = ctypes.c_float
+
+_lib = None
+
+
+class RKError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"rk error {code}: {msg}")
+        self.code = code
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("index", I32), ("name", ctypes.c_char * 64), ("arch", ctypes.c_char * 32), ("memory", I64),
+                ("compute_units", I32), ("exact", I32)]
+
+
+# name -> (restype, argtypes); the exported C-ABI, kept in step with rk.h.
+SIGNATURES = {
+    "rk_device_count": (ctypes.c_int, [P]),
+    "rk_device_info_get": (ctypes.c_int, [I32, P]),
+    "rk_device_open": (ctypes.c_int, [I32, P]),
+    "rk_device_close": (ctypes.c_int, [P]),
+    "rk_used_bytes": (I64, [P]),
+    "rk_last_error": (ctypes.c_char_p, [P]),
+    "rk_matrix_upload": (ctypes.c_int, [P, I32, I64, I64, P, P, P]),
+    "rk_matrix_free": (ctypes.c_int, [P]),
+    "rk_matrix_bytes": (I64, [P]),
+    "rk_matvecs": (ctypes.c_int, [P, I32, P, P, P, I64]),
+    "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
+    "rk_profile_start": (ctypes.c_int, [P]),
+    "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
+}
+
+
+def lib():
+    """The loaded librkhip.so; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run __graft_entry__.build() (hipcc, gfx950)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(P)
+
+
+def device_count():
+    n = I32()
+    lib().rk_device_count(ctypes.byref(n))
+    return n.value
+
+
+def device_info(index=0):
+    info = DeviceInfo()
+    rc = lib().rk_device_info_get(index, ctypes.byref(info))
+    if rc != RK_OK:
+        raise RKError(rc, lib().rk_last_error(None).decode())
+    return info
+
+
+class ProfileEntry(ctypes.Structure):
+    _fields_ = [("kernel", ctypes.c_char * 48), ("calls", I64), ("ms", ctypes.c_double)]
+
+
+class Matrix:
+    def __init__(self, dev, handle, kind, rows, cols):
+        self.dev, self.h, self.kind, self.rows, self.cols = dev, handle, kind, rows, cols
+
+    @property
+    def bytes(self):
+        return lib().rk_matrix_bytes(self.h)
+
+    def free(self):
+        if self.h:
+            self.dev._check(lib().rk_matrix_free(self.h))
+            self.h = None
+
+
+class Device:
+    """An opened GPU (internal/gpu Device)."""
+
+    def __init__(self, index=0):
+        h = P()
+        rc = lib().rk_device_open(index, ctypes.byref(h))
+        if rc != RK_OK:
+            raise RKError(rc, lib().rk_last_error(None).decode())
+        self.h = h
+
+    def _check(self, rc):
+        if rc != RK_OK:
+            raise RKError(rc, lib().rk_last_error(self.h).decode())
+        return rc
+
+    def close(self):
+        if self.h:
+            lib().rk_device_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def used(self):
+        return lib().rk_used_bytes(self.h)
+
+    def upload(self, kind, rows, cols, w, scales=None):
+        w = np.ascontiguousarray(w)
+        sp = None
+        if scales is not None:
+            scales = np.ascontiguousarray(scales, dtype=np.float32)
+            sp = _ptr(scales)
+        h = P()
+        self._check(lib().rk_matrix_upload(self.h, kind, rows, cols, _ptr(w), sp, ctypes.byref(h)))
+        return Matrix(self, h, kind, rows, cols)
+
+    def upload_q8(self, q, s, rows, cols):
+        return self.upload(Q8, rows, cols, np.ascontiguousarray(q, dtype=np.int8), s)
+
+    def upload_q4(self, q, s, rows, cols):
+        return self.upload(Q4, rows, cols, np.ascontiguousarray(q, dtype=np.uint8), s)
+
+    def matvecs(self, ms, x):
+        """outs[i] = ms[i]·x with host buffers (internal/gpu MulVecs)."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        outs = [np.empty(m.rows, np.float32) for m in ms]
+        hs = (P * len(ms))(*[m.h for m in ms])
+        ops = (P * len(ms))(*[o.ctypes.data for o in outs])
+        self._check(lib().rk_matvecs(self.h, len(ms), hs, ops, _ptr(x), x.size))
+        return outs
+
+    def matvec(self, m, x):
+        return self.matvecs([m], x)[0]
+
+    def matvecs_device(self, ms, d_outs, d_x, cols, stream=None):
+        """Enqueue products on device pointers (ints) on a HIP stream handle."""
+        hs = (P * len(ms))(*[m.h for m in ms])
+        ops = (P * len(ms))(*d_outs)
+        self._check(lib().rk_matvecs_device(self.h, len(ms), hs, ops, P(d_x), cols, P(stream) if stream else None))
+
+    def profile_start(self):
+        self._check(lib().rk_profile_start(self.h))
+
+    def profile_stop(self):
+        """{kernel: (calls, total ms)} of the launches since profile_start."""
+        n = I32()
+        buf = (ProfileEntry * 64)()
+        self._check(lib().rk_profile_stop(self.h, ctypes.cast(buf, P), 64, ctypes.byref(n)))
+        return {buf[i].kernel.decode(): (buf[i].calls, buf[i].ms) for i in range(min(n.value, 64))}

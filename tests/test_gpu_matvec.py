@@ -1,0 +1,159 @@
+"""Q8_0 / Q4_0 products on the GPU, bit for bit against the CPU oracle
+(the reference's TestKernelsMatchCPUBitForBit, internal/gpu/gpu_test.go:59-141,
+plus the benchmark shapes)."""
+import numpy as np
+import pytest
+
+import rkhip
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def awkward(rng, n, scale):
+    """internal/gpu/gpu_test.go:35-48: normal values plus denormals, -0 and
+    1e-30, each with probability 1/40."""
+    v = (rng.normal(0, 1, n) * scale).astype(np.float32)
+    pick = rng.integers(0, 40, n)
+    den = rng.integers(0, 1 << 23, n, dtype=np.uint32).view(np.float32)
+    v[pick == 0] = den[pick == 0]
+    v[pick == 1] = np.float32(-0.0)
+    v[pick == 2] = np.float32(1e-30)
+    return v
+
+
+def same_bits(got, want, what):
+    g, w = got.view(np.uint32), want.view(np.uint32)
+    if not np.array_equal(g, w):
+        i = int(np.argmax(g != w))
+        raise AssertionError(f"{what}: row {i}: GPU {got[i]!r} ({g[i]:#x}), oracle {want[i]!r} ({w[i]:#x}), "
+                             f"{int(np.sum(g != w))} rows differ")
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 32), (300, 896), (64, 4864), (1000, 96), (33, 288), (5, 768)])
+def test_awkward_inputs_match(dev, rows, cols):
+    rng = np.random.default_rng(rows * 7919 + cols)
+    w = awkward(rng, rows * cols, 0.05)
+    x = awkward(rng, cols, 1.0)
+    q8, s8 = oracle.quantize8(w)
+    m = dev.upload_q8(q8, s8, rows, cols)
+    same_bits(dev.matvec(m, x), oracle.matvec_q8(q8, s8, x, rows, cols), f"q8 {rows}x{cols}")
+    m.free()
+    q4, s4 = oracle.quantize4(w)
+    m = dev.upload_q4(q4, s4, rows, cols)
+    same_bits(dev.matvec(m, x), oracle.matvec_q4(q4, s4, x, rows, cols), f"q4 {rows}x{cols}")
+    m.free()
+    assert dev.used == 0
+
+
+@pytest.mark.parametrize("rows,cols", [(300000, 32), (40000, 1024)])
+def test_large_matrices(dev, rows, cols):
+    rng = np.random.default_rng(rows)
+    q = rng.integers(-127, 128, rows * cols, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    x = awkward(rng, cols, 1.0)
+    m = dev.upload_q8(q, s, rows, cols)
+    same_bits(dev.matvec(m, x), oracle.matvec_q8(q, s, x, rows, cols), f"q8 {rows}x{cols}")
+    m.free()
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (14336, 4096), (4096, 14336)])
+def test_benchmark_shapes_q8(dev, rows, cols):
+    """Config 2: codes uniform in [-127, 127], scales U(1e-3, 1e-2), x N(0,1)."""
+    rng = np.random.default_rng(cols * 3 + rows)
+    q = rng.integers(-127, 128, rows * cols, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    m = dev.upload_q8(q, s, rows, cols)
+    same_bits(dev.matvec(m, x), oracle.matvec_q8(q, s, x, rows, cols), f"q8 {rows}x{cols}")
+    m.free()
+
+
+@pytest.mark.parametrize("rows,cols", [(512, 3584), (512, 18944), (1000, 2048), (64, 14336)])
+def test_q4_shapes(dev, rows, cols):
+    """Config 4's widths (3584 = 112 blocks, 18944 = 592: partial chunks)."""
+    rng = np.random.default_rng(cols + rows)
+    q = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+    s = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    m = dev.upload_q4(q, s, rows, cols)
+    same_bits(dev.matvec(m, x), oracle.matvec_q4(q, s, x, rows, cols), f"q4 {rows}x{cols}")
+    m.free()
+
+
+def test_several_matrices_one_input(dev):
+    """MulVecs of Q/K/V-like matrices, mixed Q8/Q4 (q4_m keeps V in Q8), and
+    more matrices than one launch takes."""
+    rng = np.random.default_rng(21)
+    cols = 896
+    shapes = [(896, "q8"), (128, "q4"), (128, "q8"), (4864, "q4"), (4864, "q8"), (7, "q8"), (33, "q4")]
+    x = awkward(rng, cols, 1.0)
+    ms, wants = [], []
+    for rows, kind in shapes:
+        w = rng.normal(0, 0.05, rows * cols).astype(np.float32)
+        if kind == "q8":
+            q, s = oracle.quantize8(w)
+            ms.append(dev.upload_q8(q, s, rows, cols))
+            wants.append(oracle.matvec_q8(q, s, x, rows, cols))
+        else:
+            q, s = oracle.quantize4(w)
+            ms.append(dev.upload_q4(q, s, rows, cols))
+            wants.append(oracle.matvec_q4(q, s, x, rows, cols))
+    for i, (got, want) in enumerate(zip(dev.matvecs(ms, x), wants)):
+        same_bits(got, want, f"matrix {i}")
+    for m in ms:
+        m.free()
+    assert dev.used == 0
+
+
+def test_zero_and_tiny_inputs(dev):
+    """All-zero input (scale 0, codes 0), a block of only denormals (its
+    reciprocal scale overflows), and blocks of -0."""
+    rng = np.random.default_rng(22)
+    rows, cols = 64, 256
+    q = rng.integers(-127, 128, rows * cols, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    m = dev.upload_q8(q, s, rows, cols)
+    xs = [np.zeros(cols, np.float32), np.full(cols, -0.0, np.float32)]
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    x[:32] = rng.integers(1, 1 << 20, 32, dtype=np.uint32).view(np.float32)
+    x[32:64] = 0
+    x[40] = np.float32(1e-44)
+    xs.append(x)
+    for x in xs:
+        same_bits(dev.matvec(m, x), oracle.matvec_q8(q, s, x, rows, cols), "q8 special input")
+    m.free()
+
+
+def test_shape_errors(dev):
+    rng = np.random.default_rng(23)
+    q = rng.integers(-127, 128, 64 * 64, dtype=np.int8)
+    s = np.ones(64 * 2, np.float32)
+    with pytest.raises(rkhip.RKError) as e:
+        dev.upload_q8(q, s, 64, 48)  # cols not a multiple of 32
+    assert e.value.code == rkhip.RK_ERR_ARGS
+    m = dev.upload_q8(q, s, 64, 64)
+    with pytest.raises(rkhip.RKError) as e:
+        dev.matvecs([m], np.zeros(32, np.float32))
+    assert e.value.code == rkhip.RK_ERR_ARGS
+    m.free()
+    assert dev.used == 0
+
+
+def test_device_pointers_and_stream(dev):
+    """rk_matvecs_device on torch-allocated HBM and a torch stream."""
+    import torch
+
+    rng = np.random.default_rng(24)
+    rows, cols = 2048, 4096
+    q = rng.integers(-127, 128, rows * cols, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    m = dev.upload_q8(q, s, rows, cols)
+    dx = torch.from_numpy(x).cuda()
+    dout = torch.empty(rows, dtype=torch.float32, device="cuda")
+    st = torch.cuda.Stream()
+    dev.matvecs_device([m], [dout.data_ptr()], dx.data_ptr(), cols, st.cuda_stream)
+    st.synchronize()
+    same_bits(dout.cpu().numpy(), oracle.matvec_q8(q, s, x, rows, cols), "device-pointer q8")
+    m.free()
