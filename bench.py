@@ -66,30 +66,43 @@ def main():
               "DESIGN.md, not built). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    import torch
+    import ctypes
+
     import rkhip
 
     dev = rkhip.Device(0)
     info = rkhip.device_info(0)
     rng = np.random.default_rng(1)
-    q_all, s_all, xs = [], [], []
+    q_all, s_all = [], []
     for r, c in SHAPES:
         q_all.append(rng.integers(-127, 128, r * c, dtype=np.int8))
         s_all.append(rng.uniform(1e-3, 1e-2, r * c // 32).astype(np.float32))
     xs = [rng.normal(0, 1, c).astype(np.float32) for _, c in SHAPES]
     sets = [[dev.upload_q8(q, s, r, c) for (r, c), q, s in zip(SHAPES, q_all, s_all)] for _ in range(args.sets)]
-    dx = [torch.from_numpy(x).cuda() for x in xs]
-    douts = [torch.empty(r, dtype=torch.float32, device="cuda") for r, _ in SHAPES]
-    stream = torch.cuda.Stream()
-    sp = stream.cuda_stream
+    # inputs and outputs in one arena (HBM)
+    x_off, out_off, at = [], [], 0
+    for _, c in SHAPES:
+        x_off.append(at)
+        at += c
+    for r, _ in SHAPES:
+        out_off.append(at)
+        at += r
+    arena = dev.arena(at, at)
+    b = arena.begin()
+    for o, x in zip(x_off, xs):
+        b.write(o, x)
+    b.submit()
+
+    def sync():
+        arena.begin().submit()
 
     L = rkhip.lib()
-    import ctypes
     P = ctypes.c_void_p
     calls = []
     for k in range(args.sets):
         for i, (r, c) in enumerate(SHAPES):
-            calls.append(((P * 1)(sets[k][i].h), (P * 1)(douts[i].data_ptr()), P(dx[i].data_ptr()), c))
+            calls.append(((P * 1)(sets[k][i].h), (P * 1)(arena.device_ptr(out_off[i])), P(arena.device_ptr(x_off[i])),
+                          c))
     per_step = len(SHAPES)
 
     def run(steps, start):
@@ -97,18 +110,21 @@ def main():
             base = (st % args.sets) * per_step
             for j in range(per_step):
                 hs, ops, xp, c = calls[base + j]
-                rc = L.rk_matvecs_device(dev.h, 1, hs, ops, xp, c, P(sp))
+                rc = L.rk_matvecs_device(dev.h, 1, hs, ops, xp, c, None)
                 if rc:
                     raise rkhip.RKError(rc, L.rk_last_error(dev.h).decode())
 
     run(args.warmup, 0)
-    torch.cuda.synchronize()
-    dev.profile_start()
-    torch.cuda.synchronize()
+    sync()
     t0 = time.perf_counter()
     run(args.steps, args.warmup)
-    torch.cuda.synchronize()
+    sync()
     t1 = time.perf_counter()
+    # the same steps again with every kernel bracketed by HIP events on the
+    # stream it runs on (the library's profile), for per-kernel durations
+    dev.profile_start()
+    run(args.steps, args.warmup)
+    sync()
     prof = dev.profile_stop()
     ms_per_step = (t1 - t0) / args.steps * 1e3
     step_bytes = sum(q8_bytes(r, c) for r, c in SHAPES)
@@ -125,8 +141,8 @@ def main():
         dev.profile_start()
         for st in range(50):
             hs, ops, xp, cc = calls[(st % args.sets) * per_step + i]
-            L.rk_matvecs_device(dev.h, 1, hs, ops, xp, cc, P(sp))
-        torch.cuda.synchronize()
+            L.rk_matvecs_device(dev.h, 1, hs, ops, xp, cc, None)
+        sync()
         p = dev.profile_stop()
         n, ms = p["matvec_q8"]
         us = ms / n * 1e3
@@ -170,6 +186,7 @@ def main():
                                   "sample": f"{reps} passes over the three config-2 products in {el:.1f} s "
                                             "(C restatement of the reference CPU path, AVX2, rows over threads)",
                                   "bit_exact_vs_gpu": bool(exact)}
+    arena.free()
     for st in sets:
         for m in st:
             m.free()

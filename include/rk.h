@@ -101,6 +101,75 @@ int rk_matvecs(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *ou
 int rk_matvecs_device(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *d_outs, const float *d_x,
                       int64_t cols, void *stream);
 
+/* ---- Arenas, vectors and batches (internal/gpu/batch.go) ----
+ * An arena is device memory of 32-bit words holding a computation's
+ * activations, caches and tables; batch operations address it by word
+ * offsets, as the Go API does. Every span an operation names is checked
+ * against its arena or vectors; a bad one latches RK_ERR_ARGS. */
+typedef struct rk_arena rk_arena;
+typedef struct rk_vectors rk_vectors;
+typedef struct rk_batch rk_batch;
+
+/* internal/gpu/batch.go:22-49 NewArena: `words` of device memory and pinned
+ * staging for `staging_words` moved per submission. */
+int rk_arena_new(rk_device *dev, int64_t words, int64_t staging_words, rk_arena **out);
+/* internal/gpu/batch.go:51-55 SetQuantScratch: reserves room for a product's
+ * quantized input (qx_off: cols/4 words, xs_off: cols/32 words). The
+ * quantized form itself is kept in the arena's own 16-byte-aligned scratch,
+ * which products read as 128-bit vectors; the reserved words are not written. */
+int rk_arena_set_quant_scratch(rk_arena *a, int64_t qx_off, int64_t xs_off);
+/* internal/gpu/batch.go:57-58 Bytes. */
+int64_t rk_arena_bytes(const rk_arena *a);
+/* internal/gpu/batch.go:60-71 Free. */
+int rk_arena_free(rk_arena *a);
+/* Device address of word `off`, for rk_matvecs_device and other callers that
+ * pass device pointers. No reference counterpart (Vulkan never exposes one). */
+int rk_arena_device_ptr(rk_arena *a, int64_t off, void **dptr);
+
+/* internal/gpu/batch.go:82-109 UploadVectors / Vectors.Free: a layer's norm
+ * weights and biases, read by rmsnorm and addvec. */
+int rk_vectors_upload(rk_device *dev, const float *v, int64_t n, rk_vectors **out);
+int rk_vectors_free(rk_vectors *v);
+
+/* internal/gpu/batch.go:126-134 Begin: holds the device until submit.
+ * Operations return the batch's first error so far (RK_OK if none); after an
+ * error they do nothing, and submit returns it (batch.go:136-147). */
+int rk_batch_begin(rk_arena *a, rk_batch **out);
+/* internal/gpu/batch.go:149-159 Write: copies n floats to word off. */
+int rk_batch_write(rk_batch *b, int64_t off, const float *data, int64_t n);
+/* internal/gpu/batch.go:161-171 Read: n words at off into dst on submit. */
+int rk_batch_read(rk_batch *b, int64_t off, float *dst, int64_t n);
+/* internal/gpu/batch.go:212-269 MatVecs: ms[i]·x into word out_offs[i], x
+ * at in_off, quantized once (Q8/Q4 need the arena's quant scratch). */
+int rk_batch_matvecs(rk_batch *b, int32_t n, rk_matrix *const *ms, const int64_t *out_offs, int64_t in_off);
+/* internal/gpu/batch.go:277-280 Quantize: n floats at in into the scratch. */
+int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n);
+/* internal/gpu/batch.go:282-287 RMSNorm: segs segments of n floats at in
+ * (stride apart) into out: out = w·(Rsqrt32(Dot32(x,x)·recip_n + eps)·x). */
+int rk_batch_rmsnorm(rk_batch *b, rk_vectors *vecs, int64_t in, int64_t out, int64_t w, int32_t n, int32_t segs,
+                     int64_t stride, float recip_n, float eps);
+/* internal/gpu/batch.go:289-292 AddVec: n floats at word v of vecs added to out. */
+int rk_batch_addvec(rk_batch *b, rk_vectors *vecs, int64_t out, int64_t v, int64_t n);
+/* internal/gpu/batch.go:294-298 Rope: adjacent pairs of q (q_dim) and k
+ * (kv_dim) with the position's cos and sin rows (head_size/2 each). */
+int rk_batch_rope(rk_batch *b, int64_t q, int64_t k, int32_t q_dim, int32_t kv_dim, int32_t head_size, int64_t cos,
+                  int64_t sin);
+/* internal/gpu/batch.go:300-303 Copy: n words. */
+int rk_batch_copy(rk_batch *b, int64_t src, int64_t dst, int64_t n);
+/* internal/gpu/batch.go:305-316 Attention for one position: scores of q
+ * against keys (positions rows, kv_dim apart) into att (heads rows,
+ * att_stride apart), softmax, and the values weighted into out. */
+int rk_batch_attention(rk_batch *b, int64_t q, int64_t keys, int64_t vals, int64_t att, int64_t att_stride, int64_t out,
+                       int32_t positions, int32_t heads, int32_t kv_heads, int32_t head_size, int32_t kv_dim,
+                       float inv_sqrt);
+/* internal/gpu/batch.go:318-326 Residual: x += y, NaNs canonical if asked. */
+int rk_batch_residual(rk_batch *b, int64_t x, int64_t y, int64_t n, int32_t canonical);
+/* internal/gpu/batch.go:328-331 SiluMul: a = silu(a)·b. */
+int rk_batch_silumul(rk_batch *b, int64_t a, int64_t b_off, int64_t n);
+/* internal/gpu/batch.go:333-349 Submit: waits, delivers the reads, releases
+ * the device and frees the batch; returns the first error. */
+int rk_batch_submit(rk_batch *b);
+
 /* internal/gpu/profile.go:82-109 StartProfile / StopProfile. While a
  * profile is active, every kernel the library launches is bracketed by HIP
  * events on the stream it runs on; stop waits for them and returns, per

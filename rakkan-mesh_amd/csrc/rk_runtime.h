@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <condition_variable>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -13,13 +14,60 @@
 constexpr int64_t kMaxCols = (int64_t)1 << 18;
 constexpr int64_t kMaxRows = (int64_t)1 << 20;
 
+namespace rk {
+// Ownership of a device across calls: a batch holds it from begin to submit
+// (internal/gpu/batch.go:126-134), possibly on different OS threads (a Go
+// goroutine may move between cgo calls), so this is a flag and a condition
+// variable rather than a thread-affine mutex.
+class Gate {
+  public:
+    void acquire() {
+        std::unique_lock<std::mutex> l(m_);
+        cv_.wait(l, [&] { return !held_; });
+        held_ = true;
+    }
+    void release() {
+        {
+            std::lock_guard<std::mutex> l(m_);
+            held_ = false;
+        }
+        cv_.notify_one();
+    }
+
+  private:
+    std::mutex m_;
+    std::condition_variable cv_;
+    bool held_ = false;
+};
+
+// RAII hold of a device's gate for one call.
+class Hold {
+  public:
+    explicit Hold(Gate &g) : g_(g) { g_.acquire(); }
+    ~Hold() { g_.release(); }
+    Hold(const Hold &) = delete;
+    Hold &operator=(const Hold &) = delete;
+
+  private:
+    Gate &g_;
+};
+
+// Where a product's quantized input lives (device pointers).
+struct QScratch {
+    int8_t *qx;
+    float *xs;
+    int32_t *xsum;
+};
+}  // namespace rk
+
 // internal/gpu/device.go:204-236 Device.
 struct rk_device {
     int index = 0;
     int cu = 0;
     rk_device_info info{};
     hipStream_t stream = nullptr;
-    std::mutex mu;  // held for the duration of every call on the device
+    rk::Gate gate;   // held for every call on the device, and by open batches
+    std::mutex mu;   // guards `used`
     int64_t used = 0;
     std::string err;
     // Scratch of the standalone products (the reference's host arena):
@@ -31,6 +79,8 @@ struct rk_device {
     float *out = nullptr;
     float *h_stage = nullptr;
     hipEvent_t scratch_free = nullptr;
+    hipStream_t scratch_stream = nullptr;  // the last stream that used the scratch
+    bool scratch_stream_set = false;
     // Kernel timing (rk_profile_*): one event pair per launch while active.
     struct ProfRec {
         const char *kernel;
@@ -58,7 +108,8 @@ int dev_alloc(rk_device *d, void **p, size_t bytes, const char *what);
 int scratch_acquire(rk_device *d, hipStream_t s);
 int scratch_release(rk_device *d, hipStream_t s);
 int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
-                    hipStream_t s);
+                    const QScratch &q, hipStream_t s);
+void add_used(rk_device *d, int64_t bytes);
 
 // Brackets one kernel launch with events when the device is profiling.
 class ProfScope {

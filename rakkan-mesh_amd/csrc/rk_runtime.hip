@@ -43,12 +43,16 @@ int dev_alloc(rk_device *d, void **p, size_t bytes, const char *what) {
 
 // Serialise use of the device's shared scratch across streams: work that
 // uses it waits for the previous user's work, then marks its own end.
+// (Stream order already serialises uses from the stream that last had it.)
 int scratch_acquire(rk_device *d, hipStream_t s) {
-    HIP_TRY(d, hipStreamWaitEvent(s, d->scratch_free, 0), "scratch wait");
+    if (d->scratch_stream != s && d->scratch_stream_set)
+        HIP_TRY(d, hipStreamWaitEvent(s, d->scratch_free, 0), "scratch wait");
     return RK_OK;
 }
 int scratch_release(rk_device *d, hipStream_t s) {
     HIP_TRY(d, hipEventRecord(d->scratch_free, s), "scratch record");
+    d->scratch_stream = s;
+    d->scratch_stream_set = true;
     return RK_OK;
 }
 
@@ -85,21 +89,26 @@ ProfScope::~ProfScope() {
 // Enqueue ms[i]·x into outs[i]: x (cols floats) on the device; one quantize
 // of x into the device scratch, then one launch per run of up to kMaxSegs
 // matrices of one kind.
+void add_used(rk_device *d, int64_t bytes) {
+    std::lock_guard<std::mutex> g(d->mu);
+    d->used += bytes;
+}
+
 int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
-                    hipStream_t s) {
+                    const QScratch &q, hipStream_t s) {
     bool quantized = false;
     for (int i = 0; i < n; i++)
         if (ms[i]->kind == RK_Q8 || ms[i]->kind == RK_Q4) quantized = true;
     if (quantized) {
         ProfScope p(d, s, "quantize_acts");
-        launch_quantize_acts(x, cols, d->qx, d->xs, d->xsum, s);
+        launch_quantize_acts(x, cols, q.qx, q.xs, q.xsum, s);
     }
     for (int kind : {RK_Q8, RK_Q4}) {
         MatvecArgs a{};
         a.cols = (int32_t)cols;
-        a.qx = d->qx;
-        a.xs = d->xs;
-        a.xsum = d->xsum;
+        a.qx = q.qx;
+        a.xs = q.xs;
+        a.xsum = q.xsum;
         auto flush = [&]() {
             if (a.nseg == 0) return;
             ProfScope p(d, s, kind == RK_Q8 ? "matvec_q8" : "matvec_q4");
@@ -238,7 +247,7 @@ int rk_device_close(rk_device *d) {
 int64_t rk_used_bytes(rk_device *d) {
     if (!d) return -1;
     std::lock_guard<std::mutex> g(d->mu);
-    return d->used;
+    return d->used;  // read under the accounting lock only
 }
 
 const char *rk_last_error(rk_device *d) { return d ? d->err.c_str() : g_open_error.c_str(); }
@@ -260,7 +269,7 @@ int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, con
     }
     if (cols % 32 != 0 || !scales) return fail(d, RK_ERR_ARGS, "gpu: quantized matrix of the wrong shape");
     const int64_t sbytes = rows * (cols / 32) * 4;
-    std::lock_guard<std::mutex> g(d->mu);
+    Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
     rk_matrix *m = new rk_matrix();
     m->d = d;
@@ -284,7 +293,7 @@ int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, con
         return hip_fail(d, e, "matrix upload");
     }
     m->bytes = wbytes + sbytes;
-    d->used += m->bytes;
+    add_used(d, m->bytes);
     *out = m;
     return RK_OK;
 }
@@ -292,12 +301,12 @@ int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, con
 int rk_matrix_free(rk_matrix *m) {
     if (!m) return RK_ERR_ARGS;
     rk_device *d = m->d;
-    std::lock_guard<std::mutex> g(d->mu);
+    Hold hold(d->gate);
     (void)hipSetDevice(d->index);
     (void)hipStreamSynchronize(d->stream);
     (void)hipFree(m->w);
     (void)hipFree(m->scales);
-    d->used -= m->bytes;
+    add_used(d, -m->bytes);
     delete m;
     return RK_OK;
 }
@@ -311,7 +320,7 @@ int rk_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs
     if (n == 0) return RK_OK;
     if (!x || !outs) return fail(d, RK_ERR_ARGS, "rk_matvecs: null buffer");
     if (total > kMaxRows) return fail(d, RK_ERR_ARGS, "gpu: products too large for one submission");
-    std::lock_guard<std::mutex> g(d->mu);
+    Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
     hipStream_t s = d->stream;
     float *hx = d->h_stage, *hout = d->h_stage + kMaxCols;
@@ -324,7 +333,7 @@ int rk_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs
         douts[i] = d->out + at;
         at += ms[i]->rows;
     }
-    if ((rc = enqueue_matvecs(d, n, ms, douts.data(), d->x, cols, s))) return rc;
+    if ((rc = enqueue_matvecs(d, n, ms, douts.data(), d->x, cols, QScratch{d->qx, d->xs, d->xsum}, s))) return rc;
     HIP_TRY(d, hipMemcpyAsync(hout, d->out, (size_t)total * 4, hipMemcpyDeviceToHost, s), "output copy");
     if ((rc = scratch_release(d, s))) return rc;
     HIP_TRY(d, hipStreamSynchronize(s), "submit");
@@ -345,24 +354,24 @@ int rk_matvecs_device(rk_device *d, int32_t n, rk_matrix *const *ms, float *cons
     if (!d_x || !d_outs) return fail(d, RK_ERR_ARGS, "rk_matvecs_device: null buffer");
     for (int i = 0; i < n; i++)
         if (!d_outs[i]) return fail(d, RK_ERR_ARGS, "rk_matvecs_device: null output %d", i);
-    std::lock_guard<std::mutex> g(d->mu);
+    Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
     hipStream_t s = stream ? (hipStream_t)stream : d->stream;
     if ((rc = scratch_acquire(d, s))) return rc;
-    if ((rc = enqueue_matvecs(d, n, ms, d_outs, d_x, cols, s))) return rc;
+    if ((rc = enqueue_matvecs(d, n, ms, d_outs, d_x, cols, QScratch{d->qx, d->xs, d->xsum}, s))) return rc;
     return scratch_release(d, s);
 }
 
 int rk_profile_start(rk_device *d) {
     if (!d) return RK_ERR_ARGS;
-    std::lock_guard<std::mutex> g(d->mu);
+    Hold hold(d->gate);
     d->profiling = true;
     return RK_OK;
 }
 
 int rk_profile_stop(rk_device *d, rk_profile_entry *out, int32_t cap, int32_t *n) {
     if (!d || !n || (cap > 0 && !out)) return RK_ERR_ARGS;
-    std::lock_guard<std::mutex> g(d->mu);
+    Hold hold(d->gate);
     d->profiling = false;
     std::vector<rk_profile_entry> agg;
     int rc = RK_OK;

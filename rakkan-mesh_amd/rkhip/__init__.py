@@ -48,6 +48,26 @@ SIGNATURES = {
     "rk_matrix_bytes": (I64, [P]),
     "rk_matvecs": (ctypes.c_int, [P, I32, P, P, P, I64]),
     "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
+    "rk_arena_new": (ctypes.c_int, [P, I64, I64, P]),
+    "rk_arena_set_quant_scratch": (ctypes.c_int, [P, I64, I64]),
+    "rk_arena_bytes": (I64, [P]),
+    "rk_arena_free": (ctypes.c_int, [P]),
+    "rk_arena_device_ptr": (ctypes.c_int, [P, I64, P]),
+    "rk_vectors_upload": (ctypes.c_int, [P, P, I64, P]),
+    "rk_vectors_free": (ctypes.c_int, [P]),
+    "rk_batch_begin": (ctypes.c_int, [P, P]),
+    "rk_batch_write": (ctypes.c_int, [P, I64, P, I64]),
+    "rk_batch_read": (ctypes.c_int, [P, I64, P, I64]),
+    "rk_batch_matvecs": (ctypes.c_int, [P, I32, P, P, I64]),
+    "rk_batch_quantize": (ctypes.c_int, [P, I64, I64]),
+    "rk_batch_rmsnorm": (ctypes.c_int, [P, P, I64, I64, I64, I32, I32, I64, F, F]),
+    "rk_batch_addvec": (ctypes.c_int, [P, P, I64, I64, I64]),
+    "rk_batch_rope": (ctypes.c_int, [P, I64, I64, I32, I32, I32, I64, I64]),
+    "rk_batch_copy": (ctypes.c_int, [P, I64, I64, I64]),
+    "rk_batch_attention": (ctypes.c_int, [P, I64, I64, I64, I64, I64, I64, I32, I32, I32, I32, I32, F]),
+    "rk_batch_residual": (ctypes.c_int, [P, I64, I64, I64, I32]),
+    "rk_batch_silumul": (ctypes.c_int, [P, I64, I64, I64]),
+    "rk_batch_submit": (ctypes.c_int, [P]),
     "rk_profile_start": (ctypes.c_int, [P]),
     "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
 }
@@ -102,6 +122,105 @@ class Matrix:
         if self.h:
             self.dev._check(lib().rk_matrix_free(self.h))
             self.h = None
+
+
+class Vectors:
+    def __init__(self, dev, handle, n):
+        self.dev, self.h, self.n = dev, handle, n
+
+    def free(self):
+        if self.h:
+            self.dev._check(lib().rk_vectors_free(self.h))
+            self.h = None
+
+
+class Arena:
+    """Device words for a computation (internal/gpu Arena)."""
+
+    def __init__(self, dev, words, staging_words):
+        self.dev = dev
+        h = P()
+        dev._check(lib().rk_arena_new(dev.h, words, staging_words, ctypes.byref(h)))
+        self.h, self.words = h, words
+
+    def set_quant_scratch(self, qx_off, xs_off):
+        self.dev._check(lib().rk_arena_set_quant_scratch(self.h, qx_off, xs_off))
+
+    @property
+    def bytes(self):
+        return lib().rk_arena_bytes(self.h)
+
+    def device_ptr(self, off=0):
+        p = P()
+        self.dev._check(lib().rk_arena_device_ptr(self.h, off, ctypes.byref(p)))
+        return p.value
+
+    def free(self):
+        if self.h:
+            self.dev._check(lib().rk_arena_free(self.h))
+            self.h = None
+
+    def begin(self):
+        return Batch(self)
+
+
+class Batch:
+    """Recorded operations on an arena (internal/gpu Batch); the device is
+    held from begin to submit. Reads land in numpy arrays on submit."""
+
+    def __init__(self, arena):
+        self.a, self.dev = arena, arena.dev
+        h = P()
+        self.dev._check(lib().rk_batch_begin(arena.h, ctypes.byref(h)))
+        self.h = h
+        self._keep = []
+
+    def write(self, off, data):
+        data = np.ascontiguousarray(data, dtype=np.float32)
+        self._keep.append(data)
+        return lib().rk_batch_write(self.h, off, _ptr(data), data.size)
+
+    def read(self, off, n):
+        dst = np.empty(n, np.float32)
+        self._keep.append(dst)
+        lib().rk_batch_read(self.h, off, _ptr(dst), n)
+        return dst
+
+    def matvecs(self, ms, out_offs, in_off):
+        hs = (P * len(ms))(*[m.h for m in ms])
+        offs = (I64 * len(ms))(*out_offs)
+        return lib().rk_batch_matvecs(self.h, len(ms), hs, offs, in_off)
+
+    def quantize(self, inp, n):
+        return lib().rk_batch_quantize(self.h, inp, n)
+
+    def rmsnorm(self, vecs, inp, out, w, n, segs, stride, recip_n, eps):
+        return lib().rk_batch_rmsnorm(self.h, vecs.h, inp, out, w, n, segs, stride, float(recip_n), float(eps))
+
+    def addvec(self, vecs, out, v, n):
+        return lib().rk_batch_addvec(self.h, vecs.h, out, v, n)
+
+    def rope(self, q, k, q_dim, kv_dim, head_size, cos, sin):
+        return lib().rk_batch_rope(self.h, q, k, q_dim, kv_dim, head_size, cos, sin)
+
+    def copy(self, src, dst, n):
+        return lib().rk_batch_copy(self.h, src, dst, n)
+
+    def attention(self, q, keys, vals, att, att_stride, out, positions, heads, kv_heads, head_size, kv_dim, inv_sqrt):
+        return lib().rk_batch_attention(self.h, q, keys, vals, att, att_stride, out, positions, heads, kv_heads,
+                                        head_size, kv_dim, float(inv_sqrt))
+
+    def residual(self, x, y, n, canonical):
+        return lib().rk_batch_residual(self.h, x, y, n, int(canonical))
+
+    def silumul(self, a, b, n):
+        return lib().rk_batch_silumul(self.h, a, b, n)
+
+    def submit(self):
+        rc = lib().rk_batch_submit(self.h)
+        self.h = None
+        self._keep = []
+        self.dev._check(rc)
 
 
 class Device:
@@ -177,3 +296,12 @@ class Device:
         buf = (ProfileEntry * 64)()
         self._check(lib().rk_profile_stop(self.h, ctypes.cast(buf, P), 64, ctypes.byref(n)))
         return {buf[i].kernel.decode(): (buf[i].calls, buf[i].ms) for i in range(min(n.value, 64))}
+
+    def arena(self, words, staging_words):
+        return Arena(self, words, staging_words)
+
+    def upload_vectors(self, v):
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        h = P()
+        self._check(lib().rk_vectors_upload(self.h, _ptr(v), v.size, ctypes.byref(h)))
+        return Vectors(self, h, v.size)
