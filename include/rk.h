@@ -170,6 +170,22 @@ int rk_batch_silumul(rk_batch *b, int64_t a, int64_t b_off, int64_t n);
  * the device and frees the batch; returns the first error. */
 int rk_batch_submit(rk_batch *b);
 
+/* ---- Graphs ----
+ * Records the work that device-pointer calls (rk_matvecs_device with a NULL
+ * stream, and the other *_device entry points) enqueue on the device's
+ * stream between rk_graph_begin and rk_graph_end into a HIP graph, which
+ * rk_graph_launch replays: the same kernels on the same buffers, without
+ * the per-call host cost. No reference counterpart: the reference
+ * re-records its Vulkan command buffer for every submission
+ * (internal/gpu/batch.go:126-134). Only one thread may use the device while
+ * it records; batches (which wait) cannot be recorded. */
+typedef struct rk_graph rk_graph;
+int rk_graph_begin(rk_device *dev);
+int rk_graph_end(rk_device *dev, rk_graph **out);
+/* Enqueues `times` replays on the device stream and waits for them. */
+int rk_graph_launch(rk_graph *g, int32_t times);
+int rk_graph_free(rk_graph *g);
+
 /* internal/gpu/profile.go:82-109 StartProfile / StopProfile. While a
  * profile is active, every kernel the library launches is bracketed by HIP
  * events on the stream it runs on; stop waits for them and returns, per

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(64) void rmsnorm_kernel(const float *in, float *out
 void launch_rmsnorm(const float *in, float *out, const float *w, int n, int segs, int64_t stride, float recip_n,
                     float eps, hipStream_t s) {
     if (segs <= 0 || n <= 0) return;
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(segs), dim3(64), 0, s, in, out, w, n, stride, recip_n, eps);
+    RK_LAUNCH(rmsnorm_kernel, dim3(segs), dim3(64), 0, s, in, out, w, n, stride, recip_n, eps);
 }
 
 // out += v (internal/gpu/kernels.go:394-404).
@@ -64,7 +64,7 @@ __global__ void addvec_kernel(float *out, const float *v, int64_t n) {
 
 void launch_addvec(float *out, const float *v, int64_t n, hipStream_t s) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(addvec_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, v, n);
+    RK_LAUNCH(addvec_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, v, n);
 }
 
 // Rotary embedding of adjacent pairs (internal/gpu/kernels.go:406-427,
@@ -92,7 +92,7 @@ void launch_rope(float *q, float *k, int q_dim, int kv_dim, int hs, const float 
                  hipStream_t s) {
     const int pairs = q_dim / 2;
     if (pairs <= 0) return;
-    hipLaunchKernelGGL(rope_kernel, dim3((pairs + 255) / 256), dim3(256), 0, s, q, k, pairs, kv_dim, hs, cos_row,
+    RK_LAUNCH(rope_kernel, dim3((pairs + 255) / 256), dim3(256), 0, s, q, k, pairs, kv_dim, hs, cos_row,
                        sin_row);
 }
 
@@ -104,7 +104,7 @@ __global__ void copy_kernel(const uint32_t *src, uint32_t *dst, int64_t n) {
 
 void launch_copy(const void *src, void *dst, int64_t n, hipStream_t s) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint32_t *)src,
+    RK_LAUNCH(copy_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint32_t *)src,
                        (uint32_t *)dst, n);
 }
 
@@ -118,7 +118,7 @@ __global__ void residual_kernel(float *x, const float *y, int64_t n, int canon) 
 
 void launch_residual(float *x, const float *y, int64_t n, bool canon, hipStream_t s) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(residual_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n, canon ? 1 : 0);
+    RK_LAUNCH(residual_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n, canon ? 1 : 0);
 }
 
 // a = silu(a)·b (internal/gpu/kernels.go:565-577, internal/llm/model.go:657).
@@ -132,7 +132,7 @@ __global__ void silumul_kernel(float *a, const float *b, int64_t n) {
 
 void launch_silumul(float *a, const float *b, int64_t n, hipStream_t s) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(silumul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, n);
+    RK_LAUNCH(silumul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, b, n);
 }
 
 // ---------------------------------------------------------------------------
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(kAttThreads) void attention_kernel(const float *q, 
 void launch_attention(const float *q, const float *keys, const float *vals, float *att, int64_t att_stride, float *out,
                       int positions, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt, hipStream_t s) {
     if (positions <= 0 || heads <= 0) return;
-    hipLaunchKernelGGL(attention_kernel, dim3(heads), dim3(kAttThreads), 0, s, q, keys, vals, att, att_stride, out,
+    RK_LAUNCH(attention_kernel, dim3(heads), dim3(kAttThreads), 0, s, q, keys, vals, att, att_stride, out,
                        positions, heads / kv_heads, hs, kv_dim, inv_sqrt);
 }
 
@@ -246,7 +246,7 @@ __global__ void embed_kernel(const uint8_t *w, const float *scales, int kind, co
 
 void launch_embed(const uint8_t *w, const float *scales, bool q4, const int32_t *token, int dim, float *x,
                   hipStream_t s) {
-    hipLaunchKernelGGL(embed_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, w, scales, q4 ? 1 : 0, token, dim, x);
+    RK_LAUNCH(embed_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, w, scales, q4 ? 1 : 0, token, dim, x);
 }
 
 // Greedy argmax (internal/llm/sample.go:45-53): the first index holding the
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *v, int64_t n,
 }
 
 void launch_argmax(const float *v, int64_t n, int32_t *out, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, v, n, out);
+    RK_LAUNCH(argmax_kernel, dim3(1), dim3(1024), 0, s, v, n, out);
 }
 
 }  // namespace rk

@@ -11,8 +11,7 @@
 // per lane, coalesced. Q8: a lane pair holds one 32-byte block; Q4: a lane
 // holds one 16-byte block. The block terms of a chunk are gathered into the
 // lanes that own the eight running sums (cross-lane moves), which add them
-// in block order. Loads of U chunks are issued before any is consumed, and
-// many waves per CU keep HBM busy.
+// in block order.
 #include "rk_fmath.h"
 #include "rk_kernels.h"
 
@@ -68,15 +67,23 @@ void launch_quantize_acts(const float *x, int64_t n, int8_t *qx, float *xs, int3
     const int64_t nb = n / 32;
     if (nb <= 0) return;
     const int64_t threads = nb * 8;
-    hipLaunchKernelGGL(quantize_acts_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, nb, qx, xs,
+    RK_LAUNCH(quantize_acts_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, nb, qx, xs,
                        xsum);
 }
 
 // ---------------------------------------------------------------------------
 // Matrix-vector products.
+//
+// Each wavefront owns a contiguous run of rows and walks them in chunks of
+// 1 KiB of codes (one 16-byte piece per lane). The loads of the next chunk
+// (codes, their scales, and the matching quantized input and its scales) are
+// issued before the current chunk is consumed, so every wave keeps a chunk in
+// flight; the quantized input comes through the same loads (it stays in L1/
+// L2), not LDS, so the wait for the current chunk never waits on later ones.
+// Waves per CU are as many as registers allow: that, not deeper per-wave
+// prefetch, is what fills HBM (measured on MI355X).
 
 constexpr int kWaves = 4;  // wavefronts per workgroup
-constexpr int kU = 4;      // chunks in flight per wave
 
 struct RowRef {
     const uint8_t *w;
@@ -124,6 +131,24 @@ __device__ __forceinline__ bool wave_rows(int64_t total, int64_t per, int64_t &r
     return r0 < r1;
 }
 
+// The row's result: stored, or added to what the output holds (a residual
+// connection, x += W·v, internal/llm/model.go:596-598, 608-610), made
+// canonical if asked.
+__device__ __forceinline__ void put_row(const MatvecArgs &a, float *out, float res) {
+    if (a.epilogue == kEpiStore) {
+        *out = res;
+    } else {
+        const float v = *out + res;
+        *out = a.epilogue == kEpiAddCanonical ? canonical(v) : v;
+    }
+}
+
+// One chunk's operands for one lane.
+struct Q8Chunk {
+    int4 w, x;
+    float ws, xs;
+};
+
 // Q8_0: chunk c of a row is blocks [32c, 32c+32); lane pair k = lane/2 holds
 // block 32c+k. Running sum L (0..7) lives in lane 2L; in chunk c it takes the
 // blocks 32c+L, +8, +16, +24, held by lanes 2L, 2L+16, 2L+32, 2L+48.
@@ -135,71 +160,69 @@ __global__ __launch_bounds__(256) void matvec_q8_kernel(MatvecArgs a) {
     const int C = (cols + 1023) >> 10;
     const int64_t nsteps = (r1 - r0) * C;
 
-    int64_t lg = r0;  // load cursor: global row, chunk
-    int lc = 0;
-    int64_t pg = r0;  // process cursor
-    int pc = 0;
+    int64_t lg = r0, pg = r0;  // load / process cursors: global row, chunk
+    int lc = 0, pc = 0;
+    auto load = [&](Q8Chunk &k) {
+        k.w = k.x = make_int4(0, 0, 0, 0);
+        k.ws = k.xs = 0.0f;
+        const RowRef rr = locate(a, lg);
+        const int off = lc * 1024 + lane * 16;
+        if (off < cols) {
+            k.w = *reinterpret_cast<const int4 *>(rr.w + rr.r * cols + off);
+            k.ws = rr.ws[rr.r * nb + (off >> 5)];
+            k.x = *reinterpret_cast<const int4 *>(a.qx + off);
+            k.xs = a.xs[off >> 5];
+        }
+        if (++lc == C) {
+            lc = 0;
+            ++lg;
+        }
+    };
     float acc = 0.0f;
-    for (int64_t base = 0; base < nsteps; base += kU) {
-        int4 wv[kU];
-        float sv[kU];
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            wv[u] = make_int4(0, 0, 0, 0);
-            sv[u] = 0.0f;
-            if (base + u < nsteps) {
-                const RowRef rr = locate(a, lg);
-                const int off = lc * 1024 + lane * 16;
-                if (off < cols) {
-                    wv[u] = *reinterpret_cast<const int4 *>(rr.w + rr.r * cols + off);
-                    sv[u] = rr.ws[rr.r * nb + (off >> 5)];
-                }
-                if (++lc == C) {
-                    lc = 0;
-                    ++lg;
-                }
-            }
+    auto process = [&](const Q8Chunk &k) {
+        const int s = pair_sum(dot16(k.w, k.x, 0));
+        const float t = (float)s * (k.ws * k.xs);
+        const float t1 = __shfl_down(t, 16);
+        const float t2 = __shfl_down(t, 32);
+        const float t3 = __shfl_down(t, 48);
+        if (lane < 16 && (lane & 1) == 0) {
+            const int b0 = pc * 32 + (lane >> 1);
+            if (b0 < nb) acc += t;
+            if (b0 + 8 < nb) acc += t1;
+            if (b0 + 16 < nb) acc += t2;
+            if (b0 + 24 < nb) acc += t3;
         }
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            if (base + u < nsteps) {
-                const int off = pc * 1024 + lane * 16;
-                const bool active = off < cols;
-                int4 xv = make_int4(0, 0, 0, 0);
-                float xsb = 0.0f;
-                if (active) {
-                    xv = *reinterpret_cast<const int4 *>(a.qx + off);
-                    xsb = a.xs[off >> 5];
-                }
-                const int s = pair_sum(dot16(wv[u], xv, 0));
-                const float t = (float)s * (sv[u] * xsb);
-                const float t1 = __shfl_down(t, 16);
-                const float t2 = __shfl_down(t, 32);
-                const float t3 = __shfl_down(t, 48);
-                if (lane < 16 && (lane & 1) == 0) {
-                    const int b0 = pc * 32 + (lane >> 1);
-                    if (b0 < nb) acc += t;
-                    if (b0 + 8 < nb) acc += t1;
-                    if (b0 + 16 < nb) acc += t2;
-                    if (b0 + 24 < nb) acc += t3;
-                }
-                if (++pc == C) {
-                    // sums in lanes 0,2,..,14: ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7))
-                    const float p2 = acc + __shfl_down(acc, 2);
-                    const float q4 = p2 + __shfl_down(p2, 4);
-                    const float res = q4 + __shfl_down(q4, 8);
-                    if (lane == 0) {
-                        const RowRef rr = locate(a, pg);
-                        rr.out[rr.r] = res;
-                    }
-                    acc = 0.0f;
-                    pc = 0;
-                    ++pg;
-                }
+        if (++pc == C) {
+            // sums in lanes 0,2,..,14: ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7))
+            const float p2 = acc + __shfl_down(acc, 2);
+            const float q4 = p2 + __shfl_down(p2, 4);
+            const float res = q4 + __shfl_down(q4, 8);
+            if (lane == 0) {
+                const RowRef rr = locate(a, pg);
+                put_row(a, rr.out + rr.r, res);
             }
+            acc = 0.0f;
+            pc = 0;
+            ++pg;
         }
+    };
+    Q8Chunk ka, kb;
+    load(ka);
+    for (int64_t st = 0; st < nsteps;) {
+        if (st + 1 < nsteps) load(kb);
+        process(ka);
+        if (++st >= nsteps) break;
+        if (st + 1 < nsteps) load(ka);
+        process(kb);
+        ++st;
     }
 }
+
+struct Q4Chunk {
+    int4 w, x0, x1;
+    float ws, xs;
+    int xsum;
+};
 
 // Q4_0: a row has cols/2 bytes; chunk c is blocks [64c, 64c+64), lane l
 // holds block 64c+l (16 bytes: byte j = element j low, j+16 high, +8).
@@ -214,77 +237,73 @@ __global__ __launch_bounds__(256) void matvec_q4_kernel(MatvecArgs a) {
     const int C = (nb + 63) >> 6;
     const int64_t nsteps = (r1 - r0) * C;
 
-    int64_t lg = r0;
-    int lc = 0;
-    int64_t pg = r0;
-    int pc = 0;
+    int64_t lg = r0, pg = r0;
+    int lc = 0, pc = 0;
+    auto load = [&](Q4Chunk &k) {
+        k.w = k.x0 = k.x1 = make_int4(0, 0, 0, 0);
+        k.ws = k.xs = 0.0f;
+        k.xsum = 0;
+        const RowRef rr = locate(a, lg);
+        const int blk = lc * 64 + lane;
+        if (blk < nb) {
+            k.w = *reinterpret_cast<const int4 *>(rr.w + rr.r * rowb + blk * 16);
+            k.ws = rr.ws[rr.r * nb + blk];
+            k.x0 = *reinterpret_cast<const int4 *>(a.qx + blk * 32);
+            k.x1 = *reinterpret_cast<const int4 *>(a.qx + blk * 32 + 16);
+            k.xs = a.xs[blk];
+            k.xsum = a.xsum[blk];
+        }
+        if (++lc == C) {
+            lc = 0;
+            ++lg;
+        }
+    };
     float acc = 0.0f;
-    for (int64_t base = 0; base < nsteps; base += kU) {
-        int4 wv[kU];
-        float sv[kU];
+    auto process = [&](const Q4Chunk &k) {
+        const int4 w = k.w;
+        const int4 lo = make_int4(w.x & 0x0F0F0F0F, w.y & 0x0F0F0F0F, w.z & 0x0F0F0F0F, w.w & 0x0F0F0F0F);
+        const int4 hi = make_int4((int)(((uint32_t)w.x >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.y >> 4) & 0x0F0F0F0Fu),
+                                  (int)(((uint32_t)w.z >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.w >> 4) & 0x0F0F0F0Fu));
+        const int s = dot16(hi, k.x1, dot16(lo, k.x0, 0)) - 8 * k.xsum;
+        const float t = (float)s * (k.ws * k.xs);
+        float tj[8];
+        tj[0] = t;
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            wv[u] = make_int4(0, 0, 0, 0);
-            sv[u] = 0.0f;
-            if (base + u < nsteps) {
-                const RowRef rr = locate(a, lg);
-                const int blk = lc * 64 + lane;
-                if (blk < nb) {
-                    wv[u] = *reinterpret_cast<const int4 *>(rr.w + rr.r * rowb + blk * 16);
-                    sv[u] = rr.ws[rr.r * nb + blk];
-                }
-                if (++lc == C) {
-                    lc = 0;
-                    ++lg;
-                }
-            }
+        for (int j = 1; j < 8; ++j) tj[j] = __shfl_down(t, 8 * j);
+        if (lane < 8) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (pc * 64 + lane + 8 * j < nb) acc += tj[j];
         }
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            if (base + u < nsteps) {
-                const int blk = pc * 64 + lane;
-                float t = 0.0f;
-                if (blk < nb) {
-                    const int4 x0 = *reinterpret_cast<const int4 *>(a.qx + blk * 32);
-                    const int4 x1 = *reinterpret_cast<const int4 *>(a.qx + blk * 32 + 16);
-                    const int4 w = wv[u];
-                    const int4 lo = make_int4(w.x & 0x0F0F0F0F, w.y & 0x0F0F0F0F, w.z & 0x0F0F0F0F, w.w & 0x0F0F0F0F);
-                    const int4 hi = make_int4((int)(((uint32_t)w.x >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.y >> 4) & 0x0F0F0F0Fu),
-                                              (int)(((uint32_t)w.z >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.w >> 4) & 0x0F0F0F0Fu));
-                    int s = dot16(lo, x0, 0);
-                    s = dot16(hi, x1, s);
-                    s -= 8 * a.xsum[blk];
-                    t = (float)s * (sv[u] * a.xs[blk]);
-                }
-                float tj[8];
-                tj[0] = t;
-#pragma unroll
-                for (int j = 1; j < 8; ++j) tj[j] = __shfl_down(t, 8 * j);
-                if (lane < 8) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        if (pc * 64 + lane + 8 * j < nb) acc += tj[j];
-                }
-                if (++pc == C) {
-                    const float p2 = acc + __shfl_down(acc, 1);
-                    const float q4 = p2 + __shfl_down(p2, 2);
-                    const float res = q4 + __shfl_down(q4, 4);
-                    if (lane == 0) {
-                        const RowRef rr = locate(a, pg);
-                        rr.out[rr.r] = res;
-                    }
-                    acc = 0.0f;
-                    pc = 0;
-                    ++pg;
-                }
+        if (++pc == C) {
+            const float p2 = acc + __shfl_down(acc, 1);
+            const float q4 = p2 + __shfl_down(p2, 2);
+            const float res = q4 + __shfl_down(q4, 4);
+            if (lane == 0) {
+                const RowRef rr = locate(a, pg);
+                put_row(a, rr.out + rr.r, res);
             }
+            acc = 0.0f;
+            pc = 0;
+            ++pg;
         }
+    };
+    Q4Chunk ka, kb;
+    load(ka);
+    for (int64_t st = 0; st < nsteps;) {
+        if (st + 1 < nsteps) load(kb);
+        process(ka);
+        if (++st >= nsteps) break;
+        if (st + 1 < nsteps) load(ka);
+        process(kb);
+        ++st;
     }
 }
 
-// Grid: enough waves for ~16 per CU, each owning a contiguous run of rows.
+// Grid: about 64 waves per CU requested (residency is then set by
+// registers), each owning a contiguous run of rows.
 static unsigned matvec_grid(MatvecArgs &a, int cu) {
-    const int64_t target = (int64_t)(cu > 0 ? cu : 256) * 16;
+    const int64_t target = (int64_t)(cu > 0 ? cu : 256) * 64;
     a.per_wave = (a.total_rows + target - 1) / target;
     const int64_t waves = (a.total_rows + a.per_wave - 1) / a.per_wave;
     return (unsigned)((waves + kWaves - 1) / kWaves);
@@ -294,14 +313,14 @@ void launch_matvec_q8(const MatvecArgs &args, int cu, hipStream_t s) {
     if (args.total_rows <= 0) return;
     MatvecArgs a = args;
     const unsigned grid = matvec_grid(a, cu);
-    hipLaunchKernelGGL(matvec_q8_kernel, dim3(grid), dim3(64 * kWaves), 0, s, a);
+    RK_LAUNCH(matvec_q8_kernel, dim3(grid), dim3(64 * kWaves), 0, s, a);
 }
 
 void launch_matvec_q4(const MatvecArgs &args, int cu, hipStream_t s) {
     if (args.total_rows <= 0) return;
     MatvecArgs a = args;
     const unsigned grid = matvec_grid(a, cu);
-    hipLaunchKernelGGL(matvec_q4_kernel, dim3(grid), dim3(64 * kWaves), 0, s, a);
+    RK_LAUNCH(matvec_q4_kernel, dim3(grid), dim3(64 * kWaves), 0, s, a);
 }
 
 }  // namespace rk

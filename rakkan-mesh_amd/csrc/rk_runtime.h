@@ -87,8 +87,15 @@ struct rk_device {
         hipEvent_t a, b;
     };
     bool profiling = false;
+    bool capturing = false;  // the stream is recording a graph (rk_graph_*)
     std::vector<ProfRec> prof;
     std::vector<hipEvent_t> event_pool;
+};
+
+struct rk_graph {
+    rk_device *d = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 // internal/gpu/device.go:543-552 Matrix.
@@ -106,12 +113,11 @@ int fail(rk_device *d, int code, const char *fmt, ...);
 int hip_fail(rk_device *d, hipError_t e, const char *what);
 int dev_alloc(rk_device *d, void **p, size_t bytes, const char *what);
 int scratch_acquire(rk_device *d, hipStream_t s);
-int scratch_release(rk_device *d, hipStream_t s);
 int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
                     const QScratch &q, hipStream_t s);
 void add_used(rk_device *d, int64_t bytes);
 
-// Brackets one kernel launch with events when the device is profiling.
+// Times the one kernel launched in its scope when the device is profiling.
 class ProfScope {
   public:
     ProfScope(rk_device *d, hipStream_t s, const char *kernel);
@@ -120,9 +126,7 @@ class ProfScope {
     ProfScope &operator=(const ProfScope &) = delete;
 
   private:
-    rk_device *d_;
-    hipStream_t s_;
-    int idx_ = -1;
+    LaunchEvents ev_{};
 };
 }  // namespace rk
 

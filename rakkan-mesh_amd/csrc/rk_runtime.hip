@@ -13,6 +13,7 @@
 namespace rk {
 
 thread_local std::string g_open_error;
+thread_local LaunchEvents *g_launch_events = nullptr;
 
 int fail(rk_device *d, int code, const char *fmt, ...) {
     char buf[512];
@@ -41,16 +42,16 @@ int dev_alloc(rk_device *d, void **p, size_t bytes, const char *what) {
     return RK_OK;
 }
 
-// Serialise use of the device's shared scratch across streams: work that
-// uses it waits for the previous user's work, then marks its own end.
-// (Stream order already serialises uses from the stream that last had it.)
+// Serialise use of the device's shared scratch across streams: stream order
+// already serialises uses from one stream; when a call comes on another
+// stream, an event recorded on the previous one (marking all work enqueued
+// there so far) is waited for first.
 int scratch_acquire(rk_device *d, hipStream_t s) {
-    if (d->scratch_stream != s && d->scratch_stream_set)
+    if (d->capturing) return RK_OK;  // a recorded graph runs on one stream
+    if (d->scratch_stream_set && d->scratch_stream != s) {
+        HIP_TRY(d, hipEventRecord(d->scratch_free, d->scratch_stream), "scratch record");
         HIP_TRY(d, hipStreamWaitEvent(s, d->scratch_free, 0), "scratch wait");
-    return RK_OK;
-}
-int scratch_release(rk_device *d, hipStream_t s) {
-    HIP_TRY(d, hipEventRecord(d->scratch_free, s), "scratch record");
+    }
     d->scratch_stream = s;
     d->scratch_stream_set = true;
     return RK_OK;
@@ -70,21 +71,16 @@ static hipEvent_t take_event(rk_device *d) {
     return e;
 }
 
-ProfScope::ProfScope(rk_device *d, hipStream_t s, const char *kernel) : d_(d), s_(s) {
-    if (!d->profiling) return;
+ProfScope::ProfScope(rk_device *d, hipStream_t, const char *kernel) {
+    if (!d->profiling || d->capturing) return;
     hipEvent_t a = take_event(d), b = take_event(d);
     if (!a || !b) return;
-    if (hipEventRecord(a, s) != hipSuccess) {
-        (void)hipGetLastError();
-        return;
-    }
-    idx_ = (int)d->prof.size();
     d->prof.push_back({kernel, a, b});
+    ev_ = LaunchEvents{a, b};
+    g_launch_events = &ev_;
 }
 
-ProfScope::~ProfScope() {
-    if (idx_ >= 0 && hipEventRecord(d_->prof[idx_].b, s_) != hipSuccess) (void)hipGetLastError();
-}
+ProfScope::~ProfScope() { g_launch_events = nullptr; }
 
 // Enqueue ms[i]·x into outs[i]: x (cols floats) on the device; one quantize
 // of x into the device scratch, then one launch per run of up to kMaxSegs
@@ -327,6 +323,7 @@ int rk_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs
     memcpy(hx, x, (size_t)cols * 4);
     if ((rc = scratch_acquire(d, s))) return rc;
     HIP_TRY(d, hipMemcpyAsync(d->x, hx, (size_t)cols * 4, hipMemcpyHostToDevice, s), "input copy");
+    if (d->capturing) return fail(d, RK_ERR_ARGS, "rk_matvecs waits for its results: it cannot be recorded");
     std::vector<float *> douts(n);
     int64_t at = 0;
     for (int i = 0; i < n; i++) {
@@ -335,7 +332,6 @@ int rk_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs
     }
     if ((rc = enqueue_matvecs(d, n, ms, douts.data(), d->x, cols, QScratch{d->qx, d->xs, d->xsum}, s))) return rc;
     HIP_TRY(d, hipMemcpyAsync(hout, d->out, (size_t)total * 4, hipMemcpyDeviceToHost, s), "output copy");
-    if ((rc = scratch_release(d, s))) return rc;
     HIP_TRY(d, hipStreamSynchronize(s), "submit");
     at = 0;
     for (int i = 0; i < n; i++) {
@@ -357,9 +353,62 @@ int rk_matvecs_device(rk_device *d, int32_t n, rk_matrix *const *ms, float *cons
     Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
     hipStream_t s = stream ? (hipStream_t)stream : d->stream;
+    if (d->capturing && s != d->stream)
+        return fail(d, RK_ERR_ARGS, "while recording a graph, work goes on the device's stream");
     if ((rc = scratch_acquire(d, s))) return rc;
-    if ((rc = enqueue_matvecs(d, n, ms, d_outs, d_x, cols, QScratch{d->qx, d->xs, d->xsum}, s))) return rc;
-    return scratch_release(d, s);
+    return enqueue_matvecs(d, n, ms, d_outs, d_x, cols, QScratch{d->qx, d->xs, d->xsum}, s);
+}
+
+int rk_graph_begin(rk_device *d) {
+    if (!d) return RK_ERR_ARGS;
+    Hold hold(d->gate);
+    if (d->capturing) return fail(d, RK_ERR_ARGS, "rk_graph_begin: already recording");
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "graph begin");
+    HIP_TRY(d, hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal), "graph begin");
+    d->capturing = true;
+    return RK_OK;
+}
+
+int rk_graph_end(rk_device *d, rk_graph **out) {
+    if (!d || !out) return RK_ERR_ARGS;
+    *out = nullptr;
+    Hold hold(d->gate);
+    if (!d->capturing) return fail(d, RK_ERR_ARGS, "rk_graph_end: not recording");
+    d->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_TRY(d, hipStreamEndCapture(d->stream, &g), "graph end");
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        (void)hipGetLastError();
+        return hip_fail(d, e, "graph instantiate");
+    }
+    rk_graph *gr = new rk_graph();
+    gr->d = d;
+    gr->graph = g;
+    gr->exec = ex;
+    *out = gr;
+    return RK_OK;
+}
+
+int rk_graph_launch(rk_graph *g, int32_t times) {
+    if (!g || times < 0) return RK_ERR_ARGS;
+    rk_device *d = g->d;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    for (int32_t i = 0; i < times; i++) HIP_TRY(d, hipGraphLaunch(g->exec, d->stream), "graph launch");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "graph wait");
+    return RK_OK;
+}
+
+int rk_graph_free(rk_graph *g) {
+    if (!g) return RK_ERR_ARGS;
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+    return RK_OK;
 }
 
 int rk_profile_start(rk_device *d) {

@@ -68,6 +68,10 @@ SIGNATURES = {
     "rk_batch_residual": (ctypes.c_int, [P, I64, I64, I64, I32]),
     "rk_batch_silumul": (ctypes.c_int, [P, I64, I64, I64]),
     "rk_batch_submit": (ctypes.c_int, [P]),
+    "rk_graph_begin": (ctypes.c_int, [P]),
+    "rk_graph_end": (ctypes.c_int, [P, P]),
+    "rk_graph_launch": (ctypes.c_int, [P, I32]),
+    "rk_graph_free": (ctypes.c_int, [P]),
     "rk_profile_start": (ctypes.c_int, [P]),
     "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
 }
@@ -305,3 +309,26 @@ class Device:
         h = P()
         self._check(lib().rk_vectors_upload(self.h, _ptr(v), v.size, ctypes.byref(h)))
         return Vectors(self, h, v.size)
+
+    def graph_begin(self):
+        self._check(lib().rk_graph_begin(self.h))
+
+    def graph_end(self):
+        h = P()
+        self._check(lib().rk_graph_end(self.h, ctypes.byref(h)))
+        return Graph(self, h)
+
+
+class Graph:
+    """Recorded device work, replayed by launch (rk_graph_*)."""
+
+    def __init__(self, dev, handle):
+        self.dev, self.h = dev, handle
+
+    def launch(self, times=1):
+        self.dev._check(lib().rk_graph_launch(self.h, times))
+
+    def free(self):
+        if self.h:
+            lib().rk_graph_free(self.h)
+            self.h = None
