@@ -161,3 +161,37 @@ def test_device_pointers(dev):
     a.free()
     m.free()
     assert dev.used == 0
+
+
+def test_graph_replays_match(dev):
+    """Products recorded once into a graph and replayed: each replay reads
+    the arena's current input (changed by eager batches between replays)
+    and gives the oracle's bits for it."""
+    rng = np.random.default_rng(25)
+    cols = 2048
+    q8 = rng.integers(-127, 128, 1000 * cols, dtype=np.int8)
+    s8 = rng.uniform(1e-3, 1e-2, 1000 * cols // 32).astype(np.float32)
+    q4 = rng.integers(0, 256, 300 * cols // 2, dtype=np.uint8)
+    s4 = rng.uniform(1e-3, 1e-2, 300 * cols // 32).astype(np.float32)
+    m8, m4 = dev.upload_q8(q8, s8, 1000, cols), dev.upload_q4(q4, s4, 300, cols)
+    a = dev.arena(cols + 1300, cols + 1300)
+    dev.graph_begin()
+    dev.matvecs_device([m8, m4], [a.device_ptr(cols), a.device_ptr(cols + 1000)], a.device_ptr(0), cols)
+    g = dev.graph_end()
+    for rep in range(4):
+        x = rng.normal(0, 1, cols).astype(np.float32)
+        b = a.begin()
+        b.write(0, x)
+        b.write(cols, np.full(1300, np.nan, np.float32))  # stale outputs would show
+        b.submit()
+        g.launch(1)
+        b = a.begin()
+        o8, o4 = b.read(cols, 1000), b.read(cols + 1000, 300)
+        b.submit()
+        same_bits(o8, oracle.matvec_q8(q8, s8, x, 1000, cols), f"replay {rep} q8")
+        same_bits(o4, oracle.matvec_q4(q4, s4, x, 300, cols), f"replay {rep} q4")
+    g.free()
+    a.free()
+    m8.free()
+    m4.free()
+    assert dev.used == 0
