@@ -186,6 +186,81 @@ int rk_graph_end(rk_device *dev, rk_graph **out);
 int rk_graph_launch(rk_graph *g, int32_t times);
 int rk_graph_free(rk_graph *g);
 
+/* ---- Stages: a run of llama-family layers resident on one device ----
+ * internal/llm/gpustage.go (gpuStage): the layers' products, attention and
+ * caches run on the device; Stage.ForwardMany (internal/llm/model.go:
+ * 488-502) hands it token activations. This build fuses the stage: each
+ * product's kernel also does the RMSNorm and Q8 quantization of its input
+ * and the step after it (bias, RoPE and the cache store, SiLU·mul, the
+ * residual add), and every position-dependent value (position, length,
+ * tokens) is read from device memory, so one token is recorded once as a
+ * HIP graph and replayed at every position. Results are the CPU path's
+ * bits (Stage.Forward, internal/llm/model.go:522-613). */
+typedef struct rk_stage rk_stage;
+
+typedef struct {
+    int32_t dim, hidden, heads, kv_heads;
+    int32_t head_dim;   /* 0: dim/heads (internal/llm/model.go:66-71) */
+    int32_t ctx;        /* positions the caches hold */
+    int32_t qkv_bias;   /* Qwen2: q, k, v biases */
+    int32_t qk_norm;    /* Qwen3: per-head RMSNorm of q and k before RoPE */
+    float norm_eps;     /* Config.eps() (model.go:80-85) */
+    float recip_dim;    /* num.Recip32(float32(dim)) (gpustage.go:124) */
+    float recip_head;   /* num.Recip32(float32(head size)) (gpustage.go:125) */
+    float inv_sqrt;     /* float32(1/math.Sqrt(float64(head size))) (gpustage.go:126) */
+} rk_stage_config;
+
+/* One layer: its uploaded Q8/Q4 matrices (internal/llm/model.go:150-166
+ * Layer) and host copies of its vectors (NULL when the config has none). */
+typedef struct {
+    rk_matrix *wq, *wk, *wv, *wo, *w1, *w2, *w3;
+    const float *rms_att, *rms_ffn; /* dim */
+    const float *bq, *bk, *bv;      /* q_dim, kv_dim, kv_dim (qkv_bias) */
+    const float *q_norm, *k_norm;   /* head size (qk_norm) */
+} rk_stage_layer;
+
+/* internal/llm/gpustage.go:51-83 newGPUStage: caches for ctx positions and
+ * the rotary table rope_cos/rope_sin ([ctx][head size/2], NewRope,
+ * internal/llm/model.go:428-441). Matrices stay owned by the caller and
+ * must outlive the stage. */
+int rk_stage_new(rk_device *dev, const rk_stage_config *c, const rk_stage_layer *layers, int32_t n_layers,
+                 const float *rope_cos, const float *rope_sin, rk_stage **out);
+/* internal/llm/gpustage.go:100-116 forward (Stage.ForwardMany): tokens
+ * activations of dim floats at positions pos.., through the layers, in
+ * place. Blocking. */
+int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens);
+/* Device bytes the stage holds beyond its matrices (internal/llm/
+ * gpustage.go:90-98 ArenaBytes). */
+int64_t rk_stage_bytes(const rk_stage *s);
+/* internal/llm/gpustage.go:85-90 close. */
+int rk_stage_free(rk_stage *s);
+
+/* The coordinator's ends of a generation on the stage's device: the
+ * embedding table (internal/llm/model.go:660-664 Embed), the head's final
+ * RMSNorm and classifier (:667-673 Logits) and greedy sampling
+ * (sample.go:45-53 argmax). embed and wcls may be the same matrix (a
+ * shared classifier); rms_final is dim floats, copied. A stage with a head
+ * holds every layer of the model. */
+int rk_stage_set_head(rk_stage *s, rk_matrix *embed, rk_matrix *wcls, const float *rms_final);
+/* Starts a greedy generation: the prompt's tokens at positions 0..n-1. */
+int rk_stage_generate_start(rk_stage *s, const int32_t *prompt, int32_t n_prompt);
+/* Runs the next `positions` positions (embed, layers, and at the prompt's
+ * last position and after it the logits and the argmax, which becomes the
+ * next position's token). logits, if not NULL, receives each run
+ * position's vocab logits (positions before the prompt's last are left
+ * as they were). Blocking. */
+int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits);
+/* Tokens at positions from..from+n-1 (prompt and generated). */
+int rk_stage_generate_tokens(rk_stage *s, int32_t from, int32_t n, int32_t *out);
+/* start, then run n_prompt+steps-1 positions: steps generated tokens. */
+int rk_stage_generate(rk_stage *s, const int32_t *prompt, int32_t n_prompt, int32_t steps, int32_t *out);
+
+/* ---- The device's float functions (internal/num), for host callers and
+ * tests: out[i] = f(in[i]) computed by the same device code the kernels use.
+ * No reference counterpart (the Go CPU path calls package num directly). */
+enum { RK_FN_RECIP32 = 0, RK_FN_RSQRT32 = 1, RK_FN_EXP32 = 2, RK_FN_SILU = 3 };
+int rk_num_eval(rk_device *dev, int32_t fn, const float *in, float *out, int64_t n);
+
 /* internal/gpu/profile.go:82-109 StartProfile / StopProfile. While a
  * profile is active, every kernel the library launches is bracketed by HIP
  * events on the stream it runs on; stop waits for them and returns, per

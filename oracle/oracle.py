@@ -62,6 +62,7 @@ def _declare(L):
         "rko_rmsnorm": (None, [P, P, P, I64, F32]), "rko_softmax": (None, [P, I64]), "rko_silu": (F32, [F32]),
         "rko_forward": (None, [P, P, I32, P, P, P, P, I32, P, I32, P]),
         "rko_embed": (None, [P, P, I32, P]), "rko_logits": (None, [P, P, P, P, P]), "rko_argmax": (I32, [P, I64]),
+        "rko_num_eval": (None, [ctypes.c_int, P, P, I64]),
         "rko_topk": (None, [P, I32, I32, P]),
         "rko_moe_ffn": (None, [P, P, P, P, I32, I32, P, P, P, P]),
         "rko_tensor_matmul_f32": (None, [P, P, P, I64, I64, I64, ctypes.c_int]),
@@ -90,6 +91,20 @@ def rsqrt32(x):
 
 def exp32(x):
     return np.float32(lib().rko_exp32(np.float32(x)))
+
+
+def num_eval(fn, x):
+    """fn (0 Recip32, 1 Rsqrt32, 2 Exp32, 3 silu) of each of x."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().rko_num_eval(fn, ptr(x), ptr(out), x.size)
+    return out
+
+
+def argmax(v):
+    """internal/llm/sample.go:45-53."""
+    v = np.ascontiguousarray(v, np.float32)
+    return int(lib().rko_argmax(ptr(v), v.size))
 
 
 # ---- vectors and matrices -------------------------------------------------

@@ -682,6 +682,16 @@ void rko_softmax(float *x, int64_t n) {
 /* internal/llm/model.go:657 silu */
 float rko_silu(float v) { return v * rko_recip32(1.0f + rko_exp32(-v)); }
 
+/* Elementwise evaluation for the device-math parity tests: fn 0 Recip32,
+ * 1 Rsqrt32, 2 Exp32, 3 silu (internal/num/recip.go:38-93, num.go:76-97,
+ * internal/llm/model.go:657). */
+void rko_num_eval(int fn, const float *in, float *out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) {
+        float x = in[i];
+        out[i] = fn == 0 ? rko_recip32(x) : fn == 1 ? rko_rsqrt32(x) : fn == 2 ? rko_exp32(x) : rko_silu(x);
+    }
+}
+
 /* internal/llm/model.go:621-625 rotate */
 static void rotate(float *v, int i, float co, float si) {
     float v0 = v[i], v1 = v[i + 1];

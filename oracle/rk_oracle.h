@@ -102,6 +102,7 @@ void rko_rope_table(const rko_config *c, int32_t n, float *cos_t, float *sin_t);
 void rko_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps);
 void rko_softmax(float *x, int64_t n);
 float rko_silu(float v);
+void rko_num_eval(int fn, const float *in, float *out, int64_t n);
 /* One token through layers [0, nlayers) at position pos, x in place.
  * keys/vals: per layer [ctx][kvDim]. scratch: at least
  * 3*dim + 2*qDim + 2*kvDim + 2*hidden + ctx floats. */

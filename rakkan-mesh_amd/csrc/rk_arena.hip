@@ -24,14 +24,6 @@ struct rk_arena {
     int64_t bytes = 0;
 };
 
-// internal/gpu/batch.go:75-80 Vectors.
-struct rk_vectors {
-    rk_device *d = nullptr;
-    float *buf = nullptr;
-    int64_t n = 0;
-    int64_t bytes = 0;
-};
-
 // internal/gpu/batch.go:113-124 Batch.
 struct rk_batch {
     rk_arena *a = nullptr;

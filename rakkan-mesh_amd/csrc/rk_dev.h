@@ -1,0 +1,98 @@
+// rk_dev.h — device helpers shared by the gfx950 kernels: wave-level
+// integer dot products and reductions, the Dot32 summation order, the
+// activation quantizer of one 4-element group, and streaming loads.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rk_fmath.h"
+
+namespace rk {
+
+// 16-byte load marked non-temporal: weights are streamed once per product,
+// so they should not displace the activations kept in the caches.
+typedef int rk_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 load_stream16(const void *p) {
+    const rk_v4i v = __builtin_nontemporal_load(reinterpret_cast<const rk_v4i *>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
+// Exact integer sum of a lane pair (quad_perm [1,0,3,2]).
+__device__ __forceinline__ int pair_sum(int s) { return s + __builtin_amdgcn_mov_dpp(s, 0xB1, 0xF, 0xF, false); }
+
+// acc + Σ w_j·x_j over 16 signed bytes (four v_dot4_i32_i8), exact.
+__device__ __forceinline__ int dot16(int4 w, int4 x, int acc) {
+    acc = __builtin_amdgcn_sdot4(w.x, x.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(w.y, x.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(w.z, x.z, acc, false);
+    acc = __builtin_amdgcn_sdot4(w.w, x.w, acc, false);
+    return acc;
+}
+
+// Dot32 (internal/num/matvec.go:32-66) by the 32 lanes of a half-wave
+// (`hl` = lane in the half): element i goes into running sum i mod 32, in
+// order of i; then e_j = (s_j + s_j+8) + (s_j+16 + s_j+24) and the tree
+// ((e0+e1)+(e2+e3))+((e4+e5)+(e6+e7)). The result is valid in the half's
+// lane 0. Every lane of the wave must call it (cross-lane moves).
+__device__ __forceinline__ float dot32_reduce(float s) {
+    const float s8 = __shfl_down(s, 8, 32), s16 = __shfl_down(s, 16, 32), s24 = __shfl_down(s, 24, 32);
+    const float e = (s + s8) + (s16 + s24);
+    const float p = e + __shfl_down(e, 1, 32);
+    const float q = p + __shfl_down(p, 2, 32);
+    return q + __shfl_down(q, 4, 32);
+}
+
+__device__ __forceinline__ float dot32_half(const float *a, const float *b, int n, int hl, bool valid) {
+    float s = 0.0f;
+    if (valid)
+        for (int i = hl; i < n; i += 32) s += a[i] * b[i];
+    return dot32_reduce(s);
+}
+
+// Q8_0 activation quantizer (internal/num/quant.go:34-53) of one group of
+// four values, eight lanes (aligned) per 32-value block: returns the four
+// codes packed little-endian, and the block's scale and code sum (valid in
+// every lane of the eight). Every lane of the wave must call it.
+__device__ __forceinline__ uint32_t quantize_group(float v0, float v1, float v2, float v3, float &d, int &csum) {
+    float a = gomax(gomax(gomax(0.0f, fabsf(v0)), fabsf(v1)), gomax(fabsf(v2), fabsf(v3)));
+    a = gomax(a, __shfl_xor(a, 1));
+    a = gomax(a, __shfl_xor(a, 2));
+    a = gomax(a, __shfl_xor(a, 4));
+    d = a * u2f(k1_127);
+    const bool zero = (d == 0.0f) || (d != d);
+    const float id = recip32(d);
+    int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+    if (!zero) {
+        c0 = q8_code(v0, id);
+        c1 = q8_code(v1, id);
+        c2 = q8_code(v2, id);
+        c3 = q8_code(v3, id);
+    }
+    int s = c0 + c1 + c2 + c3;
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    csum = s;
+    return (uint32_t)(c0 & 255) | ((uint32_t)(c1 & 255) << 8) | ((uint32_t)(c2 & 255) << 16) |
+           ((uint32_t)(c3 & 255) << 24);
+}
+
+// a = silu(v)·b (internal/llm/model.go:657, :603-605).
+__device__ __forceinline__ float silu_mul(float v, float b) {
+    const float sl = v * recip32(1.0f + exp32(-v));
+    return sl * b;
+}
+
+// Greedy-argmax merge (internal/llm/sample.go:45-53: the first index holding
+// the largest value wins): candidate (v, i) replaces (bv, bi) if it is
+// larger, or equal at a lower index. bi < 0 marks "none yet"; NaNs are never
+// candidates.
+__device__ __forceinline__ void argmax_merge(float &bv, int &bi, float v, int i) {
+    if (i < 0) return;
+    if (bi < 0 || v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+}  // namespace rk

@@ -1,0 +1,96 @@
+// rk_fused.h — the fused quantized products of a llama layer (rk_fused.hip):
+// one kernel streams a product's weights and runs, before it, the input's
+// RMSNorm and Q8 quantization (per workgroup, into LDS) and, after it, what
+// the layer does next to each output row (bias, rotary embedding and cache
+// store, SiLU gate, residual add, greedy argmax).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rk_kernels.h"
+
+namespace rk {
+
+enum : int32_t { kFmtQ8 = 0, kFmtQ4 = 1 };
+
+// Where a product's input comes from.
+enum : int32_t {
+    kProGlobal = 0,  // already quantized (qx, xs, xsum), read from HBM/L2
+    kProQuant = 1,   // f32 x, quantized by each workgroup into LDS
+    kProNorm = 2,    // f32 x, RMSNorm'd (norm_w) then quantized into LDS
+};
+
+// What is done with each output row.
+enum : int32_t {
+    kEpStore = 0,     // out = W·x (+ bias)
+    kEpAdd = 1,       // out += W·x                         (residual, internal/llm/model.go:596-598)
+    kEpAddCanon = 2,  // out = Canonical(out + W·x)          (model.go:608-610)
+    kEpQKV = 3,       // [Wq;Wk;Wv]·x + bias, RoPE on q and k pairs, k and v into the caches at the position
+    kEpSilu = 4,      // rows interleaved W1,W3: h = silu(W1·x)·(W3·x)  (model.go:603-605)
+    kEpLogits = 5,    // logits = W·x and their greedy argmax; the position advances
+};
+
+// Largest input width the LDS prologues take (f32 staging + codes + scales).
+constexpr int kMaxLdsCols = 16384;
+
+// Device control words of a stage: the generation state lives on the GPU so
+// that one recorded token replays unchanged at every position.
+enum : int { kCtlPos = 0, kCtlPrompt = 1, kCtlDone = 2, kCtlWords = 4 };
+
+// Partial (value, index) slots of the argmax epilogue: the most workgroups a
+// logits product may use.
+constexpr int kMaxArgmaxParts = 4096;
+
+struct FusedArgs {
+    MatSeg seg[3];        // Q/K/V, or W1/W3 (interleaved row by row), or one matrix
+    int32_t nseg;
+    int32_t cols;         // input width (multiple of 32)
+    int32_t rows;         // logical output rows (all segments)
+    int32_t rows_per_wg;  // set by the launcher
+    int32_t row_base;     // kEpQKV: logical index of row 0 (a Q/K/V split over two launches)
+    // input
+    const float *x;       // f32 input (kProQuant, kProNorm)
+    const float *norm_w;  // RMSNorm weights (kProNorm)
+    float recip_n, eps;   // Recip32(f32(cols)) and the norm's epsilon
+    const int8_t *qx;     // quantized input (kProGlobal)
+    const float *xs;
+    const int32_t *xsum;
+    // epilogue
+    const float *bias;    // per logical row, or null
+    int32_t *ctl;         // control words (kCtl*)
+    const float *cos_t, *sin_t;  // rotary table [ctx][hs/2]
+    int32_t hs, qdim, kvdim;
+    float *kcache, *vcache;      // this layer's [ctx][kvdim]
+    float *part_v;               // argmax partials (kMaxArgmaxParts)
+    int32_t *part_i;
+    int32_t *tokens;             // token at each position; the argmax writes position+1's
+    int32_t tokens_len;
+    int32_t gate;                // logits: 1 = skip the product at prompt positions before the last
+    // LDS layout (bytes), set by the launcher
+    int32_t lds_xs, lds_xsum, lds_x, lds_bytes;
+};
+
+// Whether an LDS prologue (kProQuant / kProNorm) takes an input of `cols`.
+bool fused_fits(int pro, int cols);
+
+// Enqueues one fused product. fmt: kFmtQ8/kFmtQ4; returns false when the
+// shape does not fit the kernel (cols beyond kMaxLdsCols with an LDS
+// prologue, or too many workgroups for the argmax partials).
+bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s);
+
+// Attention of one position over a stage's cache (internal/llm/model.go:
+// 575-591), position and length read from ctl: scores, then softmax and the
+// weighted values (f32 out).
+void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
+                       int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt, hipStream_t s);
+void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
+                       int ctx, int heads, int kv_heads, int hs, int kv_dim, hipStream_t s);
+// QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches.
+void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                        float recip_hs, float eps, const float *cos_t, const float *sin_t, const int32_t *ctl,
+                        float *kcache, float *vcache, int heads, int kv_heads, int hs, hipStream_t s);
+// x = the embedding row of tokens[ctl[kCtlPos]] (Q8_0 or Q4_0 table).
+void launch_embed_pos(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, const int32_t *ctl,
+                      int dim, float *x, hipStream_t s);
+
+}  // namespace rk

@@ -108,6 +108,14 @@ struct rk_matrix {
     int64_t bytes = 0;
 };
 
+// internal/gpu/batch.go:75-80 Vectors: a layer's norm weights and biases.
+struct rk_vectors {
+    rk_device *d = nullptr;
+    float *buf = nullptr;
+    int64_t n = 0;
+    int64_t bytes = 0;
+};
+
 namespace rk {
 int fail(rk_device *d, int code, const char *fmt, ...);
 int hip_fail(rk_device *d, hipError_t e, const char *what);

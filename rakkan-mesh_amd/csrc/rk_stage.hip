@@ -1,0 +1,560 @@
+// rk_stage.hip — stages: llama-family layers resident on one device
+// (internal/llm/gpustage.go), and the greedy generation loop around them
+// (embedding, head, argmax) with its state on the device.
+//
+// A token runs as six launches per layer:
+//   qkv      RMSNorm(x)·[Wq;Wk;Wv] (+bias), RoPE, k and v into the caches
+//            (Qwen3: raw q/k/v, then qknorm_rope)
+//   scores   Dot32(q_h, k_t)·invSqrt for t <= position
+//   values   softmax, Σ a_t·v_t
+//   wo       x += Wo·att
+//   w13      h = silu(W1·RMSNorm(x))·(W3·RMSNorm(x))
+//   w2       x = Canonical(x + W2·h)
+// in the order and rounding of Stage.Forward (internal/llm/model.go:522-613).
+// Generation adds the embedding of the position's token before the layers
+// and RMSNorm + classifier + greedy argmax after them; the argmax writes the
+// next token and advances the position on the device. The launches of one
+// token are recorded once into a HIP graph and replayed.
+#include <cstring>
+#include <vector>
+
+#include "rk_fused.h"
+#include "rk_layer.h"
+#include "rk_runtime.h"
+
+// internal/llm/gpustage.go:23-32 gpuStage.
+struct rk_stage {
+    rk_device *d = nullptr;
+    rk_stage_config c{};
+    int hs = 0, qdim = 0, kvdim = 0, half = 0;
+    std::vector<rk_stage_layer> layers;
+    char *mem = nullptr;  // one device allocation for all of the below
+    int64_t bytes = 0;
+    float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *att_out = nullptr;
+    float *h = nullptr, *cos_t = nullptr, *sin_t = nullptr, *part_v = nullptr, *logits = nullptr,
+          *rms_final = nullptr;
+    int32_t *part_i = nullptr, *ctl = nullptr, *tokens = nullptr;
+    int8_t *qx = nullptr;
+    float *xs = nullptr;
+    int32_t *xsum = nullptr;
+    struct LayerDev {
+        float *rms_att, *rms_ffn, *bias, *q_norm, *k_norm;  // device copies
+        float *keys, *vals;
+    };
+    std::vector<LayerDev> ld;
+    // head (rk_stage_set_head)
+    rk_matrix *embed = nullptr, *wcls = nullptr;
+    // pinned staging of rk_stage_forward / generate
+    float *h_x = nullptr;
+    int32_t *h_ctl = nullptr;
+    float *h_logits = nullptr;
+    // recorded tokens: layers only (forward), or the whole generation step
+    hipGraph_t g_layers = nullptr, g_token = nullptr;
+    hipGraphExec_t x_layers = nullptr, x_token = nullptr;
+};
+
+namespace rk {
+
+static constexpr int kForwardBatch = 64;  // tokens per staging round (gpustage.go:17)
+
+static int fmt_of(const rk_matrix *m) { return m->kind == RK_Q4 ? kFmtQ4 : kFmtQ8; }
+
+// One product of a stage: input `in` (f32, `cols` wide; RMSNorm'd with
+// norm_w first when given), matrices ms[0..n) of one format, epilogue epi.
+// The input's norm and quantization run in the product's own prologue when
+// the width fits LDS, else as separate launches into the stage's scratch.
+static int stage_product(rk_stage *s, hipStream_t st, const char *name, const float *in, const float *norm_w,
+                         float recip_n, rk_matrix *const *ms, int n, float *const *outs, int epi, FusedArgs a) {
+    rk_device *d = s->d;
+    const int cols = (int)ms[0]->cols;
+    const int fmt = fmt_of(ms[0]);
+    a.nseg = n;
+    a.cols = cols;
+    int64_t rows = 0;
+    for (int i = 0; i < n; i++) {
+        a.seg[i] = MatSeg{ms[i]->w, ms[i]->scales, outs ? outs[i] : nullptr, ms[i]->rows};
+        rows += ms[i]->rows;
+    }
+    a.rows = (int32_t)rows;
+    int pro = norm_w ? kProNorm : kProQuant;
+    if (fused_fits(pro, cols)) {
+        a.x = in;
+        a.norm_w = norm_w;
+        a.recip_n = recip_n;
+        a.eps = s->c.norm_eps;
+    } else {
+        const float *src = in;
+        if (norm_w) {
+            ProfScope p(d, st, "rmsnorm");
+            launch_rmsnorm(in, s->xb, norm_w, cols, 1, 0, recip_n, s->c.norm_eps, st);
+            src = s->xb;
+        }
+        {
+            ProfScope p(d, st, "quantize_acts");
+            launch_quantize_acts(src, cols, s->qx, s->xs, s->xsum, st);
+        }
+        pro = kProGlobal;
+        a.qx = s->qx;
+        a.xs = s->xs;
+        a.xsum = s->xsum;
+    }
+    bool ok;
+    {
+        ProfScope p(d, st, name);
+        ok = launch_fused(fmt, pro, epi, a, d->cu, st);
+    }
+    if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "stage: %s product of width %d has no kernel", name, cols);
+    return RK_OK;
+}
+
+// The launches of one layer (Stage.Forward's body, model.go:530-611).
+static int enqueue_layer(rk_stage *s, int li, hipStream_t st) {
+    rk_device *d = s->d;
+    const rk_stage_config &c = s->c;
+    const rk_stage_layer &L = s->layers[li];
+    const rk_stage::LayerDev &D = s->ld[li];
+    int rc;
+    FusedArgs base{};
+    base.ctl = s->ctl;
+    base.hs = s->hs;
+    base.qdim = s->qdim;
+    base.kvdim = s->kvdim;
+    // q, k, v: runs of consecutive matrices of one format share a launch.
+    rk_matrix *qkv[3] = {L.wq, L.wk, L.wv};
+    if (!c.qk_norm) {
+        base.cos_t = s->cos_t;
+        base.sin_t = s->sin_t;
+        base.kcache = D.keys;
+        base.vcache = D.vals;
+        base.bias = D.bias;
+        int i = 0, row = 0;
+        while (i < 3) {
+            int j = i + 1;
+            while (j < 3 && qkv[j]->kind == qkv[i]->kind) j++;
+            FusedArgs a = base;
+            a.row_base = row;  // the epilogue indexes q/k/v rows and biases by row_base + row
+            float *outs[3] = {s->q, nullptr, nullptr};  // only q rows store through seg[0]
+            if (i > 0) outs[0] = nullptr;
+            if ((rc = stage_product(s, st, "qkv", s->x, D.rms_att, c.recip_dim, qkv + i, j - i, outs, kEpQKV, a)))
+                return rc;
+            for (int t = i; t < j; t++) row += (int)qkv[t]->rows;
+            i = j;
+        }
+    } else {
+        float *outs[3] = {s->q, s->k, s->v};
+        int i = 0;
+        while (i < 3) {
+            int j = i + 1;
+            while (j < 3 && qkv[j]->kind == qkv[i]->kind) j++;
+            FusedArgs a = base;
+            int row = 0;
+            for (int t = 0; t < i; t++) row += (int)qkv[t]->rows;
+            a.bias = D.bias ? D.bias + row : nullptr;
+            if ((rc = stage_product(s, st, "qkv", s->x, D.rms_att, c.recip_dim, qkv + i, j - i, outs + i, kEpStore,
+                                    a)))
+                return rc;
+            i = j;
+        }
+        ProfScope p(d, st, "qknorm_rope");
+        launch_qknorm_rope(s->q, s->k, s->v, D.q_norm, D.k_norm, c.recip_head, c.norm_eps, s->cos_t, s->sin_t,
+                           s->ctl, D.keys, D.vals, c.heads, c.kv_heads, s->hs, st);
+    }
+    {
+        ProfScope p(d, st, "att_scores");
+        launch_att_scores(s->q, D.keys, s->att, c.ctx, s->ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim,
+                          c.inv_sqrt, st);
+    }
+    {
+        ProfScope p(d, st, "att_values");
+        launch_att_values(s->att, c.ctx, D.vals, s->att_out, s->ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, st);
+    }
+    float *xo[1] = {s->x};
+    if ((rc = stage_product(s, st, "wo", s->att_out, nullptr, 0.0f, &L.wo, 1, xo, kEpAdd, base))) return rc;
+    rk_matrix *w13[2] = {L.w1, L.w3};
+    float *ho[2] = {s->h, nullptr};
+    FusedArgs a13 = base;
+    if ((rc = stage_product(s, st, "w13", s->x, D.rms_ffn, c.recip_dim, w13, 2, ho, kEpSilu, a13))) return rc;
+    // kEpSilu rows are logical: W1 row r and W3 row r interleaved.
+    if ((rc = stage_product(s, st, "w2", s->h, nullptr, 0.0f, &L.w2, 1, xo, kEpAddCanon, base))) return rc;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(d, e, "stage launch");
+    return RK_OK;
+}
+
+static int enqueue_layers(rk_stage *s, hipStream_t st) {
+    for (int li = 0; li < (int)s->layers.size(); li++) {
+        int rc = enqueue_layer(s, li, st);
+        if (rc) return rc;
+    }
+    return RK_OK;
+}
+
+// One generation step: embed the position's token, the layers, the head.
+static int enqueue_token(rk_stage *s, hipStream_t st) {
+    rk_device *d = s->d;
+    {
+        ProfScope p(d, st, "embed");
+        launch_embed_pos(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->tokens, s->ctl, s->c.dim, s->x,
+                         st);
+    }
+    int rc = enqueue_layers(s, st);
+    if (rc) return rc;
+    FusedArgs a{};
+    a.ctl = s->ctl;
+    a.part_v = s->part_v;
+    a.part_i = s->part_i;
+    a.tokens = s->tokens;
+    a.tokens_len = s->c.ctx + 1;
+    a.gate = 1;
+    float *lo[1] = {s->logits};
+    return stage_product(s, st, "logits", s->x, s->rms_final, s->c.recip_dim, &s->wcls, 1, lo, kEpLogits, a);
+}
+
+// Records `which` (layers or a whole token) into a graph, once.
+static int record(rk_stage *s, bool token) {
+    rk_device *d = s->d;
+    hipGraph_t &g = token ? s->g_token : s->g_layers;
+    hipGraphExec_t &x = token ? s->x_token : s->x_layers;
+    if (x) return RK_OK;
+    HIP_TRY(d, hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal), "stage capture");
+    d->capturing = true;
+    int rc = token ? enqueue_token(s, d->stream) : enqueue_layers(s, d->stream);
+    d->capturing = false;
+    hipGraph_t gr = nullptr;
+    hipError_t e = hipStreamEndCapture(d->stream, &gr);
+    if (rc) {
+        if (gr) (void)hipGraphDestroy(gr);
+        return rc;
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return hip_fail(d, e, "stage capture");
+    }
+    e = hipGraphInstantiate(&x, gr, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(gr);
+        (void)hipGetLastError();
+        x = nullptr;
+        return hip_fail(d, e, "stage graph");
+    }
+    g = gr;
+    return RK_OK;
+}
+
+// Runs the recorded layers / token once on the device stream; while the
+// device profiles, the launches run one by one instead, each timed.
+static int run_once(rk_stage *s, bool token) {
+    rk_device *d = s->d;
+    if (d->profiling) return token ? enqueue_token(s, d->stream) : enqueue_layers(s, d->stream);
+    int rc = record(s, token);
+    if (rc) return rc;
+    HIP_TRY(d, hipGraphLaunch(token ? s->x_token : s->x_layers, d->stream), "stage replay");
+    return RK_OK;
+}
+
+__global__ void set_ctl_kernel(int32_t *ctl, int32_t pos, int32_t prompt) {
+    ctl[kCtlPos] = pos;
+    ctl[kCtlPrompt] = prompt;
+    ctl[kCtlDone] = 0;
+}
+
+static bool valid_mat(const rk_matrix *m, rk_device *d, int64_t rows, int64_t cols) {
+    return m && m->d == d && (m->kind == RK_Q8 || m->kind == RK_Q4) && m->rows == rows && m->cols == cols;
+}
+
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" {
+
+int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *layers, int32_t n_layers,
+                 const float *rope_cos, const float *rope_sin, rk_stage **out) {
+    if (!d || !c || !out || n_layers <= 0 || !layers || !rope_cos || !rope_sin)
+        return fail(d, RK_ERR_ARGS, "rk_stage_new: bad arguments");
+    *out = nullptr;
+    const int hs = c->head_dim > 0 ? c->head_dim : (c->heads > 0 ? c->dim / c->heads : 0);
+    if (c->dim <= 0 || c->hidden <= 0 || c->heads <= 0 || c->kv_heads <= 0 || hs <= 0 || hs % 2 != 0 ||
+        c->heads % c->kv_heads != 0 || c->ctx <= 0 || c->dim % 32 != 0 || c->hidden % 32 != 0 ||
+        (c->heads * hs) % 32 != 0)
+        return fail(d, RK_ERR_ARGS, "rk_stage_new: config out of range");
+    // The softmax keeps a head's weights in LDS (values kernel).
+    if (c->ctx > 16000) return fail(d, RK_ERR_UNSUPPORTED, "rk_stage_new: ctx %d beyond 16000", c->ctx);
+    const int qdim = c->heads * hs, kvdim = c->kv_heads * hs;
+    for (int i = 0; i < n_layers; i++) {
+        const rk_stage_layer &L = layers[i];
+        if (!valid_mat(L.wq, d, qdim, c->dim) || !valid_mat(L.wk, d, kvdim, c->dim) ||
+            !valid_mat(L.wv, d, kvdim, c->dim) || !valid_mat(L.wo, d, c->dim, qdim) ||
+            !valid_mat(L.w1, d, c->hidden, c->dim) || !valid_mat(L.w3, d, c->hidden, c->dim) ||
+            !valid_mat(L.w2, d, c->dim, c->hidden))
+            return fail(d, RK_ERR_ARGS, "rk_stage_new: layer %d: a matrix is missing, of another shape or device, "
+                                        "or not Q8/Q4", i);
+        if (L.w1->kind != L.w3->kind)
+            return fail(d, RK_ERR_UNSUPPORTED, "rk_stage_new: layer %d: W1 and W3 differ in format", i);
+        if (!L.rms_att || !L.rms_ffn || (c->qkv_bias && (!L.bq || !L.bk || !L.bv)) ||
+            (c->qk_norm && (!L.q_norm || !L.k_norm)))
+            return fail(d, RK_ERR_ARGS, "rk_stage_new: layer %d: a vector is missing", i);
+    }
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    rk_stage *s = new rk_stage();
+    s->d = d;
+    s->c = *c;
+    s->hs = hs;
+    s->qdim = qdim;
+    s->kvdim = kvdim;
+    s->half = hs / 2;
+    s->layers.assign(layers, layers + n_layers);
+    // Layout: sizes in bytes, each 256-byte aligned.
+    const int64_t ctx = c->ctx;
+    const int64_t widest = std::max<int64_t>(std::max<int64_t>(c->dim, qdim), c->hidden);
+    int64_t at = 0;
+    std::vector<std::pair<void **, int64_t>> plan;
+    auto take = [&](void **p, int64_t n) { plan.push_back({p, n}); };
+    take((void **)&s->x, 4 * c->dim);
+    take((void **)&s->xb, 4 * widest);
+    take((void **)&s->q, 4 * qdim);
+    take((void **)&s->k, 4 * kvdim);
+    take((void **)&s->v, 4 * kvdim);
+    take((void **)&s->att, 4 * c->heads * ctx);
+    take((void **)&s->att_out, 4 * qdim);
+    take((void **)&s->h, 4 * c->hidden);
+    take((void **)&s->cos_t, 4 * ctx * s->half);
+    take((void **)&s->sin_t, 4 * ctx * s->half);
+    take((void **)&s->part_v, 4 * kMaxArgmaxParts);
+    take((void **)&s->part_i, 4 * kMaxArgmaxParts);
+    take((void **)&s->ctl, 4 * kCtlWords);
+    take((void **)&s->tokens, 4 * (ctx + 1));
+    take((void **)&s->qx, widest);
+    take((void **)&s->xs, 4 * (widest / 32));
+    take((void **)&s->xsum, 4 * (widest / 32));
+    take((void **)&s->rms_final, 4 * c->dim);
+    s->ld.resize(n_layers);
+    const int64_t bias_n = c->qkv_bias ? qdim + 2 * kvdim : 0;
+    for (int i = 0; i < n_layers; i++) {
+        rk_stage::LayerDev &D = s->ld[i];
+        D = rk_stage::LayerDev{};
+        take((void **)&D.rms_att, 4 * c->dim);
+        take((void **)&D.rms_ffn, 4 * c->dim);
+        if (bias_n) take((void **)&D.bias, 4 * bias_n);
+        if (c->qk_norm) {
+            take((void **)&D.q_norm, 4 * hs);
+            take((void **)&D.k_norm, 4 * hs);
+        }
+        take((void **)&D.keys, 4 * ctx * kvdim);
+        take((void **)&D.vals, 4 * ctx * kvdim);
+    }
+    for (auto &pl : plan) at += (pl.second + 255) & ~(int64_t)255;
+    int rc = dev_alloc(d, (void **)&s->mem, (size_t)at, "stage");
+    if (rc) {
+        delete s;
+        return rc;
+    }
+    s->bytes = at;
+    at = 0;
+    for (auto &pl : plan) {
+        *pl.first = s->mem + at;
+        at += (pl.second + 255) & ~(int64_t)255;
+    }
+    auto cleanup = [&](int code) {
+        (void)hipFree(s->mem);
+        if (s->h_x) (void)hipHostFree(s->h_x);
+        if (s->h_ctl) (void)hipHostFree(s->h_ctl);
+        delete s;
+        return code;
+    };
+    hipError_t e = hipMemsetAsync(s->mem, 0, (size_t)s->bytes, d->stream);
+    auto up = [&](void *dst, const void *src, int64_t bytes) {
+        if (e == hipSuccess && bytes > 0) e = hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, d->stream);
+    };
+    up(s->cos_t, rope_cos, 4 * ctx * s->half);
+    up(s->sin_t, rope_sin, 4 * ctx * s->half);
+    for (int i = 0; i < n_layers; i++) {
+        const rk_stage_layer &L = layers[i];
+        rk_stage::LayerDev &D = s->ld[i];
+        up(D.rms_att, L.rms_att, 4 * c->dim);
+        up(D.rms_ffn, L.rms_ffn, 4 * c->dim);
+        if (bias_n) {
+            up(D.bias, L.bq, 4 * qdim);
+            up(D.bias + qdim, L.bk, 4 * kvdim);
+            up(D.bias + qdim + kvdim, L.bv, 4 * kvdim);
+        }
+        if (c->qk_norm) {
+            up(D.q_norm, L.q_norm, 4 * hs);
+            up(D.k_norm, L.k_norm, 4 * hs);
+        }
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return cleanup(hip_fail(d, e, "stage upload"));
+    }
+    if ((e = hipHostMalloc((void **)&s->h_x, (size_t)4 * kForwardBatch * c->dim, hipHostMallocDefault)) !=
+            hipSuccess ||
+        (e = hipHostMalloc((void **)&s->h_ctl, (size_t)4 * (ctx + 1 + kCtlWords), hipHostMallocDefault)) !=
+            hipSuccess) {
+        (void)hipGetLastError();
+        return cleanup(hip_fail(d, e, "stage staging"));
+    }
+    add_used(d, s->bytes);
+    *out = s;
+    return RK_OK;
+}
+
+int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens) {
+    if (!s) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    if (tokens < 0 || (tokens > 0 && !xs) || pos < 0 || (int64_t)pos + tokens > s->c.ctx)
+        return fail(d, RK_ERR_ARGS, "gpu stage: positions [%d, %d) outside the context of %d", pos, pos + tokens,
+                    s->c.ctx);
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipStream_t st = d->stream;
+    const int dim = s->c.dim;
+    for (int start = 0; start < tokens; start += kForwardBatch) {
+        const int n = std::min(kForwardBatch, tokens - start);
+        memcpy(s->h_x, xs + (int64_t)start * dim, (size_t)n * dim * 4);
+        for (int t = 0; t < n; t++) {
+            HIP_TRY(d, hipMemcpyAsync(s->x, s->h_x + (int64_t)t * dim, (size_t)dim * 4, hipMemcpyHostToDevice, st),
+                    "stage input");
+            hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, st, s->ctl, pos + start + t, 0);
+            int rc = run_once(s, false);
+            if (rc) return rc;
+            HIP_TRY(d, hipMemcpyAsync(s->h_x + (int64_t)t * dim, s->x, (size_t)dim * 4, hipMemcpyDeviceToHost, st),
+                    "stage output");
+        }
+        HIP_TRY(d, hipStreamSynchronize(st), "stage submit");
+        memcpy(xs + (int64_t)start * dim, s->h_x, (size_t)n * dim * 4);
+    }
+    return RK_OK;
+}
+
+int64_t rk_stage_bytes(const rk_stage *s) { return s ? s->bytes : -1; }
+
+int rk_stage_free(rk_stage *s) {
+    if (!s) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    Hold hold(d->gate);
+    (void)hipSetDevice(d->index);
+    (void)hipStreamSynchronize(d->stream);
+    if (s->x_layers) (void)hipGraphExecDestroy(s->x_layers);
+    if (s->g_layers) (void)hipGraphDestroy(s->g_layers);
+    if (s->x_token) (void)hipGraphExecDestroy(s->x_token);
+    if (s->g_token) (void)hipGraphDestroy(s->g_token);
+    (void)hipFree(s->mem);
+    if (s->h_x) (void)hipHostFree(s->h_x);
+    if (s->h_ctl) (void)hipHostFree(s->h_ctl);
+    if (s->h_logits) (void)hipHostFree(s->h_logits);
+    (void)hipGetLastError();
+    add_used(d, -s->bytes);
+    delete s;
+    return RK_OK;
+}
+
+int rk_stage_set_head(rk_stage *s, rk_matrix *embed, rk_matrix *wcls, const float *rms_final) {
+    if (!s) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    if (!embed || !wcls || !rms_final || embed->d != d || wcls->d != d || embed->cols != s->c.dim ||
+        wcls->cols != s->c.dim || embed->rows != wcls->rows ||
+        (embed->kind != RK_Q8 && embed->kind != RK_Q4) || (wcls->kind != RK_Q8 && wcls->kind != RK_Q4))
+        return fail(d, RK_ERR_ARGS, "rk_stage_set_head: embedding or classifier of the wrong shape or format");
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    if (s->x_token) {
+        (void)hipGraphExecDestroy(s->x_token);
+        (void)hipGraphDestroy(s->g_token);
+        s->x_token = nullptr;
+        s->g_token = nullptr;
+    }
+    if (!s->logits) {
+        int rc = dev_alloc(d, (void **)&s->logits, (size_t)4 * wcls->rows, "logits");
+        if (rc) return rc;
+        hipError_t e = hipHostMalloc((void **)&s->h_logits, (size_t)4 * wcls->rows, hipHostMallocDefault);
+        if (e != hipSuccess) {
+            (void)hipFree(s->logits);
+            s->logits = nullptr;
+            return hip_fail(d, e, "logits staging");
+        }
+        s->bytes += 4 * wcls->rows;
+        add_used(d, 4 * wcls->rows);
+    }
+    HIP_TRY(d, hipMemcpyAsync(s->rms_final, rms_final, (size_t)4 * s->c.dim, hipMemcpyHostToDevice, d->stream),
+            "head upload");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "head upload");
+    s->embed = embed;
+    s->wcls = wcls;
+    return RK_OK;
+}
+
+int rk_stage_generate_start(rk_stage *s, const int32_t *prompt, int32_t n_prompt) {
+    if (!s) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    if (!s->embed) return fail(d, RK_ERR_ARGS, "rk_stage_generate: the stage has no head");
+    if (!prompt || n_prompt <= 0 || n_prompt > s->c.ctx)
+        return fail(d, RK_ERR_ARGS, "rk_stage_generate: prompt of %d tokens for a context of %d", n_prompt, s->c.ctx);
+    const int64_t vocab = s->embed->rows;
+    for (int i = 0; i < n_prompt; i++)
+        if (prompt[i] < 0 || prompt[i] >= vocab)
+            return fail(d, RK_ERR_ARGS, "rk_stage_generate: token %d out of range", prompt[i]);
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "generate start");
+    memcpy(s->h_ctl, prompt, (size_t)n_prompt * 4);
+    HIP_TRY(d, hipMemcpyAsync(s->tokens, s->h_ctl, (size_t)n_prompt * 4, hipMemcpyHostToDevice, d->stream),
+            "prompt upload");
+    hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, d->stream, s->ctl, 0, n_prompt);
+    HIP_TRY(d, hipGetLastError(), "generate start");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "generate start");
+    return RK_OK;
+}
+
+int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits) {
+    if (!s || positions < 0) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    if (!s->embed) return fail(d, RK_ERR_ARGS, "rk_stage_generate: the stage has no head");
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    // The device holds the position; the host checks the context bound.
+    int32_t pos = 0;
+    HIP_TRY(d, hipMemcpyAsync(s->h_ctl + s->c.ctx + 1, s->ctl + kCtlPos, 4, hipMemcpyDeviceToHost, d->stream),
+            "position");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "position");
+    pos = s->h_ctl[s->c.ctx + 1];
+    if ((int64_t)pos + positions > s->c.ctx)
+        return fail(d, RK_ERR_ARGS, "rk_stage_generate: positions [%d, %d) outside the context of %d", pos,
+                    pos + positions, s->c.ctx);
+    const int64_t vocab = s->wcls->rows;
+    for (int32_t i = 0; i < positions; i++) {
+        int rc = run_once(s, true);
+        if (rc) return rc;
+        if (logits) {
+            HIP_TRY(d, hipMemcpyAsync(s->h_logits, s->logits, (size_t)vocab * 4, hipMemcpyDeviceToHost, d->stream),
+                    "logits");
+            HIP_TRY(d, hipStreamSynchronize(d->stream), "generate step");
+            memcpy(logits + (int64_t)i * vocab, s->h_logits, (size_t)vocab * 4);
+        }
+    }
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "generate run");
+    return RK_OK;
+}
+
+int rk_stage_generate_tokens(rk_stage *s, int32_t from, int32_t n, int32_t *out) {
+    if (!s || !out || from < 0 || n < 0 || (int64_t)from + n > s->c.ctx + 1) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "tokens");
+    HIP_TRY(d, hipMemcpyAsync(out, s->tokens + from, (size_t)n * 4, hipMemcpyDeviceToHost, d->stream), "tokens");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "tokens");
+    return RK_OK;
+}
+
+int rk_stage_generate(rk_stage *s, const int32_t *prompt, int32_t n_prompt, int32_t steps, int32_t *out) {
+    if (!s || steps < 0 || (steps > 0 && !out)) return RK_ERR_ARGS;
+    int rc = rk_stage_generate_start(s, prompt, n_prompt);
+    if (rc || steps == 0) return rc;
+    if ((rc = rk_stage_generate_run(s, n_prompt + steps - 1, nullptr))) return rc;
+    return rk_stage_generate_tokens(s, n_prompt, steps, out);
+}
+
+}  // extern "C"

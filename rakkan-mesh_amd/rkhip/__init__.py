@@ -74,7 +74,31 @@ SIGNATURES = {
     "rk_graph_free": (ctypes.c_int, [P]),
     "rk_profile_start": (ctypes.c_int, [P]),
     "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
+    "rk_stage_new": (ctypes.c_int, [P, P, P, I32, P, P, P]),
+    "rk_stage_forward": (ctypes.c_int, [P, P, I32, I32]),
+    "rk_stage_bytes": (I64, [P]),
+    "rk_stage_free": (ctypes.c_int, [P]),
+    "rk_stage_set_head": (ctypes.c_int, [P, P, P, P]),
+    "rk_stage_generate_start": (ctypes.c_int, [P, P, I32]),
+    "rk_stage_generate_run": (ctypes.c_int, [P, I32, P]),
+    "rk_stage_generate_tokens": (ctypes.c_int, [P, I32, I32, P]),
+    "rk_stage_generate": (ctypes.c_int, [P, P, I32, I32, P]),
+    "rk_num_eval": (ctypes.c_int, [P, I32, P, P, I64]),
 }
+
+FN_RECIP32, FN_RSQRT32, FN_EXP32, FN_SILU = 0, 1, 2, 3
+
+
+class StageConfig(ctypes.Structure):
+    """rk_stage_config (include/rk.h)."""
+    _fields_ = [(n, I32) for n in ("dim", "hidden", "heads", "kv_heads", "head_dim", "ctx", "qkv_bias", "qk_norm")] + \
+               [(n, F) for n in ("norm_eps", "recip_dim", "recip_head", "inv_sqrt")]
+
+
+class StageLayer(ctypes.Structure):
+    """rk_stage_layer (include/rk.h)."""
+    _fields_ = [(n, P) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn", "bq", "bk", "bv",
+                                 "q_norm", "k_norm")]
 
 
 def lib():
@@ -310,6 +334,13 @@ class Device:
         self._check(lib().rk_vectors_upload(self.h, _ptr(v), v.size, ctypes.byref(h)))
         return Vectors(self, h, v.size)
 
+    def num_eval(self, fn, x):
+        """The device's restatement of a package-num function on each of x."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        self._check(lib().rk_num_eval(self.h, fn, _ptr(x), _ptr(out), x.size))
+        return out
+
     def graph_begin(self):
         self._check(lib().rk_graph_begin(self.h))
 
@@ -331,4 +362,84 @@ class Graph:
     def free(self):
         if self.h:
             lib().rk_graph_free(self.h)
+            self.h = None
+
+
+class Stage:
+    """A run of llama-family layers on one device (rk_stage_*; the
+    reference's gpuStage, internal/llm/gpustage.go). `layers` is a list of
+    dicts with the uploaded matrices (wq wk wv wo w1 w2 w3: Matrix) and the
+    host vectors (rms_att rms_ffn, and bq bk bv / q_norm k_norm when the
+    config has them). Constants the reference computes with package num
+    (Recip32 of the widths) come from the device's own restatement."""
+
+    def __init__(self, dev, dim, hidden, heads, kv_heads, ctx, layers, rope_cos, rope_sin, head_dim=0,
+                 norm_eps=1e-5, qkv_bias=False, qk_norm=False):
+        hs = head_dim if head_dim > 0 else dim // heads
+        rd, rh = dev.num_eval(FN_RECIP32, np.array([dim, hs], np.float32))
+        inv_sqrt = np.float32(1.0 / np.sqrt(np.float64(hs)))  # float32(1/math.Sqrt(float64(hs)))
+        self.dev, self.dim, self.ctx, self.hs = dev, dim, ctx, hs
+        self.cfg = StageConfig(dim, hidden, heads, kv_heads, head_dim, ctx, int(qkv_bias), int(qk_norm),
+                               float(np.float32(norm_eps)), float(rd), float(rh), float(inv_sqrt))
+        self._keep = []
+        arr = (StageLayer * len(layers))()
+        for i, L in enumerate(layers):
+            vals = {}
+            for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
+                vals[n] = L[n].h
+            for n in ("rms_att", "rms_ffn", "bq", "bk", "bv", "q_norm", "k_norm"):
+                v = L.get(n)
+                if v is not None:
+                    v = np.ascontiguousarray(v, np.float32)
+                    self._keep.append(v)
+                    vals[n] = v.ctypes.data
+                else:
+                    vals[n] = None
+            arr[i] = StageLayer(**vals)
+        cos = np.ascontiguousarray(rope_cos, np.float32)
+        sin = np.ascontiguousarray(rope_sin, np.float32)
+        h = P()
+        dev._check(lib().rk_stage_new(dev.h, ctypes.byref(self.cfg), arr, len(layers), _ptr(cos), _ptr(sin),
+                                      ctypes.byref(h)))
+        self.h = h
+        self.vocab = 0
+
+    def forward(self, xs, pos):
+        """Stage.ForwardMany: rows of xs (tokens x dim) at positions pos.., returned."""
+        xs = np.array(xs, np.float32, copy=True).reshape(-1, self.dim)
+        self.dev._check(lib().rk_stage_forward(self.h, _ptr(xs), pos, xs.shape[0]))
+        return xs
+
+    def set_head(self, embed, wcls, rms_final):
+        rf = np.ascontiguousarray(rms_final, np.float32)
+        self.dev._check(lib().rk_stage_set_head(self.h, embed.h, wcls.h, _ptr(rf)))
+        self.vocab = wcls.rows
+
+    def generate_start(self, prompt):
+        p = np.ascontiguousarray(prompt, np.int32)
+        self.dev._check(lib().rk_stage_generate_start(self.h, _ptr(p), len(p)))
+
+    def generate_run(self, positions, want_logits=False):
+        out = np.empty((positions, self.vocab), np.float32) if want_logits else None
+        self.dev._check(lib().rk_stage_generate_run(self.h, positions, _ptr(out) if want_logits else None))
+        return out
+
+    def tokens(self, start, n):
+        out = np.empty(n, np.int32)
+        self.dev._check(lib().rk_stage_generate_tokens(self.h, start, n, _ptr(out)))
+        return out
+
+    def generate(self, prompt, steps):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(steps, np.int32)
+        self.dev._check(lib().rk_stage_generate(self.h, _ptr(p), len(p), steps, _ptr(out)))
+        return out
+
+    @property
+    def bytes(self):
+        return lib().rk_stage_bytes(self.h)
+
+    def free(self):
+        if self.h:
+            lib().rk_stage_free(self.h)
             self.h = None
