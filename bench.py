@@ -1,21 +1,31 @@
 #!/usr/bin/env python3
 """Benchmark of the Q8 matvec hot path on one MI355X.
 
-A step is one activation vector through config 2's three Q8_0 products
-(4096x4096, 14336x4096, 4096x14336): for each, the input is quantized and
-multiplied, as num.MatVecQ8 does (internal/num/quant.go:167-180). Weights are
-synthetic (codes uniform in [-127, 127], scales U(1e-3, 1e-2)), resident in
-HBM before timing, and rotated over several copies totalling more than the
-256 MB Infinity Cache, so every step streams its weights from HBM.
+Two measurements, one JSON line:
 
-value = algorithmic bytes of a step / step time (GB/s), where a product's
-bytes are rows*cols (codes) + rows*cols/32*4 (scales) + 4*cols (x) +
-4*rows (out). roofline = the matvec_q8 kernel's bytes per launch over its
-average duration, timed with HIP events on its own stream (the library's
-profile). cpu_baseline = the C restatement of the reference CPU path (AVX2
-block sums, rows over threads) on this host, on a bounded sample.
+* value (GB/s): config 2. A step is one activation vector through the three
+  Q8_0 products 4096x4096, 14336x4096 and 4096x14336; each product
+  quantizes its input and multiplies, as num.MatVecQ8 does
+  (internal/num/quant.go:167-180). Weights are synthetic (codes uniform in
+  [-127, 127], scales U(1e-3, 1e-2)), resident in HBM before timing and
+  rotated over copies totalling more than the 256 MB Infinity Cache, so every
+  step streams its weights from HBM. value = algorithmic bytes of a step /
+  step time, a product's bytes being rows*cols (codes) + rows*cols/32*4
+  (scales) + 4*cols (x) + 4*rows (out). The timed steps are HIP graph
+  replays. roofline = the product kernel's bytes per launch over its
+  average duration, each launch stamped with HIP events on its own stream.
+* decode_tok_s: config 3, an 8B-shape llama decoder with random Q8 weights
+  (dim 4096, 32 layers, 32 q / 8 kv heads of 128, SwiGLU 14336, vocab
+  128256, RoPE theta 5e5, f32 KV cache): greedy decode of 256 tokens after
+  a 512-token seeded prompt, entirely on the device (one recorded graph per
+  token). decode_tok_s = decoded tokens / decode wall time.
+
+cpu_baseline: the C restatement of the reference CPU path (AVX2 block sums,
+rows over threads; test infrastructure under oracle/) on this host, on a
+bounded sample of config 2, bit-compared with the GPU's outputs.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -29,16 +39,22 @@ sys.path.insert(0, ROOT)
 
 SHAPES = [(4096, 4096), (14336, 4096), (4096, 14336)]
 HBM_PEAK_GBS = 8000.0
+METRIC = "Q8 matvec HBM GB/s (% of peak) + decode tok/s, 8B-shape batch 1"
 
 
 def q8_bytes(rows, cols):
     return rows * cols + rows * (cols // 32) * 4 + 4 * cols + 4 * rows
 
 
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
 def cpu_baseline(q_all, s_all, xs, threads, budget_s):
     """Times the oracle's AVX2 restatement (internal/num/dot_amd64.s block
-    sums, quant.go qrow, rows split as matvec.go:90-104) on the same shapes
-    for about budget_s seconds, and returns GB/s plus its outputs."""
+    sums, quant.go qrow, rows split as matvec.go:90-104) on the config-2
+    shapes for about budget_s seconds; returns GB/s, passes, seconds and the
+    first pass's outputs."""
     from oracle import oracle
 
     outs = [oracle.matvec_q8_avx2(q, s, x, r, c, threads) for (r, c), q, s, x in zip(SHAPES, q_all, s_all, xs)]
@@ -52,26 +68,7 @@ def cpu_baseline(q_all, s_all, xs, threads, budget_s):
     return gbs, reps, el, outs
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=300)
-    ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--sets", type=int, default=4, help="weight copies rotated per step (>256 MB total)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py runs on one GPU only: this build has no multi-GPU path (row-sharding is described in "
-              "DESIGN.md, not built). Use --gpus 1.", file=sys.stderr)
-        sys.exit(2)
-
-    import ctypes
-
-    import rkhip
-
-    dev = rkhip.Device(0)
-    info = rkhip.device_info(0)
+def matvec_bench(dev, rkhip, args):
     rng = np.random.default_rng(1)
     q_all, s_all = [], []
     for r, c in SHAPES:
@@ -79,7 +76,6 @@ def main():
         s_all.append(rng.uniform(1e-3, 1e-2, r * c // 32).astype(np.float32))
     xs = [rng.normal(0, 1, c).astype(np.float32) for _, c in SHAPES]
     sets = [[dev.upload_q8(q, s, r, c) for (r, c), q, s in zip(SHAPES, q_all, s_all)] for _ in range(args.sets)]
-    # inputs and outputs in one arena (HBM)
     x_off, out_off, at = [], [], 0
     for _, c in SHAPES:
         x_off.append(at)
@@ -114,8 +110,7 @@ def main():
                 if rc:
                     raise rkhip.RKError(rc, L.rk_last_error(dev.h).decode())
 
-    # The timed steps run as HIP graph replays (one graph = one step per
-    # weight copy), so the host's per-call cost does not pace the GPU.
+    # Timed steps: HIP graph replays (one graph = one step per weight copy).
     run(1, 0)
     sync()
     dev.graph_begin()
@@ -133,72 +128,47 @@ def main():
     if g_rem:
         g_rem.launch(1)
     t1 = time.perf_counter()
-    # The same steps again, eagerly, with each kernel's dispatch stamped by
-    # HIP events on its own stream (the library's profile): per-kernel times.
-    dev.profile_start()
-    run(args.steps, args.warmup)
-    sync()
-    prof = dev.profile_stop()
     ms_per_step = (t1 - t0) / args.steps * 1e3
     step_bytes = sum(q8_bytes(r, c) for r, c in SHAPES)
     value = step_bytes / (ms_per_step / 1e3) / 1e9
 
+    # The same steps eagerly, each launch stamped by HIP events on its stream.
+    dev.profile_start()
+    run(args.steps, args.warmup)
+    sync()
+    prof = dev.profile_stop()
     calls_mv, ms_mv = prof.get("matvec_q8", (0, 0.0))
     avg_launch_ms = ms_mv / max(calls_mv, 1)
-    bytes_per_launch = step_bytes / per_step  # average over the three shapes
+    bytes_per_launch = step_bytes / per_step  # the three shapes, equally often
     achieved = bytes_per_launch / (avg_launch_ms / 1e3) / 1e9
 
-    # per-shape kernel times in a second, profiled pass (one shape at a time)
     per_shape = {}
     for i, (r, c) in enumerate(SHAPES):
         dev.profile_start()
-        for st in range(50):
+        for st in range(100):
             hs, ops, xp, cc = calls[(st % args.sets) * per_step + i]
             L.rk_matvecs_device(dev.h, 1, hs, ops, xp, cc, None)
         sync()
         p = dev.profile_stop()
-        n, ms = p["matvec_q8"]
-        us = ms / n * 1e3
-        per_shape[f"{r}x{c}"] = {"kernel_us": round(us, 3), "GB/s": round(q8_bytes(r, c) / (us / 1e6) / 1e9, 1),
-                                 "frac": round(q8_bytes(r, c) / (us / 1e6) / 1e9 / HBM_PEAK_GBS, 4)}
+        entry = {}
+        for k, (n, ms) in p.items():
+            entry[k + "_us"] = round(ms / n * 1e3, 3)
+        us = p["matvec_q8"][1] / p["matvec_q8"][0] * 1e3
+        entry["GB/s"] = round(q8_bytes(r, c) / (us / 1e6) / 1e9, 1)
+        entry["frac"] = round(q8_bytes(r, c) / (us / 1e6) / 1e9 / HBM_PEAK_GBS, 4)
+        per_shape[f"{r}x{c}"] = entry
 
-    result = {
-        "metric": "Q8 matvec HBM GB/s (% of peak) + decode tok/s, 8B-shape batch 1",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
+    out = {
+        "value": round(value, 2), "ms_per_step": round(ms_per_step, 5),
         "data": "synthetic: Q8_0 codes U[-127,127], scales U(1e-3,1e-2), x N(0,1); weights rotated over "
                 f"{args.sets} HBM copies ({args.sets * step_bytes / 1e6:.0f} MB)",
-        "config": {"workload": "config 2: Q8_0 group-32 matvec, batch 1, shapes 4096x4096 + 14336x4096 + "
-                               "4096x14336 per step (quantize + product each)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "matvec_q8", "avg_launch_us": round(avg_launch_ms * 1e3, 3),
-                     "bytes_per_launch": bytes_per_launch},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "matvec_q8",
+                     "avg_launch_us": round(avg_launch_ms * 1e3, 3), "bytes_per_launch": bytes_per_launch},
         "per_shape": per_shape,
         "kernels_ms": {k: [v[0], round(v[1], 4)] for k, v in prof.items()},
-        "decode_tok_s": None,
-        "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cu": info.compute_units},
     }
-    if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        gbs, reps, el, outs = cpu_baseline(q_all, s_all, xs, threads, args.cpu_seconds)
-        gpu_outs = []
-        ms0 = sets[0]
-        for i, (r, c) in enumerate(SHAPES):
-            gpu_outs.append(dev.matvec(ms0[i], xs[i]))
-        exact = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(outs, gpu_outs))
-        result["cpu_baseline"] = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
-                                  "sample": f"{reps} passes over the three config-2 products in {el:.1f} s "
-                                            "(C restatement of the reference CPU path, AVX2, rows over threads)",
-                                  "bit_exact_vs_gpu": bool(exact)}
+    gpu_outs = [dev.matvec(sets[0][i], xs[i]) for i in range(len(SHAPES))]
     g_full.free()
     if g_rem:
         g_rem.free()
@@ -206,6 +176,163 @@ def main():
     for st in sets:
         for m in st:
             m.free()
+    return out, (q_all, s_all, xs, gpu_outs)
+
+
+def rope_table(theta, hs, n):
+    """Rotary table [n][hs/2] (NewRope's formula, internal/llm/model.go:
+    428-441) in numpy float64: a synthetic input here, timing only."""
+    half = hs // 2
+    p = np.arange(half, dtype=np.float64)
+    freq = np.exp(-np.log(theta) * (2 * p) / hs)
+    ang = np.arange(n, dtype=np.float64)[:, None] * freq[None, :]
+    return np.cos(ang).astype(np.float32).ravel(), np.sin(ang).astype(np.float32).ravel()
+
+
+def decode_bench(dev, rkhip, args):
+    """Config 3: 8B-shape Q8 decoder, greedy, entirely on the device."""
+    dim, hidden, heads, kv_heads, hs, vocab = 4096, 14336, 32, 8, 128, 128256
+    layers, prompt_len, steps = args.layers, args.prompt, args.decode
+    ctx = prompt_len + steps
+    kvdim = kv_heads * hs
+    rng = np.random.default_rng(3)
+    # Codes come from one random pool at per-matrix offsets (distinct
+    # matrices without generating 8 GB on the host); scales keep the
+    # activations finite through the layers.
+    pool = rng.integers(-127, 128, vocab * dim + (1 << 20), dtype=np.int8)
+    spool = rng.uniform(2e-5, 2e-4, vocab * dim // 32 + (1 << 16)).astype(np.float32)
+    mats = []
+
+    def mat(rows, cols):
+        n = rows * cols
+        o = int(rng.integers(0, pool.size - n + 1))
+        so = int(rng.integers(0, spool.size - n // 32 + 1))
+        m = dev.upload_q8(pool[o:o + n], spool[so:so + n // 32], rows, cols)
+        mats.append(m)
+        return m
+
+    t0 = time.perf_counter()
+    lay = []
+    for li in range(layers):
+        lay.append({"wq": mat(dim, dim), "wk": mat(kvdim, dim), "wv": mat(kvdim, dim), "wo": mat(dim, dim),
+                    "w1": mat(hidden, dim), "w2": mat(dim, hidden), "w3": mat(hidden, dim),
+                    "rms_att": rng.normal(1, 0.1, dim).astype(np.float32),
+                    "rms_ffn": rng.normal(1, 0.1, dim).astype(np.float32)})
+    embed, wcls = mat(vocab, dim), mat(vocab, dim)
+    log(f"decode bench: {layers} layers uploaded in {time.perf_counter() - t0:.1f} s")
+    cos, sin = rope_table(500000.0, hs, ctx)
+    st = rkhip.Stage(dev, dim, hidden, heads, kv_heads, ctx, lay, cos, sin, head_dim=hs, norm_eps=1e-5)
+    st.set_head(embed, wcls, rng.normal(1, 0.1, dim).astype(np.float32))
+    prompt = rng.integers(0, vocab, prompt_len).astype(np.int32)
+
+    if args.eager:  # one launch at a time (for tools that cannot follow graph replays)
+        dev.profile_start()
+    # warm-up: records the graph, touches every weight once
+    st.generate_start(prompt)
+    st.generate_run(4)
+    st.generate_start(prompt)
+    t0 = time.perf_counter()
+    st.generate_run(prompt_len)  # positions 0..prompt-1; the last yields the first new token
+    t1 = time.perf_counter()
+    st.generate_run(steps - 1)   # each position: layers + logits + argmax -> the next token
+    t2 = time.perf_counter()
+    if args.eager:
+        dev.profile_stop()
+    toks = st.tokens(prompt_len, steps)
+    decode_s = t2 - t1
+    tok_s = (steps - 1) / decode_s
+    # per-kernel times over 8 decode positions after the prompt (launched one
+    # by one while profiling, each launch stamped by HIP events)
+    if args.eager:
+        dev.profile_start()
+    st.generate_start(prompt)
+    st.generate_run(prompt_len)
+    if args.eager:
+        dev.profile_stop()
+    dev.profile_start()
+    st.generate_run(8)
+    prof = dev.profile_stop()
+    weight_bytes = sum(m.bytes for m in mats) - embed.bytes
+    kv_bytes = layers * 2 * kvdim * 4 * (prompt_len + steps / 2)  # average positions read per decode step
+    per_token = weight_bytes + kv_bytes + 4 * vocab
+    ms_tok = decode_s / (steps - 1) * 1e3
+    out = {
+        "decode_tok_s": round(tok_s, 2),
+        "decode": {"config": f"config 3: dim {dim}, {layers} layers, {heads} q / {kv_heads} kv heads of {hs}, "
+                             f"ffn {hidden}, vocab {vocab}, RoPE theta 5e5, f32 KV; greedy {steps} tokens after a "
+                             f"{prompt_len}-token seeded prompt; random Q8 codes, scales U(2e-5, 2e-4)",
+                   "ms_per_token": round(ms_tok, 4), "prefill_s": round(t1 - t0, 4),
+                   "prefill_tok_s": round(prompt_len / (t1 - t0), 2),
+                   "bytes_per_token": int(per_token),
+                   "effective_GB/s": round(per_token / (ms_tok / 1e3) / 1e9, 1),
+                   "frac_of_hbm_peak": round(per_token / (ms_tok / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "first_tokens": [int(t) for t in toks[:8]],
+                   "kernels_us_per_token": {k: round(v[1] / 8 * 1e3, 2) for k, v in prof.items()},
+                   "kernel_launches_per_token": {k: v[0] // 8 for k, v in prof.items()}},
+    }
+    st.free()
+    for m in mats:
+        m.free()
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--sets", type=int, default=4, help="weight copies rotated per step (>256 MB total)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--decode", type=int, default=256)
+    ap.add_argument("--eager", action="store_true", help="decode without graph replays (for profilers)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py runs on one GPU: this build has no multi-GPU path (how the products would shard is "
+              "described in DESIGN.md, not built). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import rkhip
+
+    dev = rkhip.Device(0)
+    info = rkhip.device_info(0)
+    log("matvec bench (config 2)")
+    mv, (q_all, s_all, xs, gpu_outs) = matvec_bench(dev, rkhip, args)
+    result = {
+        "metric": METRIC,
+        "value": mv.pop("value"),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": mv.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": mv.pop("data"),
+        "config": {"workload": "config 2: Q8_0 group-32 matvec, batch 1, shapes 4096x4096 + 14336x4096 + "
+                               "4096x14336 per step (quantize + product each)"},
+    }
+    result.update(mv)
+    result["decode_tok_s"] = None
+    if not args.no_decode:
+        log("decode bench (config 3)")
+        result.update(decode_bench(dev, rkhip, args))
+    result["device"] = {"name": info.name.decode(), "arch": info.arch.decode(), "cu": info.compute_units}
+    if not args.no_cpu:
+        log("cpu baseline")
+        threads = min(16, os.cpu_count() or 1)
+        gbs, reps, el, outs = cpu_baseline(q_all, s_all, xs, threads, args.cpu_seconds)
+        exact = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(outs, gpu_outs))
+        result["cpu_baseline"] = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+                                  "sample": f"{reps} passes over the three config-2 products in {el:.1f} s "
+                                            "(C restatement of the reference CPU path: AVX2 block sums, rows "
+                                            "over threads)",
+                                  "bit_exact_vs_gpu": bool(exact)}
     dev.close()
     print(json.dumps(result))
 

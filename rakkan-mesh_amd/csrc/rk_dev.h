@@ -49,15 +49,80 @@ __device__ __forceinline__ float dot32_half(const float *a, const float *b, int 
     return dot32_reduce(s);
 }
 
+// acc + p[0] + ... + p[N-1] in order (float32), p in LDS, 16-byte aligned:
+// straight-line code, so the compiler issues the reads (immediate offsets
+// from one address) well ahead of the additions that wait on them.
+template <int N>
+__device__ __forceinline__ float lds_sum_fixed(const float *p, float acc) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int k = 0; k < N / 4; k++) {
+        const float4 v = q[k];
+        acc += v.x;
+        acc += v.y;
+        acc += v.z;
+        acc += v.w;
+    }
+    return acc;
+}
+
+// acc + p[0] + p[1] + ... + p[n-1], added one at a time in order (float32),
+// from LDS (p 16-byte aligned), in fixed-size straight-line pieces.
+__device__ __forceinline__ float lds_chain_sum(const float *p, int n, float acc) {
+    int t = 0;
+    for (; t + 128 <= n; t += 128) acc = lds_sum_fixed<128>(p + t, acc);
+    for (; t + 16 <= n; t += 16) acc = lds_sum_fixed<16>(p + t, acc);
+    for (; t < n; t++) acc += p[t];
+    return acc;
+}
+
+// Dot32's running sum of lane j (< 32) for x·x: x_i·x_i for i = j, j+32,
+// ... in order, from LDS holding x transposed (xt[j·pitch + m] = x_{j+32m},
+// pitch a multiple of 4, m < steps), in fixed-size straight-line pieces.
+template <int N>
+__device__ __forceinline__ float lds_sq_fixed(const float *p, float s) {
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+#pragma unroll
+    for (int k = 0; k < N / 4; k++) {
+        const float4 v = q[k];
+        s += v.x * v.x;
+        s += v.y * v.y;
+        s += v.z * v.z;
+        s += v.w * v.w;
+    }
+    return s;
+}
+
+__device__ __forceinline__ float lds_dot32_self_t(const float *xt, int pitch, int steps, int j) {
+    const float *row = xt + j * pitch;
+    float s = 0.0f;
+    int m = 0;
+    for (; m + 64 <= steps; m += 64) s = lds_sq_fixed<64>(row + m, s);
+    for (; m + 16 <= steps; m += 16) s = lds_sq_fixed<16>(row + m, s);
+    for (; m < steps; m++) s += row[m] * row[m];
+    return s;
+}
+
+// Lane exchanges inside aligned groups of eight lanes, by DPP (no LDS
+// round trip): xor 1 and xor 2 are quad permutations, and the half-row
+// mirror (lane i <-> 7-i) pairs each quad with the other. Applied in that
+// order with an associative, commutative operation, every lane of the eight
+// ends with the result over all eight.
+__device__ __forceinline__ int dpp_x1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_x2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+__device__ __forceinline__ int dpp_mirror8(int v) { return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false); }
+
 // Q8_0 activation quantizer (internal/num/quant.go:34-53) of one group of
 // four values, eight lanes (aligned) per 32-value block: returns the four
 // codes packed little-endian, and the block's scale and code sum (valid in
-// every lane of the eight). Every lane of the wave must call it.
+// every lane of the eight). Every lane of the wave must call it. The block
+// maximum (Go max: NaN wins, +0 over -0) and the integer sum are exact in
+// any order.
 __device__ __forceinline__ uint32_t quantize_group(float v0, float v1, float v2, float v3, float &d, int &csum) {
     float a = gomax(gomax(gomax(0.0f, fabsf(v0)), fabsf(v1)), gomax(fabsf(v2), fabsf(v3)));
-    a = gomax(a, __shfl_xor(a, 1));
-    a = gomax(a, __shfl_xor(a, 2));
-    a = gomax(a, __shfl_xor(a, 4));
+    a = gomax(a, __int_as_float(dpp_x1(__float_as_int(a))));
+    a = gomax(a, __int_as_float(dpp_x2(__float_as_int(a))));
+    a = gomax(a, __int_as_float(dpp_mirror8(__float_as_int(a))));
     d = a * u2f(k1_127);
     const bool zero = (d == 0.0f) || (d != d);
     const float id = recip32(d);
@@ -69,9 +134,9 @@ __device__ __forceinline__ uint32_t quantize_group(float v0, float v1, float v2,
         c3 = q8_code(v3, id);
     }
     int s = c0 + c1 + c2 + c3;
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    s += dpp_x1(s);
+    s += dpp_x2(s);
+    s += dpp_mirror8(s);
     csum = s;
     return (uint32_t)(c0 & 255) | ((uint32_t)(c1 & 255) << 8) | ((uint32_t)(c2 & 255) << 16) |
            ((uint32_t)(c3 & 255) << 24);
@@ -93,6 +158,16 @@ __device__ __forceinline__ void argmax_merge(float &bv, int &bi, float v, int i)
         bv = v;
         bi = i;
     }
+}
+
+// 64-bit key of logit v (not NaN) at row i for a max-reduction that picks
+// the first row holding the largest value: the float's order-preserving
+// bits above (-0 taken as +0, which compare equal), the complement of the
+// row below. Never 0.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
+    uint32_t u = f2u(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
 }
 
 }  // namespace rk

@@ -17,7 +17,6 @@ enum : int32_t { kFmtQ8 = 0, kFmtQ4 = 1 };
 enum : int32_t {
     kProGlobal = 0,  // already quantized (qx, xs, xsum), read from HBM/L2
     kProQuant = 1,   // f32 x, quantized by each workgroup into LDS
-    kProNorm = 2,    // f32 x, RMSNorm'd (norm_w) then quantized into LDS
 };
 
 // What is done with each output row.
@@ -35,11 +34,23 @@ constexpr int kMaxLdsCols = 16384;
 
 // Device control words of a stage: the generation state lives on the GPU so
 // that one recorded token replays unchanged at every position.
-enum : int { kCtlPos = 0, kCtlPrompt = 1, kCtlDone = 2, kCtlWords = 4 };
+enum : int { kCtlPos = 0, kCtlPrompt = 1, kCtlWords = 4 };
 
-// Partial (value, index) slots of the argmax epilogue: the most workgroups a
-// logits product may use.
-constexpr int kMaxArgmaxParts = 4096;
+// The classifier's greedy argmax is folded into kArgmaxSlots 64-bit keys
+// (atomicMax, spread over slots so the workgroups do not queue on one
+// address); the key of logit v at row i orders by value, then by lower row.
+constexpr int kArgmaxSlots = 16;
+
+// LDS a workgroup may use on gfx950 (kernels asking more than 64 KiB set
+// their limit first).
+constexpr size_t kMaxLdsBytes = 160 * 1024;
+
+// Largest context the attention-values kernel keeps its weights for.
+int att_values_max_ctx();
+
+// Largest vector a single-workgroup norm keeps in LDS.
+constexpr int kMaxNormCols = 12288;
+
 
 struct FusedArgs {
     MatSeg seg[3];        // Q/K/V, or W1/W3 (interleaved row by row), or one matrix
@@ -49,9 +60,7 @@ struct FusedArgs {
     int32_t rows_per_wg;  // set by the launcher
     int32_t row_base;     // kEpQKV: logical index of row 0 (a Q/K/V split over two launches)
     // input
-    const float *x;       // f32 input (kProQuant, kProNorm)
-    const float *norm_w;  // RMSNorm weights (kProNorm)
-    float recip_n, eps;   // Recip32(f32(cols)) and the norm's epsilon
+    const float *x;       // f32 input (kProQuant)
     const int8_t *qx;     // quantized input (kProGlobal)
     const float *xs;
     const int32_t *xsum;
@@ -61,16 +70,16 @@ struct FusedArgs {
     const float *cos_t, *sin_t;  // rotary table [ctx][hs/2]
     int32_t hs, qdim, kvdim;
     float *kcache, *vcache;      // this layer's [ctx][kvdim]
-    float *part_v;               // argmax partials (kMaxArgmaxParts)
-    int32_t *part_i;
-    int32_t *tokens;             // token at each position; the argmax writes position+1's
-    int32_t tokens_len;
+    unsigned long long *amax;    // logits: kArgmaxSlots keys (zero before the product)
     int32_t gate;                // logits: 1 = skip the product at prompt positions before the last
+    int8_t *qx_out;              // kEpSilu: h quantized for the next product (or null)
+    float *xs_out;
+    int32_t *xsum_out;
     // LDS layout (bytes), set by the launcher
-    int32_t lds_xs, lds_xsum, lds_x, lds_bytes;
+    int32_t lds_xs, lds_xsum, lds_res, lds_ep, lds_bytes;
 };
 
-// Whether an LDS prologue (kProQuant / kProNorm) takes an input of `cols`.
+// Whether the LDS prologue (kProQuant) takes an input of `cols`.
 bool fused_fits(int pro, int cols);
 
 // Enqueues one fused product. fmt: kFmtQ8/kFmtQ4; returns false when the
@@ -83,14 +92,28 @@ bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s)
 // weighted values (f32 out).
 void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
                        int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt, hipStream_t s);
+// With qx non-null (head size a multiple of 32), the output is also
+// quantized (Q8_0 blocks of the next product's input).
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
-                       int ctx, int heads, int kv_heads, int hs, int kv_dim, hipStream_t s);
+                       int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
+                       hipStream_t s);
 // QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches.
 void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                         float recip_hs, float eps, const float *cos_t, const float *sin_t, const int32_t *ctl,
                         float *kcache, float *vcache, int heads, int kv_heads, int hs, hipStream_t s);
-// x = the embedding row of tokens[ctl[kCtlPos]] (Q8_0 or Q4_0 table).
-void launch_embed_pos(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, const int32_t *ctl,
-                      int dim, float *x, hipStream_t s);
+// x = the embedding row of tokens[ctl[kCtlPos]] (Q8_0 or Q4_0 table), and
+// RMSNorm(x) with norm_w quantized into qx/xs/xsum (one workgroup;
+// dim <= kMaxNormCols).
+void launch_embed_norm(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, const int32_t *ctl,
+                       int dim, float *x, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
+                       int32_t *xsum, hipStream_t s);
+// RMSNorm(x) with norm_w quantized into qx/xs/xsum (one workgroup; n <=
+// kMaxNormCols).
+// The greedy argmax's end (internal/llm/sample.go:45-53): folds the
+// classifier's argmax keys into the next token at position+1 (when the
+// position's logits were computed), clears them, and advances the position.
+void launch_advance(int32_t *ctl, unsigned long long *amax, int32_t *tokens, int32_t tokens_len, hipStream_t s);
+void launch_norm_quant(const float *x, int n, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
+                       int32_t *xsum, hipStream_t s);
 
 }  // namespace rk

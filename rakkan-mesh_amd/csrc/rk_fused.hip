@@ -12,9 +12,14 @@
 // A wave streams a row in 1 KiB chunks of codes, one 16-byte piece per lane
 // (coalesced global_load_dwordx4), keeping U chunks in flight. The input's
 // quantized form is either read like the weights (kProGlobal) or made by
-// the workgroup itself into LDS before the stream starts (kProQuant,
-// kProNorm): the input's loads are issued first, then the first weight
-// chunks, so the prologue runs while those weights are on their way.
+// the workgroup itself into LDS before the stream starts (kProQuant): the
+// input's loads are issued first, then the first weight chunks, so the
+// prologue runs while those weights are on their way. Results wait in LDS
+// and leave coalesced at the end; a residual product's last workgroup may
+// then RMSNorm and quantize the whole updated vector for the next product.
+#include <algorithm>
+#include <mutex>
+
 #include "rk_dev.h"
 #include "rk_fused.h"
 
@@ -65,14 +70,67 @@ __device__ __forceinline__ RowSrc row_src(const FusedArgs &a, int l, int rowbyte
 
 }  // namespace
 
+// RMSNorm (internal/llm/model.go:632-638: ss = Dot32(x,x)·recip_n + eps,
+// out_i = w_i·(Rsqrt32(ss)·x_i)) of x, then the Q8_0 quantization
+// (internal/num/quant.go:34-53) of the result into qx/xs/xsum: the input of
+// the next product. Thread t holds groups g = t + k·NT (four values each)
+// of x and w in registers, loaded before the call; sx is LDS for n floats.
+// Every thread of the NT-thread workgroup calls it.
+template <int NT, int MAXG>
+__device__ void wg_norm_quant(const float4 *xv, const float4 *wv, int n, float recip_n, float eps, int8_t *qx,
+                              float *xs, int32_t *xsum, float *sx, float *bcast) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int ng = n >> 2;
+    // x transposed for Dot32: xt[j·pitch + m] = x_{j+32m} (n a multiple of 32)
+    const int steps = n >> 5, pitch = ((steps + 3) & ~3) + 4;
+#pragma unroll
+    for (int k = 0; k < MAXG; k++) {
+        const int g = tid + k * NT;
+        if (g < ng) {
+            const int i = 4 * g;
+            float *d = sx + (i & 31) * pitch + (i >> 5);
+            d[0] = xv[k].x;
+            d[pitch] = xv[k].y;
+            d[2 * pitch] = xv[k].z;
+            d[3 * pitch] = xv[k].w;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const float s = lane < 32 ? lds_dot32_self_t(sx, pitch, steps, lane) : 0.0f;
+        const float dot = dot32_reduce(s);
+        if (lane == 0) *bcast = rsqrt32((dot * recip_n) + eps);
+    }
+    __syncthreads();
+    const float r = *bcast;
+#pragma unroll
+    for (int k = 0; k < MAXG; k++) {
+        if (k * NT < ng) {  // uniform
+            const int g = tid + k * NT;
+            float d;
+            int cs;
+            const uint32_t pk = quantize_group(wv[k].x * (r * xv[k].x), wv[k].y * (r * xv[k].y),
+                                               wv[k].z * (r * xv[k].z), wv[k].w * (r * xv[k].w), d, cs);
+            if (g < ng) {
+                reinterpret_cast<uint32_t *>(qx)[g] = pk;
+                if ((g & 7) == 0) {
+                    xs[g >> 3] = d;
+                    xsum[g >> 3] = cs;
+                }
+            }
+        }
+    }
+}
+
 template <int FMT, int PRO, int EPI, int W, int U>
 __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
     extern __shared__ __align__(16) char lds[];
-    __shared__ float s_bcast;
     __shared__ float s_wv[W];
     __shared__ int s_wi[W];
-    __shared__ int s_last;
     constexpr bool PAIR = (EPI == kEpQKV || EPI == kEpSilu);
+    // epilogues that need one value per row read before the stream: the
+    // output being added to, or the row's bias
+    constexpr bool PRE = (EPI == kEpAdd || EPI == kEpAddCanon || EPI == kEpStore || EPI == kEpQKV);
     constexpr int NT = 64 * W;
     constexpr int MAXG = PRO == kProGlobal ? 1 : (kMaxLdsCols / 4 + NT - 1) / NT;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -81,15 +139,28 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
     const int C = FMT == kFmtQ8 ? (cols + 1023) >> 10 : (nb + 63) >> 6;
 
     int pos = 0;
-    bool work = true;
     if (EPI == kEpQKV || EPI == kEpLogits) pos = a.ctl[kCtlPos];
-    if (EPI == kEpLogits && a.gate && pos + 1 < a.ctl[kCtlPrompt]) work = false;
+    const bool work = !(EPI == kEpLogits && a.gate && pos + 1 < a.ctl[kCtlPrompt]);
 
     const int R0 = blockIdx.x * a.rows_per_wg;
     const int R1 = min(a.rows, R0 + a.rows_per_wg);
-    const int n = R1 - R0;
-    int nrows = 0;
+    const int n = R1 - R0;  // >= 1: the launcher sizes the grid to the rows
+    const int half = a.hs >> 1;
+    int8_t *sqx = reinterpret_cast<int8_t *>(lds);
+    float *sxs = reinterpret_cast<float *>(lds + a.lds_xs);
+    int *sxsum = reinterpret_cast<int *>(lds + a.lds_xsum);
+    float *sres = reinterpret_cast<float *>(lds + a.lds_res);  // the workgroup's results
+    float *sep = reinterpret_cast<float *>(lds + a.lds_ep);    // per-row operands, then cos, sin
+    float best_v = 0.0f;
+    int best_i = -1;
+
+    // Everything below keeps the main loop free of loads other than the
+    // weight stream and of global stores, so each wait there is for the
+    // oldest chunk only: the loads before it are unconditional (addresses
+    // clamped into the buffers, unused values masked), per-row operands are
+    // staged in LDS first and results leave through LDS at the end.
     if (work) {
+        int nrows = 0;
         if (PAIR) {
             const int np = (n + 1) >> 1;
             if (wave < np) {
@@ -99,288 +170,293 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
         } else {
             nrows = wave < n ? (n - 1 - wave) / W + 1 : 0;
         }
-    }
-    const int nsteps = nrows * C;
-
-    // Row cursors: PAIR waves take pairs wave, wave+W, ... (both rows of
-    // each, in order); the others rows wave, wave+W, ...
-    auto row_of = [&](int p, int h) { return PAIR ? R0 + 2 * p + h : R0 + p; };
-    auto next_row = [&](int &p, int &h) {
-        if (PAIR) {
-            if (h == 0 && R0 + 2 * p + 1 < R1) {
-                h = 1;
+        const int nsteps = nrows * C;
+        // Row cursors: PAIR waves take pairs wave, wave+W, ... (both rows of
+        // each, in order); the others rows wave, wave+W, ...
+        auto row_of = [&](int p, int h) { return PAIR ? R0 + 2 * p + h : R0 + p; };
+        auto next_row = [&](int &p, int &h) {
+            if (PAIR) {
+                if (h == 0 && R0 + 2 * p + 1 < R1) {
+                    h = 1;
+                } else {
+                    p += W;
+                    h = 0;
+                }
             } else {
                 p += W;
-                h = 0;
             }
-        } else {
-            p += W;
-        }
-    };
+        };
 
-    // ---- input loads (LDS prologues): issued before any weight ----
-    float4 xv[MAXG];
-    float4 nw[PRO == kProNorm ? MAXG : 1];
-    if (PRO != kProGlobal && work) {
+        // ---- (1) loads the prologue needs: the input (and norm weights),
+        // the rows' epilogue operands, the rotary row ----
+        float4 xv[MAXG];
+        if (PRO != kProGlobal) {
+            const int ng = cols >> 2;
 #pragma unroll
-        for (int k = 0; k < MAXG; k++) {
-            const int g = threadIdx.x + k * NT;
-            xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (g < (cols >> 2)) xv[k] = reinterpret_cast<const float4 *>(a.x)[g];
-            if (PRO == kProNorm) {
-                nw[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (g < (cols >> 2)) nw[k] = reinterpret_cast<const float4 *>(a.norm_w)[g];
+            for (int k = 0; k < MAXG; k++) {
+                const int g = min((int)threadIdx.x + k * NT, ng - 1);
+                xv[k] = reinterpret_cast<const float4 *>(a.x)[g];
             }
         }
-    }
-
-    // ---- weight stream: U chunks in flight ----
-    int lp = wave, lh = 0, lc = 0;
-    RowSrc ls = row_src<EPI>(a, row_of(lp, lh), rowbytes, nb);
-    int4 wb[U], xb0[U], xb1[U];
-    float sb[U], xsb[U];
-    int xsumb[U];
-    auto load = [&](int j) {
-        wb[j] = make_int4(0, 0, 0, 0);
-        sb[j] = 0.0f;
-        if (PRO == kProGlobal) {
-            xb0[j] = xb1[j] = make_int4(0, 0, 0, 0);
-            xsb[j] = 0.0f;
-            xsumb[j] = 0;
+        float epv = 0.0f, cosv = 0.0f, sinv = 0.0f;
+        if (PRE) {
+            const int i = min((int)threadIdx.x, n - 1);
+            const bool add = EPI == kEpAdd || EPI == kEpAddCanon;
+            // no bias: read a word known to exist, unused
+            const float *src = add ? a.seg[0].out + R0 : a.bias ? a.bias + a.row_base + R0 : a.seg[0].ws;
+            epv = src[(add || a.bias) ? i : 0];
+            if (EPI == kEpQKV) {
+                const int p = min((int)threadIdx.x, half - 1);
+                cosv = a.cos_t[(int64_t)pos * half + p];
+                sinv = a.sin_t[(int64_t)pos * half + p];
+            }
         }
-        if (FMT == kFmtQ8) {
-            const int off = lc * 1024 + lane * 16;
-            if (off < cols) {
-                wb[j] = load_stream16(ls.w + off);
-                sb[j] = ls.ws[off >> 5];
+
+        // ---- (2) the weight stream: U chunks in flight ----
+        int lp = wave, lh = 0, lc = 0, lstep = 0;
+        RowSrc ls = row_src<EPI>(a, nsteps > 0 ? row_of(lp, lh) : 0, rowbytes, nb);
+        int4 wb[U], xb0[U], xb1[U];
+        float sb[U], xsb[U];
+        int xsumb[U];
+        // Lanes past a row's end read a clamped address: their blocks are
+        // excluded where terms are summed (b < nb), so their values need no
+        // masking. A load past the wave's last step (the loop keeps U in
+        // flight) reads the first words of the scales instead, which stay in
+        // the caches; its values are never used.
+        const uint8_t *dummy = reinterpret_cast<const uint8_t *>(a.seg[0].ws);
+        auto load = [&](int j) {
+            const bool live = lstep < nsteps;
+            if (FMT == kFmtQ8) {
+                const int o = min(lc * 1024 + lane * 16, cols - 16);
+                const uint8_t *wp = live ? ls.w + o : dummy;
+                const float *sp = live ? ls.ws + (o >> 5) : a.seg[0].ws;
+                wb[j] = load_stream16(wp);
+                sb[j] = *sp;
                 if (PRO == kProGlobal) {
-                    xb0[j] = *reinterpret_cast<const int4 *>(a.qx + off);
-                    xsb[j] = a.xs[off >> 5];
+                    xb0[j] = *reinterpret_cast<const int4 *>(a.qx + o);
+                    xsb[j] = a.xs[o >> 5];
+                }
+            } else {
+                const int bk = min(lc * 64 + lane, nb - 1);
+                const uint8_t *wp = live ? ls.w + bk * 16 : dummy;
+                const float *sp = live ? ls.ws + bk : a.seg[0].ws;
+                wb[j] = load_stream16(wp);
+                sb[j] = *sp;
+                if (PRO == kProGlobal) {
+                    xb0[j] = *reinterpret_cast<const int4 *>(a.qx + bk * 32);
+                    xb1[j] = *reinterpret_cast<const int4 *>(a.qx + bk * 32 + 16);
+                    xsb[j] = a.xs[bk];
+                    xsumb[j] = a.xsum[bk];
                 }
             }
-        } else {
-            const int blk = lc * 64 + lane;
-            if (blk < nb) {
-                wb[j] = load_stream16(ls.w + blk * 16);
-                sb[j] = ls.ws[blk];
-                if (PRO == kProGlobal) {
-                    xb0[j] = *reinterpret_cast<const int4 *>(a.qx + blk * 32);
-                    xb1[j] = *reinterpret_cast<const int4 *>(a.qx + blk * 32 + 16);
-                    xsb[j] = a.xs[blk];
-                    xsumb[j] = a.xsum[blk];
+            ++lstep;
+            if (++lc == C) {
+                lc = 0;
+                if (lstep < nsteps) {
+                    next_row(lp, lh);
+                    ls = row_src<EPI>(a, row_of(lp, lh), rowbytes, nb);
                 }
             }
-        }
-        if (++lc == C) {
-            lc = 0;
-            next_row(lp, lh);
-            ls = row_src<EPI>(a, row_of(lp, lh), rowbytes, nb);
-        }
-    };
+        };
 #pragma unroll
-    for (int j = 0; j < U; j++)
-        if (j < nsteps) load(j);
+        for (int j = 0; j < U; j++) load(j);
 
-    // ---- prologue: RMSNorm (internal/llm/model.go:632-638) and Q8_0
-    // quantization (internal/num/quant.go:34-53) of the input, into LDS ----
-    int8_t *sqx = reinterpret_cast<int8_t *>(lds);
-    float *sxs = reinterpret_cast<float *>(lds + a.lds_xs);
-    int *sxsum = reinterpret_cast<int *>(lds + a.lds_xsum);
-    if (PRO != kProGlobal && work) {
-        if (PRO == kProNorm) {
-            float *sx = reinterpret_cast<float *>(lds + a.lds_x);
+        // ---- (3) prologue: stage the operands; Q8_0 quantization
+        // (internal/num/quant.go:34-53) of the input into LDS ----
+        // the per-row operands matter only when added (a residual, a bias)
+        const bool use_sep = PRE && (EPI == kEpAdd || EPI == kEpAddCanon || EPI == kEpQKV || a.bias != nullptr);
+        if (use_sep) {
+            if ((int)threadIdx.x < n) sep[threadIdx.x] = epv;
+            if (EPI == kEpQKV && (int)threadIdx.x < half) {
+                sep[a.rows_per_wg + threadIdx.x] = cosv;
+                sep[a.rows_per_wg + half + threadIdx.x] = sinv;
+            }
+        }
+        if (PRO != kProGlobal) {
 #pragma unroll
             for (int k = 0; k < MAXG; k++) {
                 const int g = threadIdx.x + k * NT;
-                if (g < (cols >> 2)) reinterpret_cast<float4 *>(sx)[g] = xv[k];
-            }
-            __syncthreads();
-            if (wave == 0) {
-                float s = 0.0f;
-                if (lane < 32)
-                    for (int i = lane; i < cols; i += 32) s += sx[i] * sx[i];
-                const float dot = dot32_reduce(s);
-                if (lane == 0) s_bcast = rsqrt32((dot * a.recip_n) + a.eps);
-            }
-            __syncthreads();
-            const float r = s_bcast;
-#pragma unroll
-            for (int k = 0; k < MAXG; k++) {
-                xv[k].x = nw[k].x * (r * xv[k].x);
-                xv[k].y = nw[k].y * (r * xv[k].y);
-                xv[k].z = nw[k].z * (r * xv[k].z);
-                xv[k].w = nw[k].w * (r * xv[k].w);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < MAXG; k++) {
-            const int g = threadIdx.x + k * NT;
-            if (k * NT < (cols >> 2)) {  // uniform: the group row holds some of x
-                float d;
-                int cs;
-                const uint32_t pk = quantize_group(xv[k].x, xv[k].y, xv[k].z, xv[k].w, d, cs);
-                if (g < (cols >> 2)) {
-                    reinterpret_cast<uint32_t *>(sqx)[g] = pk;
-                    if ((g & 7) == 0) {
-                        sxs[g >> 3] = d;
-                        sxsum[g >> 3] = cs;
+                if (k * NT < (cols >> 2)) {  // uniform: the group row holds some of x
+                    float d;
+                    int cs;
+                    const uint32_t pk = quantize_group(xv[k].x, xv[k].y, xv[k].z, xv[k].w, d, cs);
+                    if (g < (cols >> 2)) {
+                        reinterpret_cast<uint32_t *>(sqx)[g] = pk;
+                        if ((g & 7) == 0) {
+                            sxs[g >> 3] = d;
+                            sxsum[g >> 3] = cs;
+                        }
                     }
                 }
             }
         }
-        __syncthreads();
-    }
+        if (use_sep || PRO != kProGlobal) __syncthreads();
 
-    // ---- stream and reduce ----
-    float acc = 0.0f, held = 0.0f;
-    float best_v = 0.0f;
-    int best_i = -1;
-    int pp = wave, ph = 0, pc = 0;
-    const int half = a.hs >> 1;
-    auto epilogue = [&](int l, float res) {
-        if (EPI == kEpSilu) {
-            if ((l & 1) == 0)
-                held = res;
-            else
-                a.seg[0].out[l >> 1] = silu_mul(held, res);
-            return;
-        }
-        if (EPI == kEpQKV) {
-            const int lg = a.row_base + l;
-            float v = res;
-            if (a.bias) v = v + a.bias[lg];
-            if ((l & 1) == 0) {
-                held = v;
-                return;
+        // ---- (4) stream, reduce, epilogue into LDS ----
+        float acc = 0.0f, held = 0.0f;
+        int pp = wave, ph = 0, pc = 0;
+        const bool has_bias = a.bias != nullptr;
+        auto epilogue = [&](int l, float res) {
+            const int i = l - R0;
+            if (EPI == kEpSilu) {
+                if ((i & 1) == 0)
+                    held = res;
+                else
+                    sres[i >> 1] = silu_mul(held, res);
+            } else if (EPI == kEpQKV) {
+                const float v = has_bias ? res + sep[i] : res;
+                if ((i & 1) == 0) {
+                    held = v;
+                } else {
+                    const float v0 = held, v1 = v;
+                    const int i0 = a.row_base + l - 1;
+                    if (i0 < a.qdim + a.kvdim) {
+                        const int ih = i0 < a.qdim ? i0 : i0 - a.qdim;
+                        const int pi = (ih % a.hs) >> 1;
+                        const float co = sep[a.rows_per_wg + pi], si = sep[a.rows_per_wg + half + pi];
+                        sres[i - 1] = (v0 * co) - (v1 * si);
+                        sres[i] = (v0 * si) + (v1 * co);
+                    } else {
+                        sres[i - 1] = v0;
+                        sres[i] = v1;
+                    }
+                }
+            } else if (EPI == kEpStore) {
+                sres[i] = has_bias ? res + sep[i] : res;
+            } else if (EPI == kEpAdd) {
+                sres[i] = sep[i] + res;
+            } else if (EPI == kEpAddCanon) {
+                sres[i] = canonical(sep[i] + res);
+            } else if (EPI == kEpLogits) {
+                sres[i] = res;
+                if (res == res) argmax_merge(best_v, best_i, res, l);
             }
-            const float v0 = held, v1 = v;
-            const int i0 = lg - 1;
-            if (i0 < a.qdim + a.kvdim) {
-                const bool isq = i0 < a.qdim;
-                const int i = isq ? i0 : i0 - a.qdim;
-                const int pi = (i % a.hs) >> 1;
-                const float co = a.cos_t[(int64_t)pos * half + pi], si = a.sin_t[(int64_t)pos * half + pi];
-                const float r0 = (v0 * co) - (v1 * si);
-                const float r1 = (v0 * si) + (v1 * co);
-                float *dst = isq ? a.seg[0].out + i : a.kcache + (int64_t)pos * a.kvdim + i;
-                dst[0] = r0;
-                dst[1] = r1;
-            } else {
-                float *dst = a.vcache + (int64_t)pos * a.kvdim + (i0 - a.qdim - a.kvdim);
-                dst[0] = v0;
-                dst[1] = v1;
-            }
-            return;
-        }
-        const RowSrc rs = row_src<EPI>(a, l, rowbytes, nb);
-        float *o = rs.out + rs.r;
-        if (EPI == kEpStore) {
-            *o = a.bias ? res + a.bias[l] : res;
-        } else if (EPI == kEpAdd) {
-            *o = *o + res;
-        } else if (EPI == kEpAddCanon) {
-            *o = canonical(*o + res);
-        } else if (EPI == kEpLogits) {
-            *o = res;
-            if (res == res) argmax_merge(best_v, best_i, res, rs.r);
-        }
-    };
+        };
 
-    auto process = [&](int j) {
-        float t;
-        if (FMT == kFmtQ8) {
-            int4 xq = xb0[j];
-            float xsv = xsb[j];
-            if (PRO != kProGlobal) {
-                const int off = pc * 1024 + lane * 16;
-                xq = make_int4(0, 0, 0, 0);
-                xsv = 0.0f;
-                if (off < cols) {
+        auto process = [&](int j) {
+            float t;
+            if (FMT == kFmtQ8) {
+                int4 xq = xb0[j];
+                float xsv = xsb[j];
+                if (PRO != kProGlobal) {
+                    const int off = min(pc * 1024 + lane * 16, cols - 16);
                     xq = *reinterpret_cast<const int4 *>(sqx + off);
                     xsv = sxs[off >> 5];
                 }
-            }
-            const int s = pair_sum(dot16(wb[j], xq, 0));
-            t = (float)s * (sb[j] * xsv);
-            // block 32pc+k is in lanes 2k, 2k+1; running sum L in lane 2L
-            // takes blocks 32pc+L, +8, +16, +24 (lanes 2L, +16, +32, +48).
-            const float t1 = __shfl_down(t, 16);
-            const float t2 = __shfl_down(t, 32);
-            const float t3 = __shfl_down(t, 48);
-            if (lane < 16 && (lane & 1) == 0) {
-                const int b0 = pc * 32 + (lane >> 1);
-                if (b0 < nb) acc += t;
-                if (b0 + 8 < nb) acc += t1;
-                if (b0 + 16 < nb) acc += t2;
-                if (b0 + 24 < nb) acc += t3;
-            }
-        } else {
-            int4 x0 = xb0[j], x1 = xb1[j];
-            float xsv = xsb[j];
-            int xsum = xsumb[j];
-            if (PRO != kProGlobal) {
-                const int blk = pc * 64 + lane;
-                x0 = x1 = make_int4(0, 0, 0, 0);
-                xsv = 0.0f;
-                xsum = 0;
-                if (blk < nb) {
+                const int s = pair_sum(dot16(wb[j], xq, 0));
+                t = (float)s * (sb[j] * xsv);
+                // block 32pc+k is in lanes 2k, 2k+1; running sum L in lane 2L
+                // takes blocks 32pc+L, +8, +16, +24 (lanes 2L, +16, +32, +48).
+                const float t1 = __shfl_down(t, 16);
+                const float t2 = __shfl_down(t, 32);
+                const float t3 = __shfl_down(t, 48);
+                if (lane < 16 && (lane & 1) == 0) {
+                    const int b0 = pc * 32 + (lane >> 1);
+                    if (b0 < nb) acc += t;
+                    if (b0 + 8 < nb) acc += t1;
+                    if (b0 + 16 < nb) acc += t2;
+                    if (b0 + 24 < nb) acc += t3;
+                }
+            } else {
+                int4 x0 = xb0[j], x1 = xb1[j];
+                float xsv = xsb[j];
+                int xsum = xsumb[j];
+                if (PRO != kProGlobal) {
+                    const int blk = min(pc * 64 + lane, nb - 1);
                     x0 = *reinterpret_cast<const int4 *>(sqx + blk * 32);
                     x1 = *reinterpret_cast<const int4 *>(sqx + blk * 32 + 16);
                     xsv = sxs[blk];
                     xsum = sxsum[blk];
                 }
-            }
-            const int4 w = wb[j];
-            const int4 lo = make_int4(w.x & 0x0F0F0F0F, w.y & 0x0F0F0F0F, w.z & 0x0F0F0F0F, w.w & 0x0F0F0F0F);
-            const int4 hi = make_int4((int)(((uint32_t)w.x >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.y >> 4) & 0x0F0F0F0Fu),
-                                      (int)(((uint32_t)w.z >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.w >> 4) & 0x0F0F0F0Fu));
-            // nibble j is w_j + 8: sum_b = Σ lo·x_j + Σ hi·x_j+16 - 8·Σ x
-            const int s = dot16(hi, x1, dot16(lo, x0, 0)) - 8 * xsum;
-            t = (float)s * (sb[j] * xsv);
-            // block 64pc+l is in lane l; running sum L (lane L) takes lanes
-            // L, L+8, ..., L+56.
-            float tj[8];
-            tj[0] = t;
+                const int4 w = wb[j];
+                const int4 lo = make_int4(w.x & 0x0F0F0F0F, w.y & 0x0F0F0F0F, w.z & 0x0F0F0F0F, w.w & 0x0F0F0F0F);
+                const int4 hi =
+                    make_int4((int)(((uint32_t)w.x >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.y >> 4) & 0x0F0F0F0Fu),
+                              (int)(((uint32_t)w.z >> 4) & 0x0F0F0F0Fu), (int)(((uint32_t)w.w >> 4) & 0x0F0F0F0Fu));
+                // nibble j is w_j + 8: sum_b = Σ lo·x_j + Σ hi·x_j+16 - 8·Σ x
+                const int s = dot16(hi, x1, dot16(lo, x0, 0)) - 8 * xsum;
+                t = (float)s * (sb[j] * xsv);
+                // block 64pc+l is in lane l; running sum L (lane L) takes
+                // lanes L, L+8, ..., L+56.
+                float tj[8];
+                tj[0] = t;
 #pragma unroll
-            for (int k = 1; k < 8; ++k) tj[k] = __shfl_down(t, 8 * k);
-            if (lane < 8) {
+                for (int k = 1; k < 8; ++k) tj[k] = __shfl_down(t, 8 * k);
+                if (lane < 8) {
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (pc * 64 + lane + 8 * k < nb) acc += tj[k];
+                    for (int k = 0; k < 8; ++k)
+                        if (pc * 64 + lane + 8 * k < nb) acc += tj[k];
+                }
             }
-        }
-        if (++pc == C) {
-            float res;
-            if (FMT == kFmtQ8) {
-                const float p2 = acc + __shfl_down(acc, 2);
-                const float q4 = p2 + __shfl_down(p2, 4);
-                res = q4 + __shfl_down(q4, 8);
-            } else {
-                const float p2 = acc + __shfl_down(acc, 1);
-                const float q4 = p2 + __shfl_down(p2, 2);
-                res = q4 + __shfl_down(q4, 4);
+            if (++pc == C) {
+                float res;
+                if (FMT == kFmtQ8) {
+                    const float p2 = acc + __shfl_down(acc, 2);
+                    const float q4 = p2 + __shfl_down(p2, 4);
+                    res = q4 + __shfl_down(q4, 8);
+                } else {
+                    const float p2 = acc + __shfl_down(acc, 1);
+                    const float q4 = p2 + __shfl_down(p2, 2);
+                    res = q4 + __shfl_down(q4, 4);
+                }
+                if (lane == 0) epilogue(row_of(pp, ph), res);
+                acc = 0.0f;
+                pc = 0;
+                next_row(pp, ph);
             }
-            if (lane == 0) epilogue(row_of(pp, ph), res);
-            acc = 0.0f;
-            pc = 0;
-            next_row(pp, ph);
-        }
-    };
+        };
 
-    for (int st = 0; st < nsteps; st += U) {
+        for (int st = 0; st < nsteps; st += U) {
 #pragma unroll
-        for (int j = 0; j < U; j++) {
-            if (st + j < nsteps) {
-                process(j);
-                if (st + j + U < nsteps) load(j);
+            for (int j = 0; j < U; j++) {
+                if (st + j < nsteps) process(j);
+                load(j);
+            }
+        }
+
+        // ---- (5) the workgroup's results, coalesced ----
+        __syncthreads();
+        if (EPI == kEpSilu) {
+            const int np = n >> 1, P0 = R0 >> 1;
+            for (int i = threadIdx.x; i < np; i += NT) a.seg[0].out[P0 + i] = sres[i];
+            if (a.qx_out) {
+                // h's Q8_0 blocks: the launcher gives each workgroup whole
+                // blocks (pairs in multiples of 32), eight lanes a block
+                for (int g0 = 0; g0 < (np >> 2); g0 += NT) {  // uniform
+                    const int g = g0 + threadIdx.x;
+                    const int gc = min(g, (np >> 2) - 1);
+                    const float4 v = reinterpret_cast<const float4 *>(sres)[gc];
+                    float d;
+                    int cs;
+                    const uint32_t pk = quantize_group(v.x, v.y, v.z, v.w, d, cs);
+                    if (g < (np >> 2)) {
+                        reinterpret_cast<uint32_t *>(a.qx_out + P0)[g] = pk;
+                        if ((g & 7) == 0) {
+                            a.xs_out[(P0 >> 5) + (g >> 3)] = d;
+                            a.xsum_out[(P0 >> 5) + (g >> 3)] = cs;
+                        }
+                    }
+                }
+            }
+        } else if (EPI == kEpQKV) {
+            for (int i = threadIdx.x; i < n; i += NT) {
+                const int lg = a.row_base + R0 + i;
+                float *dst = lg < a.qdim             ? a.seg[0].out + lg
+                             : lg < a.qdim + a.kvdim ? a.kcache + (int64_t)pos * a.kvdim + (lg - a.qdim)
+                                                     : a.vcache + (int64_t)pos * a.kvdim + (lg - a.qdim - a.kvdim);
+                *dst = sres[i];
+            }
+        } else {
+            for (int i = threadIdx.x; i < n; i += NT) {
+                const RowSrc rs = row_src<EPI>(a, R0 + i, rowbytes, nb);
+                rs.out[rs.r] = sres[i];
             }
         }
     }
 
-    if (EPI == kEpLogits) {
-        // Greedy argmax over all rows: per wave, per workgroup, then the last
-        // workgroup to finish merges the partials, stores the next token and
-        // advances the position (all other workgroups read it already).
+    if (EPI == kEpLogits && work) {
+        // Greedy argmax: per wave, per workgroup, then one atomicMax of the
+        // workgroup's key into a slot (launch_advance folds the slots).
         if (lane == 0) {
             s_wv[wave] = best_v;
             s_wi[wave] = best_i;
@@ -390,39 +466,11 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
             float bv = 0.0f;
             int bi = -1;
             for (int w = 0; w < W; w++) argmax_merge(bv, bi, s_wv[w], s_wi[w]);
-            a.part_v[blockIdx.x] = bv;
-            a.part_i[blockIdx.x] = bi;
-            __threadfence();
-            s_last = atomicAdd(&a.ctl[kCtlDone], 1) == (int)gridDim.x - 1;
-        }
-        __syncthreads();
-        if (s_last) {
-            __threadfence();
-            float bv = 0.0f;
-            int bi = -1;
-            for (int i = threadIdx.x; i < (int)gridDim.x; i += NT) argmax_merge(bv, bi, a.part_v[i], a.part_i[i]);
-            // the merge is a maximum under a total order: any fold order
-            for (int w = 1; w < 64; w <<= 1) {
-                const float ov = __shfl_xor(bv, w);
-                const int oi = __shfl_xor(bi, w);
-                argmax_merge(bv, bi, ov, oi);
-            }
-            if (lane == 0) {
-                s_wv[wave] = bv;
-                s_wi[wave] = bi;
-            }
-            __syncthreads();
-            if (threadIdx.x == 0) {
-                float fv = 0.0f;
-                int fi = -1;
-                for (int w = 0; w < W; w++) argmax_merge(fv, fi, s_wv[w], s_wi[w]);
-                if (work && pos + 1 < a.tokens_len) {
-                    const float l0 = a.seg[0].out[0];
-                    a.tokens[pos + 1] = (fi < 0 || l0 != l0) ? 0 : fi;
-                }
-                a.ctl[kCtlPos] = pos + 1;
-                a.ctl[kCtlDone] = 0;
-            }
+            unsigned long long key = bi < 0 ? 0ull : argmax_key(bv, bi);
+            // A NaN first logit makes the argmax 0 (nothing compares above
+            // it): the largest key, row 0.
+            if (R0 == 0 && sres[0] != sres[0]) key = ~0ull;
+            if (key) atomicMax(&a.amax[blockIdx.x % kArgmaxSlots], key);
         }
     }
 }
@@ -431,9 +479,11 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
 // Launch: the host sizes the grid (about two workgroups per CU, rows split
 // evenly, pairs kept whole) and the LDS layout.
 
+// Chunks in flight per wave: 2 when the input comes quantized, 4 to cover
+// an LDS prologue (measured).
 template <int FMT, int PRO, int EPI, int W>
 static void launch_one(const FusedArgs &a, unsigned grid, size_t lds, hipStream_t s) {
-    RK_LAUNCH((fused_kernel<FMT, PRO, EPI, W, 2>), dim3(grid), dim3(64 * W), lds, s, a);
+    RK_LAUNCH((fused_kernel<FMT, PRO, EPI, W, PRO == kProGlobal ? 2 : 4>), dim3(grid), dim3(64 * W), lds, s, a);
 }
 
 template <int FMT, int PRO, int W>
@@ -454,7 +504,6 @@ static bool launch_pro(int pro, int epi, const FusedArgs &a, unsigned grid, size
     switch (pro) {
         case kProGlobal: return launch_epi<FMT, kProGlobal, W>(epi, a, grid, lds, s);
         case kProQuant: return launch_epi<FMT, kProQuant, W>(epi, a, grid, lds, s);
-        case kProNorm: return launch_epi<FMT, kProNorm, W>(epi, a, grid, lds, s);
     }
     return false;
 }
@@ -464,139 +513,300 @@ static inline int align16(int v) { return (v + 15) & ~15; }
 // Dynamic LDS a launch may ask for without raising the kernel's limit.
 constexpr int kMaxDynLds = 64 * 1024;
 
-static void lds_layout(FusedArgs &a, int pro) {
+static void lds_layout(FusedArgs &a, int pro, int epi) {
     const int cols = a.cols, nb = cols >> 5;
-    a.lds_xs = align16(cols);
-    a.lds_xsum = a.lds_xs + align16(nb * 4);
-    a.lds_x = a.lds_xsum + align16(nb * 4);
-    a.lds_bytes = a.lds_x + (pro == kProNorm ? cols * 4 : 0);
+    int at = 0;
+    if (pro != kProGlobal) {
+        a.lds_xs = align16(cols);
+        a.lds_xsum = a.lds_xs + align16(nb * 4);
+        at = a.lds_xsum + align16(nb * 4);
+    }
+    a.lds_res = at;
+    at += align16(a.rows_per_wg * 4);
+    a.lds_ep = at;
+    if (epi != kEpSilu && epi != kEpLogits) at += align16(a.rows_per_wg * 4 + (epi == kEpQKV ? 4 * a.hs : 0));
+    a.lds_bytes = at;
 }
 
+// Rows per workgroup at most: per-row operands are loaded one per thread of
+// the smallest workgroup, and results wait in LDS.
+constexpr int kMaxRowsPerWg = 512;
+
 bool fused_fits(int pro, int cols) {
+    if (cols <= 0 || cols % 32 != 0) return false;
     if (pro == kProGlobal) return true;
-    if (cols > kMaxLdsCols || cols % 32 != 0) return false;
+    if (cols > kMaxLdsCols) return false;
     FusedArgs a{};
     a.cols = cols;
-    lds_layout(a, pro);
+    a.rows_per_wg = kMaxRowsPerWg;
+    a.hs = 1024;
+    lds_layout(a, pro, kEpQKV);
     return a.lds_bytes <= kMaxDynLds;
 }
 
 bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s) {
     if (a.rows <= 0) return true;
-    if (a.cols <= 0 || a.cols % 32 != 0 || !fused_fits(pro, a.cols)) return false;
-    size_t lds = 0;
-    if (pro != kProGlobal) {
-        lds_layout(a, pro);
-        lds = (size_t)a.lds_bytes;
-    }
+    if (!fused_fits(pro, a.cols)) return false;
+    if ((epi == kEpAdd || epi == kEpAddCanon || epi == kEpLogits) && a.nseg != 1) return false;
+    if (epi == kEpQKV && (a.hs <= 0 || a.hs > 1024 || (a.rows & 1) || (a.row_base & 1))) return false;
     const bool pair = epi == kEpQKV || epi == kEpSilu;
-    const int64_t target = (int64_t)(cu > 0 ? cu : 256) * 2;
+    // Workgroup shape (measured on MI355X): with the input already
+    // quantized, 8 waves x 2 workgroups per CU, or 16 waves x 1 for mid-size
+    // row counts; with an LDS prologue, 16 waves x 1 up to 8192 rows, else
+    // 8 x 2.
+    const int64_t ncu = cu > 0 ? cu : 256;
+    bool w16;
+    int per_cu;
+    if (pro == kProGlobal) {
+        w16 = a.rows > 5000 && a.rows < 20000;
+        per_cu = w16 ? 1 : 2;
+    } else {
+        w16 = a.rows <= 8192;
+        per_cu = w16 ? 1 : 2;
+    }
+    const int64_t target = ncu * per_cu;
     int64_t rpw = (a.rows + target - 1) / target;
-    if (pair) rpw = (rpw + 1) & ~1;
-    if (epi == kEpLogits) {
-        const int64_t min_rpw = (a.rows + kMaxArgmaxParts - 1) / kMaxArgmaxParts;
-        if (rpw < min_rpw) rpw = min_rpw;
+    if (rpw > kMaxRowsPerWg) rpw = kMaxRowsPerWg;
+    if (pair) rpw = (rpw + 1) & ~(int64_t)1;
+    if (epi == kEpSilu && a.qx_out) {
+        if (a.rows % 64 != 0) return false;
+        rpw = (rpw + 63) & ~(int64_t)63;
     }
     a.rows_per_wg = (int32_t)rpw;
     const unsigned grid = (unsigned)((a.rows + rpw - 1) / rpw);
-    const int64_t units = pair ? (rpw + 1) / 2 : rpw;
-    const bool wide = units >= 12;
+    lds_layout(a, pro, epi);
+    const size_t lds = (size_t)a.lds_bytes;
+    if (lds > (size_t)kMaxDynLds) return false;
     if (fmt == kFmtQ8)
-        return wide ? launch_pro<kFmtQ8, 16>(pro, epi, a, grid, lds, s) : launch_pro<kFmtQ8, 8>(pro, epi, a, grid, lds, s);
-    return wide ? launch_pro<kFmtQ4, 16>(pro, epi, a, grid, lds, s) : launch_pro<kFmtQ4, 8>(pro, epi, a, grid, lds, s);
+        return w16 ? launch_pro<kFmtQ8, 16>(pro, epi, a, grid, lds, s) : launch_pro<kFmtQ8, 8>(pro, epi, a, grid, lds, s);
+    return w16 ? launch_pro<kFmtQ4, 16>(pro, epi, a, grid, lds, s) : launch_pro<kFmtQ4, 8>(pro, epi, a, grid, lds, s);
 }
 
 // ---------------------------------------------------------------------------
 // Attention of the position ctl[kCtlPos] (internal/llm/model.go:575-591).
 
-constexpr int kScorePositions = 32;  // positions per workgroup
+// Scores: score_t = float32(Dot32(q_h, k_t)·invSqrt) for t <= position.
+// Four lanes (a quad) per position, 64 positions per workgroup, grid
+// (heads, position tiles); tiles past the position exit. Lane `sub` of the
+// quad keeps Dot32's running sums j = 8·sub .. 8·sub+7 (element i goes to
+// sum i mod 32, in order of i); the quad then forms e_j = (s_j + s_j+8) +
+// (s_j+16 + s_j+24) by two DPP exchanges and lane 0 the final tree.
+constexpr int kScoreTile = 64;
 
-// score_t = float32(Dot32(q_h, k_t)·invSqrt), t <= position: a half-wave
-// per position, grid (heads, position tiles); tiles past the position exit.
+__device__ __forceinline__ float dppf_x1(float v) { return __int_as_float(dpp_x1(__float_as_int(v))); }
+__device__ __forceinline__ float dppf_x2(float v) { return __int_as_float(dpp_x2(__float_as_int(v))); }
+
+template <int HS>  // head size when fixed at compile time (all loads issued at once), else 0
 __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const float *keys, float *att,
-                                                         int32_t att_stride, const int32_t *ctl, int kv_mul, int hs,
+                                                         int32_t att_stride, const int32_t *ctl, int kv_mul, int hs_rt,
                                                          int kv_dim, float inv_sqrt) {
+    const int hs = HS ? HS : hs_rt;
     const int T = ctl[kCtlPos] + 1;
-    const int t0 = blockIdx.y * kScorePositions;
+    const int t0 = blockIdx.y * kScoreTile;
     if (t0 >= T) return;
     const int h = blockIdx.x, g = h / kv_mul;
-    const int half = threadIdx.x >> 5, hl = threadIdx.x & 31;
+    const int sub = threadIdx.x & 3;
+    const int t = t0 + (threadIdx.x >> 2);
+    const bool valid = t < T;
+    const float *kt = keys + (int64_t)(valid ? t : t0) * kv_dim + (int64_t)g * hs;
     const float *qh = q + (int64_t)h * hs;
-    for (int tt = half; tt < kScorePositions; tt += 8) {
-        const int t = t0 + tt;
-        const bool valid = t < T;
-        const float *kt = keys + (int64_t)(valid ? t : 0) * kv_dim + (int64_t)g * hs;
-        const float d = dot32_half(qh, kt, hs, hl, valid);
-        if (valid && hl == 0) att[(int64_t)h * att_stride + t] = d * inv_sqrt;
+    float s[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) s[k] = 0.0f;
+    if ((hs & 7) == 0 && (kv_dim & 3) == 0) {
+        for (int base = 8 * sub; base < hs; base += 32) {  // unrolled when HS is fixed
+            const float4 k0 = *reinterpret_cast<const float4 *>(kt + base);
+            const float4 k1 = *reinterpret_cast<const float4 *>(kt + base + 4);
+            const float4 q0 = *reinterpret_cast<const float4 *>(qh + base);
+            const float4 q1 = *reinterpret_cast<const float4 *>(qh + base + 4);
+            s[0] += q0.x * k0.x;
+            s[1] += q0.y * k0.y;
+            s[2] += q0.z * k0.z;
+            s[3] += q0.w * k0.w;
+            s[4] += q1.x * k1.x;
+            s[5] += q1.y * k1.y;
+            s[6] += q1.z * k1.z;
+            s[7] += q1.w * k1.w;
+        }
+    } else {
+        for (int base = 8 * sub; base < hs; base += 32)
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (base + k < hs) s[k] += qh[base + k] * kt[base + k];
     }
+    float e[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float u = s[k] + dppf_x1(s[k]);  // lane 0: s_j + s_j+8; lane 2: s_j+16 + s_j+24
+        e[k] = u + dppf_x2(u);                 // lane 0: e_j
+    }
+    const float dot = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    if (sub == 0 && valid) att[(int64_t)h * att_stride + t] = dot * inv_sqrt;
 }
 
 void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
                        int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt, hipStream_t s) {
-    const dim3 grid(heads, (ctx + kScorePositions - 1) / kScorePositions);
-    RK_LAUNCH(att_scores_kernel, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, heads / kv_heads, hs, kv_dim,
-              inv_sqrt);
+    const dim3 grid(heads, (ctx + kScoreTile - 1) / kScoreTile);
+    if (hs == 128)
+        RK_LAUNCH(att_scores_kernel<128>, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, heads / kv_heads, hs,
+                  kv_dim, inv_sqrt);
+    else
+        RK_LAUNCH(att_scores_kernel<0>, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, heads / kv_heads, hs,
+                  kv_dim, inv_sqrt);
 }
 
-// Softmax of a head's scores (Go max, Exp32, one sequential sum, ·Recip32)
-// and the weighted values, out_i = Σ_t a_t·v_t,i in t order from +0. One
-// wave per 64 elements of a head: grid (heads, ceil(hs/64)); each wave
-// redoes its head's softmax (cheap) so no wave waits on another.
-__global__ __launch_bounds__(64) void att_values_kernel(const float *att, int32_t att_stride, const float *vals,
-                                                        float *out, const int32_t *ctl, int kv_mul, int hs,
-                                                        int kv_dim) {
-    extern __shared__ float sa[];  // [T] weights
+// Softmax and weighted values for a 32-element slice of one head per
+// workgroup (grid: heads, ceil(hs/32)). The order is the CPU's: Go max,
+// e_t = Exp32(s_t - max), one sequential sum, inv = Recip32(sum), a_t =
+// e_t·inv, then out_i = Σ_t a_t·v_t,i in t order from +0. The slice's values
+// for up to kValChunk positions are loaded at the start (in flight during
+// the softmax); their products a_t·v_t,i are formed in parallel into LDS,
+// transposed, and each element's sequential sum reads them four at a time
+// in straight-line code. A slice holding a whole Q8 block is quantized for
+// the next product. LDS beyond 64 KiB (gfx950 gives a workgroup 160 KiB).
+constexpr int kValSlice = 32;
+constexpr int kValThreads = 512;
+constexpr int kValChunk = 768;
+constexpr int kValPitch = kValChunk + 4;                              // floats per element row (odd 16-byte units)
+constexpr int kValLoads = kValChunk * kValSlice / 4 / kValThreads;    // float4 loads per thread per chunk
+constexpr int kValRows = kValThreads / (kValSlice / 4);               // positions per load round
+
+__global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *att, int32_t att_stride,
+                                                                 const float *vals, float *out, const int32_t *ctl,
+                                                                 int kv_mul, int hs, int kv_dim, int ctx_pad,
+                                                                 int8_t *qx, float *xs, int32_t *xsum) {
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float s_red[kValThreads / 64];
+    __shared__ float s_inv;
+    float *sa = smem;            // [ctx_pad] scores -> weights
+    float *sp = smem + ctx_pad;  // [kValSlice][kValPitch] products of a chunk
     const int T = ctl[kCtlPos] + 1;
     const int h = blockIdx.x, g = h / kv_mul;
-    const int lane = threadIdx.x;
+    const int e0 = blockIdx.y * kValSlice;
+    const int ne = min(kValSlice, hs - e0);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *vbase = vals + (int64_t)g * hs + e0;
+    const bool vec = (hs & 3) == 0 && (kv_dim & 3) == 0;
+    // thread -> (float4 column fq of the slice, positions pr + kValRows·k)
+    const int fq = tid & 7, pr = tid >> 3;
+
+    float4 vr[kValLoads];
+    auto load_chunk = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < kValLoads; k++) {
+            const int t = min(c0 + pr + kValRows * k, T - 1);
+            const float *p = vbase + (int64_t)t * kv_dim + 4 * fq;
+            if (vec && 4 * fq + 3 < ne) {
+                vr[k] = *reinterpret_cast<const float4 *>(p);
+            } else {
+                const int n4 = ne - 4 * fq;
+                vr[k].x = n4 > 0 ? p[0] : 0.0f;
+                vr[k].y = n4 > 1 ? p[1] : 0.0f;
+                vr[k].z = n4 > 2 ? p[2] : 0.0f;
+                vr[k].w = n4 > 3 ? p[3] : 0.0f;
+            }
+        }
+    };
+    // the head's scores (the first 1024 with the values, all in flight)
     const float *ah = att + (int64_t)h * att_stride;
-    float m = ah[0];
-    for (int t = lane; t < T; t += 64) {
+    constexpr int kScPer = 2;
+    float sv[kScPer];
+#pragma unroll
+    for (int k = 0; k < kScPer; k++) sv[k] = ah[min(tid + kValThreads * k, T - 1)];
+    load_chunk(0);
+
+    // softmax of the head's scores
+    float m = sv[0];
+#pragma unroll
+    for (int k = 0; k < kScPer; k++) {
+        if (tid + kValThreads * k < T) {
+            sa[tid + kValThreads * k] = sv[k];
+            m = gomax(m, sv[k]);
+        }
+    }
+    for (int t = tid + kValThreads * kScPer; t < T; t += kValThreads) {
         const float v = ah[t];
         sa[t] = v;
         m = gomax(m, v);
     }
     for (int w = 1; w < 64; w <<= 1) m = gomax(m, __shfl_xor(m, w));
-    for (int t = lane; t < T; t += 64) sa[t] = exp32(sa[t] - m);
+    if (lane == 0) s_red[wave] = m;
     __syncthreads();
-    if (lane == 0) {
-        float sum = 0.0f;
-        int t = 0;
-        for (; t + 8 <= T; t += 8) {
-            float v[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = sa[t + j];
-#pragma unroll
-            for (int j = 0; j < 8; j++) sum += v[j];
-        }
-        for (; t < T; t++) sum += sa[t];
-        sa[T] = recip32(sum);
-    }
+    m = s_red[0];
+    for (int w = 1; w < kValThreads / 64; w++) m = gomax(m, s_red[w]);
+    for (int t = tid; t < T; t += kValThreads) sa[t] = exp32(sa[t] - m);
     __syncthreads();
-    const float inv = sa[T];
-    for (int t = lane; t < T; t += 64) sa[t] = sa[t] * inv;
+    if (tid == 0) s_inv = recip32(lds_chain_sum(sa, T, 0.0f));
     __syncthreads();
-    const int i = blockIdx.y * 64 + lane;
-    if (i >= hs) return;
-    const float *v = vals + (int64_t)g * hs + i;
+    const float inv = s_inv;
+    for (int t = tid; t < T; t += kValThreads) sa[t] = sa[t] * inv;
+    __syncthreads();
+
     float acc = 0.0f;
-    int t = 0;
-    for (; t + 8 <= T; t += 8) {
-        float vv[8];
+    for (int c0 = 0; c0 < T; c0 += kValChunk) {
+        // products of this chunk, transposed: sp[i][t - c0]
 #pragma unroll
-        for (int j = 0; j < 8; j++) vv[j] = v[(int64_t)(t + j) * kv_dim];
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc += sa[t + j] * vv[j];
+        for (int k = 0; k < kValLoads; k++) {
+            const int tt = pr + kValRows * k;
+            const float a_t = sa[min(c0 + tt, T - 1)];
+            float *dst = sp + (4 * fq) * kValPitch + tt;
+            dst[0] = a_t * vr[k].x;
+            dst[kValPitch] = a_t * vr[k].y;
+            dst[2 * kValPitch] = a_t * vr[k].z;
+            dst[3 * kValPitch] = a_t * vr[k].w;
+        }
+        if (c0 + kValChunk < T) load_chunk(c0 + kValChunk);  // in flight while this chunk is summed
+        __syncthreads();
+        const int n = min(kValChunk, T - c0);
+        if (wave == 0 && lane < kValSlice) acc = lds_chain_sum(sp + lane * kValPitch, n, acc);
+        __syncthreads();
     }
-    for (; t < T; t++) acc += sa[t] * v[(int64_t)t * kv_dim];
-    out[(int64_t)h * hs + i] = acc;
+    if (wave == 0 && lane < ne) out[(int64_t)h * hs + e0 + lane] = acc;
+    if (qx && ne == kValSlice) {
+        // the slice is one Q8_0 block of the next input (e0 is a multiple
+        // of 32): lanes 0-7 take four values each
+        if (wave == 0 && lane < kValSlice) sp[lane] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            const int q = min(lane, 7);
+            const float4 v4 = reinterpret_cast<const float4 *>(sp)[q];
+            float d;
+            int cs;
+            const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
+            const int64_t base = (int64_t)h * hs + e0;
+            if (lane < 8) {
+                reinterpret_cast<uint32_t *>(qx + base)[lane] = pk;
+                if (lane == 0) {
+                    xs[base >> 5] = d;
+                    xsum[base >> 5] = cs;
+                }
+            }
+        }
+    }
 }
 
+// Dynamic LDS of the values kernel for a context of ctx positions.
+static size_t att_values_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + kValSlice * kValPitch) * 4; }
+
+// Dynamic LDS the values kernel may ask for: the device's 160 KiB less
+// room for its static LDS.
+constexpr size_t kValMaxDynLds = kMaxLdsBytes - 1024;
+
+int att_values_max_ctx() { return (int)(kValMaxDynLds / 4 - kValSlice * kValPitch) & ~3; }
+
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
-                       int ctx, int heads, int kv_heads, int hs, int kv_dim, hipStream_t s) {
-    const dim3 grid(heads, (hs + 63) / 64);
-    RK_LAUNCH(att_values_kernel, grid, dim3(64), (size_t)(ctx + 1) * 4, s, att, att_stride, vals, out, ctl,
-              heads / kv_heads, hs, kv_dim);
+                       int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
+                       hipStream_t s) {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute((const void *)att_values_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)kValMaxDynLds);
+    });
+    const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice);
+    if (hs % 32 != 0) qx = nullptr;
+    const int ctx_pad = (ctx + 3) & ~3;
+    RK_LAUNCH(att_values_kernel, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals, out, ctl,
+              heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
 }
 
 // QK-norm (internal/llm/model.go:551-558) and RoPE (:563-572) of one head
@@ -641,26 +851,100 @@ void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q
 }
 
 // Embedding row of the token at the position (internal/llm/model.go:216-231
-// Row, :660-664 Embed): x_i = float32(q_i·scale_i/32).
-__global__ void embed_pos_kernel(const uint8_t *w, const float *scales, int q4, const int32_t *tokens,
-                                 const int32_t *ctl, int dim, float *x) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= dim) return;
+// Row, :660-664 Embed): x_i = float32(q_i·scale_i/32); then RMSNorm(x) with
+// the first layer's weights, quantized for its QKV product. One workgroup;
+// every load is issued before the first use.
+constexpr int kNormThreads = 1024;
+
+// LDS of wg_norm_quant for n values: x transposed, 32 rows of the pitch.
+static size_t norm_lds(int n) { return (size_t)32 * ((((n >> 5) + 3) & ~3) + 4) * 4; }
+constexpr int kNormGroups = (kMaxNormCols / 4 + kNormThreads - 1) / kNormThreads;
+
+__global__ __launch_bounds__(kNormThreads) void embed_norm_kernel(const uint8_t *w, const float *scales, int q4,
+                                                                  const int32_t *tokens, const int32_t *ctl, int dim,
+                                                                  float *x, const float *norm_w, float recip_n,
+                                                                  float eps, int8_t *qx, float *xs, int32_t *xsum) {
+    extern __shared__ __align__(16) float sxe[];
+    __shared__ float bcast;
     const int64_t tok = tokens[ctl[kCtlPos]];
-    const int nb = dim >> 5;
-    const float d = scales[tok * nb + (i >> 5)];
-    if (!q4) {
-        x[i] = (float)reinterpret_cast<const int8_t *>(w)[tok * dim + i] * d;
-    } else {
-        const uint8_t b = w[tok * (dim / 2) + (i >> 5) * 16 + (i & 15)];
-        const int c = ((i & 31) < 16 ? (b & 15) : (b >> 4)) - 8;
-        x[i] = (float)c * d;
+    const int nb = dim >> 5, ng = dim >> 2;
+    uint32_t cw[kNormGroups];
+    float sc[kNormGroups];
+    float4 wv[kNormGroups], xv[kNormGroups];
+#pragma unroll
+    for (int k = 0; k < kNormGroups; k++) {
+        const int g = min((int)threadIdx.x + k * kNormThreads, ng - 1);  // elements 4g..4g+3
+        const int i = 4 * g;
+        // four codes: Q8 bytes 4g..; Q4 bytes of block i/32 holding j..j+3 (j = i mod 32)
+        const uint8_t *cp = q4 ? w + tok * (dim / 2) + (i >> 5) * 16 + (i & 15) : w + tok * dim + i;
+        cw[k] = *reinterpret_cast<const uint32_t *>(cp);
+        sc[k] = scales[tok * nb + (i >> 5)];
+        wv[k] = reinterpret_cast<const float4 *>(norm_w)[g];
+    }
+#pragma unroll
+    for (int k = 0; k < kNormGroups; k++) {
+        const int g = threadIdx.x + k * kNormThreads;
+        int c[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int b = (int)((cw[k] >> (8 * e)) & 255u);
+            c[e] = !q4 ? (int)(int8_t)b : ((((4 * g) & 31) < 16 ? (b & 15) : (b >> 4)) - 8);
+        }
+        xv[k] = make_float4((float)c[0] * sc[k], (float)c[1] * sc[k], (float)c[2] * sc[k], (float)c[3] * sc[k]);
+        if (g < ng) reinterpret_cast<float4 *>(x)[g] = xv[k];
+    }
+    wg_norm_quant<kNormThreads, kNormGroups>(xv, wv, dim, recip_n, eps, qx, xs, xsum, sxe, &bcast);
+}
+
+void launch_embed_norm(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, const int32_t *ctl,
+                       int dim, float *x, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
+                       int32_t *xsum, hipStream_t s) {
+    RK_LAUNCH(embed_norm_kernel, dim3(1), dim3(kNormThreads), norm_lds(dim), s, w, scales, q4 ? 1 : 0, tokens, ctl,
+              dim, x, norm_w, recip_n, eps, qx, xs, xsum);
+}
+
+__global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(const float *x, int n, const float *norm_w,
+                                                                  float recip_n, float eps, int8_t *qx, float *xs,
+                                                                  int32_t *xsum) {
+    extern __shared__ __align__(16) float sxn[];
+    __shared__ float bcast;
+    const int ng = n >> 2;
+    float4 xv[kNormGroups], wv[kNormGroups];
+#pragma unroll
+    for (int k = 0; k < kNormGroups; k++) {
+        const int g = min((int)threadIdx.x + k * kNormThreads, ng - 1);
+        xv[k] = reinterpret_cast<const float4 *>(x)[g];
+        wv[k] = reinterpret_cast<const float4 *>(norm_w)[g];
+    }
+    wg_norm_quant<kNormThreads, kNormGroups>(xv, wv, n, recip_n, eps, qx, xs, xsum, sxn, &bcast);
+}
+
+void launch_norm_quant(const float *x, int n, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
+                       int32_t *xsum, hipStream_t s) {
+    RK_LAUNCH(norm_quant_kernel, dim3(1), dim3(kNormThreads), norm_lds(n), s, x, n, norm_w, recip_n, eps, qx, xs,
+              xsum);
+}
+
+__global__ __launch_bounds__(64) void advance_kernel(int32_t *ctl, unsigned long long *amax, int32_t *tokens,
+                                                     int32_t tokens_len) {
+    const int lane = threadIdx.x;
+    unsigned long long k = lane < kArgmaxSlots ? amax[lane] : 0ull;
+    for (int w = 1; w < 64; w <<= 1) {
+        const unsigned long long o = __shfl_xor(k, w);
+        k = o > k ? o : k;
+    }
+    if (lane < kArgmaxSlots) amax[lane] = 0ull;
+    if (lane == 0) {
+        const int pos = ctl[kCtlPos];
+        // no key: every logit NaN, and the first index stays (sample.go:46)
+        if (pos + 1 >= ctl[kCtlPrompt] && pos + 1 < tokens_len)
+            tokens[pos + 1] = k ? (int32_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull)) : 0;
+        ctl[kCtlPos] = pos + 1;
     }
 }
 
-void launch_embed_pos(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, const int32_t *ctl,
-                      int dim, float *x, hipStream_t s) {
-    RK_LAUNCH(embed_pos_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, w, scales, q4 ? 1 : 0, tokens, ctl, dim, x);
+void launch_advance(int32_t *ctl, unsigned long long *amax, int32_t *tokens, int32_t tokens_len, hipStream_t s) {
+    RK_LAUNCH(advance_kernel, dim3(1), dim3(64), 0, s, ctl, amax, tokens, tokens_len);
 }
 
 }  // namespace rk

@@ -4,6 +4,8 @@
 // function whose body it replaces.
 #include "rk_runtime.h"
 
+#include "rk_fused.h"
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -82,46 +84,60 @@ ProfScope::ProfScope(rk_device *d, hipStream_t, const char *kernel) {
 
 ProfScope::~ProfScope() { g_launch_events = nullptr; }
 
-// Enqueue ms[i]·x into outs[i]: x (cols floats) on the device; one quantize
-// of x into the device scratch, then one launch per run of up to kMaxSegs
-// matrices of one kind.
+// Device bytes held (Device.Used), under the accounting lock.
 void add_used(rk_device *d, int64_t bytes) {
     std::lock_guard<std::mutex> g(d->mu);
     d->used += bytes;
 }
 
+// Products of n matrices sharing cols with one input: each run of up to
+// three matrices of one format is one launch. Inputs up to 8192 wide that
+// are 16-byte aligned are quantized by every workgroup into LDS (no extra
+// launch; measured faster there); wider or unaligned ones by one quantize
+// launch into the scratch q, which the products then read.
 int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
                     const QScratch &q, hipStream_t s) {
+    const bool in_lds = cols <= 8192 && ((uintptr_t)x & 15) == 0 && fused_fits(kProQuant, (int)cols);
     bool quantized = false;
-    for (int i = 0; i < n; i++)
-        if (ms[i]->kind == RK_Q8 || ms[i]->kind == RK_Q4) quantized = true;
-    if (quantized) {
-        ProfScope p(d, s, "quantize_acts");
-        launch_quantize_acts(x, cols, q.qx, q.xs, q.xsum, s);
-    }
     for (int kind : {RK_Q8, RK_Q4}) {
-        MatvecArgs a{};
+        FusedArgs a{};
         a.cols = (int32_t)cols;
-        a.qx = q.qx;
-        a.xs = q.xs;
-        a.xsum = q.xsum;
-        auto flush = [&]() {
-            if (a.nseg == 0) return;
-            ProfScope p(d, s, kind == RK_Q8 ? "matvec_q8" : "matvec_q4");
-            if (kind == RK_Q8)
-                launch_matvec_q8(a, d->cu, s);
-            else
-                launch_matvec_q4(a, d->cu, s);
+        auto flush = [&]() -> int {
+            if (a.nseg == 0) return RK_OK;
+            int pro = kProQuant;
+            if (in_lds) {
+                a.x = x;
+            } else {
+                if (!quantized) {
+                    ProfScope p(d, s, "quantize_acts");
+                    launch_quantize_acts(x, cols, q.qx, q.xs, q.xsum, s);
+                    quantized = true;
+                }
+                pro = kProGlobal;
+                a.qx = q.qx;
+                a.xs = q.xs;
+                a.xsum = q.xsum;
+            }
+            bool ok;
+            {
+                ProfScope p(d, s, kind == RK_Q8 ? "matvec_q8" : "matvec_q4");
+                ok = launch_fused(kind == RK_Q8 ? kFmtQ8 : kFmtQ4, pro, kEpStore, a, d->cu, s);
+            }
             a.nseg = 0;
-            a.total_rows = 0;
+            a.rows = 0;
+            return ok ? RK_OK : fail(d, RK_ERR_UNSUPPORTED, "matvec: width %lld has no kernel", (long long)cols);
         };
         for (int i = 0; i < n; i++) {
             if (ms[i]->kind != kind) continue;
             a.seg[a.nseg] = MatSeg{ms[i]->w, ms[i]->scales, outs[i], ms[i]->rows};
-            a.total_rows += ms[i]->rows;
-            if (++a.nseg == kMaxSegs) flush();
+            a.rows += (int32_t)ms[i]->rows;
+            if (++a.nseg == 3) {
+                int rc = flush();
+                if (rc) return rc;
+            }
         }
-        flush();
+        int rc = flush();
+        if (rc) return rc;
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(d, e, "matvec launch");

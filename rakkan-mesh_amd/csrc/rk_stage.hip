@@ -2,19 +2,21 @@
 // (internal/llm/gpustage.go), and the greedy generation loop around them
 // (embedding, head, argmax) with its state on the device.
 //
-// A token runs as six launches per layer:
-//   qkv      RMSNorm(x)·[Wq;Wk;Wv] (+bias), RoPE, k and v into the caches
+// A token runs as six launches per layer, every product reading its input
+// already quantized (Q8_0 codes, block scales, block code sums):
+//   qkv      [Wq;Wk;Wv]·xn (+bias), RoPE, k and v into the caches
 //            (Qwen3: raw q/k/v, then qknorm_rope)
 //   scores   Dot32(q_h, k_t)·invSqrt for t <= position
-//   values   softmax, Σ a_t·v_t
-//   wo       x += Wo·att
-//   w13      h = silu(W1·RMSNorm(x))·(W3·RMSNorm(x))
-//   w2       x = Canonical(x + W2·h)
+//   values   softmax, Σ a_t·v_t, quantized
+//   wo       x += Wo·att; its last workgroup: xn = RMSNorm_ffn(x), quantized
+//   w13      h = silu(W1·xn)·(W3·xn), quantized
+//   w2       x = Canonical(x + W2·h); its last workgroup: xn = RMSNorm of the
+//            next layer (or the head), quantized
 // in the order and rounding of Stage.Forward (internal/llm/model.go:522-613).
-// Generation adds the embedding of the position's token before the layers
-// and RMSNorm + classifier + greedy argmax after them; the argmax writes the
-// next token and advances the position on the device. The launches of one
-// token are recorded once into a HIP graph and replayed.
+// Generation embeds the position's token first (and RMSNorms it for the
+// first layer) and ends with the classifier and the greedy argmax, which
+// writes the next token and advances the position on the device. The
+// launches of one token are recorded once into a HIP graph and replayed.
 #include <cstring>
 #include <vector>
 
@@ -31,12 +33,15 @@ struct rk_stage {
     char *mem = nullptr;  // one device allocation for all of the below
     int64_t bytes = 0;
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *att_out = nullptr;
-    float *h = nullptr, *cos_t = nullptr, *sin_t = nullptr, *part_v = nullptr, *logits = nullptr,
-          *rms_final = nullptr;
-    int32_t *part_i = nullptr, *ctl = nullptr, *tokens = nullptr;
-    int8_t *qx = nullptr;
+    float *h = nullptr, *cos_t = nullptr, *sin_t = nullptr, *logits = nullptr, *rms_final = nullptr;
+    int32_t *ctl = nullptr, *tokens = nullptr;
+    unsigned long long *amax = nullptr;  // the classifier's argmax keys
+    int8_t *qx = nullptr;  // the fallback quantize's output
     float *xs = nullptr;
     int32_t *xsum = nullptr;
+    // Quantized inputs passed between launches: A (attention -> Wo, W1/W3
+    // -> W2) and B (norm tails and the embedding -> QKV, W1/W3, classifier).
+    rk::QScratch qa{}, qb{};
     struct LayerDev {
         float *rms_att, *rms_ffn, *bias, *q_norm, *k_norm;  // device copies
         float *keys, *vals;
@@ -59,12 +64,11 @@ static constexpr int kForwardBatch = 64;  // tokens per staging round (gpustage.
 
 static int fmt_of(const rk_matrix *m) { return m->kind == RK_Q4 ? kFmtQ4 : kFmtQ8; }
 
-// One product of a stage: input `in` (f32, `cols` wide; RMSNorm'd with
-// norm_w first when given), matrices ms[0..n) of one format, epilogue epi.
-// The input's norm and quantization run in the product's own prologue when
-// the width fits LDS, else as separate launches into the stage's scratch.
-static int stage_product(rk_stage *s, hipStream_t st, const char *name, const float *in, const float *norm_w,
-                         float recip_n, rk_matrix *const *ms, int n, float *const *outs, int epi, FusedArgs a) {
+// One product of a stage: matrices ms[0..n) of one format, epilogue epi;
+// input quantized in q, or (q null) f32 `in` quantized by the product's own
+// prologue (or, too wide for that, by a separate launch into s->qx).
+static int stage_product(rk_stage *s, hipStream_t st, const char *name, const QScratch *q, const float *in,
+                         rk_matrix *const *ms, int n, float *const *outs, int epi, FusedArgs a) {
     rk_device *d = s->d;
     const int cols = (int)ms[0]->cols;
     const int fmt = fmt_of(ms[0]);
@@ -76,24 +80,19 @@ static int stage_product(rk_stage *s, hipStream_t st, const char *name, const fl
         rows += ms[i]->rows;
     }
     a.rows = (int32_t)rows;
-    int pro = norm_w ? kProNorm : kProQuant;
-    if (fused_fits(pro, cols)) {
+    int pro = kProGlobal;
+    if (q) {
+        a.qx = q->qx;
+        a.xs = q->xs;
+        a.xsum = q->xsum;
+    } else if (fused_fits(kProQuant, cols)) {
+        pro = kProQuant;
         a.x = in;
-        a.norm_w = norm_w;
-        a.recip_n = recip_n;
-        a.eps = s->c.norm_eps;
     } else {
-        const float *src = in;
-        if (norm_w) {
-            ProfScope p(d, st, "rmsnorm");
-            launch_rmsnorm(in, s->xb, norm_w, cols, 1, 0, recip_n, s->c.norm_eps, st);
-            src = s->xb;
-        }
         {
             ProfScope p(d, st, "quantize_acts");
-            launch_quantize_acts(src, cols, s->qx, s->xs, s->xsum, st);
+            launch_quantize_acts(in, cols, s->qx, s->xs, s->xsum, st);
         }
-        pro = kProGlobal;
         a.qx = s->qx;
         a.xs = s->xs;
         a.xsum = s->xsum;
@@ -107,8 +106,17 @@ static int stage_product(rk_stage *s, hipStream_t st, const char *name, const fl
     return RK_OK;
 }
 
-// The launches of one layer (Stage.Forward's body, model.go:530-611).
-static int enqueue_layer(rk_stage *s, int li, hipStream_t st) {
+// RMSNorm(x) with w, quantized into qb: the next product's input.
+static void norm_into_qb(rk_stage *s, hipStream_t st, const float *w) {
+    if (!w) return;
+    ProfScope p(s->d, st, "norm_quant");
+    launch_norm_quant(s->x, s->c.dim, w, s->c.recip_dim, s->c.norm_eps, s->qb.qx, s->qb.xs, s->qb.xsum, st);
+}
+
+// The launches of one layer (Stage.Forward's body, model.go:530-611). On
+// entry qb holds RMSNorm_att(x) quantized; next_norm is the norm whose
+// input qb must hold on exit (the next layer's, the head's, or none).
+static int enqueue_layer(rk_stage *s, int li, hipStream_t st, const float *next_norm) {
     rk_device *d = s->d;
     const rk_stage_config &c = s->c;
     const rk_stage_layer &L = s->layers[li];
@@ -133,10 +141,8 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st) {
             while (j < 3 && qkv[j]->kind == qkv[i]->kind) j++;
             FusedArgs a = base;
             a.row_base = row;  // the epilogue indexes q/k/v rows and biases by row_base + row
-            float *outs[3] = {s->q, nullptr, nullptr};  // only q rows store through seg[0]
-            if (i > 0) outs[0] = nullptr;
-            if ((rc = stage_product(s, st, "qkv", s->x, D.rms_att, c.recip_dim, qkv + i, j - i, outs, kEpQKV, a)))
-                return rc;
+            float *outs[3] = {i == 0 ? s->q : nullptr, nullptr, nullptr};  // only q rows store through seg[0]
+            if ((rc = stage_product(s, st, "qkv", &s->qb, nullptr, qkv + i, j - i, outs, kEpQKV, a))) return rc;
             for (int t = i; t < j; t++) row += (int)qkv[t]->rows;
             i = j;
         }
@@ -150,8 +156,7 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st) {
             int row = 0;
             for (int t = 0; t < i; t++) row += (int)qkv[t]->rows;
             a.bias = D.bias ? D.bias + row : nullptr;
-            if ((rc = stage_product(s, st, "qkv", s->x, D.rms_att, c.recip_dim, qkv + i, j - i, outs + i, kEpStore,
-                                    a)))
+            if ((rc = stage_product(s, st, "qkv", &s->qb, nullptr, qkv + i, j - i, outs + i, kEpStore, a)))
                 return rc;
             i = j;
         }
@@ -164,29 +169,48 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st) {
         launch_att_scores(s->q, D.keys, s->att, c.ctx, s->ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim,
                           c.inv_sqrt, st);
     }
+    // The attention output comes quantized when its Q8 blocks fall within
+    // heads (head size a multiple of 32).
+    const bool att_q = s->hs % 32 == 0;
     {
         ProfScope p(d, st, "att_values");
-        launch_att_values(s->att, c.ctx, D.vals, s->att_out, s->ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, st);
+        launch_att_values(s->att, c.ctx, D.vals, s->att_out, s->ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim,
+                          att_q ? s->qa.qx : nullptr, s->qa.xs, s->qa.xsum, st);
     }
     float *xo[1] = {s->x};
-    if ((rc = stage_product(s, st, "wo", s->att_out, nullptr, 0.0f, &L.wo, 1, xo, kEpAdd, base))) return rc;
+    if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, &L.wo, 1, xo, kEpAdd, base)))
+        return rc;
+    norm_into_qb(s, st, D.rms_ffn);
+    // W1 row r and W3 row r interleaved (logical rows); h leaves quantized in qa.
     rk_matrix *w13[2] = {L.w1, L.w3};
     float *ho[2] = {s->h, nullptr};
     FusedArgs a13 = base;
-    if ((rc = stage_product(s, st, "w13", s->x, D.rms_ffn, c.recip_dim, w13, 2, ho, kEpSilu, a13))) return rc;
-    // kEpSilu rows are logical: W1 row r and W3 row r interleaved.
-    if ((rc = stage_product(s, st, "w2", s->h, nullptr, 0.0f, &L.w2, 1, xo, kEpAddCanon, base))) return rc;
+    a13.qx_out = s->qa.qx;
+    a13.xs_out = s->qa.xs;
+    a13.xsum_out = s->qa.xsum;
+    if ((rc = stage_product(s, st, "w13", &s->qb, nullptr, w13, 2, ho, kEpSilu, a13))) return rc;
+    if ((rc = stage_product(s, st, "w2", &s->qa, nullptr, &L.w2, 1, xo, kEpAddCanon, base))) return rc;
+    norm_into_qb(s, st, next_norm);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(d, e, "stage launch");
     return RK_OK;
 }
 
-static int enqueue_layers(rk_stage *s, hipStream_t st) {
-    for (int li = 0; li < (int)s->layers.size(); li++) {
-        int rc = enqueue_layer(s, li, st);
+// All layers; on entry qb holds the first layer's normed input. `last_norm`
+// is the head's norm (generation) or null (a stage's forward).
+static int enqueue_layers(rk_stage *s, hipStream_t st, const float *last_norm) {
+    const int n = (int)s->layers.size();
+    for (int li = 0; li < n; li++) {
+        int rc = enqueue_layer(s, li, st, li + 1 < n ? s->ld[li + 1].rms_att : last_norm);
         if (rc) return rc;
     }
     return RK_OK;
+}
+
+// Layers on the activation the host wrote to x.
+static int enqueue_forward(rk_stage *s, hipStream_t st) {
+    norm_into_qb(s, st, s->ld[0].rms_att);
+    return enqueue_layers(s, st, nullptr);
 }
 
 // One generation step: embed the position's token, the layers, the head.
@@ -194,20 +218,20 @@ static int enqueue_token(rk_stage *s, hipStream_t st) {
     rk_device *d = s->d;
     {
         ProfScope p(d, st, "embed");
-        launch_embed_pos(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->tokens, s->ctl, s->c.dim, s->x,
-                         st);
+        launch_embed_norm(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->tokens, s->ctl, s->c.dim, s->x,
+                          s->ld[0].rms_att, s->c.recip_dim, s->c.norm_eps, s->qb.qx, s->qb.xs, s->qb.xsum, st);
     }
-    int rc = enqueue_layers(s, st);
+    int rc = enqueue_layers(s, st, s->rms_final);
     if (rc) return rc;
     FusedArgs a{};
     a.ctl = s->ctl;
-    a.part_v = s->part_v;
-    a.part_i = s->part_i;
-    a.tokens = s->tokens;
-    a.tokens_len = s->c.ctx + 1;
+    a.amax = s->amax;
     a.gate = 1;
     float *lo[1] = {s->logits};
-    return stage_product(s, st, "logits", s->x, s->rms_final, s->c.recip_dim, &s->wcls, 1, lo, kEpLogits, a);
+    if ((rc = stage_product(s, st, "logits", &s->qb, nullptr, &s->wcls, 1, lo, kEpLogits, a))) return rc;
+    ProfScope p(d, st, "advance");
+    launch_advance(s->ctl, s->amax, s->tokens, s->c.ctx + 1, st);
+    return RK_OK;
 }
 
 // Records `which` (layers or a whole token) into a graph, once.
@@ -218,7 +242,7 @@ static int record(rk_stage *s, bool token) {
     if (x) return RK_OK;
     HIP_TRY(d, hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal), "stage capture");
     d->capturing = true;
-    int rc = token ? enqueue_token(s, d->stream) : enqueue_layers(s, d->stream);
+    int rc = token ? enqueue_token(s, d->stream) : enqueue_forward(s, d->stream);
     d->capturing = false;
     hipGraph_t gr = nullptr;
     hipError_t e = hipStreamEndCapture(d->stream, &gr);
@@ -245,17 +269,17 @@ static int record(rk_stage *s, bool token) {
 // device profiles, the launches run one by one instead, each timed.
 static int run_once(rk_stage *s, bool token) {
     rk_device *d = s->d;
-    if (d->profiling) return token ? enqueue_token(s, d->stream) : enqueue_layers(s, d->stream);
+    if (d->profiling) return token ? enqueue_token(s, d->stream) : enqueue_forward(s, d->stream);
     int rc = record(s, token);
     if (rc) return rc;
     HIP_TRY(d, hipGraphLaunch(token ? s->x_token : s->x_layers, d->stream), "stage replay");
     return RK_OK;
 }
 
-__global__ void set_ctl_kernel(int32_t *ctl, int32_t pos, int32_t prompt) {
+__global__ void set_ctl_kernel(int32_t *ctl, unsigned long long *amax, int32_t pos, int32_t prompt) {
     ctl[kCtlPos] = pos;
     ctl[kCtlPrompt] = prompt;
-    ctl[kCtlDone] = 0;
+    for (int i = 0; i < kArgmaxSlots; i++) amax[i] = 0ull;
 }
 
 static bool valid_mat(const rk_matrix *m, rk_device *d, int64_t rows, int64_t cols) {
@@ -274,12 +298,14 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
         return fail(d, RK_ERR_ARGS, "rk_stage_new: bad arguments");
     *out = nullptr;
     const int hs = c->head_dim > 0 ? c->head_dim : (c->heads > 0 ? c->dim / c->heads : 0);
+    if (c->dim > kMaxNormCols) return fail(d, RK_ERR_UNSUPPORTED, "rk_stage_new: dim %d beyond %d", c->dim, kMaxNormCols);
     if (c->dim <= 0 || c->hidden <= 0 || c->heads <= 0 || c->kv_heads <= 0 || hs <= 0 || hs % 2 != 0 ||
         c->heads % c->kv_heads != 0 || c->ctx <= 0 || c->dim % 32 != 0 || c->hidden % 32 != 0 ||
         (c->heads * hs) % 32 != 0)
         return fail(d, RK_ERR_ARGS, "rk_stage_new: config out of range");
-    // The softmax keeps a head's weights in LDS (values kernel).
-    if (c->ctx > 16000) return fail(d, RK_ERR_UNSUPPORTED, "rk_stage_new: ctx %d beyond 16000", c->ctx);
+    // The values kernel keeps a head's weights and a chunk of products in LDS.
+    if (c->ctx > att_values_max_ctx())
+        return fail(d, RK_ERR_UNSUPPORTED, "rk_stage_new: ctx %d beyond %d", c->ctx, att_values_max_ctx());
     const int qdim = c->heads * hs, kvdim = c->kv_heads * hs;
     for (int i = 0; i < n_layers; i++) {
         const rk_stage_layer &L = layers[i];
@@ -321,13 +347,17 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
     take((void **)&s->h, 4 * c->hidden);
     take((void **)&s->cos_t, 4 * ctx * s->half);
     take((void **)&s->sin_t, 4 * ctx * s->half);
-    take((void **)&s->part_v, 4 * kMaxArgmaxParts);
-    take((void **)&s->part_i, 4 * kMaxArgmaxParts);
+    take((void **)&s->amax, 8 * kArgmaxSlots);
     take((void **)&s->ctl, 4 * kCtlWords);
     take((void **)&s->tokens, 4 * (ctx + 1));
     take((void **)&s->qx, widest);
     take((void **)&s->xs, 4 * (widest / 32));
     take((void **)&s->xsum, 4 * (widest / 32));
+    for (QScratch *q : {&s->qa, &s->qb}) {
+        take((void **)&q->qx, widest);
+        take((void **)&q->xs, 4 * (widest / 32));
+        take((void **)&q->xsum, 4 * (widest / 32));
+    }
     take((void **)&s->rms_final, 4 * c->dim);
     s->ld.resize(n_layers);
     const int64_t bias_n = c->qkv_bias ? qdim + 2 * kvdim : 0;
@@ -417,7 +447,7 @@ int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens) {
         for (int t = 0; t < n; t++) {
             HIP_TRY(d, hipMemcpyAsync(s->x, s->h_x + (int64_t)t * dim, (size_t)dim * 4, hipMemcpyHostToDevice, st),
                     "stage input");
-            hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, st, s->ctl, pos + start + t, 0);
+            hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, st, s->ctl, s->amax, pos + start + t, 0);
             int rc = run_once(s, false);
             if (rc) return rc;
             HIP_TRY(d, hipMemcpyAsync(s->h_x + (int64_t)t * dim, s->x, (size_t)dim * 4, hipMemcpyDeviceToHost, st),
@@ -502,7 +532,7 @@ int rk_stage_generate_start(rk_stage *s, const int32_t *prompt, int32_t n_prompt
     memcpy(s->h_ctl, prompt, (size_t)n_prompt * 4);
     HIP_TRY(d, hipMemcpyAsync(s->tokens, s->h_ctl, (size_t)n_prompt * 4, hipMemcpyHostToDevice, d->stream),
             "prompt upload");
-    hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, d->stream, s->ctl, 0, n_prompt);
+    hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, d->stream, s->ctl, s->amax, 0, n_prompt);
     HIP_TRY(d, hipGetLastError(), "generate start");
     HIP_TRY(d, hipStreamSynchronize(d->stream), "generate start");
     return RK_OK;
