@@ -66,11 +66,60 @@ __device__ __forceinline__ float lds_sum_fixed(const float *p, float acc) {
     return acc;
 }
 
+// Software pipeline of a sequential LDS sum: batches of kChainBatch float4,
+// the next batch's reads issued before the current batch's additions. The
+// scheduling barriers keep the compiler from sinking the reads next to their
+// uses (it otherwise keeps one read in flight to save registers, and every
+// four additions then wait out a whole LDS latency).
+constexpr int kChainBatch = 8;
+
+__device__ __forceinline__ void lds_load_batch(float4 (&b)[kChainBatch], const float4 *q) {
+#pragma unroll
+    for (int k = 0; k < kChainBatch; k++) b[k] = q[k];
+}
+
+__device__ __forceinline__ float add_batch(const float4 (&b)[kChainBatch], float acc) {
+#pragma unroll
+    for (int k = 0; k < kChainBatch; k++) {
+        acc += b[k].x;
+        acc += b[k].y;
+        acc += b[k].z;
+        acc += b[k].w;
+    }
+    return acc;
+}
+
 // acc + p[0] + p[1] + ... + p[n-1], added one at a time in order (float32),
-// from LDS (p 16-byte aligned), in fixed-size straight-line pieces.
+// from LDS (p 16-byte aligned).
 __device__ __forceinline__ float lds_chain_sum(const float *p, int n, float acc) {
-    int t = 0;
-    for (; t + 128 <= n; t += 128) acc = lds_sum_fixed<128>(p + t, acc);
+    constexpr int kPer = 4 * kChainBatch;  // floats per batch
+    const float4 *q = reinterpret_cast<const float4 *>(p);
+    const int nb = n / kPer;
+    if (nb > 0) {
+        float4 a[kChainBatch], b[kChainBatch];
+        lds_load_batch(a, q);
+        int k = 1;
+        for (; k + 1 < nb; k += 2) {
+            lds_load_batch(b, q + k * kChainBatch);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(a, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_load_batch(a, q + (k + 1) * kChainBatch);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(b, acc);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (k < nb) {
+            lds_load_batch(b, q + k * kChainBatch);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(a, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(b, acc);
+        } else {
+            acc = add_batch(a, acc);
+        }
+    }
+    int t = nb * kPer;
     for (; t + 16 <= n; t += 16) acc = lds_sum_fixed<16>(p + t, acc);
     for (; t < n; t++) acc += p[t];
     return acc;

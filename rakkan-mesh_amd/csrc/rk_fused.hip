@@ -15,8 +15,7 @@
 // the workgroup itself into LDS before the stream starts (kProQuant): the
 // input's loads are issued first, then the first weight chunks, so the
 // prologue runs while those weights are on their way. Results wait in LDS
-// and leave coalesced at the end; a residual product's last workgroup may
-// then RMSNorm and quantize the whole updated vector for the next product.
+// and leave coalesced at the end.
 #include <algorithm>
 #include <mutex>
 
@@ -596,6 +595,22 @@ constexpr int kScoreTile = 64;
 __device__ __forceinline__ float dppf_x1(float v) { return __int_as_float(dpp_x1(__float_as_int(v))); }
 __device__ __forceinline__ float dppf_x2(float v) { return __int_as_float(dpp_x2(__float_as_int(v))); }
 
+// Go max over the wave, valid in every lane: inside each row of 16 lanes by
+// DPP (xor 1, xor 2, half-row mirror, row mirror), then the four rows by
+// readlane. Go max (NaN wins, +0 over -0) is associative and commutative, so
+// the order is free. Every lane of the wave must call it.
+__device__ __forceinline__ float wave_gomax(float m) {
+    m = gomax(m, dppf_x1(m));
+    m = gomax(m, dppf_x2(m));
+    m = gomax(m, __int_as_float(dpp_mirror8(__float_as_int(m))));
+    m = gomax(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x140, 0xF, 0xF, false)));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+    return gomax(gomax(r0, r1), gomax(r2, r3));
+}
+
 template <int HS>  // head size when fixed at compile time (all loads issued at once), else 0
 __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const float *keys, float *att,
                                                          int32_t att_stride, const int32_t *ctl, int kv_mul, int hs_rt,
@@ -659,18 +674,27 @@ void launch_att_scores(const float *q, const float *keys, float *att, int32_t at
 // workgroup (grid: heads, ceil(hs/32)). The order is the CPU's: Go max,
 // e_t = Exp32(s_t - max), one sequential sum, inv = Recip32(sum), a_t =
 // e_t·inv, then out_i = Σ_t a_t·v_t,i in t order from +0. The slice's values
-// for up to kValChunk positions are loaded at the start (in flight during
-// the softmax); their products a_t·v_t,i are formed in parallel into LDS,
-// transposed, and each element's sequential sum reads them four at a time
-// in straight-line code. A slice holding a whole Q8 block is quantized for
-// the next product. LDS beyond 64 KiB (gfx950 gives a workgroup 160 KiB).
+// for a chunk of positions are loaded up front (the first chunk's during the
+// softmax, each next one's during the previous chunk's sums); a thread takes
+// four consecutive positions of four elements, so the products a_t·v_t,i go
+// to LDS transposed as 16-byte writes, and each element's sequential sum
+// (wave 0, one lane per element) reads them four at a time. The product
+// tiles are double-buffered: the other waves write chunk c+1's while wave 0
+// sums chunk c. A slice holding a whole Q8 block is quantized for the next
+// product. The LDS can exceed 64 KiB (gfx950 gives a workgroup 160 KiB).
 constexpr int kValSlice = 32;
-constexpr int kValThreads = 512;
-constexpr int kValChunk = 768;
-constexpr int kValPitch = kValChunk + 4;                              // floats per element row (odd 16-byte units)
-constexpr int kValLoads = kValChunk * kValSlice / 4 / kValThreads;    // float4 loads per thread per chunk
-constexpr int kValRows = kValThreads / (kValSlice / 4);               // positions per load round
+constexpr int kValThreads = 256;
+constexpr int kValChunk = 256;
+constexpr int kValPitch = kValChunk + 4;  // floats per element row (odd count of 16-byte units)
+// thread -> float4 column fq (elements 4fq..4fq+3) and position quad pq
+// (positions 4pq..4pq+3 of a round); rounds cover the chunk
+constexpr int kValQuads = kValThreads / (kValSlice / 4);             // position quads per round
+constexpr int kValRounds = kValChunk / (4 * kValQuads);              // rounds per chunk
 
+// VEC: head size and value-row stride are multiples of 4, so a thread's four
+// elements are one 16-byte load (a separate instance: a run-time choice would
+// be if-converted into four 4-byte loads for every shape).
+template <bool VEC>
 __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *att, int32_t att_stride,
                                                                  const float *vals, float *out, const int32_t *ctl,
                                                                  int kv_mul, int hs, int kv_dim, int ctx_pad,
@@ -679,37 +703,41 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
     __shared__ float s_red[kValThreads / 64];
     __shared__ float s_inv;
     float *sa = smem;            // [ctx_pad] scores -> weights
-    float *sp = smem + ctx_pad;  // [kValSlice][kValPitch] products of a chunk
+    float *sp = smem + ctx_pad;  // [2][kValSlice][kValPitch] product tiles of two chunks
     const int T = ctl[kCtlPos] + 1;
     const int h = blockIdx.x, g = h / kv_mul;
     const int e0 = blockIdx.y * kValSlice;
     const int ne = min(kValSlice, hs - e0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *vbase = vals + (int64_t)g * hs + e0;
-    const bool vec = (hs & 3) == 0 && (kv_dim & 3) == 0;
-    // thread -> (float4 column fq of the slice, positions pr + kValRows·k)
-    const int fq = tid & 7, pr = tid >> 3;
+    const int fq = tid & 7, pq = tid >> 3;
 
-    float4 vr[kValLoads];
+    // One chunk of values in registers, loaded during the softmax (the
+    // first) or the previous chunk's sums. Loads are unconditional (position
+    // clamped to T-1, element column to the slice): values past T or the
+    // slice give products that are never summed or output.
+    float4 vr[kValRounds][4];  // [round][position within the quad]
     auto load_chunk = [&](int c0) {
 #pragma unroll
-        for (int k = 0; k < kValLoads; k++) {
-            const int t = min(c0 + pr + kValRows * k, T - 1);
-            const float *p = vbase + (int64_t)t * kv_dim + 4 * fq;
-            if (vec && 4 * fq + 3 < ne) {
-                vr[k] = *reinterpret_cast<const float4 *>(p);
-            } else {
-                const int n4 = ne - 4 * fq;
-                vr[k].x = n4 > 0 ? p[0] : 0.0f;
-                vr[k].y = n4 > 1 ? p[1] : 0.0f;
-                vr[k].z = n4 > 2 ? p[2] : 0.0f;
-                vr[k].w = n4 > 3 ? p[3] : 0.0f;
+        for (int r = 0; r < kValRounds; r++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int t = min(c0 + 4 * (pq + kValQuads * r) + j, T - 1);
+                const float *row = vbase + (int64_t)t * kv_dim;
+                if (VEC) {
+                    vr[r][j] = *reinterpret_cast<const float4 *>(row + min(4 * fq, ne - 4));
+                } else {
+                    vr[r][j].x = row[min(4 * fq, ne - 1)];
+                    vr[r][j].y = row[min(4 * fq + 1, ne - 1)];
+                    vr[r][j].z = row[min(4 * fq + 2, ne - 1)];
+                    vr[r][j].w = row[min(4 * fq + 3, ne - 1)];
+                }
             }
         }
     };
     // the head's scores (the first 1024 with the values, all in flight)
     const float *ah = att + (int64_t)h * att_stride;
-    constexpr int kScPer = 2;
+    constexpr int kScPer = 1024 / kValThreads;
     float sv[kScPer];
 #pragma unroll
     for (int k = 0; k < kScPer; k++) sv[k] = ah[min(tid + kValThreads * k, T - 1)];
@@ -729,10 +757,11 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
         sa[t] = v;
         m = gomax(m, v);
     }
-    for (int w = 1; w < 64; w <<= 1) m = gomax(m, __shfl_xor(m, w));
+    m = wave_gomax(m);
     if (lane == 0) s_red[wave] = m;
     __syncthreads();
     m = s_red[0];
+#pragma unroll
     for (int w = 1; w < kValThreads / 64; w++) m = gomax(m, s_red[w]);
     for (int t = tid; t < T; t += kValThreads) sa[t] = exp32(sa[t] - m);
     __syncthreads();
@@ -742,29 +771,38 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
     for (int t = tid; t < T; t += kValThreads) sa[t] = sa[t] * inv;
     __syncthreads();
 
+    // Chunk c: its products into tile c mod 2, chunk c+1's loads, a barrier,
+    // then wave 0's sums over the tile. The tile was last read by wave 0's
+    // sums two chunks ago, which ended before it reached the previous barrier,
+    // so the other waves write chunk c+1's products while wave 0 sums chunk c.
     float acc = 0.0f;
-    for (int c0 = 0; c0 < T; c0 += kValChunk) {
-        // products of this chunk, transposed: sp[i][t - c0]
+    int buf = 0;
+    for (int c0 = 0; c0 < T; c0 += kValChunk, buf ^= 1) {
+        float *tile = sp + buf * (kValSlice * kValPitch);
 #pragma unroll
-        for (int k = 0; k < kValLoads; k++) {
-            const int tt = pr + kValRows * k;
-            const float a_t = sa[min(c0 + tt, T - 1)];
-            float *dst = sp + (4 * fq) * kValPitch + tt;
-            dst[0] = a_t * vr[k].x;
-            dst[kValPitch] = a_t * vr[k].y;
-            dst[2 * kValPitch] = a_t * vr[k].z;
-            dst[3 * kValPitch] = a_t * vr[k].w;
+        for (int r = 0; r < kValRounds; r++) {
+            const int tt = 4 * (pq + kValQuads * r);
+            const float4 a4 = *reinterpret_cast<const float4 *>(sa + min(c0 + tt, ctx_pad - 4));
+            float *dst = tile + (4 * fq) * kValPitch + tt;
+            *reinterpret_cast<float4 *>(dst) =
+                make_float4(a4.x * vr[r][0].x, a4.y * vr[r][1].x, a4.z * vr[r][2].x, a4.w * vr[r][3].x);
+            *reinterpret_cast<float4 *>(dst + kValPitch) =
+                make_float4(a4.x * vr[r][0].y, a4.y * vr[r][1].y, a4.z * vr[r][2].y, a4.w * vr[r][3].y);
+            *reinterpret_cast<float4 *>(dst + 2 * kValPitch) =
+                make_float4(a4.x * vr[r][0].z, a4.y * vr[r][1].z, a4.z * vr[r][2].z, a4.w * vr[r][3].z);
+            *reinterpret_cast<float4 *>(dst + 3 * kValPitch) =
+                make_float4(a4.x * vr[r][0].w, a4.y * vr[r][1].w, a4.z * vr[r][2].w, a4.w * vr[r][3].w);
         }
-        if (c0 + kValChunk < T) load_chunk(c0 + kValChunk);  // in flight while this chunk is summed
+        load_chunk(c0 + kValChunk);  // in flight while this chunk is summed
         __syncthreads();
         const int n = min(kValChunk, T - c0);
-        if (wave == 0 && lane < kValSlice) acc = lds_chain_sum(sp + lane * kValPitch, n, acc);
-        __syncthreads();
+        if (wave == 0 && lane < kValSlice) acc = lds_chain_sum(tile + lane * kValPitch, n, acc);
     }
     if (wave == 0 && lane < ne) out[(int64_t)h * hs + e0 + lane] = acc;
     if (qx && ne == kValSlice) {
         // the slice is one Q8_0 block of the next input (e0 is a multiple
         // of 32): lanes 0-7 take four values each
+        __syncthreads();  // every wave is past its last product write
         if (wave == 0 && lane < kValSlice) sp[lane] = acc;
         __syncthreads();
         if (wave == 0) {
@@ -786,27 +824,33 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
 }
 
 // Dynamic LDS of the values kernel for a context of ctx positions.
-static size_t att_values_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + kValSlice * kValPitch) * 4; }
+static size_t att_values_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + 2 * kValSlice * kValPitch) * 4; }
 
 // Dynamic LDS the values kernel may ask for: the device's 160 KiB less
 // room for its static LDS.
 constexpr size_t kValMaxDynLds = kMaxLdsBytes - 1024;
 
-int att_values_max_ctx() { return (int)(kValMaxDynLds / 4 - kValSlice * kValPitch) & ~3; }
+int att_values_max_ctx() { return (int)(kValMaxDynLds / 4 - 2 * kValSlice * kValPitch) & ~3; }
 
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                        int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
                        hipStream_t s) {
     static std::once_flag once;
     std::call_once(once, [] {
-        (void)hipFuncSetAttribute((const void *)att_values_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (void)hipFuncSetAttribute((const void *)att_values_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)kValMaxDynLds);
+        (void)hipFuncSetAttribute((const void *)att_values_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)kValMaxDynLds);
     });
     const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice);
     if (hs % 32 != 0) qx = nullptr;
     const int ctx_pad = (ctx + 3) & ~3;
-    RK_LAUNCH(att_values_kernel, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals, out, ctl,
-              heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
+    if (hs % 4 == 0 && kv_dim % 4 == 0)
+        RK_LAUNCH(att_values_kernel<true>, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals, out,
+                  ctl, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
+    else
+        RK_LAUNCH(att_values_kernel<false>, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals,
+                  out, ctl, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
 }
 
 // QK-norm (internal/llm/model.go:551-558) and RoPE (:563-572) of one head

@@ -2,16 +2,17 @@
 // (internal/llm/gpustage.go), and the greedy generation loop around them
 // (embedding, head, argmax) with its state on the device.
 //
-// A token runs as six launches per layer, every product reading its input
+// A token runs as eight launches per layer, every product reading its input
 // already quantized (Q8_0 codes, block scales, block code sums):
 //   qkv      [Wq;Wk;Wv]·xn (+bias), RoPE, k and v into the caches
 //            (Qwen3: raw q/k/v, then qknorm_rope)
 //   scores   Dot32(q_h, k_t)·invSqrt for t <= position
 //   values   softmax, Σ a_t·v_t, quantized
-//   wo       x += Wo·att; its last workgroup: xn = RMSNorm_ffn(x), quantized
+//   wo       x += Wo·att
+//   norm     xn = RMSNorm_ffn(x), quantized
 //   w13      h = silu(W1·xn)·(W3·xn), quantized
-//   w2       x = Canonical(x + W2·h); its last workgroup: xn = RMSNorm of the
-//            next layer (or the head), quantized
+//   w2       x = Canonical(x + W2·h)
+//   norm     xn = RMSNorm of the next layer (or the head), quantized
 // in the order and rounding of Stage.Forward (internal/llm/model.go:522-613).
 // Generation embeds the position's token first (and RMSNorms it for the
 // first layer) and ends with the classifier and the greedy argmax, which
