@@ -101,6 +101,20 @@ int rk_matvecs(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *ou
 int rk_matvecs_device(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *d_outs, const float *d_x,
                       int64_t cols, void *stream);
 
+/* ---- Batched products (prompt prefill) ----
+ * No reference counterpart: the reference runs a prompt one token at a time
+ * (internal/llm/model.go:504-518), each token's products through MulVecs
+ * (internal/gpu/device.go:769-793). For each of `tokens` inputs
+ * x_t = x + t·cols: outs[i] + t·rows_i receives ms[i]·x_t, bit for bit what
+ * rk_matvecs gives for x_t alone. The block sums run on int8 MFMA. Host
+ * buffers, blocking. */
+int rk_matmul_t(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
+                int32_t tokens);
+/* The same with device-resident x ([tokens][cols]) and outputs
+ * ([tokens][rows_i]), enqueued on `stream` (NULL: the device's own). */
+int rk_matmul_t_device(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *d_outs, const float *d_x,
+                       int64_t cols, int32_t tokens, void *stream);
+
 /* ---- Arenas, vectors and batches (internal/gpu/batch.go) ----
  * An arena is device memory of 32-bit words holding a computation's
  * activations, caches and tables; batch operations address it by word

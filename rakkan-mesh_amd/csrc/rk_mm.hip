@@ -1,0 +1,400 @@
+// rk_mm.hip — batched quantized products for prompt prefill, on gfx950's
+// int8 matrix cores. The reference runs a prompt one token at a time
+// (internal/llm/model.go:504-518), each token's products through MatVecQ8/Q4
+// (internal/num/quant.go:158-196); a batch here gives every (token, row) the
+// bits of that token's own product:
+//
+//   out[t][r] = ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)),
+//   s_(b mod 8) += float32(sum_b[r][t])·float32(ws[r][b]·xs[t][b]) in order of b,
+//
+// with sum_b the exact integer dot of block b. One v_mfma_i32_16x16x32_i8
+// (K = 32 = one block, accumulator zero) gives sum_b for 16 rows × 16 tokens;
+// the f32 steps above then run on the vector ALUs in that order, so those
+// four operations per (row, token, block) bound the kernel, not the MFMA.
+//
+// Work layout: a workgroup (four waves, 2×2) owns 64 rows × 64 tokens and
+// walks the blocks in chunks of eight (one per running sum). A chunk's codes
+// and scales are staged in LDS (Q4_0 unpacked to signed codes once there),
+// double-buffered: the next chunk's global loads are in flight while the
+// current one is multiplied. Tiles are numbered so that each XCD takes a
+// contiguous run, keeping a row tile's token tiles on one L2.
+#include <mutex>
+
+#include "rk_dev.h"
+#include "rk_mm.h"
+
+namespace rk {
+
+namespace {
+
+constexpr int kMmRows = 64;      // output rows per workgroup (kEpSilu: 32 rows of W1 and of W3)
+constexpr int kMmToks = 64;      // tokens per workgroup
+constexpr int kMmKB = 8;         // blocks per staged chunk, one per running sum
+constexpr int kMmThreads = 256;  // four waves: (row half, token half)
+// Bytes per staged row: 16 rows read at one offset fall in distinct banks.
+constexpr int kMmPitch = kMmKB * 32 + 8;
+constexpr int kHbPitch = 36;  // kEpSilu: floats per token row of h
+
+struct MmStage {
+    int8_t w[kMmRows][kMmPitch];  // codes of the staged rows (Q4 unpacked)
+    int8_t x[kMmToks][kMmPitch];  // codes of the staged tokens
+    float ws[kMmKB][kMmRows];     // weight scales, block-major
+    float xs[kMmKB][kMmToks];     // input scales, block-major
+};
+static_assert(sizeof(MmStage) % 16 == 0, "stage buffers stay 16-byte aligned");
+static_assert(kMmToks * kHbPitch * 4 <= (int)sizeof(MmStage), "h tile fits a stage buffer");
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+
+// 16 bytes into LDS that is 8-byte aligned (staged rows have an odd count
+// of 8-byte units).
+__device__ __forceinline__ void lds_put16(int8_t *p, v4i v) {
+    reinterpret_cast<v2i *>(p)[0] = v2i{v.x, v.y};
+    reinterpret_cast<v2i *>(p)[1] = v2i{v.z, v.w};
+}
+
+// Four Q4 nibbles (0..15, one per byte) to their signed codes n-8 (one per
+// byte): the OR keeps every byte >= 8 so the subtraction borrows nowhere.
+__device__ __forceinline__ uint32_t nib_signed(uint32_t n) { return ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+
+// Source of logical output row g (< rows): segment and row in it.
+__device__ __forceinline__ const MatSeg &seg_of(const MmArgs &a, int g, int &r) {
+    r = g;
+    if (a.nseg > 1 && r >= a.seg[0].rows) {
+        r -= (int)a.seg[0].rows;
+        if (a.nseg > 2 && r >= a.seg[1].rows) {
+            r -= (int)a.seg[1].rows;
+            return a.seg[2];
+        }
+        return a.seg[1];
+    }
+    return a.seg[0];
+}
+
+}  // namespace
+
+template <int FMT, int EPI>
+__global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
+    extern __shared__ __align__(16) char lds[];
+    MmStage *stg = reinterpret_cast<MmStage *>(lds);  // two buffers
+    constexpr bool SILU = EPI == kEpSilu;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave & 1, wt = wave >> 1;
+    const int lq = lane >> 4, ln = lane & 15;
+    const int cols = a.cols, nb = cols >> 5, T = a.tokens;
+    const int rowbytes = FMT == kFmtQ8 ? cols : cols >> 1;
+
+    // this workgroup's tile: XCD x (workgroups x, x+8, ...) takes tiles
+    // [x·per, (x+1)·per), row-tile major
+    const int ntr = SILU ? (a.rows + 31) >> 5 : (a.rows + kMmRows - 1) / kMmRows;
+    const int ntt = (T + kMmToks - 1) / kMmToks;
+    const int total = ntr * ntt;
+    const int per = (total + 7) >> 3;
+    const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (tile >= total) return;
+    const int rt = tile / ntt, tt = tile - rt * ntt;
+    const int row0 = rt * (SILU ? 32 : kMmRows);
+    const int tok0 = tt * kMmToks;
+
+    // staged row m -> its codes and scales (rows past the end clamped: their
+    // results are never stored)
+    auto row_src = [&](int m, const uint8_t *&w, const float *&ws) __attribute__((always_inline)) {
+        int r;
+        const MatSeg *s;
+        if (SILU) {
+            r = min(row0 + (m & 31), a.rows - 1);
+            s = m < 32 ? &a.seg[0] : &a.seg[1];
+        } else {
+            s = &seg_of(a, min(row0 + m, a.rows - 1), r);
+        }
+        w = s->w + (int64_t)r * rowbytes;
+        ws = s->ws + (int64_t)r * nb;
+    };
+
+    // ---- staging: each thread's rows and tokens, fixed for the kernel ----
+    // Q8 codes: 16-byte piece p = tid + 256j of the chunk's 64 rows x 256
+    // bytes (row p>>4, piece p&15); Q4: p = tid + 256j of 64 rows x 8 blocks
+    // (row p>>3, block p&7). Scales: p = tid + 256j of 64 rows x 8 blocks.
+    constexpr int NW = FMT == kFmtQ8 ? 4 : 2;
+    const uint8_t *wrow[NW];
+    const float *dummy_ws;
+#pragma unroll
+    for (int j = 0; j < NW; j++) row_src(FMT == kFmtQ8 ? (tid >> 4) + 16 * j : (tid >> 3) + 32 * j, wrow[j], dummy_ws);
+    const float *wsrow[2];
+    const uint8_t *dummy_w;
+#pragma unroll
+    for (int j = 0; j < 2; j++) row_src((tid >> 3) + 32 * j, dummy_w, wsrow[j]);
+    const int8_t *xrow[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) xrow[j] = a.qx + (int64_t)min(tok0 + (tid >> 4) + 16 * j, T - 1) * cols;
+    const float *xsrow[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) xsrow[j] = a.xs + (int64_t)min(tok0 + (tid >> 3) + 32 * j, T - 1) * nb;
+
+    const int nchunks = (nb + kMmKB - 1) / kMmKB;
+    v4i rw[NW], rx[4];
+    float rws[2], rxs[2];
+    // loads of the chunk starting at block c (blocks past nb read the last
+    // block: never used)
+    auto stage_load = [&](int c) __attribute__((always_inline)) {
+        c = min(c, (nchunks - 1) * kMmKB);
+#pragma unroll
+        for (int j = 0; j < NW; j++) {
+            if (FMT == kFmtQ8) {
+                const int o = min(c * 32 + (tid & 15) * 16, cols - 16);
+                rw[j] = *reinterpret_cast<const v4i *>(wrow[j] + o);
+            } else {
+                const int bk = min(c + (tid & 7), nb - 1);
+                rw[j] = *reinterpret_cast<const v4i *>(wrow[j] + bk * 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int o = min(c * 32 + (tid & 15) * 16, cols - 16);
+            rx[j] = *reinterpret_cast<const v4i *>(xrow[j] + o);
+        }
+        const int bk = min(c + (tid & 7), nb - 1);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            rws[j] = wsrow[j][bk];
+            rxs[j] = xsrow[j][bk];
+        }
+    };
+    auto stage_store = [&](MmStage &S) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NW; j++) {
+            if (FMT == kFmtQ8) {
+                lds_put16(&S.w[(tid >> 4) + 16 * j][(tid & 15) * 16], rw[j]);
+            } else {
+                // byte i of the block: low nibble w_i, high nibble w_(i+16)
+                const v4i v = rw[j];
+                const v4i lo = v4i{(int)nib_signed(v.x & 0x0F0F0F0Fu), (int)nib_signed(v.y & 0x0F0F0F0Fu),
+                                   (int)nib_signed(v.z & 0x0F0F0F0Fu), (int)nib_signed(v.w & 0x0F0F0F0Fu)};
+                const v4i hi = v4i{(int)nib_signed(((uint32_t)v.x >> 4) & 0x0F0F0F0Fu),
+                                   (int)nib_signed(((uint32_t)v.y >> 4) & 0x0F0F0F0Fu),
+                                   (int)nib_signed(((uint32_t)v.z >> 4) & 0x0F0F0F0Fu),
+                                   (int)nib_signed(((uint32_t)v.w >> 4) & 0x0F0F0F0Fu)};
+                int8_t *dst = &S.w[(tid >> 3) + 32 * j][(tid & 7) * 32];
+                lds_put16(dst, lo);
+                lds_put16(dst + 16, hi);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) lds_put16(&S.x[(tid >> 4) + 16 * j][(tid & 15) * 16], rx[j]);
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            S.ws[tid & 7][(tid >> 3) + 32 * j] = rws[j];
+            S.xs[tid & 7][(tid >> 3) + 32 * j] = rxs[j];
+        }
+    };
+
+    // ---- products: the wave's 2x2 tiles of 16 rows x 16 tokens ----
+    // Row tile ti of the wave: staged rows rb(ti).. +16 (kEpSilu: W1 rows
+    // for ti = 0 and the same W3 rows for ti = 1). A lane holds, per tile,
+    // token tb(tj) + ln and rows rb(ti) + 4·lq + i, i < 4.
+    auto rb = [&](int ti) { return SILU ? 32 * ti + 16 * wr : 32 * wr + 16 * ti; };
+    auto tb = [&](int tj) { return 32 * wt + 16 * tj; };
+    float acc[2][2][kMmKB][4];
+#pragma unroll
+    for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+        for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+            for (int k = 0; k < kMmKB; k++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[ti][tj][k][i] = 0.0f;
+
+    stage_load(0);
+    stage_store(stg[0]);
+    __syncthreads();
+    for (int ci = 0; ci < nchunks; ci++) {
+        const int c0 = ci * kMmKB;
+        // the next chunk's loads (past the last chunk they re-read it and
+        // fill the idle buffer, which nothing reads)
+        stage_load(c0 + kMmKB);
+        const MmStage &S = stg[ci & 1];
+#pragma unroll
+        for (int k = 0; k < kMmKB; k++) {
+            if (c0 + k < nb) {  // absent blocks are skipped, not added as zeros
+                long fa[2], fb[2];
+#pragma unroll
+                for (int ti = 0; ti < 2; ti++)
+                    fa[ti] = *reinterpret_cast<const long *>(&S.w[rb(ti) + ln][k * 32 + 8 * lq]);
+#pragma unroll
+                for (int tj = 0; tj < 2; tj++)
+                    fb[tj] = *reinterpret_cast<const long *>(&S.x[tb(tj) + ln][k * 32 + 8 * lq]);
+                v4i d[2][2];
+#pragma unroll
+                for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+                    for (int tj = 0; tj < 2; tj++)
+                        d[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], v4i{0, 0, 0, 0}, 0, 0, 0);
+                float4 wsv[2];
+                float xsv[2];
+#pragma unroll
+                for (int ti = 0; ti < 2; ti++) wsv[ti] = *reinterpret_cast<const float4 *>(&S.ws[k][rb(ti) + 4 * lq]);
+#pragma unroll
+                for (int tj = 0; tj < 2; tj++) xsv[tj] = S.xs[k][tb(tj) + ln];
+#pragma unroll
+                for (int ti = 0; ti < 2; ti++) {
+                    const float w4[4] = {wsv[ti].x, wsv[ti].y, wsv[ti].z, wsv[ti].w};
+#pragma unroll
+                    for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            acc[ti][tj][k][i] += (float)d[ti][tj][i] * (w4[i] * xsv[tj]);
+                }
+            }
+        }
+        stage_store(stg[(ci + 1) & 1]);
+        __syncthreads();
+    }
+
+    // ---- results: the fixed tree of the eight running sums, then the
+    // epilogue per (row, token) ----
+    float res[2][2][4];
+#pragma unroll
+    for (int ti = 0; ti < 2; ti++)
+#pragma unroll
+        for (int tj = 0; tj < 2; tj++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float p0 = acc[ti][tj][0][i] + acc[ti][tj][1][i], p1 = acc[ti][tj][2][i] + acc[ti][tj][3][i];
+                const float p2 = acc[ti][tj][4][i] + acc[ti][tj][5][i], p3 = acc[ti][tj][6][i] + acc[ti][tj][7][i];
+                res[ti][tj][i] = (p0 + p1) + (p2 + p3);
+            }
+
+    if (SILU) {
+        // h = silu(W1·x)·(W3·x) into LDS [token][32 rows], then each token's
+        // 32 values (one Q8_0 block of h) quantized by eight lanes
+        float *hb = reinterpret_cast<float *>(lds);
+#pragma unroll
+        for (int tj = 0; tj < 2; tj++) {
+            float4 h4;
+            h4.x = silu_mul(res[0][tj][0], res[1][tj][0]);
+            h4.y = silu_mul(res[0][tj][1], res[1][tj][1]);
+            h4.z = silu_mul(res[0][tj][2], res[1][tj][2]);
+            h4.w = silu_mul(res[0][tj][3], res[1][tj][3]);
+            *reinterpret_cast<float4 *>(&hb[(tb(tj) + ln) * kHbPitch + 16 * wr + 4 * lq]) = h4;
+        }
+        __syncthreads();
+        const int nbh = a.rows >> 5;
+#pragma unroll
+        for (int rnd = 0; rnd < kMmToks * 8 / kMmThreads; rnd++) {
+            const int task = tid + kMmThreads * rnd;
+            const int n = task >> 3, g = task & 7;
+            const float4 v = *reinterpret_cast<const float4 *>(&hb[n * kHbPitch + 4 * g]);
+            float dsc;
+            int cs;
+            const uint32_t pk = quantize_group(v.x, v.y, v.z, v.w, dsc, cs);
+            const int t = tok0 + n;
+            if (t < T) {
+                reinterpret_cast<uint32_t *>(a.qx_out + (int64_t)t * a.rows + row0)[g] = pk;
+                if (g == 0) {
+                    a.xs_out[(int64_t)t * nbh + (row0 >> 5)] = dsc;
+                    a.xsum_out[(int64_t)t * nbh + (row0 >> 5)] = cs;
+                }
+            }
+        }
+        return;
+    }
+
+#pragma unroll
+    for (int tj = 0; tj < 2; tj++) {
+        const int t = tok0 + tb(tj) + ln;
+        if (t >= T) continue;
+#pragma unroll
+        for (int ti = 0; ti < 2; ti++) {
+            const int gb = row0 + rb(ti) + 4 * lq;  // the lane's first row
+            if (EPI == kEpQKV) {
+                const int pos = a.pos0 + t, half = a.hs >> 1;
+#pragma unroll
+                for (int pr = 0; pr < 2; pr++) {
+                    const int g0 = gb + 2 * pr;  // an even row: a rotary pair with g0 + 1
+                    float v0 = res[ti][tj][2 * pr], v1 = res[ti][tj][2 * pr + 1];
+                    if (a.bias) {
+                        v0 = v0 + a.bias[min(g0, a.rows - 1)];
+                        v1 = v1 + a.bias[min(g0 + 1, a.rows - 1)];
+                    }
+                    if (g0 < a.qdim + a.kvdim) {
+                        const int ih = g0 < a.qdim ? g0 : g0 - a.qdim;
+                        const int pi = (ih % a.hs) >> 1;
+                        const float co = a.cos_t[(int64_t)pos * half + pi], si = a.sin_t[(int64_t)pos * half + pi];
+                        const float r0 = (v0 * co) - (v1 * si);
+                        const float r1 = (v0 * si) + (v1 * co);
+                        v0 = r0;
+                        v1 = r1;
+                    }
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const int g = g0 + h;
+                        if (g >= a.rows) continue;
+                        float *dst = g < a.qdim ? a.q + (int64_t)t * a.qdim + g
+                                     : g < a.qdim + a.kvdim
+                                         ? a.kcache + (int64_t)pos * a.kvdim + (g - a.qdim)
+                                         : a.vcache + (int64_t)pos * a.kvdim + (g - a.qdim - a.kvdim);
+                        *dst = h ? v1 : v0;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int g = gb + i;
+                    if (g >= a.rows) continue;
+                    const float v = res[ti][tj][i];
+                    if (EPI == kEpStore) {
+                        int r;
+                        const MatSeg &s = seg_of(a, g, r);
+                        s.out[(int64_t)t * s.rows + r] = a.bias ? v + a.bias[g] : v;
+                    } else if (EPI == kEpAdd) {
+                        float *p = a.x + (int64_t)t * a.ldx + g;
+                        *p = *p + v;
+                    } else if (EPI == kEpAddCanon) {
+                        float *p = a.x + (int64_t)t * a.ldx + g;
+                        *p = canonical(*p + v);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, int EPI>
+static void launch_mm_one(const MmArgs &a, unsigned grid, hipStream_t s) {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute((const void *)mm_kernel<FMT, EPI>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)(2 * sizeof(MmStage)));
+    });
+    RK_LAUNCH((mm_kernel<FMT, EPI>), dim3(grid), dim3(kMmThreads), 2 * sizeof(MmStage), s, a);
+}
+
+template <int FMT>
+static bool launch_mm_epi(int epi, const MmArgs &a, unsigned grid, hipStream_t s) {
+    switch (epi) {
+        case kEpStore: launch_mm_one<FMT, kEpStore>(a, grid, s); return true;
+        case kEpAdd: launch_mm_one<FMT, kEpAdd>(a, grid, s); return true;
+        case kEpAddCanon: launch_mm_one<FMT, kEpAddCanon>(a, grid, s); return true;
+        case kEpQKV: launch_mm_one<FMT, kEpQKV>(a, grid, s); return true;
+        case kEpSilu: launch_mm_one<FMT, kEpSilu>(a, grid, s); return true;
+    }
+    return false;
+}
+
+bool launch_mm(int fmt, int epi, const MmArgs &a, hipStream_t s) {
+    if (a.tokens <= 0 || a.rows <= 0) return true;
+    if (a.cols < 32 || a.cols % 32 != 0) return false;
+    if (epi == kEpSilu && (a.rows % 32 != 0 || a.nseg != 2)) return false;
+    if (epi == kEpQKV && (a.hs % 2 != 0 || a.qdim % 2 != 0 || a.kvdim % 2 != 0)) return false;
+    const int ntr = epi == kEpSilu ? a.rows / 32 : (a.rows + kMmRows - 1) / kMmRows;
+    const int ntt = (a.tokens + kMmToks - 1) / kMmToks;
+    const int64_t total = (int64_t)ntr * ntt;
+    const int64_t grid = ((total + 7) / 8) * 8;
+    if (grid > INT32_MAX) return false;
+    if (fmt == kFmtQ8) return launch_mm_epi<kFmtQ8>(epi, a, (unsigned)grid, s);
+    if (fmt == kFmtQ4) return launch_mm_epi<kFmtQ4>(epi, a, (unsigned)grid, s);
+    return false;
+}
+
+}  // namespace rk

@@ -78,6 +78,15 @@ struct rk_device {
     int32_t *xsum = nullptr;
     float *out = nullptr;
     float *h_stage = nullptr;
+    // Scratch of the batched products (rk_matmul_t*), grown on demand:
+    // quantized inputs [tokens][cols] (codes; scales and code sums per block),
+    // and f32 input/output for the host-buffer call.
+    int8_t *bqx = nullptr;
+    float *bxs = nullptr;
+    int32_t *bxsum = nullptr;
+    int64_t bq_cap = 0;  // codes
+    float *bx = nullptr, *bout = nullptr;
+    int64_t bx_cap = 0, bout_cap = 0;  // floats
     hipEvent_t scratch_free = nullptr;
     hipStream_t scratch_stream = nullptr;  // the last stream that used the scratch
     bool scratch_stream_set = false;

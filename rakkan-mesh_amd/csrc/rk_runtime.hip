@@ -2,6 +2,7 @@
 // entry points of include/rk.h for them. The object model mirrors
 // internal/gpu (Device, Matrix, MulVecs); each C entry point cites the Go
 // function whose body it replaces.
+#include "rk_mm.h"
 #include "rk_runtime.h"
 
 #include "rk_fused.h"
@@ -160,6 +161,95 @@ int check_products(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, 
     return RK_OK;
 }
 
+// Grows a device buffer to `need` elements of `elem` bytes (contents not
+// kept). Work already enqueued on any stream may still use the old buffer,
+// so the device is drained first.
+static int grow(rk_device *d, void **p, int64_t &cap, int64_t need, size_t elem, const char *what) {
+    if (need <= cap) return RK_OK;
+    if (d->capturing) return fail(d, RK_ERR_ARGS, "%s: scratch must grow, which cannot be recorded", what);
+    HIP_TRY(d, hipDeviceSynchronize(), what);
+    (void)hipFree(*p);
+    *p = nullptr;
+    cap = 0;
+    int rc = dev_alloc(d, p, (size_t)need * elem, what);
+    if (rc) return rc;
+    cap = need;
+    return RK_OK;
+}
+
+// The batched products' quantized input for `codes` codes (tokens·cols).
+static int batch_scratch(rk_device *d, int64_t codes) {
+    if (codes <= d->bq_cap) return RK_OK;
+    if (d->capturing) return fail(d, RK_ERR_ARGS, "batch scratch must grow, which cannot be recorded");
+    HIP_TRY(d, hipDeviceSynchronize(), "batch scratch");
+    (void)hipFree(d->bqx);
+    (void)hipFree(d->bxs);
+    (void)hipFree(d->bxsum);
+    d->bqx = nullptr;
+    d->bxs = nullptr;
+    d->bxsum = nullptr;
+    d->bq_cap = 0;
+    int rc;
+    if ((rc = dev_alloc(d, (void **)&d->bqx, (size_t)codes, "batch scratch")) ||
+        (rc = dev_alloc(d, (void **)&d->bxs, (size_t)(codes / 32) * 4, "batch scratch")) ||
+        (rc = dev_alloc(d, (void **)&d->bxsum, (size_t)(codes / 32) * 4, "batch scratch")))
+        return rc;
+    d->bq_cap = codes;
+    return RK_OK;
+}
+
+// Batched products: quantize the tokens' inputs once, then one MFMA launch
+// per format (up to three matrices each).
+int enqueue_matmuls(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
+                    int32_t tokens, hipStream_t s) {
+    {
+        ProfScope p(d, s, "quantize_acts");
+        launch_quantize_acts(x, cols * tokens, d->bqx, d->bxs, d->bxsum, s);
+    }
+    for (int kind : {RK_Q8, RK_Q4}) {
+        MmArgs a{};
+        a.cols = (int32_t)cols;
+        a.tokens = tokens;
+        a.qx = d->bqx;
+        a.xs = d->bxs;
+        auto flush = [&]() -> int {
+            if (a.nseg == 0) return RK_OK;
+            bool ok;
+            {
+                ProfScope p(d, s, kind == RK_Q8 ? "matmul_q8" : "matmul_q4");
+                ok = launch_mm(kind == RK_Q8 ? kFmtQ8 : kFmtQ4, kEpStore, a, s);
+            }
+            a.nseg = 0;
+            a.rows = 0;
+            return ok ? RK_OK : fail(d, RK_ERR_UNSUPPORTED, "matmul: shape has no kernel");
+        };
+        for (int i = 0; i < n; i++) {
+            if (ms[i]->kind != kind) continue;
+            a.seg[a.nseg] = MatSeg{ms[i]->w, ms[i]->scales, outs[i], ms[i]->rows};
+            a.rows += (int32_t)ms[i]->rows;
+            if (++a.nseg == 3) {
+                int rc = flush();
+                if (rc) return rc;
+            }
+        }
+        int rc = flush();
+        if (rc) return rc;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(d, e, "matmul launch");
+    return RK_OK;
+}
+
+static int check_matmul(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, int32_t tokens, int64_t *total) {
+    int rc = check_products(d, n, ms, cols, total);
+    if (rc) return rc;
+    if (tokens < 0) return fail(d, RK_ERR_ARGS, "rk_matmul_t: %d tokens", tokens);
+    if ((int64_t)tokens * cols > ((int64_t)1 << 31) - 32 || (int64_t)tokens * *total > ((int64_t)1 << 31))
+        return fail(d, RK_ERR_ARGS, "rk_matmul_t: %d tokens of %lld columns is too large for one call", tokens,
+                    (long long)cols);
+    return RK_OK;
+}
+
 }  // namespace rk
 
 using namespace rk;
@@ -243,6 +333,11 @@ int rk_device_close(rk_device *d) {
     (void)hipFree(d->xs);
     (void)hipFree(d->xsum);
     (void)hipFree(d->out);
+    (void)hipFree(d->bqx);
+    (void)hipFree(d->bxs);
+    (void)hipFree(d->bxsum);
+    (void)hipFree(d->bx);
+    (void)hipFree(d->bout);
     if (d->h_stage) (void)hipHostFree(d->h_stage);
     if (d->scratch_free) (void)hipEventDestroy(d->scratch_free);
     for (auto &r : d->prof) {
@@ -373,6 +468,61 @@ int rk_matvecs_device(rk_device *d, int32_t n, rk_matrix *const *ms, float *cons
         return fail(d, RK_ERR_ARGS, "while recording a graph, work goes on the device's stream");
     if ((rc = scratch_acquire(d, s))) return rc;
     return enqueue_matvecs(d, n, ms, d_outs, d_x, cols, QScratch{d->qx, d->xs, d->xsum}, s);
+}
+
+int rk_matmul_t(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
+                int32_t tokens) {
+    int64_t total;
+    int rc = check_matmul(d, n, ms, cols, tokens, &total);
+    if (rc) return rc;
+    if (n == 0 || tokens == 0) return RK_OK;
+    if (!x || !outs) return fail(d, RK_ERR_ARGS, "rk_matmul_t: null buffer");
+    for (int i = 0; i < n; i++)
+        if (!outs[i]) return fail(d, RK_ERR_ARGS, "rk_matmul_t: null output %d", i);
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    if (d->capturing) return fail(d, RK_ERR_ARGS, "rk_matmul_t waits for its results: it cannot be recorded");
+    hipStream_t s = d->stream;
+    if ((rc = scratch_acquire(d, s))) return rc;
+    if ((rc = grow(d, (void **)&d->bx, d->bx_cap, cols * tokens, 4, "batch input")) ||
+        (rc = grow(d, (void **)&d->bout, d->bout_cap, total * tokens, 4, "batch output")) ||
+        (rc = batch_scratch(d, cols * tokens)))
+        return rc;
+    HIP_TRY(d, hipMemcpyAsync(d->bx, x, (size_t)(cols * tokens) * 4, hipMemcpyHostToDevice, s), "input copy");
+    std::vector<float *> douts(n);
+    int64_t at = 0;
+    for (int i = 0; i < n; i++) {
+        douts[i] = d->bout + at;
+        at += ms[i]->rows * tokens;
+    }
+    if ((rc = enqueue_matmuls(d, n, ms, douts.data(), d->bx, cols, tokens, s))) return rc;
+    at = 0;
+    for (int i = 0; i < n; i++) {
+        HIP_TRY(d, hipMemcpyAsync(outs[i], d->bout + at, (size_t)(ms[i]->rows * tokens) * 4, hipMemcpyDeviceToHost, s),
+                "output copy");
+        at += ms[i]->rows * tokens;
+    }
+    HIP_TRY(d, hipStreamSynchronize(s), "submit");
+    return RK_OK;
+}
+
+int rk_matmul_t_device(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *d_outs, const float *d_x,
+                       int64_t cols, int32_t tokens, void *stream) {
+    int64_t total;
+    int rc = check_matmul(d, n, ms, cols, tokens, &total);
+    if (rc) return rc;
+    if (n == 0 || tokens == 0) return RK_OK;
+    if (!d_x || !d_outs) return fail(d, RK_ERR_ARGS, "rk_matmul_t_device: null buffer");
+    for (int i = 0; i < n; i++)
+        if (!d_outs[i]) return fail(d, RK_ERR_ARGS, "rk_matmul_t_device: null output %d", i);
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipStream_t s = stream ? (hipStream_t)stream : d->stream;
+    if (d->capturing && s != d->stream)
+        return fail(d, RK_ERR_ARGS, "while recording a graph, work goes on the device's stream");
+    if ((rc = scratch_acquire(d, s))) return rc;
+    if ((rc = batch_scratch(d, cols * tokens))) return rc;
+    return enqueue_matmuls(d, n, ms, d_outs, d_x, cols, tokens, s);
 }
 
 int rk_graph_begin(rk_device *d) {

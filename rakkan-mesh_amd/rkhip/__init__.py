@@ -48,6 +48,8 @@ SIGNATURES = {
     "rk_matrix_bytes": (I64, [P]),
     "rk_matvecs": (ctypes.c_int, [P, I32, P, P, P, I64]),
     "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
+    "rk_matmul_t": (ctypes.c_int, [P, I32, P, P, P, I64, I32]),
+    "rk_matmul_t_device": (ctypes.c_int, [P, I32, P, P, P, I64, I32, P]),
     "rk_arena_new": (ctypes.c_int, [P, I64, I64, P]),
     "rk_arena_set_quant_scratch": (ctypes.c_int, [P, I64, I64]),
     "rk_arena_bytes": (I64, [P]),
@@ -308,6 +310,24 @@ class Device:
 
     def matvec(self, m, x):
         return self.matvecs([m], x)[0]
+
+    def matmul_t(self, ms, x):
+        """Batched products: x is [tokens][cols]; returns [tokens][rows_i] per
+        matrix, each row what matvecs gives for that token alone."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        tokens, cols = x.shape
+        outs = [np.empty((tokens, m.rows), np.float32) for m in ms]
+        hs = (P * len(ms))(*[m.h for m in ms])
+        ops = (P * len(ms))(*[_ptr(o) for o in outs])
+        self._check(lib().rk_matmul_t(self.h, len(ms), hs, ops, _ptr(x), cols, tokens))
+        return outs
+
+    def matmul_t_device(self, ms, d_outs, d_x, cols, tokens, stream=None):
+        """Enqueue batched products on device pointers (ints)."""
+        hs = (P * len(ms))(*[m.h for m in ms])
+        ops = (P * len(ms))(*d_outs)
+        self._check(lib().rk_matmul_t_device(self.h, len(ms), hs, ops, P(d_x), cols, tokens,
+                                             P(stream) if stream else None))
 
     def matvecs_device(self, ms, d_outs, d_x, cols, stream=None):
         """Enqueue products on device pointers (ints) on a HIP stream handle."""
