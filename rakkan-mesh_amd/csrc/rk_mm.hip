@@ -12,7 +12,7 @@
 // the f32 steps above then run on the vector ALUs in that order, so those
 // four operations per (row, token, block) bound the kernel, not the MFMA.
 //
-// Work layout: a workgroup (four waves, 2×2) owns 64 rows × 64 tokens and
+// Work layout: a workgroup (eight waves) owns 64 rows × 64 tokens and
 // walks the blocks in chunks of eight (one per running sum). A chunk's codes
 // and scales are staged in LDS (Q4_0 unpacked to signed codes once there),
 // double-buffered: the next chunk's global loads are in flight while the
@@ -30,7 +30,7 @@ namespace {
 constexpr int kMmRows = 64;      // output rows per workgroup (kEpSilu: 32 rows of W1 and of W3)
 constexpr int kMmToks = 64;      // tokens per workgroup
 constexpr int kMmKB = 8;         // blocks per staged chunk, one per running sum
-constexpr int kMmThreads = 256;  // four waves: (row half, token half)
+constexpr int kMmThreads = 512;  // eight waves
 // Bytes per staged row: 16 rows read at one offset fall in distinct banks.
 constexpr int kMmPitch = kMmKB * 32 + 8;
 constexpr int kHbPitch = 36;  // kEpSilu: floats per token row of h
@@ -79,8 +79,10 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
     extern __shared__ __align__(16) char lds[];
     MmStage *stg = reinterpret_cast<MmStage *>(lds);  // two buffers
     constexpr bool SILU = EPI == kEpSilu;
+    // A wave's tiles of 16 rows x 16 tokens: one row tile and two token
+    // tiles, or (kEpSilu) the same rows of W1 and of W3 and one token tile.
+    constexpr int TI = SILU ? 2 : 1, TJ = SILU ? 1 : 2;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wr = wave & 1, wt = wave >> 1;
     const int lq = lane >> 4, ln = lane & 15;
     const int cols = a.cols, nb = cols >> 5, T = a.tokens;
     const int rowbytes = FMT == kFmtQ8 ? cols : cols >> 1;
@@ -113,59 +115,49 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
     };
 
     // ---- staging: each thread's rows and tokens, fixed for the kernel ----
-    // Q8 codes: 16-byte piece p = tid + 256j of the chunk's 64 rows x 256
-    // bytes (row p>>4, piece p&15); Q4: p = tid + 256j of 64 rows x 8 blocks
-    // (row p>>3, block p&7). Scales: p = tid + 256j of 64 rows x 8 blocks.
-    constexpr int NW = FMT == kFmtQ8 ? 4 : 2;
+    // Q8 codes: 16-byte piece p = tid + 512j of the chunk's 64 rows x 256
+    // bytes (row p>>4, piece p&15); Q4: piece tid of 64 rows x 8 blocks (row
+    // tid>>3, block tid&7); inputs like Q8 codes. Scales: row (or token)
+    // tid>>3, block tid&7.
+    constexpr int NW = FMT == kFmtQ8 ? 2 : 1;
     const uint8_t *wrow[NW];
-    const float *dummy_ws;
+    const float *wsrow;
+    const uint8_t *unused_w;
+    const float *unused_ws;
 #pragma unroll
-    for (int j = 0; j < NW; j++) row_src(FMT == kFmtQ8 ? (tid >> 4) + 16 * j : (tid >> 3) + 32 * j, wrow[j], dummy_ws);
-    const float *wsrow[2];
-    const uint8_t *dummy_w;
+    for (int j = 0; j < NW; j++) row_src(FMT == kFmtQ8 ? (tid >> 4) + 32 * j : tid >> 3, wrow[j], unused_ws);
+    row_src(tid >> 3, unused_w, wsrow);
+    const int8_t *xrow[2];
 #pragma unroll
-    for (int j = 0; j < 2; j++) row_src((tid >> 3) + 32 * j, dummy_w, wsrow[j]);
-    const int8_t *xrow[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) xrow[j] = a.qx + (int64_t)min(tok0 + (tid >> 4) + 16 * j, T - 1) * cols;
-    const float *xsrow[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) xsrow[j] = a.xs + (int64_t)min(tok0 + (tid >> 3) + 32 * j, T - 1) * nb;
+    for (int j = 0; j < 2; j++) xrow[j] = a.qx + (int64_t)min(tok0 + (tid >> 4) + 32 * j, T - 1) * cols;
+    const float *xsrow = a.xs + (int64_t)min(tok0 + (tid >> 3), T - 1) * nb;
 
     const int nchunks = (nb + kMmKB - 1) / kMmKB;
-    v4i rw[NW], rx[4];
-    float rws[2], rxs[2];
-    // loads of the chunk starting at block c (blocks past nb read the last
-    // block: never used)
+    v4i rw[NW], rx[2];
+    float rws, rxs;
+    // loads of the chunk starting at block c (past the last chunk: the last
+    // chunk again; blocks past nb read the last block: never used)
     auto stage_load = [&](int c) __attribute__((always_inline)) {
         c = min(c, (nchunks - 1) * kMmKB);
-#pragma unroll
-        for (int j = 0; j < NW; j++) {
-            if (FMT == kFmtQ8) {
-                const int o = min(c * 32 + (tid & 15) * 16, cols - 16);
-                rw[j] = *reinterpret_cast<const v4i *>(wrow[j] + o);
-            } else {
-                const int bk = min(c + (tid & 7), nb - 1);
-                rw[j] = *reinterpret_cast<const v4i *>(wrow[j] + bk * 16);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int o = min(c * 32 + (tid & 15) * 16, cols - 16);
-            rx[j] = *reinterpret_cast<const v4i *>(xrow[j] + o);
-        }
+        const int o = min(c * 32 + (tid & 15) * 16, cols - 16);
         const int bk = min(c + (tid & 7), nb - 1);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            rws[j] = wsrow[j][bk];
-            rxs[j] = xsrow[j][bk];
+        for (int j = 0; j < NW; j++) {
+            if (FMT == kFmtQ8)
+                rw[j] = *reinterpret_cast<const v4i *>(wrow[j] + o);
+            else
+                rw[j] = *reinterpret_cast<const v4i *>(wrow[j] + bk * 16);
         }
+#pragma unroll
+        for (int j = 0; j < 2; j++) rx[j] = *reinterpret_cast<const v4i *>(xrow[j] + o);
+        rws = wsrow[bk];
+        rxs = xsrow[bk];
     };
     auto stage_store = [&](MmStage &S) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NW; j++) {
             if (FMT == kFmtQ8) {
-                lds_put16(&S.w[(tid >> 4) + 16 * j][(tid & 15) * 16], rw[j]);
+                lds_put16(&S.w[(tid >> 4) + 32 * j][(tid & 15) * 16], rw[j]);
             } else {
                 // byte i of the block: low nibble w_i, high nibble w_(i+16)
                 const v4i v = rw[j];
@@ -175,35 +167,62 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
                                    (int)nib_signed(((uint32_t)v.y >> 4) & 0x0F0F0F0Fu),
                                    (int)nib_signed(((uint32_t)v.z >> 4) & 0x0F0F0F0Fu),
                                    (int)nib_signed(((uint32_t)v.w >> 4) & 0x0F0F0F0Fu)};
-                int8_t *dst = &S.w[(tid >> 3) + 32 * j][(tid & 7) * 32];
+                int8_t *dst = &S.w[tid >> 3][(tid & 7) * 32];
                 lds_put16(dst, lo);
                 lds_put16(dst + 16, hi);
             }
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) lds_put16(&S.x[(tid >> 4) + 16 * j][(tid & 15) * 16], rx[j]);
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            S.ws[tid & 7][(tid >> 3) + 32 * j] = rws[j];
-            S.xs[tid & 7][(tid >> 3) + 32 * j] = rxs[j];
-        }
+        for (int j = 0; j < 2; j++) lds_put16(&S.x[(tid >> 4) + 32 * j][(tid & 15) * 16], rx[j]);
+        S.ws[tid & 7][tid >> 3] = rws;
+        S.xs[tid & 7][tid >> 3] = rxs;
     };
 
-    // ---- products: the wave's 2x2 tiles of 16 rows x 16 tokens ----
-    // Row tile ti of the wave: staged rows rb(ti).. +16 (kEpSilu: W1 rows
-    // for ti = 0 and the same W3 rows for ti = 1). A lane holds, per tile,
-    // token tb(tj) + ln and rows rb(ti) + 4·lq + i, i < 4.
-    auto rb = [&](int ti) { return SILU ? 32 * ti + 16 * wr : 32 * wr + 16 * ti; };
-    auto tb = [&](int tj) { return 32 * wt + 16 * tj; };
-    float acc[2][2][kMmKB][4];
+    // ---- products ----
+    // A lane holds, per tile, token tb(tj) + ln and rows rb(ti) + 4·lq + i,
+    // i < 4 (the MFMA's 16x16 result layout).
+    const int wr = SILU ? (wave & 1) : (wave & 3);
+    const int wt = SILU ? (wave >> 1) : (wave >> 2);
+    auto rb = [&](int ti) { return SILU ? 32 * ti + 16 * wr : 16 * wr; };
+    auto tb = [&](int tj) { return SILU ? 16 * wt : 32 * wt + 16 * tj; };
+    float acc[TI][TJ][kMmKB][4];
 #pragma unroll
-    for (int ti = 0; ti < 2; ti++)
+    for (int ti = 0; ti < TI; ti++)
 #pragma unroll
-        for (int tj = 0; tj < 2; tj++)
+        for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
             for (int k = 0; k < kMmKB; k++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[ti][tj][k][i] = 0.0f;
+
+    // block k of the staged chunk into running sum k
+    auto kstep = [&](const MmStage &S, int k) __attribute__((always_inline)) {
+        long fa[TI], fb[TJ];
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++) fa[ti] = *reinterpret_cast<const long *>(&S.w[rb(ti) + ln][k * 32 + 8 * lq]);
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) fb[tj] = *reinterpret_cast<const long *>(&S.x[tb(tj) + ln][k * 32 + 8 * lq]);
+        v4i d[TI][TJ];
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++)
+#pragma unroll
+            for (int tj = 0; tj < TJ; tj++)
+                d[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], v4i{0, 0, 0, 0}, 0, 0, 0);
+        float4 wsv[TI];
+        float xsv[TJ];
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++) wsv[ti] = *reinterpret_cast<const float4 *>(&S.ws[k][rb(ti) + 4 * lq]);
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) xsv[tj] = S.xs[k][tb(tj) + ln];
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++) {
+            const float w4[4] = {wsv[ti].x, wsv[ti].y, wsv[ti].z, wsv[ti].w};
+#pragma unroll
+            for (int tj = 0; tj < TJ; tj++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[ti][tj][k][i] += (float)d[ti][tj][i] * (w4[i] * xsv[tj]);
+        }
+    };
 
     stage_load(0);
     stage_store(stg[0]);
@@ -214,38 +233,13 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
         // fill the idle buffer, which nothing reads)
         stage_load(c0 + kMmKB);
         const MmStage &S = stg[ci & 1];
+        if (c0 + kMmKB <= nb) {
 #pragma unroll
-        for (int k = 0; k < kMmKB; k++) {
-            if (c0 + k < nb) {  // absent blocks are skipped, not added as zeros
-                long fa[2], fb[2];
+            for (int k = 0; k < kMmKB; k++) kstep(S, k);
+        } else {
 #pragma unroll
-                for (int ti = 0; ti < 2; ti++)
-                    fa[ti] = *reinterpret_cast<const long *>(&S.w[rb(ti) + ln][k * 32 + 8 * lq]);
-#pragma unroll
-                for (int tj = 0; tj < 2; tj++)
-                    fb[tj] = *reinterpret_cast<const long *>(&S.x[tb(tj) + ln][k * 32 + 8 * lq]);
-                v4i d[2][2];
-#pragma unroll
-                for (int ti = 0; ti < 2; ti++)
-#pragma unroll
-                    for (int tj = 0; tj < 2; tj++)
-                        d[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], v4i{0, 0, 0, 0}, 0, 0, 0);
-                float4 wsv[2];
-                float xsv[2];
-#pragma unroll
-                for (int ti = 0; ti < 2; ti++) wsv[ti] = *reinterpret_cast<const float4 *>(&S.ws[k][rb(ti) + 4 * lq]);
-#pragma unroll
-                for (int tj = 0; tj < 2; tj++) xsv[tj] = S.xs[k][tb(tj) + ln];
-#pragma unroll
-                for (int ti = 0; ti < 2; ti++) {
-                    const float w4[4] = {wsv[ti].x, wsv[ti].y, wsv[ti].z, wsv[ti].w};
-#pragma unroll
-                    for (int tj = 0; tj < 2; tj++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            acc[ti][tj][k][i] += (float)d[ti][tj][i] * (w4[i] * xsv[tj]);
-                }
-            }
+            for (int k = 0; k < kMmKB; k++)
+                if (c0 + k < nb) kstep(S, k);  // absent blocks are skipped, not added as zeros
         }
         stage_store(stg[(ci + 1) & 1]);
         __syncthreads();
@@ -253,11 +247,11 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
 
     // ---- results: the fixed tree of the eight running sums, then the
     // epilogue per (row, token) ----
-    float res[2][2][4];
+    float res[TI][TJ][4];
 #pragma unroll
-    for (int ti = 0; ti < 2; ti++)
+    for (int ti = 0; ti < TI; ti++)
 #pragma unroll
-        for (int tj = 0; tj < 2; tj++)
+        for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float p0 = acc[ti][tj][0][i] + acc[ti][tj][1][i], p1 = acc[ti][tj][2][i] + acc[ti][tj][3][i];
@@ -269,43 +263,37 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
         // h = silu(W1·x)·(W3·x) into LDS [token][32 rows], then each token's
         // 32 values (one Q8_0 block of h) quantized by eight lanes
         float *hb = reinterpret_cast<float *>(lds);
-#pragma unroll
-        for (int tj = 0; tj < 2; tj++) {
-            float4 h4;
-            h4.x = silu_mul(res[0][tj][0], res[1][tj][0]);
-            h4.y = silu_mul(res[0][tj][1], res[1][tj][1]);
-            h4.z = silu_mul(res[0][tj][2], res[1][tj][2]);
-            h4.w = silu_mul(res[0][tj][3], res[1][tj][3]);
-            *reinterpret_cast<float4 *>(&hb[(tb(tj) + ln) * kHbPitch + 16 * wr + 4 * lq]) = h4;
-        }
+        float4 h4;
+        h4.x = silu_mul(res[0][0][0], res[1][0][0]);
+        h4.y = silu_mul(res[0][0][1], res[1][0][1]);
+        h4.z = silu_mul(res[0][0][2], res[1][0][2]);
+        h4.w = silu_mul(res[0][0][3], res[1][0][3]);
+        *reinterpret_cast<float4 *>(&hb[(tb(0) + ln) * kHbPitch + 16 * wr + 4 * lq]) = h4;
         __syncthreads();
         const int nbh = a.rows >> 5;
-#pragma unroll
-        for (int rnd = 0; rnd < kMmToks * 8 / kMmThreads; rnd++) {
-            const int task = tid + kMmThreads * rnd;
-            const int n = task >> 3, g = task & 7;
-            const float4 v = *reinterpret_cast<const float4 *>(&hb[n * kHbPitch + 4 * g]);
-            float dsc;
-            int cs;
-            const uint32_t pk = quantize_group(v.x, v.y, v.z, v.w, dsc, cs);
-            const int t = tok0 + n;
-            if (t < T) {
-                reinterpret_cast<uint32_t *>(a.qx_out + (int64_t)t * a.rows + row0)[g] = pk;
-                if (g == 0) {
-                    a.xs_out[(int64_t)t * nbh + (row0 >> 5)] = dsc;
-                    a.xsum_out[(int64_t)t * nbh + (row0 >> 5)] = cs;
-                }
+        static_assert(kMmToks * 8 == kMmThreads, "one quantizer task per thread");
+        const int n = tid >> 3, g = tid & 7;
+        const float4 v = *reinterpret_cast<const float4 *>(&hb[n * kHbPitch + 4 * g]);
+        float dsc;
+        int cs;
+        const uint32_t pk = quantize_group(v.x, v.y, v.z, v.w, dsc, cs);
+        const int t = tok0 + n;
+        if (t < T) {
+            reinterpret_cast<uint32_t *>(a.qx_out + (int64_t)t * a.rows + row0)[g] = pk;
+            if (g == 0) {
+                a.xs_out[(int64_t)t * nbh + (row0 >> 5)] = dsc;
+                a.xsum_out[(int64_t)t * nbh + (row0 >> 5)] = cs;
             }
         }
         return;
     }
 
 #pragma unroll
-    for (int tj = 0; tj < 2; tj++) {
+    for (int tj = 0; tj < TJ; tj++) {
         const int t = tok0 + tb(tj) + ln;
         if (t >= T) continue;
 #pragma unroll
-        for (int ti = 0; ti < 2; ti++) {
+        for (int ti = 0; ti < TI; ti++) {
             const int gb = row0 + rb(ti) + 4 * lq;  // the lane's first row
             if (EPI == kEpQKV) {
                 const int pos = a.pos0 + t, half = a.hs >> 1;
