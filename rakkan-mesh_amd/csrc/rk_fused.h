@@ -87,20 +87,31 @@ bool fused_fits(int pro, int cols);
 // prologue, or too many workgroups for the argmax partials).
 bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s);
 
+// A batch of consecutive positions for the attention kernels: token z sits
+// at pos0 + z and attends to positions 0..pos0+z; its rows are z·stride
+// floats into the q, scores and output buffers. Used when ctl is null.
+struct AttBatch {
+    int32_t pos0 = 0, tokens = 1;
+    int64_t q_stride = 0, att_stride = 0, out_stride = 0;
+};
+
 // Attention of one position over a stage's cache (internal/llm/model.go:
-// 575-591), position and length read from ctl: scores, then softmax and the
-// weighted values (f32 out).
+// 575-591), position and length read from ctl (or, ctl null, a batch):
+// scores, then softmax and the weighted values (f32 out).
 void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
-                       int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt, hipStream_t s);
+                       const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt,
+                       hipStream_t s);
 // With qx non-null (head size a multiple of 32), the output is also
 // quantized (Q8_0 blocks of the next product's input).
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
-                       int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
-                       hipStream_t s);
-// QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches.
+                       const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx,
+                       float *xs, int32_t *xsum, hipStream_t s);
+// QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches, at
+// the position in ctl (or, ctl null, for `tokens` rows at pos0, pos0+1, ...).
 void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                         float recip_hs, float eps, const float *cos_t, const float *sin_t, const int32_t *ctl,
-                        float *kcache, float *vcache, int heads, int kv_heads, int hs, hipStream_t s);
+                        int32_t pos0, int tokens, float *kcache, float *vcache, int heads, int kv_heads, int hs,
+                        hipStream_t s);
 // x = the embedding row of tokens[ctl[kCtlPos]] (Q8_0 or Q4_0 table), and
 // RMSNorm(x) with norm_w quantized into qx/xs/xsum (one workgroup;
 // dim <= kMaxNormCols).
@@ -113,7 +124,8 @@ void launch_embed_norm(const uint8_t *w, const float *scales, bool q4, const int
 // classifier's argmax keys into the next token at position+1 (when the
 // position's logits were computed), clears them, and advances the position.
 void launch_advance(int32_t *ctl, unsigned long long *amax, int32_t *tokens, int32_t tokens_len, hipStream_t s);
+// `tokens` rows of [tokens][n] at once (one workgroup each).
 void launch_norm_quant(const float *x, int n, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
-                       int32_t *xsum, hipStream_t s);
+                       int32_t *xsum, hipStream_t s, int tokens = 1);
 
 }  // namespace rk

@@ -613,10 +613,13 @@ __device__ __forceinline__ float wave_gomax(float m) {
 
 template <int HS>  // head size when fixed at compile time (all loads issued at once), else 0
 __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const float *keys, float *att,
-                                                         int32_t att_stride, const int32_t *ctl, int kv_mul, int hs_rt,
-                                                         int kv_dim, float inv_sqrt) {
+                                                         int32_t att_stride, const int32_t *ctl, AttBatch bt,
+                                                         int kv_mul, int hs_rt, int kv_dim, float inv_sqrt) {
     const int hs = HS ? HS : hs_rt;
-    const int T = ctl[kCtlPos] + 1;
+    const int z = blockIdx.z;  // token of a batch (0 when the position comes from ctl)
+    const int T = (ctl ? ctl[kCtlPos] : bt.pos0 + z) + 1;
+    q += (int64_t)z * bt.q_stride;
+    att += (int64_t)z * bt.att_stride;
     const int t0 = blockIdx.y * kScoreTile;
     if (t0 >= T) return;
     const int h = blockIdx.x, g = h / kv_mul;
@@ -660,13 +663,16 @@ __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const f
 }
 
 void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
-                       int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt, hipStream_t s) {
-    const dim3 grid(heads, (ctx + kScoreTile - 1) / kScoreTile);
+                       const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt,
+                       hipStream_t s) {
+    // decode: positions up to ctx; a batch: up to its last token's
+    const int npos = ctl ? ctx : bt.pos0 + bt.tokens;
+    const dim3 grid(heads, (npos + kScoreTile - 1) / kScoreTile, ctl ? 1 : bt.tokens);
     if (hs == 128)
-        RK_LAUNCH(att_scores_kernel<128>, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, heads / kv_heads, hs,
-                  kv_dim, inv_sqrt);
+        RK_LAUNCH(att_scores_kernel<128>, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, bt, heads / kv_heads,
+                  hs, kv_dim, inv_sqrt);
     else
-        RK_LAUNCH(att_scores_kernel<0>, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, heads / kv_heads, hs,
+        RK_LAUNCH(att_scores_kernel<0>, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, bt, heads / kv_heads, hs,
                   kv_dim, inv_sqrt);
 }
 
@@ -697,14 +703,22 @@ constexpr int kValRounds = kValChunk / (4 * kValQuads);              // rounds p
 template <bool VEC>
 __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *att, int32_t att_stride,
                                                                  const float *vals, float *out, const int32_t *ctl,
-                                                                 int kv_mul, int hs, int kv_dim, int ctx_pad,
-                                                                 int8_t *qx, float *xs, int32_t *xsum) {
+                                                                 AttBatch bt, int kv_mul, int hs, int kv_dim,
+                                                                 int ctx_pad, int8_t *qx, float *xs, int32_t *xsum) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float s_red[kValThreads / 64];
     __shared__ float s_inv;
     float *sa = smem;            // [ctx_pad] scores -> weights
     float *sp = smem + ctx_pad;  // [2][kValSlice][kValPitch] product tiles of two chunks
-    const int T = ctl[kCtlPos] + 1;
+    const int z = blockIdx.z;  // token of a batch (0 when the position comes from ctl)
+    const int T = (ctl ? ctl[kCtlPos] : bt.pos0 + z) + 1;
+    att += (int64_t)z * bt.att_stride;
+    out += (int64_t)z * bt.out_stride;
+    if (qx) {
+        qx += (int64_t)z * bt.out_stride;
+        xs += (int64_t)z * (bt.out_stride >> 5);
+        xsum += (int64_t)z * (bt.out_stride >> 5);
+    }
     const int h = blockIdx.x, g = h / kv_mul;
     const int e0 = blockIdx.y * kValSlice;
     const int ne = min(kValSlice, hs - e0);
@@ -833,8 +847,8 @@ constexpr size_t kValMaxDynLds = kMaxLdsBytes - 1024;
 int att_values_max_ctx() { return (int)(kValMaxDynLds / 4 - 2 * kValSlice * kValPitch) & ~3; }
 
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
-                       int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
-                       hipStream_t s) {
+                       const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx,
+                       float *xs, int32_t *xsum, hipStream_t s) {
     static std::once_flag once;
     std::call_once(once, [] {
         (void)hipFuncSetAttribute((const void *)att_values_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -842,15 +856,15 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
         (void)hipFuncSetAttribute((const void *)att_values_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)kValMaxDynLds);
     });
-    const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice);
+    const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice, ctl ? 1 : bt.tokens);
     if (hs % 32 != 0) qx = nullptr;
     const int ctx_pad = (ctx + 3) & ~3;
     if (hs % 4 == 0 && kv_dim % 4 == 0)
         RK_LAUNCH(att_values_kernel<true>, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals, out,
-                  ctl, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
+                  ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
     else
         RK_LAUNCH(att_values_kernel<false>, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals,
-                  out, ctl, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
+                  out, ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
 }
 
 // QK-norm (internal/llm/model.go:551-558) and RoPE (:563-572) of one head
@@ -859,10 +873,16 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
 __global__ __launch_bounds__(64) void qknorm_rope_kernel(float *q, const float *k, const float *v,
                                                          const float *q_norm, const float *k_norm, float recip_hs,
                                                          float eps, const float *cos_t, const float *sin_t,
-                                                         const int32_t *ctl, float *kcache, float *vcache, int heads,
-                                                         int hs, int kv_dim) {
+                                                         const int32_t *ctl, int32_t pos0, float *kcache,
+                                                         float *vcache, int heads, int hs, int kv_dim) {
     extern __shared__ float sy[];  // [hs]
-    const int pos = ctl[kCtlPos];
+    // a batch: token blockIdx.y at pos0 + blockIdx.y, rows [tokens][heads·hs]
+    // and [tokens][kv_dim]
+    const int z = blockIdx.y;
+    const int pos = ctl ? ctl[kCtlPos] : pos0 + z;
+    q += (int64_t)z * heads * hs;
+    k += (int64_t)z * kv_dim;
+    v += (int64_t)z * kv_dim;
     const int lane = threadIdx.x;
     const bool isq = (int)blockIdx.x < heads;
     const int head = isq ? blockIdx.x : blockIdx.x - heads;
@@ -889,9 +909,10 @@ __global__ __launch_bounds__(64) void qknorm_rope_kernel(float *q, const float *
 
 void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                         float recip_hs, float eps, const float *cos_t, const float *sin_t, const int32_t *ctl,
-                        float *kcache, float *vcache, int heads, int kv_heads, int hs, hipStream_t s) {
-    RK_LAUNCH(qknorm_rope_kernel, dim3(heads + kv_heads), dim3(64), (size_t)hs * 4, s, q, k, v, q_norm, k_norm,
-              recip_hs, eps, cos_t, sin_t, ctl, kcache, vcache, heads, hs, kv_heads * hs);
+                        int32_t pos0, int tokens, float *kcache, float *vcache, int heads, int kv_heads, int hs,
+                        hipStream_t s) {
+    RK_LAUNCH(qknorm_rope_kernel, dim3(heads + kv_heads, ctl ? 1 : tokens), dim3(64), (size_t)hs * 4, s, q, k, v,
+              q_norm, k_norm, recip_hs, eps, cos_t, sin_t, ctl, pos0, kcache, vcache, heads, hs, kv_heads * hs);
 }
 
 // Embedding row of the token at the position (internal/llm/model.go:216-231
@@ -952,6 +973,11 @@ __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(const float *x
                                                                   int32_t *xsum) {
     extern __shared__ __align__(16) float sxn[];
     __shared__ float bcast;
+    // a batch: vector blockIdx.x of [tokens][n]
+    x += (int64_t)blockIdx.x * n;
+    qx += (int64_t)blockIdx.x * n;
+    xs += (int64_t)blockIdx.x * (n >> 5);
+    xsum += (int64_t)blockIdx.x * (n >> 5);
     const int ng = n >> 2;
     float4 xv[kNormGroups], wv[kNormGroups];
 #pragma unroll
@@ -964,8 +990,8 @@ __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(const float *x
 }
 
 void launch_norm_quant(const float *x, int n, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
-                       int32_t *xsum, hipStream_t s) {
-    RK_LAUNCH(norm_quant_kernel, dim3(1), dim3(kNormThreads), norm_lds(n), s, x, n, norm_w, recip_n, eps, qx, xs,
+                       int32_t *xsum, hipStream_t s, int tokens) {
+    RK_LAUNCH(norm_quant_kernel, dim3(tokens), dim3(kNormThreads), norm_lds(n), s, x, n, norm_w, recip_n, eps, qx, xs,
               xsum);
 }
 

@@ -25,6 +25,7 @@ struct MmArgs {
     const float *bias;           // per output row (kEpStore, kEpQKV), or null
     float *x;                    // kEpAdd / kEpAddCanon: residual [tokens][ldx]
     int32_t ldx;
+    int32_t row_base;            // kEpQKV: logical q/k/v row (and bias index) of row 0
     int32_t pos0;                // kEpQKV: position of token 0
     int32_t hs, qdim, kvdim;     // kEpQKV: head size, q rows, k rows (= v rows)
     const float *cos_t, *sin_t;  // kEpQKV: rotary table [ctx][hs/2]

@@ -300,13 +300,14 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
 #pragma unroll
                 for (int pr = 0; pr < 2; pr++) {
                     const int g0 = gb + 2 * pr;  // an even row: a rotary pair with g0 + 1
+                    const int l0 = a.row_base + g0;  // its logical q/k/v row
                     float v0 = res[ti][tj][2 * pr], v1 = res[ti][tj][2 * pr + 1];
                     if (a.bias) {
-                        v0 = v0 + a.bias[min(g0, a.rows - 1)];
-                        v1 = v1 + a.bias[min(g0 + 1, a.rows - 1)];
+                        v0 = v0 + a.bias[a.row_base + min(g0, a.rows - 1)];
+                        v1 = v1 + a.bias[a.row_base + min(g0 + 1, a.rows - 1)];
                     }
-                    if (g0 < a.qdim + a.kvdim) {
-                        const int ih = g0 < a.qdim ? g0 : g0 - a.qdim;
+                    if (l0 < a.qdim + a.kvdim) {
+                        const int ih = l0 < a.qdim ? l0 : l0 - a.qdim;
                         const int pi = (ih % a.hs) >> 1;
                         const float co = a.cos_t[(int64_t)pos * half + pi], si = a.sin_t[(int64_t)pos * half + pi];
                         const float r0 = (v0 * co) - (v1 * si);
@@ -316,12 +317,12 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
                     }
 #pragma unroll
                     for (int h = 0; h < 2; h++) {
-                        const int g = g0 + h;
-                        if (g >= a.rows) continue;
-                        float *dst = g < a.qdim ? a.q + (int64_t)t * a.qdim + g
-                                     : g < a.qdim + a.kvdim
-                                         ? a.kcache + (int64_t)pos * a.kvdim + (g - a.qdim)
-                                         : a.vcache + (int64_t)pos * a.kvdim + (g - a.qdim - a.kvdim);
+                        if (g0 + h >= a.rows) continue;
+                        const int l = l0 + h;
+                        float *dst = l < a.qdim ? a.q + (int64_t)t * a.qdim + l
+                                     : l < a.qdim + a.kvdim
+                                         ? a.kcache + (int64_t)pos * a.kvdim + (l - a.qdim)
+                                         : a.vcache + (int64_t)pos * a.kvdim + (l - a.qdim - a.kvdim);
                         *dst = h ? v1 : v0;
                     }
                 }
@@ -374,7 +375,7 @@ bool launch_mm(int fmt, int epi, const MmArgs &a, hipStream_t s) {
     if (a.tokens <= 0 || a.rows <= 0) return true;
     if (a.cols < 32 || a.cols % 32 != 0) return false;
     if (epi == kEpSilu && (a.rows % 32 != 0 || a.nseg != 2)) return false;
-    if (epi == kEpQKV && (a.hs % 2 != 0 || a.qdim % 2 != 0 || a.kvdim % 2 != 0)) return false;
+    if (epi == kEpQKV && (a.hs % 2 != 0 || a.qdim % 2 != 0 || a.kvdim % 2 != 0 || a.row_base % 2 != 0)) return false;
     const int ntr = epi == kEpSilu ? a.rows / 32 : (a.rows + kMmRows - 1) / kMmRows;
     const int ntt = (a.tokens + kMmToks - 1) / kMmToks;
     const int64_t total = (int64_t)ntr * ntt;

@@ -23,6 +23,7 @@
 
 #include "rk_fused.h"
 #include "rk_layer.h"
+#include "rk_mm.h"
 #include "rk_runtime.h"
 
 // internal/llm/gpustage.go:23-32 gpuStage.
@@ -57,6 +58,14 @@ struct rk_stage {
     // recorded tokens: layers only (forward), or the whole generation step
     hipGraph_t g_layers = nullptr, g_token = nullptr;
     hipGraphExec_t x_layers = nullptr, x_token = nullptr;
+    // Batches of consecutive positions (a forward of several tokens): rows
+    // [bcap][...] of the residual, q/k/v, scores, attention output and the
+    // two quantized inputs; one allocation, made on first use.
+    int bcap = 0;
+    char *bmem = nullptr;
+    int64_t bbytes = 0;
+    float *bx = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *batt = nullptr, *batt_out = nullptr;
+    rk::QScratch bqa{}, bqb{};
 };
 
 namespace rk {
@@ -163,20 +172,20 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, const float *next_
         }
         ProfScope p(d, st, "qknorm_rope");
         launch_qknorm_rope(s->q, s->k, s->v, D.q_norm, D.k_norm, c.recip_head, c.norm_eps, s->cos_t, s->sin_t,
-                           s->ctl, D.keys, D.vals, c.heads, c.kv_heads, s->hs, st);
+                           s->ctl, 0, 1, D.keys, D.vals, c.heads, c.kv_heads, s->hs, st);
     }
     {
         ProfScope p(d, st, "att_scores");
-        launch_att_scores(s->q, D.keys, s->att, c.ctx, s->ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim,
-                          c.inv_sqrt, st);
+        launch_att_scores(s->q, D.keys, s->att, c.ctx, s->ctl, AttBatch{}, c.ctx, c.heads, c.kv_heads, s->hs,
+                          s->kvdim, c.inv_sqrt, st);
     }
     // The attention output comes quantized when its Q8 blocks fall within
     // heads (head size a multiple of 32).
     const bool att_q = s->hs % 32 == 0;
     {
         ProfScope p(d, st, "att_values");
-        launch_att_values(s->att, c.ctx, D.vals, s->att_out, s->ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim,
-                          att_q ? s->qa.qx : nullptr, s->qa.xs, s->qa.xsum, st);
+        launch_att_values(s->att, c.ctx, D.vals, s->att_out, s->ctl, AttBatch{}, c.ctx, c.heads, c.kv_heads, s->hs,
+                          s->kvdim, att_q ? s->qa.qx : nullptr, s->qa.xs, s->qa.xsum, st);
     }
     float *xo[1] = {s->x};
     if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, &L.wo, 1, xo, kEpAdd, base)))
@@ -274,6 +283,189 @@ static int run_once(rk_stage *s, bool token) {
     int rc = record(s, token);
     if (rc) return rc;
     HIP_TRY(d, hipGraphLaunch(token ? s->x_token : s->x_layers, d->stream), "stage replay");
+    return RK_OK;
+}
+
+// ---- Batches of consecutive positions (prompt prefill) ----
+// The same per-token operations as enqueue_layer, each launch covering n
+// tokens at positions pos0..pos0+n-1: products on int8 MFMA (rk_mm.hip),
+// norms one workgroup per token, attention one grid slice per token. Every
+// token's results are those of its own decode-path forward, bit for bit.
+
+// Largest batch the buffers take: 256 tokens, fewer when the scores of a
+// batch ([tokens][heads][ctx] floats) would pass 512 MiB.
+static int batch_cap(const rk_stage_config &c) {
+    const int64_t per = (int64_t)4 * c.heads * c.ctx;
+    int64_t cap = ((int64_t)512 << 20) / std::max<int64_t>(per, 1);
+    cap = std::min<int64_t>(cap, 256);
+    return (int)std::max<int64_t>(cap, 1);
+}
+
+static int batch_alloc(rk_stage *s) {
+    if (s->bmem) return RK_OK;
+    rk_device *d = s->d;
+    const rk_stage_config &c = s->c;
+    const int64_t B = batch_cap(c);
+    const int64_t widest = std::max<int64_t>(std::max<int64_t>(c.dim, s->qdim), c.hidden);
+    std::vector<std::pair<void **, int64_t>> plan;
+    auto take = [&](void **p, int64_t n) { plan.push_back({p, n}); };
+    take((void **)&s->bx, 4 * B * c.dim);
+    take((void **)&s->bq, 4 * B * s->qdim);
+    take((void **)&s->bk, 4 * B * s->kvdim);
+    take((void **)&s->bv, 4 * B * s->kvdim);
+    take((void **)&s->batt, 4 * B * c.heads * c.ctx);
+    take((void **)&s->batt_out, 4 * B * s->qdim);
+    for (QScratch *q : {&s->bqa, &s->bqb}) {
+        take((void **)&q->qx, B * widest);
+        take((void **)&q->xs, 4 * B * (widest / 32));
+        take((void **)&q->xsum, 4 * B * (widest / 32));
+    }
+    int64_t at = 0;
+    for (auto &pl : plan) at += (pl.second + 255) & ~(int64_t)255;
+    int rc = dev_alloc(d, (void **)&s->bmem, (size_t)at, "stage batch");
+    if (rc) return rc;
+    s->bbytes = at;
+    at = 0;
+    for (auto &pl : plan) {
+        *pl.first = s->bmem + at;
+        at += (pl.second + 255) & ~(int64_t)255;
+    }
+    s->bcap = (int)B;
+    s->bytes += s->bbytes;
+    add_used(d, s->bbytes);
+    return RK_OK;
+}
+
+// One batched product: matrices ms[0..n) of one format (concatenated rows;
+// kEpSilu: W1 and W3 paired).
+static int batch_product(rk_stage *s, hipStream_t st, const char *name, rk_matrix *const *ms, int n, int epi,
+                         MmArgs a) {
+    rk_device *d = s->d;
+    a.nseg = n;
+    a.cols = (int32_t)ms[0]->cols;
+    a.rows = 0;
+    for (int i = 0; i < n; i++) {
+        a.seg[i].w = ms[i]->w;
+        a.seg[i].ws = ms[i]->scales;
+        a.seg[i].rows = ms[i]->rows;
+        if (epi != kEpSilu || i == 0) a.rows += (int32_t)ms[i]->rows;
+    }
+    bool ok;
+    {
+        ProfScope p(d, st, name);
+        ok = launch_mm(fmt_of(ms[0]), epi, a, st);
+    }
+    if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "stage: batched %s product has no kernel", name);
+    return RK_OK;
+}
+
+// RMSNorm of the batch's rows with w, quantized into bqb.
+static void batch_norm(rk_stage *s, hipStream_t st, const float *w, int n) {
+    if (!w) return;
+    ProfScope p(s->d, st, "norm_quant");
+    launch_norm_quant(s->bx, s->c.dim, w, s->c.recip_dim, s->c.norm_eps, s->bqb.qx, s->bqb.xs, s->bqb.xsum, st, n);
+}
+
+// One layer for n tokens; on entry bqb holds their RMSNorm_att(x) quantized.
+static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, int pos0, const float *next_norm) {
+    rk_device *d = s->d;
+    const rk_stage_config &c = s->c;
+    const rk_stage_layer &L = s->layers[li];
+    const rk_stage::LayerDev &D = s->ld[li];
+    int rc;
+    MmArgs base{};
+    base.tokens = n;
+    base.qx = s->bqb.qx;
+    base.xs = s->bqb.xs;
+    rk_matrix *qkv[3] = {L.wq, L.wk, L.wv};
+    int i = 0, row = 0;
+    while (i < 3) {  // runs of consecutive matrices of one format share a launch
+        int j = i + 1;
+        while (j < 3 && qkv[j]->kind == qkv[i]->kind) j++;
+        MmArgs a = base;
+        if (!c.qk_norm) {
+            a.row_base = row;
+            a.bias = D.bias;
+            a.pos0 = pos0;
+            a.hs = s->hs;
+            a.qdim = s->qdim;
+            a.kvdim = s->kvdim;
+            a.cos_t = s->cos_t;
+            a.sin_t = s->sin_t;
+            a.q = s->bq;
+            a.kcache = D.keys;
+            a.vcache = D.vals;
+            if ((rc = batch_product(s, st, "qkv", qkv + i, j - i, kEpQKV, a))) return rc;
+        } else {
+            float *outs[3] = {s->bq, s->bk, s->bv};
+            for (int t = i; t < j; t++) a.seg[t - i].out = outs[t];
+            a.bias = D.bias ? D.bias + row : nullptr;
+            if ((rc = batch_product(s, st, "qkv", qkv + i, j - i, kEpStore, a))) return rc;
+        }
+        for (int t = i; t < j; t++) row += (int)qkv[t]->rows;
+        i = j;
+    }
+    if (c.qk_norm) {
+        ProfScope p(d, st, "qknorm_rope");
+        launch_qknorm_rope(s->bq, s->bk, s->bv, D.q_norm, D.k_norm, c.recip_head, c.norm_eps, s->cos_t, s->sin_t,
+                           nullptr, pos0, n, D.keys, D.vals, c.heads, c.kv_heads, s->hs, st);
+    }
+    AttBatch bt;
+    bt.pos0 = pos0;
+    bt.tokens = n;
+    bt.q_stride = s->qdim;
+    bt.att_stride = (int64_t)c.heads * c.ctx;
+    bt.out_stride = s->qdim;
+    {
+        ProfScope p(d, st, "att_scores");
+        launch_att_scores(s->bq, D.keys, s->batt, c.ctx, nullptr, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim,
+                          c.inv_sqrt, st);
+    }
+    // the attention output comes quantized when its Q8 blocks fall within
+    // heads; else it is quantized by a launch of its own
+    const bool att_q = s->hs % 32 == 0;
+    {
+        ProfScope p(d, st, "att_values");
+        launch_att_values(s->batt, c.ctx, D.vals, s->batt_out, nullptr, bt, c.ctx, c.heads, c.kv_heads, s->hs,
+                          s->kvdim, att_q ? s->bqa.qx : nullptr, s->bqa.xs, s->bqa.xsum, st);
+    }
+    if (!att_q) {
+        ProfScope p(d, st, "quantize_acts");
+        launch_quantize_acts(s->batt_out, (int64_t)n * s->qdim, s->bqa.qx, s->bqa.xs, s->bqa.xsum, st);
+    }
+    MmArgs a = base;
+    a.qx = s->bqa.qx;
+    a.xs = s->bqa.xs;
+    a.x = s->bx;
+    a.ldx = c.dim;
+    if ((rc = batch_product(s, st, "wo", &L.wo, 1, kEpAdd, a))) return rc;
+    batch_norm(s, st, D.rms_ffn, n);
+    rk_matrix *w13[2] = {L.w1, L.w3};
+    a = base;
+    a.qx_out = s->bqa.qx;
+    a.xs_out = s->bqa.xs;
+    a.xsum_out = s->bqa.xsum;
+    if ((rc = batch_product(s, st, "w13", w13, 2, kEpSilu, a))) return rc;
+    a = base;
+    a.qx = s->bqa.qx;
+    a.xs = s->bqa.xs;
+    a.x = s->bx;
+    a.ldx = c.dim;
+    if ((rc = batch_product(s, st, "w2", &L.w2, 1, kEpAddCanon, a))) return rc;
+    batch_norm(s, st, next_norm, n);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(d, e, "stage launch");
+    return RK_OK;
+}
+
+// Every layer over n tokens whose activations are in bx.
+static int enqueue_forward_batch(rk_stage *s, hipStream_t st, int n, int pos0) {
+    batch_norm(s, st, s->ld[0].rms_att, n);
+    const int nl = (int)s->layers.size();
+    for (int li = 0; li < nl; li++) {
+        int rc = enqueue_layer_batch(s, li, st, n, pos0, li + 1 < nl ? s->ld[li + 1].rms_att : nullptr);
+        if (rc) return rc;
+    }
     return RK_OK;
 }
 
@@ -442,6 +634,21 @@ int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens) {
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
     hipStream_t st = d->stream;
     const int dim = s->c.dim;
+    if (tokens > 1) {
+        // several tokens: the batched path (same bits as one at a time)
+        int rc = batch_alloc(s);
+        if (rc) return rc;
+        for (int start = 0; start < tokens; start += s->bcap) {
+            const int n = std::min(s->bcap, tokens - start);
+            HIP_TRY(d, hipMemcpyAsync(s->bx, xs + (int64_t)start * dim, (size_t)n * dim * 4, hipMemcpyHostToDevice, st),
+                    "stage input");
+            if ((rc = enqueue_forward_batch(s, st, n, pos + start))) return rc;
+            HIP_TRY(d, hipMemcpyAsync(xs + (int64_t)start * dim, s->bx, (size_t)n * dim * 4, hipMemcpyDeviceToHost, st),
+                    "stage output");
+            HIP_TRY(d, hipStreamSynchronize(st), "stage submit");
+        }
+        return RK_OK;
+    }
     for (int start = 0; start < tokens; start += kForwardBatch) {
         const int n = std::min(kForwardBatch, tokens - start);
         memcpy(s->h_x, xs + (int64_t)start * dim, (size_t)n * dim * 4);
@@ -473,6 +680,7 @@ int rk_stage_free(rk_stage *s) {
     if (s->x_token) (void)hipGraphExecDestroy(s->x_token);
     if (s->g_token) (void)hipGraphDestroy(s->g_token);
     (void)hipFree(s->mem);
+    (void)hipFree(s->bmem);
     if (s->h_x) (void)hipHostFree(s->h_x);
     if (s->h_ctl) (void)hipHostFree(s->h_ctl);
     if (s->h_logits) (void)hipHostFree(s->h_logits);

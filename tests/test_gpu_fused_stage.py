@@ -222,3 +222,66 @@ def test_generation_real_shapes_one_layer(dev, name):
                    rope_theta=1000000.0, qk_norm=True, norm_eps=1e-6, dtype="q8_0")
     m = coded_model(c, 5)
     check_generation(dev, m, [11, 7000, 123, 99], 12, 64)
+
+
+def forward_one_by_one(st, xs, pos0):
+    return np.stack([st.forward(xs[t], pos0 + t)[0] for t in range(len(xs))])
+
+
+@pytest.mark.parametrize("ci", range(len(CONFIGS)))
+def test_batched_forward_matches_token_by_token(dev, ci):
+    """A forward of many tokens (the batched prefill path: MFMA products,
+    per-token norms and attention) equals one token at a time (the decode
+    path), at a nonzero start position and over more tokens than one batch
+    holds (256)."""
+    c = Config(**{**CONFIGS[ci].__dict__, "dtype": "q4_m"})
+    m = Model(c, random_model(c, 4))
+    ctx = 600
+    a, mats_a = make_stage(dev, m, ctx)
+    b, mats_b = make_stage(dev, m, ctx)
+    xs = np.stack([m.embed_token((i * 11 + 5) % c.vocab) for i in range(300)])
+    head = forward_one_by_one(a, xs[:20], 0)
+    same_bits(forward_one_by_one(b, xs[:20], 0), head, "first 20 positions")
+    got = a.forward(xs[20:], 20)
+    want = forward_one_by_one(b, xs[20:], 20)
+    for t in range(len(want)):
+        same_bits(got[t], want[t], f"position {20 + t}")
+    # and decode continues from the batch's cache entries
+    x = m.embed_token(3)
+    same_bits(a.forward(x, 300)[0], b.forward(x, 300)[0], "decode after the batch")
+    for st in (a, b):
+        st.free()
+    for mt in mats_a + mats_b:
+        mt.free()
+    assert dev.used == 0
+
+
+@pytest.mark.parametrize("name", ["llama8b", "qwen7b_q4", "qwen3_attn"])
+def test_batched_forward_real_shapes_one_layer(dev, name):
+    """The prefill path at the 8B / Qwen-7B (Q4, QKV bias, hidden 18944) /
+    Qwen3 (QK-norm, q_dim != dim) layer shapes: 130 tokens at once equal the
+    decode path token by token, which the generation tests pin to the
+    oracle."""
+    if name == "llama8b":
+        c = Config(dim=4096, hidden=14336, layers=1, heads=32, kv_heads=8, vocab=16, seq_len=160,
+                   rope_theta=500000.0, dtype="q8_0")
+    elif name == "qwen7b_q4":
+        c = Config(dim=3584, hidden=18944, layers=1, heads=28, kv_heads=4, vocab=16, seq_len=160,
+                   rope_theta=1000000.0, qkv_bias=True, norm_eps=1e-6, dtype="q4_0")
+    else:
+        c = Config(dim=2048, hidden=768, layers=1, heads=32, kv_heads=4, vocab=16, seq_len=160, head_dim=128,
+                   rope_theta=1000000.0, qk_norm=True, norm_eps=1e-6, dtype="q8_0")
+    m = coded_model(c, 6)
+    rng = np.random.default_rng(2)
+    xs = rng.normal(0, 1, (130, c.dim)).astype(np.float32)
+    a, mats_a = make_stage(dev, m, 160)
+    b, mats_b = make_stage(dev, m, 160)
+    got = a.forward(xs, 0)
+    want = forward_one_by_one(b, xs, 0)
+    for t in range(len(want)):
+        same_bits(got[t], want[t], f"{name} position {t}")
+    for st in (a, b):
+        st.free()
+    for mt in mats_a + mats_b:
+        mt.free()
+    assert dev.used == 0
