@@ -118,6 +118,10 @@ void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q
 void launch_embed_norm(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, const int32_t *ctl,
                        int dim, float *x, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
                        int32_t *xsum, hipStream_t s);
+// Embedding rows of tokens[pos0..pos0+n) (Q8_0 or Q4_0 table) into x
+// [n][dim], as embed_norm gives them one position at a time.
+void launch_embed_rows(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, int32_t pos0, int n,
+                       int dim, float *x, hipStream_t s);
 // RMSNorm(x) with norm_w quantized into qx/xs/xsum (one workgroup; n <=
 // kMaxNormCols).
 // The greedy argmax's end (internal/llm/sample.go:45-53): folds the

@@ -968,6 +968,35 @@ void launch_embed_norm(const uint8_t *w, const float *scales, bool q4, const int
               dim, x, norm_w, recip_n, eps, qx, xs, xsum);
 }
 
+// Embedding rows of tokens[pos0..pos0+n) into x [n][dim] (the values
+// embed_norm_kernel gives one position): workgroup per row, four elements a
+// thread.
+__global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t *w, const float *scales, int q4,
+                                                         const int32_t *tokens, int32_t pos0, int dim, float *x) {
+    const int64_t tok = tokens[pos0 + blockIdx.x];
+    const int nb = dim >> 5, ng = dim >> 2;
+    float *xr = x + (int64_t)blockIdx.x * dim;
+    for (int g = threadIdx.x; g < ng; g += 256) {
+        const int i = 4 * g;
+        const uint8_t *cp = q4 ? w + tok * (dim / 2) + (i >> 5) * 16 + (i & 15) : w + tok * dim + i;
+        const uint32_t cw = *reinterpret_cast<const uint32_t *>(cp);
+        const float sc = scales[tok * nb + (i >> 5)];
+        int c[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int b = (int)((cw >> (8 * e)) & 255u);
+            c[e] = !q4 ? (int)(int8_t)b : (((i & 31) < 16 ? (b & 15) : (b >> 4)) - 8);
+        }
+        reinterpret_cast<float4 *>(xr)[g] =
+            make_float4((float)c[0] * sc, (float)c[1] * sc, (float)c[2] * sc, (float)c[3] * sc);
+    }
+}
+
+void launch_embed_rows(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, int32_t pos0, int n,
+                       int dim, float *x, hipStream_t s) {
+    RK_LAUNCH(embed_rows_kernel, dim3(n), dim3(256), 0, s, w, scales, q4 ? 1 : 0, tokens, pos0, dim, x);
+}
+
 __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(const float *x, int n, const float *norm_w,
                                                                   float recip_n, float eps, int8_t *qx, float *xs,
                                                                   int32_t *xsum) {

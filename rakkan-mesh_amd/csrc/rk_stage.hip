@@ -62,6 +62,7 @@ struct rk_stage {
     // [bcap][...] of the residual, q/k/v, scores, attention output and the
     // two quantized inputs; one allocation, made on first use.
     int bcap = 0;
+    int32_t prompt_n = 0;  // the current generation's prompt length
     char *bmem = nullptr;
     int64_t bbytes = 0;
     float *bx = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *batt = nullptr, *batt_out = nullptr;
@@ -743,6 +744,7 @@ int rk_stage_generate_start(rk_stage *s, const int32_t *prompt, int32_t n_prompt
             "prompt upload");
     hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, d->stream, s->ctl, s->amax, 0, n_prompt);
     HIP_TRY(d, hipGetLastError(), "generate start");
+    s->prompt_n = n_prompt;
     HIP_TRY(d, hipStreamSynchronize(d->stream), "generate start");
     return RK_OK;
 }
@@ -763,6 +765,30 @@ int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits) {
         return fail(d, RK_ERR_ARGS, "rk_stage_generate: positions [%d, %d) outside the context of %d", pos,
                     pos + positions, s->c.ctx);
     const int64_t vocab = s->wcls->rows;
+    // Prompt positions before the last compute no logits: with no logits
+    // asked for, two or more of them go through the batched path (their
+    // embeddings, the layers; the same cache entries), then the position
+    // moves on.
+    if (!logits && pos + 2 < s->prompt_n && positions >= 2) {
+        int rc = batch_alloc(s);
+        if (rc) return rc;
+        hipStream_t st = d->stream;
+        int left = std::min(positions, s->prompt_n - 1 - pos);
+        positions -= left;
+        while (left > 0) {
+            const int n = std::min(left, s->bcap);
+            {
+                ProfScope p(d, st, "embed");
+                launch_embed_rows(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->tokens, pos, n, s->c.dim,
+                                  s->bx, st);
+            }
+            if ((rc = enqueue_forward_batch(s, st, n, pos))) return rc;
+            pos += n;
+            left -= n;
+            hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, st, s->ctl, s->amax, pos, s->prompt_n);
+            HIP_TRY(d, hipGetLastError(), "generate prefill");
+        }
+    }
     for (int32_t i = 0; i < positions; i++) {
         int rc = run_once(s, true);
         if (rc) return rc;
