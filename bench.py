@@ -14,6 +14,11 @@ Two measurements, one JSON line:
   (scales) + 4*cols (x) + 4*rows (out). The timed steps are HIP graph
   replays. roofline = the product kernel's bytes per launch over its
   average duration, each launch stamped with HIP events on its own stream.
+* prefill_tok_s / decode_q4_tok_s: config 4, a Qwen-7B-shape decoder with
+  Q4_0 layers: a 512-token prompt through the batched prefill (int8 MFMA
+  block sums, the per-token f32 steps on the vector ALUs), then batch-1
+  decode. The products' int8 multiply-accumulate rate is reported against
+  the MFMA peak and against the ceiling the f32 steps set.
 * decode_tok_s: config 3, an 8B-shape llama decoder with random Q8 weights
   (dim 4096, 32 layers, 32 q / 8 kv heads of 128, SwiGLU 14336, vocab
   128256, RoPE theta 5e5, f32 KV cache): greedy decode of 256 tokens after
@@ -276,6 +281,101 @@ def decode_bench(dev, rkhip, args):
     return out
 
 
+INT8_MFMA_PEAK_TMACS = 2500.0   # MI355X dense int8: 5.0 POPS = 2.5 P multiply-accumulates/s
+VALU_PEAK_TOPS = 39.32          # 256 CUs x 4 SIMD x 16 lanes x 2.4 GHz, non-packed f32 lane-ops/s
+
+
+def prefill_bench(dev, rkhip, args):
+    """Config 4: Qwen-7B-shape decoder with Q4_0 layers (Q8 embedding and
+    classifier): the 512-token prompt through the batched prefill (int8 MFMA
+    block sums, per-token f32 epilogue), then batch-1 greedy decode."""
+    dim, hidden, heads, kv_heads, hs, vocab = 3584, 18944, 28, 4, 128, 152064
+    layers, prompt_len, steps = args.prefill_layers, args.prefill_prompt, args.prefill_decode
+    ctx = prompt_len + steps
+    qdim, kvdim = heads * hs, kv_heads * hs
+    rng = np.random.default_rng(4)
+    pool = rng.integers(0, 256, hidden * dim // 2 + (1 << 20), dtype=np.uint8)
+    pool8 = rng.integers(-127, 128, vocab * dim + (1 << 20), dtype=np.int8)
+    spool = rng.uniform(2e-5, 2e-4, vocab * dim // 32 + (1 << 16)).astype(np.float32)
+    mats = []
+
+    def mat(rows, cols, q4=True):
+        n = rows * cols
+        src = pool if q4 else pool8
+        nbytes = n // 2 if q4 else n
+        o = int(rng.integers(0, src.size - nbytes + 1))
+        so = int(rng.integers(0, spool.size - n // 32 + 1))
+        m = (dev.upload_q4 if q4 else dev.upload_q8)(src[o:o + nbytes], spool[so:so + n // 32], rows, cols)
+        mats.append(m)
+        return m
+
+    t0 = time.perf_counter()
+    lay = []
+    for _ in range(layers):
+        lay.append({"wq": mat(qdim, dim), "wk": mat(kvdim, dim), "wv": mat(kvdim, dim), "wo": mat(dim, qdim),
+                    "w1": mat(hidden, dim), "w2": mat(dim, hidden), "w3": mat(hidden, dim),
+                    "rms_att": rng.normal(1, 0.1, dim).astype(np.float32),
+                    "rms_ffn": rng.normal(1, 0.1, dim).astype(np.float32),
+                    "bq": rng.normal(0, 0.5, qdim).astype(np.float32),
+                    "bk": rng.normal(0, 0.5, kvdim).astype(np.float32),
+                    "bv": rng.normal(0, 0.5, kvdim).astype(np.float32)})
+    embed, wcls = mat(vocab, dim, False), mat(vocab, dim, False)
+    log(f"prefill bench: {layers} layers uploaded in {time.perf_counter() - t0:.1f} s")
+    cos, sin = rope_table(1000000.0, hs, ctx)
+    st = rkhip.Stage(dev, dim, hidden, heads, kv_heads, ctx, lay, cos, sin, head_dim=hs, norm_eps=1e-6,
+                     qkv_bias=True)
+    st.set_head(embed, wcls, rng.normal(1, 0.1, dim).astype(np.float32))
+    prompt = rng.integers(0, vocab, prompt_len).astype(np.int32)
+    # warm-up (batch buffers, graphs), then the timed prompt and decode
+    st.generate_start(prompt)
+    st.generate_run(prompt_len)
+    st.generate_start(prompt)
+    t0 = time.perf_counter()
+    st.generate_run(prompt_len - 1)  # positions 0..prompt-2: the batched path
+    t1 = time.perf_counter()
+    st.generate_run(1)               # the last prompt position: the first new token
+    t2 = time.perf_counter()
+    st.generate_run(steps - 1)
+    t3 = time.perf_counter()
+    # per-kernel times of the batched prompt, launches stamped one by one
+    st.generate_start(prompt)
+    dev.profile_start()
+    st.generate_run(prompt_len - 1)
+    prof = dev.profile_stop()
+    n_pre = prompt_len - 1
+    layer_weights = qdim * dim + 2 * kvdim * dim + dim * qdim + 3 * hidden * dim
+    macs = float(n_pre) * layers * layer_weights
+    mm_ms = sum(prof.get(k, (0, 0.0))[1] for k in ("qkv", "wo", "w13", "w2"))
+    mm_tmacs = macs / (mm_ms / 1e3) / 1e12 if mm_ms else None
+    pre_s = t1 - t0
+    dec_s = t3 - t2
+    out = {
+        "prefill_tok_s": round(n_pre / pre_s, 1),
+        "prefill": {
+            "config": f"config 4: Qwen-7B shape, dim {dim}, {layers} layers, {heads} q / {kv_heads} kv heads of "
+                      f"{hs}, ffn {hidden}, vocab {vocab}, QKV bias, RoPE theta 1e6; Q4_0 layers, Q8_0 embedding "
+                      f"and classifier; random codes, scales U(2e-5, 2e-4); {prompt_len}-token seeded prompt",
+            "tokens": n_pre, "seconds": round(pre_s, 4), "ms_per_layer": round(pre_s / layers * 1e3, 3),
+            "products_int8_macs": macs,
+            "products_ms": round(mm_ms, 3),
+            "products_TMAC_s": round(mm_tmacs, 1) if mm_tmacs else None,
+            "mfma_frac_of_int8_peak": round(mm_tmacs / INT8_MFMA_PEAK_TMACS, 4) if mm_tmacs else None,
+            # each (row, token, block) needs cvt, mul, mul, add on the vector ALUs in a fixed order:
+            # 4 lane-ops per 32 MACs cap the products at VALU_PEAK * 8 MACs
+            "f32_step_ceiling_TMAC_s": round(VALU_PEAK_TOPS * 8, 1),
+            "frac_of_f32_step_ceiling": round(mm_tmacs / (VALU_PEAK_TOPS * 8), 4) if mm_tmacs else None,
+            "kernels_ms": {k: round(v[1], 3) for k, v in prof.items()},
+        },
+        "decode_q4_tok_s": round((steps - 1) / dec_s, 2),
+        "decode_q4": {"config": "config 4, batch-1 greedy decode after the prompt",
+                      "steps": steps - 1, "ms_per_token": round(dec_s / (steps - 1) * 1e3, 4)},
+    }
+    st.free()
+    for m in mats:
+        m.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -289,6 +389,10 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--decode", type=int, default=256)
     ap.add_argument("--eager", action="store_true", help="decode without graph replays (for profilers)")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-layers", type=int, default=28)
+    ap.add_argument("--prefill-prompt", type=int, default=512)
+    ap.add_argument("--prefill-decode", type=int, default=64)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU: this build has no multi-GPU path (how the products would shard is "
@@ -322,6 +426,9 @@ def main():
     if not args.no_decode:
         log("decode bench (config 3)")
         result.update(decode_bench(dev, rkhip, args))
+    if not args.no_prefill:
+        log("prefill bench (config 4)")
+        result.update(prefill_bench(dev, rkhip, args))
     result["device"] = {"name": info.name.decode(), "arch": info.arch.decode(), "cu": info.compute_units}
     if not args.no_cpu:
         log("cpu baseline")
