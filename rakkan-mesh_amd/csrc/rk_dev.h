@@ -161,6 +161,41 @@ __device__ __forceinline__ int dpp_x1(int v) { return __builtin_amdgcn_mov_dpp(v
 __device__ __forceinline__ int dpp_x2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
 __device__ __forceinline__ int dpp_mirror8(int v) { return __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false); }
 
+__device__ __forceinline__ float dppf_x1(float v) { return __int_as_float(dpp_x1(__float_as_int(v))); }
+__device__ __forceinline__ float dppf_x2(float v) { return __int_as_float(dpp_x2(__float_as_int(v))); }
+
+// Go max inside each row of 16 lanes, valid in every lane of the row: DPP
+// xor 1, xor 2, half-row mirror, row mirror. Go max (NaN wins, +0 over -0)
+// is associative and commutative, so the order is free.
+__device__ __forceinline__ float row16_gomax(float m) {
+    m = gomax(m, dppf_x1(m));
+    m = gomax(m, dppf_x2(m));
+    m = gomax(m, __int_as_float(dpp_mirror8(__float_as_int(m))));
+    return gomax(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x140, 0xF, 0xF, false)));
+}
+
+// Go max over each half-wave (lanes 0-31, 32-63), valid in every lane of
+// the half. Every lane of the wave must call it.
+__device__ __forceinline__ float half_gomax(float m) {
+    m = row16_gomax(m);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+    return (threadIdx.x & 32) ? gomax(r2, r3) : gomax(r0, r1);
+}
+
+// Go max over the wave, valid in every lane: the rows, then the four rows by
+// readlane. Every lane of the wave must call it.
+__device__ __forceinline__ float wave_gomax(float m) {
+    m = row16_gomax(m);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+    return gomax(gomax(r0, r1), gomax(r2, r3));
+}
+
 // Q8_0 activation quantizer (internal/num/quant.go:34-53) of one group of
 // four values, eight lanes (aligned) per 32-value block: returns the four
 // codes packed little-endian, and the block's scale and code sum (valid in

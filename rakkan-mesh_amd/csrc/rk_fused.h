@@ -101,6 +101,14 @@ struct AttBatch {
 void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt,
                        hipStream_t s);
+// Batches up to 1024 positions (head size a multiple of 32) run a group of
+// tokens per workgroup (rk_attn_batch.hip); the results are the same.
+bool att_group_fits(const AttBatch &bt, int hs, int kv_dim);
+void launch_att_scores_group(const float *q, const float *keys, float *att, int32_t att_stride, const AttBatch &bt,
+                             int heads, int kv_heads, int kv_dim, float inv_sqrt, hipStream_t s);
+void launch_att_values_group(const float *att, int32_t att_stride, const float *vals, float *out, const AttBatch &bt,
+                             int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
+                             hipStream_t s);
 // With qx non-null (head size a multiple of 32), the output is also
 // quantized (Q8_0 blocks of the next product's input).
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,

@@ -592,25 +592,6 @@ bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s)
 // (s_j+16 + s_j+24) by two DPP exchanges and lane 0 the final tree.
 constexpr int kScoreTile = 64;
 
-__device__ __forceinline__ float dppf_x1(float v) { return __int_as_float(dpp_x1(__float_as_int(v))); }
-__device__ __forceinline__ float dppf_x2(float v) { return __int_as_float(dpp_x2(__float_as_int(v))); }
-
-// Go max over the wave, valid in every lane: inside each row of 16 lanes by
-// DPP (xor 1, xor 2, half-row mirror, row mirror), then the four rows by
-// readlane. Go max (NaN wins, +0 over -0) is associative and commutative, so
-// the order is free. Every lane of the wave must call it.
-__device__ __forceinline__ float wave_gomax(float m) {
-    m = gomax(m, dppf_x1(m));
-    m = gomax(m, dppf_x2(m));
-    m = gomax(m, __int_as_float(dpp_mirror8(__float_as_int(m))));
-    m = gomax(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), 0x140, 0xF, 0xF, false)));
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
-    return gomax(gomax(r0, r1), gomax(r2, r3));
-}
-
 template <int HS>  // head size when fixed at compile time (all loads issued at once), else 0
 __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const float *keys, float *att,
                                                          int32_t att_stride, const int32_t *ctl, AttBatch bt,
@@ -665,6 +646,10 @@ __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const f
 void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt,
                        hipStream_t s) {
+    if (!ctl && hs == 128 && att_group_fits(bt, hs, kv_dim)) {
+        launch_att_scores_group(q, keys, att, att_stride, bt, heads, kv_heads, kv_dim, inv_sqrt, s);
+        return;
+    }
     // decode: positions up to ctx; a batch: up to its last token's
     const int npos = ctl ? ctx : bt.pos0 + bt.tokens;
     const dim3 grid(heads, (npos + kScoreTile - 1) / kScoreTile, ctl ? 1 : bt.tokens);
@@ -856,6 +841,10 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
         (void)hipFuncSetAttribute((const void *)att_values_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)kValMaxDynLds);
     });
+    if (!ctl && att_group_fits(bt, hs, kv_dim)) {
+        launch_att_values_group(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s);
+        return;
+    }
     const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice, ctl ? 1 : bt.tokens);
     if (hs % 32 != 0) qx = nullptr;
     const int ctx_pad = (ctx + 3) & ~3;
