@@ -275,6 +275,32 @@ int rk_stage_generate(rk_stage *s, const int32_t *prompt, int32_t n_prompt, int3
 enum { RK_FN_RECIP32 = 0, RK_FN_RSQRT32 = 1, RK_FN_EXP32 = 2, RK_FN_SILU = 3 };
 int rk_num_eval(rk_device *dev, int32_t fn, const float *in, float *out, int64_t n);
 
+/* ---- rakkan_tensor_v1 operators (internal/sandbox/tensor.go) ----
+ * Element types as the tensor table's (tensor.go:42-44). */
+enum { RK_TENSOR_F32 = 0, RK_TENSOR_I8 = 1, RK_TENSOR_I32 = 2 };
+
+/* tensor.go:286-339 tenMatmul: c = a[m,k]·b with b[k,n] (transposed = 0,
+ * matmul) or b[n,k] (transposed = 1, matmul_t). RK_TENSOR_F32: f32 in and
+ * out, acc += float32(a·b) for p = 0..k-1 from +0, Canonical(acc).
+ * RK_TENSOR_I8: int8 in, int32 out, Go int32 wraparound. Any other dtype
+ * (i32 inputs included) or a dimension outside 1..2^24 (tensor.go:60) is
+ * RK_ERR_ARGS, as tenErrArgs (-1). The caller charges gas m·n·k·8 and keeps
+ * the memory budget (tensor.go:300-310) before calling. Host buffers,
+ * blocking. */
+int rk_tensor_matmul(rk_device *dev, int32_t dtype, int32_t transposed, int64_t m, int64_t k, int64_t n,
+                     const void *a, const void *b, void *c);
+/* The same on device-resident a, b, c, enqueued on `stream` (NULL: the
+ * device's own) without waiting. */
+int rk_tensor_matmul_device(rk_device *dev, int32_t dtype, int32_t transposed, int64_t m, int64_t k, int64_t n,
+                            const void *d_a, const void *d_b, void *d_c, void *stream);
+/* tensor.go:445-461 tenQuantize: q = int8(max(-127, min(127,
+ * float32(RoundToEven(v/k))))) with a true f32 division; k > 0. A NaN
+ * quotient gives 0 (amd64's conversion of NaN). */
+int rk_tensor_quantize(rk_device *dev, const float *a, int8_t *q, int64_t n, float k);
+/* tensor.go:366-387 tenScale: out = Canonical(float32(v)·k) for an f32 or
+ * i32 input (dtype RK_TENSOR_F32 / RK_TENSOR_I32; i8 is RK_ERR_ARGS). */
+int rk_tensor_scale(rk_device *dev, int32_t dtype, const void *a, float *out, int64_t n, float k);
+
 /* internal/gpu/profile.go:82-109 StartProfile / StopProfile. While a
  * profile is active, every kernel the library launches is bracketed by HIP
  * events on the stream it runs on; stop waits for them and returns, per

@@ -86,7 +86,13 @@ SIGNATURES = {
     "rk_stage_generate_tokens": (ctypes.c_int, [P, I32, I32, P]),
     "rk_stage_generate": (ctypes.c_int, [P, P, I32, I32, P]),
     "rk_num_eval": (ctypes.c_int, [P, I32, P, P, I64]),
+    "rk_tensor_matmul": (ctypes.c_int, [P, I32, I32, I64, I64, I64, P, P, P]),
+    "rk_tensor_matmul_device": (ctypes.c_int, [P, I32, I32, I64, I64, I64, P, P, P, P]),
+    "rk_tensor_quantize": (ctypes.c_int, [P, P, P, I64, ctypes.c_float]),
+    "rk_tensor_scale": (ctypes.c_int, [P, I32, P, P, I64, ctypes.c_float]),
 }
+
+TENSOR_F32, TENSOR_I8, TENSOR_I32 = 0, 1, 2
 
 FN_RECIP32, FN_RSQRT32, FN_EXP32, FN_SILU = 0, 1, 2, 3
 
@@ -328,6 +334,37 @@ class Device:
         ops = (P * len(ms))(*d_outs)
         self._check(lib().rk_matmul_t_device(self.h, len(ms), hs, ops, P(d_x), cols, tokens,
                                              P(stream) if stream else None))
+
+    def tensor_matmul(self, a, b, transposed=False):
+        """rakkan_tensor_v1 matmul (b [k][n]) / matmul_t (b [n][k]) of 2-D
+        float32 or int8 arrays; float32 or int32 result [m][n]."""
+        if a.dtype != b.dtype or a.dtype not in (np.float32, np.int8):
+            raise RKError(-1, "tensor matmul: f32 or i8 inputs of one type")
+        a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+        m, k = a.shape
+        n = b.shape[0] if transposed else b.shape[1]
+        if (b.shape[1] if transposed else b.shape[0]) != k:
+            raise RKError(-1, "tensor matmul: shapes differ")
+        dt = TENSOR_F32 if a.dtype == np.float32 else TENSOR_I8
+        c = np.empty((m, n), np.float32 if dt == TENSOR_F32 else np.int32)
+        self._check(lib().rk_tensor_matmul(self.h, dt, int(bool(transposed)), m, k, n, _ptr(a), _ptr(b), _ptr(c)))
+        return c
+
+    def tensor_quantize(self, a, k):
+        a = np.ascontiguousarray(a, np.float32)
+        q = np.empty(a.shape, np.int8)
+        self._check(lib().rk_tensor_quantize(self.h, _ptr(a), _ptr(q), a.size, k))
+        return q
+
+    def tensor_scale(self, a, k):
+        a = np.ascontiguousarray(a)
+        dt = {np.dtype(np.int32): TENSOR_I32, np.dtype(np.float32): TENSOR_F32, np.dtype(np.int8): TENSOR_I8}.get(
+            a.dtype)
+        if dt is None:
+            raise RKError(-1, "tensor scale: f32 or i32 input")
+        out = np.empty(a.shape, np.float32)
+        self._check(lib().rk_tensor_scale(self.h, dt, _ptr(a), _ptr(out), a.size, k))
+        return out
 
     def matvecs_device(self, ms, d_outs, d_x, cols, stream=None):
         """Enqueue products on device pointers (ints) on a HIP stream handle."""
