@@ -275,6 +275,30 @@ int rk_stage_generate(rk_stage *s, const int32_t *prompt, int32_t n_prompt, int3
 enum { RK_FN_RECIP32 = 0, RK_FN_RSQRT32 = 1, RK_FN_EXP32 = 2, RK_FN_SILU = 3 };
 int rk_num_eval(rk_device *dev, int32_t fn, const float *in, float *out, int64_t n);
 
+/* ---- Mixture-of-experts feed-forward (config 5, Qwen3-MoE shape) ----
+ * No counterpart in the reference's llama path: the contract is this
+ * build's, after the order of internal/llm/dsv41/ops.go:67-74 (topK) and
+ * forward.go:355-413 (moe). For each token's RMS-normed input xn:
+ * z = router·xn (a Q8 product), p = softmax(z) (Go max, Exp32, one
+ * sequential sum, Recip32; internal/llm/model.go:640-654), the top-k experts
+ * by p (a stable order by cmp.Compare: larger first, lower index on ties,
+ * NaN last), w_i = p_i·Recip32(Σ p_i) (the sum in selection order), and
+ * y = Σ W2_e·(w_e·(silu(W1_e·xn)·(W3_e·xn))) over the selected experts in
+ * ascending index, from +0, in float32. Experts are Q8 W1/W3 [hidden][dim]
+ * and W2 [dim][hidden]; the router is Q8 [experts][dim]. The matrices stay
+ * the caller's (free them after rk_moe_free). */
+typedef struct rk_moe rk_moe;
+int rk_moe_new(rk_device *dev, rk_matrix *router, int32_t experts, rk_matrix *const *w1, rk_matrix *const *w2,
+               rk_matrix *const *w3, int32_t topk, rk_moe **out);
+/* xn, y: [tokens][dim] host buffers; sel, wsel (either may be NULL):
+ * [tokens][topk] selected experts and their weights. Blocking. */
+int rk_moe_ffn(rk_moe *moe, const float *xn, int32_t tokens, float *y, int32_t *sel, float *wsel);
+/* The same on device buffers, enqueued on `stream` (NULL: the device's). */
+int rk_moe_ffn_device(rk_moe *moe, const float *d_xn, int32_t tokens, float *d_y, void *stream);
+/* Device bytes of the scratch the handle keeps (grown to the largest batch). */
+int64_t rk_moe_bytes(const rk_moe *moe);
+int rk_moe_free(rk_moe *moe);
+
 /* ---- rakkan_tensor_v1 operators (internal/sandbox/tensor.go) ----
  * Element types as the tensor table's (tensor.go:42-44). */
 enum { RK_TENSOR_F32 = 0, RK_TENSOR_I8 = 1, RK_TENSOR_I32 = 2 };

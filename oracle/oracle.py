@@ -203,6 +203,29 @@ def softmax(x):
     return x
 
 
+def topk(v, k):
+    v = _c(v, np.float32)
+    idx = np.empty(k, np.int32)
+    lib().rko_topk(ptr(v), v.size, k, ptr(idx))
+    return idx
+
+
+def moe_ffn(router, w1, w2, w3, topk_n, xn):
+    """The build's MoE feed-forward contract for one normed input (Mat
+    objects of oracle.model): y, selected experts, their weights."""
+    from .model import RkoMat
+    n = len(w1)
+    arr = lambda ms: (RkoMat * n)(*[m.ctype() for m in ms])  # noqa: E731
+    a1, a2, a3 = arr(w1), arr(w2), arr(w3)
+    rt = router.ctype()
+    xn = _c(xn, np.float32)
+    y = np.empty(router.cols, np.float32)
+    sel = np.empty(topk_n, np.int32)
+    w = np.empty(topk_n, np.float32)
+    lib().rko_moe_ffn(ctypes.byref(rt), a1, a2, a3, n, topk_n, ptr(xn), ptr(y), ptr(sel), ptr(w))
+    return y, sel, w
+
+
 def tensor_matmul_f32(a, b, transposed):
     a, b = _c(a, np.float32), _c(b, np.float32)
     m, k = a.shape

@@ -795,15 +795,22 @@ int32_t rko_argmax(const float *v, int64_t n) {
  *   w_i = p[sel_i] · Recip32(sum);
  *   h_e = float32(w_e · float32(silu(W1_e xn) · W3_e xn));  o_e = W2_e h_e;
  *   y = 0; y += o_e for e ascending. */
+/* Go's cmp.Compare on float32: NaN below every number, NaNs equal, -0 == +0. */
+static int cmp_compare(float x, float y) {
+    const int xn = x != x, yn = y != y;
+    if (xn || yn) return xn && yn ? 0 : (xn ? -1 : 1);
+    return x < y ? -1 : (x > y ? 1 : 0);
+}
 void rko_topk(const float *v, int32_t n, int32_t k, int32_t *idx) {
-    /* stable selection: repeatedly take the first index holding the largest
-     * remaining value (equivalent to a stable descending sort's prefix). */
+    /* internal/llm/dsv41/ops.go:67-74 topK: a stable sort by
+     * cmp.Compare(v[b], v[a]), first k. As a selection: repeatedly the first
+     * index whose value no remaining value compares above. */
     unsigned char *used = calloc((size_t)n, 1);
     for (int32_t s = 0; s < k; s++) {
         int32_t best = -1;
         for (int32_t i = 0; i < n; i++) {
             if (used[i]) continue;
-            if (best < 0 || v[i] > v[best]) best = i;
+            if (best < 0 || cmp_compare(v[i], v[best]) > 0) best = i;
         }
         used[best] = 1;
         idx[s] = best;

@@ -1,0 +1,468 @@
+// rk_moe.hip — a mixture-of-experts feed-forward on the device (config 5,
+// Qwen3-MoE shape). The reference has no llama-family MoE; the contract is
+// this build's, after the dsv41 precedent (internal/llm/dsv41/ops.go:67-74
+// topK, forward.go:355-413 moe), for each token's RMS-normed input xn:
+//
+//   z = router·xn                       Q8 product, MatVecQ8's bits
+//   p = softmax(z)                      Go max, Exp32, one sequential sum,
+//                                       Recip32 (internal/llm/model.go:640-654)
+//   sel = topK(p, k)                    stable by cmp.Compare: larger first,
+//                                       lower index on ties, NaN last
+//   w_i = p_sel_i·Recip32(Σ_i p_sel_i)  the sum in selection order
+//   h = float32(w·float32(silu(W1·xn)·(W3·xn)))  per selected expert
+//   y = Σ W2·h over the selected experts in ascending index, from +0
+//
+// Launches: the input quantized once; the router's product; the routing
+// (one workgroup per token); the selected experts' W1/W3 rows with the
+// gate and weight; h quantized; their W2 rows; the ascending-order sum.
+// Every expert product is a row dot of MatVecQ8 (integer block sums, the
+// eight ordered running sums), so each token's bits do not depend on the
+// batch.
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "rk_dev.h"
+#include "rk_fused.h"
+#include "rk_mm.h"
+#include "rk_runtime.h"
+
+struct rk_moe {
+    rk_device *d = nullptr;
+    rk_matrix *router = nullptr;
+    int32_t experts = 0, topk = 0, dim = 0, hidden = 0;
+    // device tables: codes and scales of W1, W3, W2 per expert
+    const uint8_t **w1 = nullptr, **w3 = nullptr, **w2 = nullptr;
+    const float **s1 = nullptr, **s3 = nullptr, **s2 = nullptr;
+    void *tables = nullptr;
+    // scratch for up to `cap` tokens
+    int cap = 0;
+    void *mem = nullptr;
+    float *x = nullptr, *logits = nullptr, *wsel = nullptr, *h = nullptr, *o = nullptr, *y = nullptr;
+    int32_t *sel = nullptr;
+    int8_t *qx = nullptr, *hq = nullptr;
+    float *xs = nullptr, *hs = nullptr;
+    int32_t *xsum = nullptr, *hsum = nullptr;
+    int64_t bytes = 0;
+};
+
+namespace rk {
+
+namespace {
+
+constexpr int kMoeMaxK = 32;        // experts per token
+constexpr int kMoeMaxExperts = 1024;
+constexpr int kMoeMaxCols = 8192;   // widest expert input (chunks of 1 KiB per row)
+constexpr int kMoeRows = 4;         // rows per wave in the expert kernels
+
+// Go's cmp.Compare(x, y) > 0 on float32: NaN below every number, NaNs
+// equal, -0 == +0.
+__device__ __forceinline__ bool cmp_above(float x, float y) {
+    const bool xn = x != x, yn = y != y;
+    if (xn || yn) return yn && !xn;
+    return x > y;
+}
+
+// Four Q8 rows dotted with one quantized input (MatVecQ8's order per row:
+// exact block sums; block b into running sum b mod 8 in order of b; the
+// fixed tree). Lane 0 returns the results. Every lane of the wave calls it.
+__device__ __forceinline__ void wave_rows_q8(const uint8_t *const (&w)[kMoeRows], const float *const (&ws)[kMoeRows],
+                                             const int8_t *qx, const float *xs, int cols, float (&res)[kMoeRows]) {
+    const int lane = threadIdx.x & 63;
+    const int nb = cols >> 5, C = (cols + 1023) >> 10;
+    float acc[kMoeRows];
+#pragma unroll
+    for (int r = 0; r < kMoeRows; r++) acc[r] = 0.0f;
+    for (int c = 0; c < C; c++) {
+        const int o = min(c * 1024 + lane * 16, cols - 16);  // lanes past the row's end: blocks excluded below
+        const int4 xv = *reinterpret_cast<const int4 *>(qx + o);
+        const float sx = xs[o >> 5];
+        int4 wv[kMoeRows];
+        float sw[kMoeRows];
+#pragma unroll
+        for (int r = 0; r < kMoeRows; r++) {
+            wv[r] = load_stream16(w[r] + o);
+            sw[r] = ws[r][o >> 5];
+        }
+#pragma unroll
+        for (int r = 0; r < kMoeRows; r++) {
+            const int s = pair_sum(dot16(wv[r], xv, 0));
+            const float t = (float)s * (sw[r] * sx);
+            // block 32c+k is in lanes 2k, 2k+1; running sum L (lane 2L) takes
+            // blocks 32c+L, +8, +16, +24
+            const float t1 = __shfl_down(t, 16), t2 = __shfl_down(t, 32), t3 = __shfl_down(t, 48);
+            if (lane < 16 && (lane & 1) == 0) {
+                const int b0 = c * 32 + (lane >> 1);
+                if (b0 < nb) acc[r] += t;
+                if (b0 + 8 < nb) acc[r] += t1;
+                if (b0 + 16 < nb) acc[r] += t2;
+                if (b0 + 24 < nb) acc[r] += t3;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kMoeRows; r++) {
+        const float p2 = acc[r] + __shfl_down(acc[r], 2);
+        const float q4 = p2 + __shfl_down(p2, 4);
+        res[r] = q4 + __shfl_down(q4, 8);
+    }
+}
+
+// Routing of one token per workgroup (64 threads): softmax, stable top-k,
+// normalized weights.
+__global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int experts, int k, int32_t *sel,
+                                                       float *wsel) {
+    extern __shared__ float sp[];  // [experts] probabilities
+    __shared__ float s_inv;
+    const int t = blockIdx.x, lane = threadIdx.x;
+    const float *z = logits + (int64_t)t * experts;
+    float m = z[0];
+    for (int e = lane; e < experts; e += 64) {
+        sp[e] = z[e];
+        m = gomax(m, z[e]);
+    }
+    m = wave_gomax(m);
+    for (int e = lane; e < experts; e += 64) sp[e] = exp32(sp[e] - m);
+    __syncthreads();
+    if (lane == 0) s_inv = recip32(lds_chain_sum(sp, experts, 0.0f));
+    __syncthreads();
+    const float inv = s_inv;
+    for (int e = lane; e < experts; e += 64) sp[e] = sp[e] * inv;
+    __syncthreads();
+    // top-k: k rounds of "first index no remaining value compares above"
+    __shared__ int s_sel[kMoeMaxK];
+    for (int r = 0; r < k; r++) {
+        float bv = 0.0f;
+        int bi = -1;
+        for (int e = lane; e < experts; e += 64) {
+            bool taken = false;
+            for (int q = 0; q < r; q++) taken |= s_sel[q] == e;
+            if (taken) continue;
+            const float v = sp[e];
+            if (bi < 0 || cmp_above(v, bv)) {  // e ascends: ties keep the lower index
+                bv = v;
+                bi = e;
+            }
+        }
+        for (int off = 1; off < 64; off <<= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (oi >= 0 && (bi < 0 || cmp_above(ov, bv) || (!cmp_above(bv, ov) && oi < bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) s_sel[r] = bi;
+        __syncthreads();
+    }
+    if (lane == 0) {
+        float sum = 0.0f;
+        for (int r = 0; r < k; r++) sum += sp[s_sel[r]];
+        s_inv = recip32(sum);
+    }
+    __syncthreads();
+    if (lane < k) {
+        sel[(int64_t)t * k + lane] = s_sel[lane];
+        wsel[(int64_t)t * k + lane] = sp[s_sel[lane]] * s_inv;
+    }
+}
+
+// W1 and W3 rows of each (token, slot)'s expert: h = w·(silu(W1·xn)·(W3·xn)).
+// Workgroup (pair, block of 8 hidden rows); wave w takes hidden rows 2w, 2w+1
+// (W1 and W3 of each: four row dots).
+__global__ __launch_bounds__(256) void moe_up_kernel(const uint8_t *const *w1, const float *const *s1,
+                                                     const uint8_t *const *w3, const float *const *s3,
+                                                     const int32_t *sel, const float *wsel, int k, const int8_t *qx,
+                                                     const float *xs, int dim, int hidden, float *h) {
+    const int pr = blockIdx.x, t = pr / k;
+    const int e = sel[pr];
+    const float wt = wsel[pr];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int j0 = blockIdx.y * 8 + 2 * wave;  // hidden rows j0, j0 + 1
+    const int nb = dim >> 5;
+    const uint8_t *w[kMoeRows];
+    const float *ws[kMoeRows];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int j = min(j0 + q, hidden - 1);
+        w[2 * q] = w1[e] + (int64_t)j * dim;
+        ws[2 * q] = s1[e] + (int64_t)j * nb;
+        w[2 * q + 1] = w3[e] + (int64_t)j * dim;
+        ws[2 * q + 1] = s3[e] + (int64_t)j * nb;
+    }
+    float res[kMoeRows];
+    wave_rows_q8(w, ws, qx + (int64_t)t * dim, xs + (int64_t)t * nb, dim, res);
+    if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+            if (j0 + q < hidden) h[(int64_t)pr * hidden + j0 + q] = wt * silu_mul(res[2 * q], res[2 * q + 1]);
+    }
+}
+
+// W2 rows of each (token, slot)'s expert on its quantized h. Workgroup
+// (pair, block of 16 output rows), four rows a wave.
+__global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t *const *w2, const float *const *s2,
+                                                       const int32_t *sel, const int8_t *hq, const float *hs,
+                                                       int dim, int hidden, float *o) {
+    const int pr = blockIdx.x;
+    const int e = sel[pr];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i0 = blockIdx.y * 16 + kMoeRows * wave;
+    const int nb = hidden >> 5;
+    const uint8_t *w[kMoeRows];
+    const float *ws[kMoeRows];
+#pragma unroll
+    for (int r = 0; r < kMoeRows; r++) {
+        const int i = min(i0 + r, dim - 1);
+        w[r] = w2[e] + (int64_t)i * hidden;
+        ws[r] = s2[e] + (int64_t)i * nb;
+    }
+    float res[kMoeRows];
+    wave_rows_q8(w, ws, hq + (int64_t)pr * hidden, hs + (int64_t)pr * nb, hidden, res);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < kMoeRows; r++)
+            if (i0 + r < dim) o[(int64_t)pr * dim + i0 + r] = res[r];
+    }
+}
+
+// y_t = Σ o over the token's experts in ascending index, from +0.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, int k, const float *o, int dim,
+                                                          float *y) {
+    __shared__ int order[kMoeMaxK];  // the token's slots by ascending expert
+    const int t = blockIdx.x;
+    if (threadIdx.x == 0) {
+        for (int s = 0; s < k; s++) order[s] = s;
+        for (int a = 1; a < k; a++)  // insertion sort of k <= 32 slots
+            for (int b = a; b > 0 && sel[(int64_t)t * k + order[b]] < sel[(int64_t)t * k + order[b - 1]]; b--) {
+                const int tmp = order[b];
+                order[b] = order[b - 1];
+                order[b - 1] = tmp;
+            }
+    }
+    __syncthreads();
+    const int i = blockIdx.y * 256 + threadIdx.x;
+    if (i >= dim) return;
+    float acc = 0.0f;
+    for (int s = 0; s < k; s++) acc += o[((int64_t)t * k + order[s]) * dim + i];
+    y[(int64_t)t * dim + i] = acc;
+}
+
+}  // namespace
+
+static int moe_scratch(rk_moe *m, int tokens) {
+    if (tokens <= m->cap) return RK_OK;
+    rk_device *d = m->d;
+    if (d->capturing) return fail(d, RK_ERR_ARGS, "rk_moe: scratch must grow, which cannot be recorded");
+    HIP_TRY(d, hipDeviceSynchronize(), "moe scratch");
+    (void)hipFree(m->mem);
+    m->mem = nullptr;
+    add_used(d, -m->bytes);
+    m->bytes = 0;
+    m->cap = 0;
+    const int64_t T = std::max(tokens, 16), K = m->topk, E = m->experts, D = m->dim, H = m->hidden;
+    std::vector<std::pair<void **, int64_t>> plan = {
+        {(void **)&m->x, 4 * T * D},          {(void **)&m->qx, T * D},
+        {(void **)&m->xs, 4 * T * (D / 32)},  {(void **)&m->xsum, 4 * T * (D / 32)},
+        {(void **)&m->logits, 4 * T * E},     {(void **)&m->sel, 4 * T * K},
+        {(void **)&m->wsel, 4 * T * K},       {(void **)&m->h, 4 * T * K * H},
+        {(void **)&m->hq, T * K * H},         {(void **)&m->hs, 4 * T * K * (H / 32)},
+        {(void **)&m->hsum, 4 * T * K * (H / 32)}, {(void **)&m->o, 4 * T * K * D},
+        {(void **)&m->y, 4 * T * D}};
+    int64_t at = 0;
+    for (auto &p : plan) at += (p.second + 255) & ~(int64_t)255;
+    int rc = dev_alloc(d, &m->mem, (size_t)at, "moe scratch");
+    if (rc) return rc;
+    at = 0;
+    for (auto &p : plan) {
+        *p.first = static_cast<char *>(m->mem) + at;
+        at += (p.second + 255) & ~(int64_t)255;
+    }
+    m->bytes = at;
+    m->cap = (int)T;
+    add_used(d, m->bytes);
+    return RK_OK;
+}
+
+// The launches of one MoE feed-forward over `tokens` inputs at d_xn; the
+// result to d_y ([tokens][dim]).
+static int enqueue_moe(rk_moe *m, const float *d_xn, int tokens, float *d_y, hipStream_t s) {
+    rk_device *d = m->d;
+    const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
+    {
+        ProfScope p(d, s, "quantize_acts");
+        launch_quantize_acts(d_xn, (int64_t)tokens * D, m->qx, m->xs, m->xsum, s);
+    }
+    bool ok;
+    if (tokens == 1) {
+        FusedArgs a{};
+        a.seg[0] = MatSeg{m->router->w, m->router->scales, m->logits, m->router->rows};
+        a.nseg = 1;
+        a.cols = D;
+        a.rows = E;
+        a.qx = m->qx;
+        a.xs = m->xs;
+        a.xsum = m->xsum;
+        ProfScope p(d, s, "moe_router");
+        ok = launch_fused(kFmtQ8, kProGlobal, kEpStore, a, d->cu, s);
+    } else {
+        MmArgs a{};
+        a.seg[0] = MatSeg{m->router->w, m->router->scales, m->logits, m->router->rows};
+        a.nseg = 1;
+        a.cols = D;
+        a.rows = E;
+        a.tokens = tokens;
+        a.qx = m->qx;
+        a.xs = m->xs;
+        ProfScope p(d, s, "moe_router");
+        ok = launch_mm(kFmtQ8, kEpStore, a, s);
+    }
+    if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
+    {
+        ProfScope p(d, s, "moe_route");
+        RK_LAUNCH(moe_route_kernel, dim3(tokens), dim3(64), (size_t)E * 4, s, m->logits, E, K, m->sel, m->wsel);
+    }
+    const unsigned pairs = (unsigned)(tokens * K);
+    {
+        ProfScope p(d, s, "moe_up");
+        RK_LAUNCH(moe_up_kernel, dim3(pairs, (unsigned)((H + 7) / 8)), dim3(256), 0, s, m->w1, m->s1, m->w3, m->s3,
+                  m->sel, m->wsel, K, m->qx, m->xs, D, H, m->h);
+    }
+    {
+        ProfScope p(d, s, "quantize_acts");
+        launch_quantize_acts(m->h, (int64_t)pairs * H, m->hq, m->hs, m->hsum, s);
+    }
+    {
+        ProfScope p(d, s, "moe_down");
+        RK_LAUNCH(moe_down_kernel, dim3(pairs, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2, m->s2, m->sel,
+                  m->hq, m->hs, D, H, m->o);
+    }
+    {
+        ProfScope p(d, s, "moe_combine");
+        RK_LAUNCH(moe_combine_kernel, dim3((unsigned)tokens, (unsigned)((D + 255) / 256)), dim3(256), 0, s, m->sel, K,
+                  m->o, D, d_y);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(d, e, "moe launch");
+    return RK_OK;
+}
+
+}  // namespace rk
+
+using namespace rk;
+
+extern "C" {
+
+int rk_moe_new(rk_device *d, rk_matrix *router, int32_t experts, rk_matrix *const *w1, rk_matrix *const *w2,
+               rk_matrix *const *w3, int32_t topk, rk_moe **out) {
+    if (!d || !out || !router || !w1 || !w2 || !w3) return fail(d, RK_ERR_ARGS, "rk_moe_new: null argument");
+    *out = nullptr;
+    if (experts <= 0 || experts > kMoeMaxExperts || topk <= 0 || topk > kMoeMaxK || topk > experts)
+        return fail(d, RK_ERR_ARGS, "rk_moe_new: %d experts, top %d", experts, topk);
+    const int64_t dim = router->cols, hidden = w1[0] ? w1[0]->rows : 0;
+    if (router->d != d || router->rows != experts || router->kind != RK_Q8)
+        return fail(d, RK_ERR_ARGS, "rk_moe_new: the router must be a Q8 %d-row matrix on the device", experts);
+    if (dim > kMoeMaxCols || hidden <= 0 || hidden > kMoeMaxCols || dim % 32 || hidden % 32)
+        return fail(d, RK_ERR_UNSUPPORTED, "rk_moe_new: dim %lld / hidden %lld", (long long)dim, (long long)hidden);
+    for (int e = 0; e < experts; e++) {
+        const rk_matrix *a = w1[e], *b = w3[e], *c = w2[e];
+        if (!a || !b || !c || a->d != d || b->d != d || c->d != d || a->kind != RK_Q8 || b->kind != RK_Q8 ||
+            c->kind != RK_Q8 || a->rows != hidden || a->cols != dim || b->rows != hidden || b->cols != dim ||
+            c->rows != dim || c->cols != hidden)
+            return fail(d, RK_ERR_ARGS, "rk_moe_new: expert %d: W1/W3 %lldx%lld and W2 %lldx%lld Q8 matrices expected",
+                        e, (long long)hidden, (long long)dim, (long long)dim, (long long)hidden);
+    }
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    rk_moe *m = new rk_moe();
+    m->d = d;
+    m->router = router;
+    m->experts = experts;
+    m->topk = topk;
+    m->dim = (int32_t)dim;
+    m->hidden = (int32_t)hidden;
+    std::vector<const void *> tab(6 * (size_t)experts);
+    for (int e = 0; e < experts; e++) {
+        tab[e] = w1[e]->w;
+        tab[experts + e] = w3[e]->w;
+        tab[2 * experts + e] = w2[e]->w;
+        tab[3 * experts + e] = w1[e]->scales;
+        tab[4 * experts + e] = w3[e]->scales;
+        tab[5 * experts + e] = w2[e]->scales;
+    }
+    int rc = dev_alloc(d, &m->tables, tab.size() * sizeof(void *), "moe tables");
+    if (rc) {
+        delete m;
+        return rc;
+    }
+    const void **t = static_cast<const void **>(m->tables);
+    m->w1 = reinterpret_cast<const uint8_t **>(t);
+    m->w3 = reinterpret_cast<const uint8_t **>(t + experts);
+    m->w2 = reinterpret_cast<const uint8_t **>(t + 2 * experts);
+    m->s1 = reinterpret_cast<const float **>(t + 3 * experts);
+    m->s3 = reinterpret_cast<const float **>(t + 4 * experts);
+    m->s2 = reinterpret_cast<const float **>(t + 5 * experts);
+    hipError_t e = hipMemcpy(m->tables, tab.data(), tab.size() * sizeof(void *), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(m->tables);
+        delete m;
+        return hip_fail(d, e, "moe tables");
+    }
+    *out = m;
+    return RK_OK;
+}
+
+int rk_moe_ffn(rk_moe *m, const float *xn, int32_t tokens, float *y, int32_t *sel, float *wsel) {
+    if (!m) return RK_ERR_ARGS;
+    rk_device *d = m->d;
+    if (tokens < 0 || (tokens > 0 && (!xn || !y))) return fail(d, RK_ERR_ARGS, "rk_moe_ffn: bad arguments");
+    if (tokens == 0) return RK_OK;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    if (d->capturing) return fail(d, RK_ERR_ARGS, "rk_moe_ffn waits for its results: it cannot be recorded");
+    int rc = moe_scratch(m, tokens);
+    if (rc) return rc;
+    hipStream_t s = d->stream;
+    const size_t xb = (size_t)tokens * m->dim * 4;
+    HIP_TRY(d, hipMemcpyAsync(m->x, xn, xb, hipMemcpyHostToDevice, s), "moe input");
+    if ((rc = enqueue_moe(m, m->x, tokens, m->y, s))) return rc;
+    HIP_TRY(d, hipMemcpyAsync(y, m->y, xb, hipMemcpyDeviceToHost, s), "moe output");
+    if (sel)
+        HIP_TRY(d, hipMemcpyAsync(sel, m->sel, (size_t)tokens * m->topk * 4, hipMemcpyDeviceToHost, s), "moe sel");
+    if (wsel)
+        HIP_TRY(d, hipMemcpyAsync(wsel, m->wsel, (size_t)tokens * m->topk * 4, hipMemcpyDeviceToHost, s), "moe w");
+    HIP_TRY(d, hipStreamSynchronize(s), "moe");
+    return RK_OK;
+}
+
+int rk_moe_ffn_device(rk_moe *m, const float *d_xn, int32_t tokens, float *d_y, void *stream) {
+    if (!m) return RK_ERR_ARGS;
+    rk_device *d = m->d;
+    if (tokens < 0 || (tokens > 0 && (!d_xn || !d_y))) return fail(d, RK_ERR_ARGS, "rk_moe_ffn_device: bad arguments");
+    if (tokens == 0) return RK_OK;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipStream_t s = stream ? (hipStream_t)stream : d->stream;
+    if (d->capturing && s != d->stream)
+        return fail(d, RK_ERR_ARGS, "while recording a graph, work goes on the device's stream");
+    int rc = moe_scratch(m, tokens);
+    if (rc) return rc;
+    return enqueue_moe(m, d_xn, tokens, d_y, s);
+}
+
+int64_t rk_moe_bytes(const rk_moe *m) { return m ? m->bytes : -1; }
+
+int rk_moe_free(rk_moe *m) {
+    if (!m) return RK_ERR_ARGS;
+    rk_device *d = m->d;
+    Hold hold(d->gate);
+    (void)hipSetDevice(d->index);
+    (void)hipStreamSynchronize(d->stream);
+    (void)hipFree(m->tables);
+    (void)hipFree(m->mem);
+    add_used(d, -m->bytes);
+    delete m;
+    return RK_OK;
+}
+
+}  // extern "C"

@@ -86,6 +86,11 @@ SIGNATURES = {
     "rk_stage_generate_tokens": (ctypes.c_int, [P, I32, I32, P]),
     "rk_stage_generate": (ctypes.c_int, [P, P, I32, I32, P]),
     "rk_num_eval": (ctypes.c_int, [P, I32, P, P, I64]),
+    "rk_moe_new": (ctypes.c_int, [P, P, I32, P, P, P, I32, P]),
+    "rk_moe_ffn": (ctypes.c_int, [P, P, I32, P, P, P]),
+    "rk_moe_ffn_device": (ctypes.c_int, [P, P, I32, P, P]),
+    "rk_moe_bytes": (I64, [P]),
+    "rk_moe_free": (ctypes.c_int, [P]),
     "rk_tensor_matmul": (ctypes.c_int, [P, I32, I32, I64, I64, I64, P, P, P]),
     "rk_tensor_matmul_device": (ctypes.c_int, [P, I32, I32, I64, I64, I64, P, P, P, P]),
     "rk_tensor_quantize": (ctypes.c_int, [P, P, P, I64, ctypes.c_float]),
@@ -419,6 +424,42 @@ class Graph:
     def free(self):
         if self.h:
             lib().rk_graph_free(self.h)
+            self.h = None
+
+
+class Moe:
+    """A mixture-of-experts feed-forward on one device (rk_moe_*): a Q8
+    router [experts][dim] and per expert Q8 W1/W3 [hidden][dim], W2
+    [dim][hidden] (uploaded Matrix objects, kept by the caller)."""
+
+    def __init__(self, dev, router, w1, w2, w3, topk):
+        self.dev, self.topk = dev, topk
+        self.dim = router.cols
+        n = len(w1)
+        arr = lambda ms: (P * n)(*[m.h for m in ms])  # noqa: E731
+        h = P()
+        dev._check(lib().rk_moe_new(dev.h, router.h, n, arr(w1), arr(w2), arr(w3), topk, ctypes.byref(h)))
+        self.h = h
+
+    def ffn(self, xn):
+        """y [tokens][dim], selected experts and weights [tokens][topk]."""
+        xn = np.ascontiguousarray(xn, np.float32).reshape(-1, self.dim)
+        t = xn.shape[0]
+        y = np.empty_like(xn)
+        sel = np.empty((t, self.topk), np.int32)
+        w = np.empty((t, self.topk), np.float32)
+        self.dev._check(lib().rk_moe_ffn(self.h, _ptr(xn), t, _ptr(y), _ptr(sel), _ptr(w)))
+        return y, sel, w
+
+    def ffn_device(self, d_xn, tokens, d_y, stream=None):
+        self.dev._check(lib().rk_moe_ffn_device(self.h, P(d_xn), tokens, P(d_y), P(stream) if stream else None))
+
+    def bytes(self):
+        return lib().rk_moe_bytes(self.h)
+
+    def free(self):
+        if self.h:
+            self.dev._check(lib().rk_moe_free(self.h))
             self.h = None
 
 
