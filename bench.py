@@ -376,6 +376,87 @@ def prefill_bench(dev, rkhip, args):
     return out
 
 
+def moe_bench(dev, rkhip, args):
+    """Config 5's mixture-of-experts feed-forward (Qwen3-MoE shape: dim 2048,
+    128 Q8 experts of ffn 768, Q8 router, top 8) at batch 1 and 16: the
+    time of one layer's FFN, over distinct layers whose experts (604 MB
+    each) stream from HBM."""
+    dim, hidden, experts, topk = 2048, 768, 128, 8
+    nl = args.moe_layers
+    rng = np.random.default_rng(5)
+    pool = rng.integers(-127, 128, experts * hidden * dim + (1 << 20), dtype=np.int8)
+    spool = rng.uniform(1e-3, 1e-2, experts * hidden * dim // 32 + (1 << 16)).astype(np.float32)
+    mats = []
+
+    def mat(rows, cols, lo=1.0):
+        n = rows * cols
+        o = int(rng.integers(0, pool.size - n + 1))
+        so = int(rng.integers(0, spool.size - n // 32 + 1))
+        m = dev.upload_q8(pool[o:o + n], spool[so:so + n // 32] * np.float32(lo), rows, cols)
+        mats.append(m)
+        return m
+
+    t0 = time.perf_counter()
+    layers = []
+    for _ in range(nl):
+        router = mat(experts, dim, 0.3)
+        w1 = [mat(hidden, dim) for _ in range(experts)]
+        w3 = [mat(hidden, dim) for _ in range(experts)]
+        w2 = [mat(dim, hidden, 0.1) for _ in range(experts)]
+        layers.append(rkhip.Moe(dev, router, w1, w2, w3, topk))
+    log(f"moe bench: {nl} layers uploaded in {time.perf_counter() - t0:.1f} s")
+    expert_bytes = 3 * hidden * dim * 33 // 32
+    router_bytes = experts * dim * 33 // 32
+    out = {}
+    for batch in (1, 16):
+        x = rng.normal(0, 1, (batch, dim)).astype(np.float32)
+        arena = dev.arena(2 * batch * dim, batch * dim)
+        b = arena.begin()
+        b.write(0, x)
+        b.submit()
+        dx, dy = arena.device_ptr(0), arena.device_ptr(batch * dim)
+        # distinct experts a step streams (routing depends on the input only)
+        _, sel, _ = layers[0].ffn(x)
+        distinct = len(set(int(e) for e in sel.ravel()))
+        for m in layers:
+            m.ffn_device(dx, batch, dy)
+        dev.graph_begin()
+        for m in layers:
+            m.ffn_device(dx, batch, dy)
+        g = dev.graph_end()
+        g.launch(2)
+        reps = max(1, args.moe_reps)
+        t0 = time.perf_counter()
+        g.launch(reps)
+        el = time.perf_counter() - t0
+        ms_layer = el / (reps * nl) * 1e3
+        step_bytes = distinct * expert_bytes + router_bytes
+        dev.profile_start()
+        for m in layers:
+            m.ffn_device(dx, batch, dy)
+        arena.begin().submit()
+        prof = dev.profile_stop()
+        out[f"batch{batch}"] = {
+            "ms_per_layer": round(ms_layer, 4),
+            "ms_per_48_layers": round(ms_layer * 48, 3),
+            "tok_s_48_layer_ffn": round(batch / (ms_layer * 48 / 1e3), 1),
+            "distinct_experts": distinct,
+            "bytes_per_layer": step_bytes,
+            "effective_GB/s": round(step_bytes / (ms_layer / 1e3) / 1e9, 1),
+            "kernels_us_per_layer": {k: round(v[1] / nl * 1e3, 2) for k, v in prof.items()},
+        }
+        g.free()
+        arena.free()
+    for m in layers:
+        m.free()
+    for m in mats:
+        m.free()
+    return {"moe": {"config": f"config 5 MoE FFN: dim {dim}, {experts} Q8 experts of ffn {hidden}, Q8 router, top "
+                              f"{topk}; {nl} distinct layers replayed as one graph; router codes scaled so the routing "
+                              f"spreads; the 48-layer figures are {nl}-layer times x 48 (attention not included)",
+                    **out}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -390,6 +471,9 @@ def main():
     ap.add_argument("--decode", type=int, default=256)
     ap.add_argument("--eager", action="store_true", help="decode without graph replays (for profilers)")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--moe-layers", type=int, default=4)
+    ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--prefill-layers", type=int, default=28)
     ap.add_argument("--prefill-prompt", type=int, default=512)
     ap.add_argument("--prefill-decode", type=int, default=64)
@@ -429,6 +513,9 @@ def main():
     if not args.no_prefill:
         log("prefill bench (config 4)")
         result.update(prefill_bench(dev, rkhip, args))
+    if not args.no_moe:
+        log("moe bench (config 5)")
+        result.update(moe_bench(dev, rkhip, args))
     result["device"] = {"name": info.name.decode(), "arch": info.arch.decode(), "cu": info.compute_units}
     if not args.no_cpu:
         log("cpu baseline")
