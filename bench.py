@@ -327,6 +327,8 @@ def prefill_bench(dev, rkhip, args):
     st.set_head(embed, wcls, rng.normal(1, 0.1, dim).astype(np.float32))
     prompt = rng.integers(0, vocab, prompt_len).astype(np.int32)
     # warm-up (batch buffers, graphs), then the timed prompt and decode
+    if args.eager:  # one launch at a time (for tools that cannot follow graph replays)
+        dev.profile_start()
     st.generate_start(prompt)
     st.generate_run(prompt_len)
     st.generate_start(prompt)
@@ -337,6 +339,8 @@ def prefill_bench(dev, rkhip, args):
     t2 = time.perf_counter()
     st.generate_run(steps - 1)
     t3 = time.perf_counter()
+    if args.eager:
+        dev.profile_stop()
     # per-kernel times of the batched prompt, launches stamped one by one
     st.generate_start(prompt)
     dev.profile_start()
@@ -420,15 +424,25 @@ def moe_bench(dev, rkhip, args):
         distinct = len(set(int(e) for e in sel.ravel()))
         for m in layers:
             m.ffn_device(dx, batch, dy)
-        dev.graph_begin()
-        for m in layers:
-            m.ffn_device(dx, batch, dy)
-        g = dev.graph_end()
-        g.launch(2)
         reps = max(1, args.moe_reps)
-        t0 = time.perf_counter()
-        g.launch(reps)
-        el = time.perf_counter() - t0
+        g = None
+        if args.eager:  # launches one by one (for tools that cannot follow graph replays)
+            arena.begin().submit()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                for m in layers:
+                    m.ffn_device(dx, batch, dy)
+            arena.begin().submit()
+            el = time.perf_counter() - t0
+        else:
+            dev.graph_begin()
+            for m in layers:
+                m.ffn_device(dx, batch, dy)
+            g = dev.graph_end()
+            g.launch(2)
+            t0 = time.perf_counter()
+            g.launch(reps)
+            el = time.perf_counter() - t0
         ms_layer = el / (reps * nl) * 1e3
         step_bytes = distinct * expert_bytes + router_bytes
         dev.profile_start()
@@ -445,7 +459,8 @@ def moe_bench(dev, rkhip, args):
             "effective_GB/s": round(step_bytes / (ms_layer / 1e3) / 1e9, 1),
             "kernels_us_per_layer": {k: round(v[1] / nl * 1e3, 2) for k, v in prof.items()},
         }
-        g.free()
+        if g:
+            g.free()
         arena.free()
     for m in layers:
         m.free()

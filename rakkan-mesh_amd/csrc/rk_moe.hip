@@ -14,7 +14,8 @@
 //
 // Launches: the input quantized once; the router's product; the routing
 // (one workgroup per token); the selected experts' W1/W3 rows with the
-// gate and weight; h quantized; their W2 rows; the ascending-order sum.
+// gate and weight, h quantized in the same workgroup; their W2 rows; the
+// ascending-order sum.
 // Every expert product is a row dot of MatVecQ8 (integer block sums, the
 // eight ordered running sums), so each token's bits do not depend on the
 // batch.
@@ -38,7 +39,7 @@ struct rk_moe {
     // scratch for up to `cap` tokens
     int cap = 0;
     void *mem = nullptr;
-    float *x = nullptr, *logits = nullptr, *wsel = nullptr, *h = nullptr, *o = nullptr, *y = nullptr;
+    float *x = nullptr, *logits = nullptr, *wsel = nullptr, *o = nullptr, *y = nullptr;
     int32_t *sel = nullptr;
     int8_t *qx = nullptr, *hq = nullptr;
     float *xs = nullptr, *hs = nullptr;
@@ -55,37 +56,30 @@ constexpr int kMoeMaxExperts = 1024;
 constexpr int kMoeMaxCols = 8192;   // widest expert input (chunks of 1 KiB per row)
 constexpr int kMoeRows = 4;         // rows per wave in the expert kernels
 
-// Go's cmp.Compare(x, y) > 0 on float32: NaN below every number, NaNs
-// equal, -0 == +0.
-__device__ __forceinline__ bool cmp_above(float x, float y) {
-    const bool xn = x != x, yn = y != y;
-    if (xn || yn) return yn && !xn;
-    return x > y;
-}
-
-// Four Q8 rows dotted with one quantized input (MatVecQ8's order per row:
+// NR Q8 rows dotted with one quantized input (MatVecQ8's order per row:
 // exact block sums; block b into running sum b mod 8 in order of b; the
 // fixed tree). Lane 0 returns the results. Every lane of the wave calls it.
-__device__ __forceinline__ void wave_rows_q8(const uint8_t *const (&w)[kMoeRows], const float *const (&ws)[kMoeRows],
-                                             const int8_t *qx, const float *xs, int cols, float (&res)[kMoeRows]) {
+template <int NR>
+__device__ __forceinline__ void wave_rows_q8(const uint8_t *const (&w)[NR], const float *const (&ws)[NR],
+                                             const int8_t *qx, const float *xs, int cols, float (&res)[NR]) {
     const int lane = threadIdx.x & 63;
     const int nb = cols >> 5, C = (cols + 1023) >> 10;
-    float acc[kMoeRows];
+    float acc[NR];
 #pragma unroll
-    for (int r = 0; r < kMoeRows; r++) acc[r] = 0.0f;
+    for (int r = 0; r < NR; r++) acc[r] = 0.0f;
     for (int c = 0; c < C; c++) {
         const int o = min(c * 1024 + lane * 16, cols - 16);  // lanes past the row's end: blocks excluded below
         const int4 xv = *reinterpret_cast<const int4 *>(qx + o);
         const float sx = xs[o >> 5];
-        int4 wv[kMoeRows];
-        float sw[kMoeRows];
+        int4 wv[NR];
+        float sw[NR];
 #pragma unroll
-        for (int r = 0; r < kMoeRows; r++) {
+        for (int r = 0; r < NR; r++) {
             wv[r] = load_stream16(w[r] + o);
             sw[r] = ws[r][o >> 5];
         }
 #pragma unroll
-        for (int r = 0; r < kMoeRows; r++) {
+        for (int r = 0; r < NR; r++) {
             const int s = pair_sum(dot16(wv[r], xv, 0));
             const float t = (float)s * (sw[r] * sx);
             // block 32c+k is in lanes 2k, 2k+1; running sum L (lane 2L) takes
@@ -101,19 +95,63 @@ __device__ __forceinline__ void wave_rows_q8(const uint8_t *const (&w)[kMoeRows]
         }
     }
 #pragma unroll
-    for (int r = 0; r < kMoeRows; r++) {
+    for (int r = 0; r < NR; r++) {
         const float p2 = acc[r] + __shfl_down(acc[r], 2);
         const float q4 = p2 + __shfl_down(p2, 4);
         res[r] = q4 + __shfl_down(q4, 8);
     }
 }
 
-// Routing of one token per workgroup (64 threads): softmax, stable top-k,
+// 64-bit key of probability v at expert e for a max-reduction that picks
+// what a stable sort by cmp.Compare puts first: order-preserving value bits
+// above (-0 as +0; NaN lowest of all), the complement of the index below.
+// Never 0, so 0 marks a taken entry.
+__device__ __forceinline__ unsigned long long route_key(float v, int e) {
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    if (v != v) u = 0;
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)e);
+}
+
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long k, int ctrl_tag) {
+    uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    switch (ctrl_tag) {  // the DPP control must be a constant
+        case 0: lo = __builtin_amdgcn_mov_dpp(lo, 0xB1, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0xB1, 0xF, 0xF, false); break;
+        case 1: lo = __builtin_amdgcn_mov_dpp(lo, 0x4E, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0x4E, 0xF, 0xF, false); break;
+        case 2: lo = __builtin_amdgcn_mov_dpp(lo, 0x141, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0x141, 0xF, 0xF, false); break;
+        default: lo = __builtin_amdgcn_mov_dpp(lo, 0x140, 0xF, 0xF, false); hi = __builtin_amdgcn_mov_dpp(hi, 0x140, 0xF, 0xF, false); break;
+    }
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// Largest key over the wave, valid in every lane: rows of 16 by DPP, then
+// the four rows by readlane. Every lane of the wave must call it.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const unsigned long long o = dpp_u64(k, c);
+        k = o > k ? o : k;
+    }
+    unsigned long long best = 0;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)k, 16 * r);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(k >> 32), 16 * r);
+        const unsigned long long v = ((unsigned long long)hi << 32) | lo;
+        best = v > best ? v : best;
+    }
+    return best;
+}
+
+constexpr int kRoutePer = kMoeMaxExperts / 64;  // experts per lane at most
+
+// Routing of one token per workgroup (one wave): softmax, stable top-k,
 // normalized weights.
 __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int experts, int k, int32_t *sel,
                                                        float *wsel) {
     extern __shared__ float sp[];  // [experts] probabilities
     __shared__ float s_inv;
+    __shared__ int s_sel[kMoeMaxK];
     const int t = blockIdx.x, lane = threadIdx.x;
     const float *z = logits + (int64_t)t * experts;
     float m = z[0];
@@ -127,34 +165,29 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
     if (lane == 0) s_inv = recip32(lds_chain_sum(sp, experts, 0.0f));
     __syncthreads();
     const float inv = s_inv;
-    for (int e = lane; e < experts; e += 64) sp[e] = sp[e] * inv;
-    __syncthreads();
-    // top-k: k rounds of "first index no remaining value compares above"
-    __shared__ int s_sel[kMoeMaxK];
-    for (int r = 0; r < k; r++) {
-        float bv = 0.0f;
-        int bi = -1;
-        for (int e = lane; e < experts; e += 64) {
-            bool taken = false;
-            for (int q = 0; q < r; q++) taken |= s_sel[q] == e;
-            if (taken) continue;
-            const float v = sp[e];
-            if (bi < 0 || cmp_above(v, bv)) {  // e ascends: ties keep the lower index
-                bv = v;
-                bi = e;
-            }
+    unsigned long long key[kRoutePer];
+#pragma unroll
+    for (int j = 0; j < kRoutePer; j++) {
+        const int e = lane + 64 * j;
+        key[j] = 0;
+        if (e < experts) {
+            const float p = sp[e] * inv;
+            sp[e] = p;
+            key[j] = route_key(p, e);
         }
-        for (int off = 1; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(bv, off);
-            const int oi = __shfl_xor(bi, off);
-            if (oi >= 0 && (bi < 0 || cmp_above(ov, bv) || (!cmp_above(bv, ov) && oi < bi))) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        if (lane == 0) s_sel[r] = bi;
-        __syncthreads();
     }
+    // top-k: k rounds of the largest remaining key
+    for (int r = 0; r < k; r++) {
+        unsigned long long b = 0;
+#pragma unroll
+        for (int j = 0; j < kRoutePer; j++) b = key[j] > b ? key[j] : b;
+        b = wave_max_u64(b);
+#pragma unroll
+        for (int j = 0; j < kRoutePer; j++)
+            if (key[j] == b) key[j] = 0;
+        if (lane == 0) s_sel[r] = (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+    }
+    __syncthreads();
     if (lane == 0) {
         float sum = 0.0f;
         for (int r = 0; r < k; r++) sum += sp[s_sel[r]];
@@ -167,35 +200,53 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
     }
 }
 
-// W1 and W3 rows of each (token, slot)'s expert: h = w·(silu(W1·xn)·(W3·xn)).
-// Workgroup (pair, block of 8 hidden rows); wave w takes hidden rows 2w, 2w+1
-// (W1 and W3 of each: four row dots).
-__global__ __launch_bounds__(256) void moe_up_kernel(const uint8_t *const *w1, const float *const *s1,
+// W1 and W3 rows of each (token, slot)'s expert: h = w·(silu(W1·xn)·(W3·xn)),
+// then h's Q8_0 block. Workgroup (pair, block of 32 hidden rows), eight
+// waves of four hidden rows (W1 and W3 of each: eight row dots).
+constexpr int kUpRows = 8;
+__global__ __launch_bounds__(512) void moe_up_kernel(const uint8_t *const *w1, const float *const *s1,
                                                      const uint8_t *const *w3, const float *const *s3,
                                                      const int32_t *sel, const float *wsel, int k, const int8_t *qx,
-                                                     const float *xs, int dim, int hidden, float *h) {
+                                                     const float *xs, int dim, int hidden, int8_t *hq, float *hs,
+                                                     int32_t *hsum) {
+    __shared__ __align__(16) float sh[32];
     const int pr = blockIdx.x, t = pr / k;
     const int e = sel[pr];
     const float wt = wsel[pr];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int j0 = blockIdx.y * 8 + 2 * wave;  // hidden rows j0, j0 + 1
+    const int j0 = blockIdx.y * 32 + 4 * wave;  // hidden rows j0 .. j0+3
     const int nb = dim >> 5;
-    const uint8_t *w[kMoeRows];
-    const float *ws[kMoeRows];
+    const uint8_t *w[kUpRows];
+    const float *ws[kUpRows];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
-        const int j = min(j0 + q, hidden - 1);
+    for (int q = 0; q < 4; q++) {
+        const int j = j0 + q;  // hidden is a multiple of 32
         w[2 * q] = w1[e] + (int64_t)j * dim;
         ws[2 * q] = s1[e] + (int64_t)j * nb;
         w[2 * q + 1] = w3[e] + (int64_t)j * dim;
         ws[2 * q + 1] = s3[e] + (int64_t)j * nb;
     }
-    float res[kMoeRows];
-    wave_rows_q8(w, ws, qx + (int64_t)t * dim, xs + (int64_t)t * nb, dim, res);
+    float res[kUpRows];
+    wave_rows_q8<kUpRows>(w, ws, qx + (int64_t)t * dim, xs + (int64_t)t * nb, dim, res);
     if (lane == 0) {
 #pragma unroll
-        for (int q = 0; q < 2; q++)
-            if (j0 + q < hidden) h[(int64_t)pr * hidden + j0 + q] = wt * silu_mul(res[2 * q], res[2 * q + 1]);
+        for (int q = 0; q < 4; q++) sh[4 * wave + q] = wt * silu_mul(res[2 * q], res[2 * q + 1]);
+    }
+    __syncthreads();
+    if (wave == 0) {  // the block of h: lanes 0-7, four values each
+        const int g = min(lane, 7);
+        const float4 v4 = reinterpret_cast<const float4 *>(sh)[g];
+        float d;
+        int cs;
+        const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
+        const int64_t base = (int64_t)pr * hidden + blockIdx.y * 32;
+        if (lane < 8) {
+            reinterpret_cast<uint32_t *>(hq + base)[lane] = pk;
+            if (lane == 0) {
+                hs[base >> 5] = d;
+                hsum[base >> 5] = cs;
+            }
+        }
     }
 }
 
@@ -218,7 +269,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t *const *w2,
         ws[r] = s2[e] + (int64_t)i * nb;
     }
     float res[kMoeRows];
-    wave_rows_q8(w, ws, hq + (int64_t)pr * hidden, hs + (int64_t)pr * nb, hidden, res);
+    wave_rows_q8<kMoeRows>(w, ws, hq + (int64_t)pr * hidden, hs + (int64_t)pr * nb, hidden, res);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < kMoeRows; r++)
@@ -265,7 +316,7 @@ static int moe_scratch(rk_moe *m, int tokens) {
         {(void **)&m->x, 4 * T * D},          {(void **)&m->qx, T * D},
         {(void **)&m->xs, 4 * T * (D / 32)},  {(void **)&m->xsum, 4 * T * (D / 32)},
         {(void **)&m->logits, 4 * T * E},     {(void **)&m->sel, 4 * T * K},
-        {(void **)&m->wsel, 4 * T * K},       {(void **)&m->h, 4 * T * K * H},
+        {(void **)&m->wsel, 4 * T * K},
         {(void **)&m->hq, T * K * H},         {(void **)&m->hs, 4 * T * K * (H / 32)},
         {(void **)&m->hsum, 4 * T * K * (H / 32)}, {(void **)&m->o, 4 * T * K * D},
         {(void **)&m->y, 4 * T * D}};
@@ -325,12 +376,8 @@ static int enqueue_moe(rk_moe *m, const float *d_xn, int tokens, float *d_y, hip
     const unsigned pairs = (unsigned)(tokens * K);
     {
         ProfScope p(d, s, "moe_up");
-        RK_LAUNCH(moe_up_kernel, dim3(pairs, (unsigned)((H + 7) / 8)), dim3(256), 0, s, m->w1, m->s1, m->w3, m->s3,
-                  m->sel, m->wsel, K, m->qx, m->xs, D, H, m->h);
-    }
-    {
-        ProfScope p(d, s, "quantize_acts");
-        launch_quantize_acts(m->h, (int64_t)pairs * H, m->hq, m->hs, m->hsum, s);
+        RK_LAUNCH(moe_up_kernel, dim3(pairs, (unsigned)(H / 32)), dim3(512), 0, s, m->w1, m->s1, m->w3, m->s3, m->sel,
+                  m->wsel, K, m->qx, m->xs, D, H, m->hq, m->hs, m->hsum);
     }
     {
         ProfScope p(d, s, "moe_down");
