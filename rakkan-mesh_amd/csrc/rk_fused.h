@@ -17,7 +17,11 @@ enum : int32_t { kFmtQ8 = 0, kFmtQ4 = 1 };
 enum : int32_t {
     kProGlobal = 0,  // already quantized (qx, xs, xsum), read from HBM/L2
     kProQuant = 1,   // f32 x, quantized by each workgroup into LDS
+    kProNorm = 2,    // f32 x, RMSNorm'd with norm_w and quantized by each workgroup into LDS
 };
+
+// Widest input the RMSNorm prologue takes (x transposed in LDS beside the codes).
+constexpr int kMaxNormProCols = 8192;
 
 // What is done with each output row.
 enum : int32_t {
@@ -60,7 +64,9 @@ struct FusedArgs {
     int32_t rows_per_wg;  // set by the launcher
     int32_t row_base;     // kEpQKV: logical index of row 0 (a Q/K/V split over two launches)
     // input
-    const float *x;       // f32 input (kProQuant)
+    const float *x;       // f32 input (kProQuant, kProNorm)
+    const float *norm_w;  // kProNorm: RMSNorm weights (internal/llm/model.go:632-638)
+    float recip_n, norm_eps;
     const int8_t *qx;     // quantized input (kProGlobal)
     const float *xs;
     const int32_t *xsum;
@@ -76,7 +82,7 @@ struct FusedArgs {
     float *xs_out;
     int32_t *xsum_out;
     // LDS layout (bytes), set by the launcher
-    int32_t lds_xs, lds_xsum, lds_res, lds_ep, lds_bytes;
+    int32_t lds_xs, lds_xsum, lds_norm, lds_res, lds_ep, lds_bytes;
 };
 
 // Whether the LDS prologue (kProQuant) takes an input of `cols`.

@@ -75,6 +75,9 @@ __device__ __forceinline__ RowSrc row_src(const FusedArgs &a, int l, int rowbyte
 // the next product. Thread t holds groups g = t + k·NT (four values each)
 // of x and w in registers, loaded before the call; sx is LDS for n floats.
 // Every thread of the NT-thread workgroup calls it.
+// LDS of wg_norm_quant for n values: x transposed, 32 rows of the pitch.
+static size_t norm_lds(int n) { return (size_t)32 * ((((n >> 5) + 3) & ~3) + 4) * 4; }
+
 template <int NT, int MAXG>
 __device__ void wg_norm_quant(const float4 *xv, const float4 *wv, int n, float recip_n, float eps, int8_t *qx,
                               float *xs, int32_t *xsum, float *sx, float *bcast) {
@@ -131,7 +134,10 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
     // output being added to, or the row's bias
     constexpr bool PRE = (EPI == kEpAdd || EPI == kEpAddCanon || EPI == kEpStore || EPI == kEpQKV);
     constexpr int NT = 64 * W;
-    constexpr int MAXG = PRO == kProGlobal ? 1 : (kMaxLdsCols / 4 + NT - 1) / NT;
+    constexpr int MAXG = PRO == kProGlobal ? 1
+                         : PRO == kProNorm ? (kMaxNormProCols / 4 + NT - 1) / NT
+                                           : (kMaxLdsCols / 4 + NT - 1) / NT;
+    __shared__ float s_rn;  // kProNorm: the broadcast Rsqrt32
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cols = a.cols, nb = cols >> 5;
     const int rowbytes = FMT == kFmtQ8 ? cols : cols >> 1;
@@ -188,13 +194,14 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
 
         // ---- (1) loads the prologue needs: the input (and norm weights),
         // the rows' epilogue operands, the rotary row ----
-        float4 xv[MAXG];
+        float4 xv[MAXG], wv[MAXG];
         if (PRO != kProGlobal) {
             const int ng = cols >> 2;
 #pragma unroll
             for (int k = 0; k < MAXG; k++) {
                 const int g = min((int)threadIdx.x + k * NT, ng - 1);
                 xv[k] = reinterpret_cast<const float4 *>(a.x)[g];
+                if (PRO == kProNorm) wv[k] = reinterpret_cast<const float4 *>(a.norm_w)[g];
             }
         }
         float epv = 0.0f, cosv = 0.0f, sinv = 0.0f;
@@ -271,7 +278,12 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
                 sep[a.rows_per_wg + half + threadIdx.x] = sinv;
             }
         }
-        if (PRO != kProGlobal) {
+        if (PRO == kProNorm) {
+            // RMSNorm (Dot32 over x held transposed, Rsqrt32) and the Q8 of
+            // w·(r·x), as the stand-alone norm kernel computes it
+            wg_norm_quant<NT, MAXG>(xv, wv, cols, a.recip_n, a.norm_eps, sqx, sxs, sxsum,
+                                    reinterpret_cast<float *>(lds + a.lds_norm), &s_rn);
+        } else if (PRO == kProQuant) {
 #pragma unroll
             for (int k = 0; k < MAXG; k++) {
                 const int g = threadIdx.x + k * NT;
@@ -479,7 +491,7 @@ __global__ __launch_bounds__(64 * W) void fused_kernel(FusedArgs a) {
 // evenly, pairs kept whole) and the LDS layout.
 
 // Chunks in flight per wave: 2 when the input comes quantized, 4 to cover
-// an LDS prologue (measured).
+// an LDS prologue (measured; 6 under the RMSNorm prologue measured slower).
 template <int FMT, int PRO, int EPI, int W>
 static void launch_one(const FusedArgs &a, unsigned grid, size_t lds, hipStream_t s) {
     RK_LAUNCH((fused_kernel<FMT, PRO, EPI, W, PRO == kProGlobal ? 2 : 4>), dim3(grid), dim3(64 * W), lds, s, a);
@@ -503,6 +515,7 @@ static bool launch_pro(int pro, int epi, const FusedArgs &a, unsigned grid, size
     switch (pro) {
         case kProGlobal: return launch_epi<FMT, kProGlobal, W>(epi, a, grid, lds, s);
         case kProQuant: return launch_epi<FMT, kProQuant, W>(epi, a, grid, lds, s);
+        case kProNorm: return launch_epi<FMT, kProNorm, W>(epi, a, grid, lds, s);
     }
     return false;
 }
@@ -520,6 +533,10 @@ static void lds_layout(FusedArgs &a, int pro, int epi) {
         a.lds_xsum = a.lds_xs + align16(nb * 4);
         at = a.lds_xsum + align16(nb * 4);
     }
+    if (pro == kProNorm) {  // x transposed for Dot32 (wg_norm_quant)
+        a.lds_norm = at;
+        at += (int)norm_lds(cols);
+    }
     a.lds_res = at;
     at += align16(a.rows_per_wg * 4);
     a.lds_ep = at;
@@ -534,7 +551,7 @@ constexpr int kMaxRowsPerWg = 512;
 bool fused_fits(int pro, int cols) {
     if (cols <= 0 || cols % 32 != 0) return false;
     if (pro == kProGlobal) return true;
-    if (cols > kMaxLdsCols) return false;
+    if (cols > (pro == kProNorm ? kMaxNormProCols : kMaxLdsCols)) return false;
     FusedArgs a{};
     a.cols = cols;
     a.rows_per_wg = kMaxRowsPerWg;
@@ -559,7 +576,7 @@ bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s)
     if (pro == kProGlobal) {
         w16 = a.rows > 5000 && a.rows < 20000;
         per_cu = w16 ? 1 : 2;
-    } else {
+    } else {  // an LDS prologue (quantize, or RMSNorm and quantize)
         w16 = a.rows <= 8192;
         per_cu = w16 ? 1 : 2;
     }
@@ -910,8 +927,6 @@ void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q
 // every load is issued before the first use.
 constexpr int kNormThreads = 1024;
 
-// LDS of wg_norm_quant for n values: x transposed, 32 rows of the pitch.
-static size_t norm_lds(int n) { return (size_t)32 * ((((n >> 5) + 3) & ~3) + 4) * 4; }
 constexpr int kNormGroups = (kMaxNormCols / 4 + kNormThreads - 1) / kNormThreads;
 
 __global__ __launch_bounds__(kNormThreads) void embed_norm_kernel(const uint8_t *w, const float *scales, int q4,

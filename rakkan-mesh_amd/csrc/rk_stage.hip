@@ -2,17 +2,17 @@
 // (internal/llm/gpustage.go), and the greedy generation loop around them
 // (embedding, head, argmax) with its state on the device.
 //
-// A token runs as eight launches per layer, every product reading its input
-// already quantized (Q8_0 codes, block scales, block code sums):
-//   qkv      [Wq;Wk;Wv]·xn (+bias), RoPE, k and v into the caches
+// A token runs as six launches per layer; each product takes its input
+// quantized, or normalizes and quantizes it in its own prologue:
+//   qkv      xn = RMSNorm_att(x) (prologue; layer 0: the embedding kernel's),
+//            [Wq;Wk;Wv]·xn (+bias), RoPE, k and v into the caches
 //            (Qwen3: raw q/k/v, then qknorm_rope)
 //   scores   Dot32(q_h, k_t)·invSqrt for t <= position
 //   values   softmax, Σ a_t·v_t, quantized
 //   wo       x += Wo·att
-//   norm     xn = RMSNorm_ffn(x), quantized
-//   w13      h = silu(W1·xn)·(W3·xn), quantized
+//   w13      xn = RMSNorm_ffn(x) (prologue), h = silu(W1·xn)·(W3·xn), quantized
 //   w2       x = Canonical(x + W2·h)
-//   norm     xn = RMSNorm of the next layer (or the head), quantized
+// and the head's norm runs in the classifier's prologue.
 // in the order and rounding of Stage.Forward (internal/llm/model.go:522-613).
 // Generation embeds the position's token first (and RMSNorms it for the
 // first layer) and ends with the classifier and the greedy argmax, which
@@ -77,9 +77,10 @@ static int fmt_of(const rk_matrix *m) { return m->kind == RK_Q4 ? kFmtQ4 : kFmtQ
 
 // One product of a stage: matrices ms[0..n) of one format, epilogue epi;
 // input quantized in q, or (q null) f32 `in` quantized by the product's own
-// prologue (or, too wide for that, by a separate launch into s->qx).
+// prologue, RMSNorm'd with `norm` first when given (or, too wide for that,
+// by a separate launch into s->qx).
 static int stage_product(rk_stage *s, hipStream_t st, const char *name, const QScratch *q, const float *in,
-                         rk_matrix *const *ms, int n, float *const *outs, int epi, FusedArgs a) {
+                         const float *norm, rk_matrix *const *ms, int n, float *const *outs, int epi, FusedArgs a) {
     rk_device *d = s->d;
     const int cols = (int)ms[0]->cols;
     const int fmt = fmt_of(ms[0]);
@@ -96,11 +97,20 @@ static int stage_product(rk_stage *s, hipStream_t st, const char *name, const QS
         a.qx = q->qx;
         a.xs = q->xs;
         a.xsum = q->xsum;
-    } else if (fused_fits(kProQuant, cols)) {
+    } else if (norm && fused_fits(kProNorm, cols)) {
+        pro = kProNorm;
+        a.x = in;
+        a.norm_w = norm;
+        a.recip_n = s->c.recip_dim;
+        a.norm_eps = s->c.norm_eps;
+    } else if (!norm && fused_fits(kProQuant, cols)) {
         pro = kProQuant;
         a.x = in;
     } else {
-        {
+        if (norm) {
+            ProfScope p(d, st, "norm_quant");
+            launch_norm_quant(in, cols, norm, s->c.recip_dim, s->c.norm_eps, s->qx, s->xs, s->xsum, st);
+        } else {
             ProfScope p(d, st, "quantize_acts");
             launch_quantize_acts(in, cols, s->qx, s->xs, s->xsum, st);
         }
@@ -117,17 +127,10 @@ static int stage_product(rk_stage *s, hipStream_t st, const char *name, const QS
     return RK_OK;
 }
 
-// RMSNorm(x) with w, quantized into qb: the next product's input.
-static void norm_into_qb(rk_stage *s, hipStream_t st, const float *w) {
-    if (!w) return;
-    ProfScope p(s->d, st, "norm_quant");
-    launch_norm_quant(s->x, s->c.dim, w, s->c.recip_dim, s->c.norm_eps, s->qb.qx, s->qb.xs, s->qb.xsum, st);
-}
-
-// The launches of one layer (Stage.Forward's body, model.go:530-611). On
-// entry qb holds RMSNorm_att(x) quantized; next_norm is the norm whose
-// input qb must hold on exit (the next layer's, the head's, or none).
-static int enqueue_layer(rk_stage *s, int li, hipStream_t st, const float *next_norm) {
+// The launches of one layer (Stage.Forward's body, model.go:530-611). The
+// norms run in the prologues of the products that read them (QKV: the
+// attention norm, unless qb already holds it; W1/W3: the ffn norm).
+static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
     rk_device *d = s->d;
     const rk_stage_config &c = s->c;
     const rk_stage_layer &L = s->layers[li];
@@ -153,7 +156,9 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, const float *next_
             FusedArgs a = base;
             a.row_base = row;  // the epilogue indexes q/k/v rows and biases by row_base + row
             float *outs[3] = {i == 0 ? s->q : nullptr, nullptr, nullptr};  // only q rows store through seg[0]
-            if ((rc = stage_product(s, st, "qkv", &s->qb, nullptr, qkv + i, j - i, outs, kEpQKV, a))) return rc;
+            if ((rc = stage_product(s, st, "qkv", qb_ready ? &s->qb : nullptr, s->x, qb_ready ? nullptr : D.rms_att,
+                                    qkv + i, j - i, outs, kEpQKV, a)))
+                return rc;
             for (int t = i; t < j; t++) row += (int)qkv[t]->rows;
             i = j;
         }
@@ -167,7 +172,8 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, const float *next_
             int row = 0;
             for (int t = 0; t < i; t++) row += (int)qkv[t]->rows;
             a.bias = D.bias ? D.bias + row : nullptr;
-            if ((rc = stage_product(s, st, "qkv", &s->qb, nullptr, qkv + i, j - i, outs + i, kEpStore, a)))
+            if ((rc = stage_product(s, st, "qkv", qb_ready ? &s->qb : nullptr, s->x, qb_ready ? nullptr : D.rms_att,
+                                    qkv + i, j - i, outs + i, kEpStore, a)))
                 return rc;
             i = j;
         }
@@ -189,9 +195,8 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, const float *next_
                           s->kvdim, att_q ? s->qa.qx : nullptr, s->qa.xs, s->qa.xsum, st);
     }
     float *xo[1] = {s->x};
-    if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, &L.wo, 1, xo, kEpAdd, base)))
+    if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, nullptr, &L.wo, 1, xo, kEpAdd, base)))
         return rc;
-    norm_into_qb(s, st, D.rms_ffn);
     // W1 row r and W3 row r interleaved (logical rows); h leaves quantized in qa.
     rk_matrix *w13[2] = {L.w1, L.w3};
     float *ho[2] = {s->h, nullptr};
@@ -199,30 +204,26 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, const float *next_
     a13.qx_out = s->qa.qx;
     a13.xs_out = s->qa.xs;
     a13.xsum_out = s->qa.xsum;
-    if ((rc = stage_product(s, st, "w13", &s->qb, nullptr, w13, 2, ho, kEpSilu, a13))) return rc;
-    if ((rc = stage_product(s, st, "w2", &s->qa, nullptr, &L.w2, 1, xo, kEpAddCanon, base))) return rc;
-    norm_into_qb(s, st, next_norm);
+    if ((rc = stage_product(s, st, "w13", nullptr, s->x, D.rms_ffn, w13, 2, ho, kEpSilu, a13))) return rc;
+    if ((rc = stage_product(s, st, "w2", &s->qa, nullptr, nullptr, &L.w2, 1, xo, kEpAddCanon, base))) return rc;
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(d, e, "stage launch");
     return RK_OK;
 }
 
-// All layers; on entry qb holds the first layer's normed input. `last_norm`
-// is the head's norm (generation) or null (a stage's forward).
-static int enqueue_layers(rk_stage *s, hipStream_t st, const float *last_norm) {
+// All layers on x; qb_ready: qb already holds the first layer's normed
+// input (the embedding kernel's).
+static int enqueue_layers(rk_stage *s, hipStream_t st, bool qb_ready) {
     const int n = (int)s->layers.size();
     for (int li = 0; li < n; li++) {
-        int rc = enqueue_layer(s, li, st, li + 1 < n ? s->ld[li + 1].rms_att : last_norm);
+        int rc = enqueue_layer(s, li, st, li == 0 && qb_ready);
         if (rc) return rc;
     }
     return RK_OK;
 }
 
 // Layers on the activation the host wrote to x.
-static int enqueue_forward(rk_stage *s, hipStream_t st) {
-    norm_into_qb(s, st, s->ld[0].rms_att);
-    return enqueue_layers(s, st, nullptr);
-}
+static int enqueue_forward(rk_stage *s, hipStream_t st) { return enqueue_layers(s, st, false); }
 
 // One generation step: embed the position's token, the layers, the head.
 static int enqueue_token(rk_stage *s, hipStream_t st) {
@@ -232,14 +233,14 @@ static int enqueue_token(rk_stage *s, hipStream_t st) {
         launch_embed_norm(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->tokens, s->ctl, s->c.dim, s->x,
                           s->ld[0].rms_att, s->c.recip_dim, s->c.norm_eps, s->qb.qx, s->qb.xs, s->qb.xsum, st);
     }
-    int rc = enqueue_layers(s, st, s->rms_final);
+    int rc = enqueue_layers(s, st, true);
     if (rc) return rc;
     FusedArgs a{};
     a.ctl = s->ctl;
     a.amax = s->amax;
     a.gate = 1;
     float *lo[1] = {s->logits};
-    if ((rc = stage_product(s, st, "logits", &s->qb, nullptr, &s->wcls, 1, lo, kEpLogits, a))) return rc;
+    if ((rc = stage_product(s, st, "logits", nullptr, s->x, s->rms_final, &s->wcls, 1, lo, kEpLogits, a))) return rc;
     ProfScope p(d, st, "advance");
     launch_advance(s->ctl, s->amax, s->tokens, s->c.ctx + 1, st);
     return RK_OK;
