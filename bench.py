@@ -168,7 +168,7 @@ def matvec_bench(dev, rkhip, args):
         "data": "synthetic: Q8_0 codes U[-127,127], scales U(1e-3,1e-2), x N(0,1); weights rotated over "
                 f"{args.sets} HBM copies ({args.sets * step_bytes / 1e6:.0f} MB)",
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "matvec_q8",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": pmc_traffic(), "kernel": "matvec_q8",
                      "avg_launch_us": round(avg_launch_ms * 1e3, 3), "bytes_per_launch": bytes_per_launch},
         "per_shape": per_shape,
         "kernels_ms": {k: [v[0], round(v[1], 4)] for k, v in prof.items()},
@@ -182,6 +182,57 @@ def matvec_bench(dev, rkhip, args):
         for m in st:
             m.free()
     return out, (q_all, s_all, xs, gpu_outs)
+
+
+PMC_COPY_WORDS = 1 << 26  # the calibration copy: 256 MiB read, 256 MiB written
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "q8_matvec_config2_pmc.md")
+
+
+def pmc_pass(dev, rkhip, args):
+    """What the PMC runs count (rocprofv3 --pmc FETCH_SIZE, then
+    WRITE_SIZE): each config-2 product as rk_matvecs_device runs it,
+    `steps` times over the rotated weight copies, then one copy kernel of
+    PMC_COPY_WORDS words, whose counters against its known bytes give the
+    scale of each counter."""
+    rng = np.random.default_rng(1)
+    sets = []
+    for _ in range(args.sets):
+        sets.append([dev.upload_q8(rng.integers(-127, 128, r * c, dtype=np.int8),
+                                   rng.uniform(1e-3, 1e-2, r * c // 32).astype(np.float32), r, c) for r, c in SHAPES])
+    at, offs = 0, []
+    for r, c in SHAPES:
+        offs.append((at, at + c))
+        at += r + c
+    arena = dev.arena(max(at, 2 * PMC_COPY_WORDS), sum(c for _, c in SHAPES))
+    b = arena.begin()
+    for (xo, _), (r, c) in zip(offs, SHAPES):
+        b.write(xo, rng.normal(0, 1, c).astype(np.float32))
+    b.submit()
+    for st in range(args.steps):
+        for i, (r, c) in enumerate(SHAPES):
+            xo, oo = offs[i]
+            dev.matvecs_device([sets[st % args.sets][i]], [arena.device_ptr(oo)], arena.device_ptr(xo), c)
+    arena.begin().submit()
+    b = arena.begin()
+    b.copy(0, PMC_COPY_WORDS, PMC_COPY_WORDS)
+    b.submit()
+    arena.free()
+    for st in sets:
+        for m in st:
+            m.free()
+    log(f"pmc pass: {args.steps} x {len(SHAPES)} products, one copy of {PMC_COPY_WORDS} words")
+
+
+def pmc_traffic():
+    """HBM bytes per matvec_q8 launch from the committed PMC summary (the
+    `traffic_bytes_per_launch` line), or None."""
+    try:
+        for line in open(PMC_SUMMARY):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def rope_table(theta, hs, n):
@@ -485,6 +536,8 @@ def main():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--decode", type=int, default=256)
     ap.add_argument("--eager", action="store_true", help="decode without graph replays (for profilers)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="only the launches the PMC runs count (config-2 products and a calibration copy)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--moe-layers", type=int, default=4)
@@ -502,6 +555,10 @@ def main():
 
     dev = rkhip.Device(0)
     info = rkhip.device_info(0)
+    if args.pmc_pass:
+        pmc_pass(dev, rkhip, args)
+        dev.close()
+        return
     log("matvec bench (config 2)")
     mv, (q_all, s_all, xs, gpu_outs) = matvec_bench(dev, rkhip, args)
     result = {
