@@ -585,8 +585,11 @@ bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s)
     if (rpw > kMaxRowsPerWg) rpw = kMaxRowsPerWg;
     if (pair) rpw = (rpw + 1) & ~(int64_t)1;
     if (epi == kEpSilu && a.qx_out) {
+        // whole Q8 blocks of h per workgroup: 64 interleaved rows (32 of h)
+        // each, as many workgroups as that gives (rounding up to 128 rows
+        // left too few workgroups to keep the weight stream busy)
         if (a.rows % 64 != 0) return false;
-        rpw = (rpw + 63) & ~(int64_t)63;
+        rpw = 64;
     }
     a.rows_per_wg = (int32_t)rpw;
     const unsigned grid = (unsigned)((a.rows + rpw - 1) / rpw);
