@@ -90,8 +90,16 @@ bool fused_fits(int pro, int cols);
 
 // Enqueues one fused product. fmt: kFmtQ8/kFmtQ4; returns false when the
 // shape does not fit the kernel (cols beyond kMaxLdsCols with an LDS
-// prologue, or too many workgroups for the argmax partials).
+// prologue, or too many workgroups for the argmax partials). Widths with a
+// static-schedule instance (rk_stream.hip) run there, the others in
+// fused_kernel; the results are the same.
 bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s);
+
+// The static-schedule products (rk_stream.hip): false when no instance
+// takes (fmt, pro, epi) at this width and shape.
+bool launch_stream(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s);
+// Whether an instance exists for (fmt, pro, epi) at width cols.
+bool stream_has(int fmt, int pro, int epi, int cols);
 
 // A batch of consecutive positions for the attention kernels: token z sits
 // at pos0 + z and attends to positions 0..pos0+z; its rows are z·stride

@@ -562,6 +562,7 @@ bool fused_fits(int pro, int cols) {
 
 bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s) {
     if (a.rows <= 0) return true;
+    if (launch_stream(fmt, pro, epi, a, cu, s)) return true;
     if (!fused_fits(pro, a.cols)) return false;
     if ((epi == kEpAdd || epi == kEpAddCanon || epi == kEpLogits) && a.nseg != 1) return false;
     if (epi == kEpQKV && (a.hs <= 0 || a.hs > 1024 || (a.rows & 1) || (a.row_base & 1))) return false;

@@ -98,15 +98,20 @@ void add_used(rk_device *d, int64_t bytes) {
 // launch into the scratch q, which the products then read.
 int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
                     const QScratch &q, hipStream_t s) {
-    const bool in_lds = cols <= 8192 && ((uintptr_t)x & 15) == 0 && fused_fits(kProQuant, (int)cols);
+    const bool aligned = ((uintptr_t)x & 15) == 0;
+    const bool in_lds = cols <= 8192 && aligned && fused_fits(kProQuant, (int)cols);
     bool quantized = false;
     for (int kind : {RK_Q8, RK_Q4}) {
         FusedArgs a{};
         a.cols = (int32_t)cols;
+        // each workgroup quantizes x itself, unless the input is wide and no
+        // static-schedule instance takes it (then one quantize launch first)
+        const bool q_in = in_lds || (aligned && cols <= kMaxLdsCols &&
+                                     stream_has(kind == RK_Q8 ? kFmtQ8 : kFmtQ4, kProQuant, kEpStore, (int)cols));
         auto flush = [&]() -> int {
             if (a.nseg == 0) return RK_OK;
             int pro = kProQuant;
-            if (in_lds) {
+            if (q_in) {
                 a.x = x;
             } else {
                 if (!quantized) {
