@@ -203,10 +203,11 @@ __device__ __forceinline__ float wave_gomax(float m) {
 // maximum (Go max: NaN wins, +0 over -0) and the integer sum are exact in
 // any order.
 __device__ __forceinline__ uint32_t quantize_group(float v0, float v1, float v2, float v3, float &d, int &csum) {
-    float a = gomax(gomax(gomax(0.0f, fabsf(v0)), fabsf(v1)), gomax(fabsf(v2), fabsf(v3)));
-    a = gomax(a, __int_as_float(dpp_x1(__float_as_int(a))));
-    a = gomax(a, __int_as_float(dpp_x2(__float_as_int(a))));
-    a = gomax(a, __int_as_float(dpp_mirror8(__float_as_int(a))));
+    float a = abs_max3(abs_max3(0.0f, v0, v1), v2, v3);
+    a = __builtin_elementwise_maximum(a, dppf_x1(a));
+    a = __builtin_elementwise_maximum(a, dppf_x2(a));
+    a = __builtin_elementwise_maximum(a, __int_as_float(dpp_mirror8(__float_as_int(a))));
+    a = canonical(a);  // Go max gives the canonical NaN
     d = a * u2f(k1_127);
     const bool zero = (d == 0.0f) || (d != d);
     const float id = recip32(d);
@@ -224,6 +225,34 @@ __device__ __forceinline__ uint32_t quantize_group(float v0, float v1, float v2,
     csum = s;
     return (uint32_t)(c0 & 255) | ((uint32_t)(c1 & 255) << 8) | ((uint32_t)(c2 & 255) << 16) |
            ((uint32_t)(c3 & 255) << 24);
+}
+
+// Q8_0 quantization (internal/num/quant.go:34-53) of one 32-value block
+// held by one lane: Recip32 once per block. Codes packed little-endian four
+// to a word; the block's scale and code sum.
+__device__ __forceinline__ void quantize_block32(const float4 (&v)[8], uint32_t (&pk)[8], float &d, int &csum) {
+    float a = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) a = abs_max3(abs_max3(a, v[k].x, v[k].y), v[k].z, v[k].w);
+    a = canonical(a);
+    d = a * u2f(k1_127);
+    const bool zero = (d == 0.0f) || (d != d);
+    const float id = recip32(d);
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
+        if (!zero) {
+            c0 = q8_code(v[k].x, id);
+            c1 = q8_code(v[k].y, id);
+            c2 = q8_code(v[k].z, id);
+            c3 = q8_code(v[k].w, id);
+        }
+        s += (c0 + c1) + (c2 + c3);
+        pk[k] = (uint32_t)(c0 & 255) | ((uint32_t)(c1 & 255) << 8) | ((uint32_t)(c2 & 255) << 16) |
+                ((uint32_t)(c3 & 255) << 24);
+    }
+    csum = s;
 }
 
 // a = silu(v)·b (internal/llm/model.go:657, :603-605).

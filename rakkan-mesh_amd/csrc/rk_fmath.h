@@ -125,10 +125,16 @@ __device__ __forceinline__ float exp32(float x) {
 // int8(max(-127, min(127, RoundToEven(float32(v*id))))); a NaN product
 // (0·Inf, from a denormal scale) gives 0, as amd64's conversion does.
 __device__ __forceinline__ int q8_code(float v, float id) {
-    float r = __builtin_rintf(v * id);
-    if (r != r) return 0;
-    r = r > 127.0f ? 127.0f : (r < -127.0f ? -127.0f : r);
-    return (int)r;
+    const float r = __builtin_rintf(v * id);
+    const float c = __builtin_amdgcn_fmed3f(r, -127.0f, 127.0f);  // exact: the middle of r and the bounds
+    return r != r ? 0 : (int)c;
+}
+
+// Go's max of the magnitudes |a|, |b|, |c| and m (m >= +0 or NaN): gfx950's
+// IEEE maximum propagates NaN and orders -0 below +0, which is Go max on
+// these operands except for which NaN it returns (the callers canonicalize).
+__device__ __forceinline__ float abs_max3(float m, float a, float b) {
+    return __builtin_elementwise_maximum(m, __builtin_elementwise_maximum(fabsf(a), fabsf(b)));
 }
 
 }  // namespace rk

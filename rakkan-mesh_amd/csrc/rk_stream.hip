@@ -184,8 +184,9 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
     constexpr int NS = K * C;
     static_assert(NS % U == 0, "a batch is a whole number of load rounds");
     constexpr int GPC = Q8 ? 256 : 512;  // groups of four input values per chunk
-    constexpr int MG = PRO == kProGlobal ? 1 : (C * GPC + 64 * stream_wmin(FMT, PRO, C) - 1) / (64 * stream_wmin(FMT, PRO, C));
     constexpr int NTMIN = 64 * stream_wmin(FMT, PRO, C);
+    constexpr int MG = PRO == kProNorm ? (C * GPC + NTMIN - 1) / NTMIN : 1;
+    static_assert(PRO != kProQuant || (Q8 ? C * 32 : C * 64) <= NTMIN, "the quantize prologue takes one block per thread");
     constexpr int MQ = ((Q8 ? 64 : 128) * C + NTMIN - 1) / NTMIN;  // 16-byte pieces of qx per thread
     constexpr int MB = ((Q8 ? 32 : 64) * C + NTMIN - 1) / NTMIN;   // blocks per thread
     constexpr bool PAIR = EPI == kEpQKV || EPI == kEpSilu;
@@ -220,20 +221,25 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
     };
 
     // ---- (1) the input's loads ----
-    float4 xv[PRO == kProGlobal ? 1 : MG], wv[PRO == kProNorm ? MG : 1];
+    float4 xv[PRO == kProNorm ? MG : 1], wv[PRO == kProNorm ? MG : 1];
+    float4 xb[8];  // kProQuant: the thread's block of x (block threadIdx.x)
     int4 xq0[XR ? C : 1], xq1[(XR && !Q8) ? C : 1];
     float xsr[XR ? C : 1];
     int xsm[(XR && !Q8) ? C : 1];
     // (every thread loads its MG/MQ/MB pieces, clamped into the vector, so
     // the pieces stay in registers)
-    if (PRO != kProGlobal) {
+    if (PRO == kProNorm) {
         const int ng = cols >> 2;
 #pragma unroll
         for (int k = 0; k < MG; k++) {
             const int g = min((int)threadIdx.x + k * nt, ng - 1);
             xv[k] = reinterpret_cast<const float4 *>(a.x)[g];
-            if (PRO == kProNorm) wv[k] = reinterpret_cast<const float4 *>(a.norm_w)[g];
+            wv[k] = reinterpret_cast<const float4 *>(a.norm_w)[g];
         }
+    } else if (PRO == kProQuant) {
+        const float4 *xp = reinterpret_cast<const float4 *>(a.x) + 8 * min((int)threadIdx.x, nb - 1);
+#pragma unroll
+        for (int k = 0; k < 8; k++) xb[k] = xp[k];
     } else if (XR) {
 #pragma unroll
         for (int c = 0; c < C; c++) {
@@ -329,22 +335,17 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
         norm_quant_rt<MG>(xv, wv, cols, nt, a.recip_n, a.norm_eps, sqx, sxs, sxsum,
                           reinterpret_cast<float *>(lds + a.lds_norm), &s_rn);
     } else if (PRO == kProQuant) {
-        const int ng = cols >> 2;
-#pragma unroll
-        for (int k = 0; k < MG; k++) {
-            if (k * nt < ng) {  // uniform
-                const int gi = threadIdx.x + k * nt;
-                float d;
-                int cs;
-                const uint32_t pk = quantize_group(xv[k].x, xv[k].y, xv[k].z, xv[k].w, d, cs);
-                if (gi < ng) {
-                    reinterpret_cast<uint32_t *>(sqx)[gi] = pk;
-                    if ((gi & 7) == 0) {
-                        sxs[gi >> 3] = d;
-                        sxsum[gi >> 3] = cs;
-                    }
-                }
-            }
+        // one block per thread (Recip32 once a block)
+        if ((int)threadIdx.x < nb) {
+            uint32_t pk[8];
+            float d;
+            int cs;
+            quantize_block32(xb, pk, d, cs);
+            uint4 *q = reinterpret_cast<uint4 *>(sqx + 32 * threadIdx.x);
+            q[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            q[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+            sxs[threadIdx.x] = d;
+            sxsum[threadIdx.x] = cs;
         }
     } else if (!XR) {
         // the LDS stores of the loads above: done once no more than the 2U
