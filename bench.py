@@ -528,7 +528,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=300)
     ap.add_argument("--warmup", type=int, default=30)
-    ap.add_argument("--sets", type=int, default=4, help="weight copies rotated per step (>256 MB total)")
+    ap.add_argument("--sets", type=int, default=8, help="weight copies rotated per step (1.2 GB: far past the 256 MB MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
