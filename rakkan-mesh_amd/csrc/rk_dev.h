@@ -66,6 +66,16 @@ __device__ __forceinline__ float lds_sum_fixed(const float *p, float acc) {
     return acc;
 }
 
+// The LDS address space form of a pointer into the kernel's LDS (the
+// destination operand of a direct-to-LDS load).
+__device__ __forceinline__ __attribute__((address_space(3))) void *lds_ptr(void *p) {
+    return (__attribute__((address_space(3))) void *)p;
+}
+
+// s_waitcnt operand (gfx9) waiting for vector memory operations until at
+// most n remain outstanding, and for nothing else.
+constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 // Software pipeline of a sequential LDS sum: batches of kChainBatch float4,
 // the next batch's reads issued before the current batch's additions. The
 // scheduling barriers keep the compiler from sinking the reads next to their

@@ -843,6 +843,199 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
     }
 }
 
+// The same result for contexts up to kVrMaxCtx positions, with every
+// position's values of the slice in registers from the start. Waves 0-3
+// take the scores and the softmax as above (lane 0 of wave 0 adds the
+// e_t); waves 4-7 load the slice's values of chunks of kVrChunk positions
+// (two position quads of one float4 column a thread a chunk, loads only
+// for chunks below T) and, once inv is known, write a chunk's products
+// a_t·v_t,i transposed into a tile while wave 0 adds the previous chunk's
+// (lane i < 32: its element's products in position order). Tile row i
+// keeps logical float4 q of the row at q ^ vr_swz(i): with that swizzle
+// both the products' 16-byte writes (eight lanes: eight rows 4 apart, one
+// column) and the sums' reads (eight lanes: eight consecutive rows, one
+// logical column) touch 32 distinct banks.
+constexpr int kVrThreads = 512;
+constexpr int kVrChunk = 256;
+constexpr int kVrMaxChunks = 4;
+constexpr int kVrMaxCtx = kVrChunk * kVrMaxChunks;
+
+__device__ __forceinline__ int vr_swz(int i) { return ((i >> 2) ^ ((i & 3) << 1)) & 7; }
+
+// acc + row[0] + ... + row[n-1] in order for a tile row with swizzle key
+// `key` (logical float4 q at q ^ key), n <= kVrChunk: batches of 32 values,
+// the next batch's reads in flight during the current batch's additions.
+__device__ __forceinline__ void swz_load_batch(float4 (&b)[kChainBatch], const float4 *q, int key) {
+#pragma unroll
+    for (int k = 0; k < kChainBatch; k++) b[k] = q[k ^ key];
+}
+
+__device__ __forceinline__ float swz_chain_sum(const float *row, int n, int key, float acc) {
+    const float4 *q = reinterpret_cast<const float4 *>(row);
+    const int nb = n >> 5;
+    if (nb > 0) {
+        float4 a[kChainBatch], b[kChainBatch];
+        swz_load_batch(a, q, key);
+        int k = 1;
+        for (; k + 1 < nb; k += 2) {
+            swz_load_batch(b, q + k * kChainBatch, key);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(a, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            swz_load_batch(a, q + (k + 1) * kChainBatch, key);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(b, acc);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (k < nb) {
+            swz_load_batch(b, q + k * kChainBatch, key);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(a, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = add_batch(b, acc);
+        } else {
+            acc = add_batch(a, acc);
+        }
+    }
+    for (int t = nb * 32; t < n; t += 4) {  // the last partial batch, a float4 at a time
+        const int l = t >> 2;
+        const float4 v = q[l ^ key];
+        acc += v.x;
+        if (t + 1 < n) acc += v.y;
+        if (t + 2 < n) acc += v.z;
+        if (t + 3 < n) acc += v.w;
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float *att, int32_t att_stride,
+                                                                    const float *vals, float *out, const int32_t *ctl,
+                                                                    AttBatch bt, int kv_mul, int hs, int kv_dim,
+                                                                    int nsl, int ctx_pad, int8_t *qx, float *xs,
+                                                                    int32_t *xsum) {
+    extern __shared__ __align__(16) float smem[];
+    __shared__ float s_red[4];
+    __shared__ float s_inv;
+    __shared__ __align__(16) float s_res[kValSlice];
+    float *sa = smem;               // [ctx_pad] scores -> e_t
+    float *tiles = smem + ctx_pad;  // [2][32][kVrChunk] products, swizzled rows
+    const int z = blockIdx.y;       // token of a batch (0 when the position comes from ctl)
+    const int T = (ctl ? ctl[kCtlPos] : bt.pos0 + z) + 1;
+    const int nch = (T + kVrChunk - 1) / kVrChunk;
+    att += (int64_t)z * bt.att_stride;
+    out += (int64_t)z * bt.out_stride;
+    if (qx) {
+        qx += (int64_t)z * bt.out_stride;
+        xs += (int64_t)z * (bt.out_stride >> 5);
+        xsum += (int64_t)z * (bt.out_stride >> 5);
+    }
+    const int h = blockIdx.x / nsl, e0 = (blockIdx.x % nsl) * kValSlice;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // waves 4-7: float4 column fq (elements 4fq..4fq+3) and position quads
+    // pq, pq + 32 of each chunk
+    const int u = tid - 256, fq = u & 7, pq = u >> 3;
+    float4 vr[kVrMaxChunks][2][4];  // [chunk][quad][position in the quad]
+    float sc[4];
+    if (wave < 4) {
+        const float *ah = att + (int64_t)h * att_stride;
+#pragma unroll
+        for (int k = 0; k < 4; k++) sc[k] = ah[min(tid + 256 * k, T - 1)];
+        float m = sc[0];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + 256 * k < T) m = gomax(m, sc[k]);
+        m = wave_gomax(m);
+        if (lane == 0) s_red[wave] = m;
+    } else {
+        // positions past T-1 load T-1's values (their products are never summed)
+        const float *vb = vals + (int64_t)(h / kv_mul) * hs + e0 + 4 * fq;
+#pragma unroll
+        for (int c = 0; c < kVrMaxChunks; c++)
+            if (c < nch) {  // uniform
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int t = min(c * kVrChunk + 4 * (pq + 32 * q) + j, T - 1);
+                        vr[c][q][j] = *reinterpret_cast<const float4 *>(vb + (int64_t)t * kv_dim);
+                    }
+            }
+    }
+    __syncthreads();
+    if (wave < 4) {
+        float m = s_red[0];
+#pragma unroll
+        for (int w = 1; w < 4; w++) m = gomax(m, s_red[w]);
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (tid + 256 * k < T) sa[tid + 256 * k] = exp32(sc[k] - m);
+    }
+    __syncthreads();
+    if (tid == 0) s_inv = recip32(lds_chain_sum(sa, T, 0.0f));
+    __syncthreads();
+    const float inv = s_inv;
+
+    // chunk c's products into tile c mod 2 (waves 4-7); positions past T
+    // take a clamped weight and give products that are never summed
+    auto products = [&](int c) {
+        float *tile = tiles + (c & 1) * (kValSlice * kVrChunk);
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int qd = pq + 32 * q;  // the quad within the chunk
+            const float4 e4 = *reinterpret_cast<const float4 *>(sa + min(c * kVrChunk + 4 * qd, ctx_pad - 4));
+            const float4 a4 = make_float4(e4.x * inv, e4.y * inv, e4.z * inv, e4.w * inv);
+            const float4(&v)[4] = vr[c][q];
+            const float4 p[4] = {make_float4(a4.x * v[0].x, a4.y * v[1].x, a4.z * v[2].x, a4.w * v[3].x),
+                                 make_float4(a4.x * v[0].y, a4.y * v[1].y, a4.z * v[2].y, a4.w * v[3].y),
+                                 make_float4(a4.x * v[0].z, a4.y * v[1].z, a4.z * v[2].z, a4.w * v[3].z),
+                                 make_float4(a4.x * v[0].w, a4.y * v[1].w, a4.z * v[2].w, a4.w * v[3].w)};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = 4 * fq + j;
+                reinterpret_cast<float4 *>(tile + i * kVrChunk)[qd ^ vr_swz(i)] = p[j];
+            }
+        }
+    };
+    if (wave >= 4) products(0);
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kVrMaxChunks; c++) {
+        if (c < nch) {  // uniform
+            if (wave == 0) {
+                if (lane < kValSlice)
+                    acc = swz_chain_sum(tiles + (c & 1) * (kValSlice * kVrChunk) + lane * kVrChunk,
+                                        min(kVrChunk, T - c * kVrChunk), vr_swz(lane), acc);
+            } else if (wave >= 4 && c + 1 < nch) {
+                products(c + 1);
+            }
+            __syncthreads();
+        }
+    }
+    if (wave != 0) return;
+    if (lane < kValSlice) out[(int64_t)h * hs + e0 + lane] = acc;
+    if (qx) {
+        // the slice is one Q8_0 block of the next input: lanes 0-7 take
+        // four values each
+        if (lane < kValSlice) s_res[lane] = acc;
+        const int q = min(lane, 7);
+        const float4 v4 = reinterpret_cast<const float4 *>(s_res)[q];
+        float d;
+        int cs;
+        const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
+        const int64_t base = (int64_t)h * hs + e0;
+        if (lane < 8) {
+            reinterpret_cast<uint32_t *>(qx + base)[lane] = pk;
+            if (lane == 0) {
+                xs[base >> 5] = d;
+                xsum[base >> 5] = cs;
+            }
+        }
+    }
+}
+
+static size_t att_values_reg_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + 2 * kValSlice * kVrChunk) * 4; }
+
 // Dynamic LDS of the values kernel for a context of ctx positions.
 static size_t att_values_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + 2 * kValSlice * kValPitch) * 4; }
 
@@ -861,13 +1054,22 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
                                   (int)kValMaxDynLds);
         (void)hipFuncSetAttribute((const void *)att_values_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)kValMaxDynLds);
+        (void)hipFuncSetAttribute((const void *)att_values_reg_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)att_values_reg_lds(kVrMaxCtx));
     });
     if (!ctl && att_group_fits(bt, hs, kv_dim)) {
         launch_att_values_group(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s);
         return;
     }
-    const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice, ctl ? 1 : bt.tokens);
     if (hs % 32 != 0) qx = nullptr;
+    if (ctx <= kVrMaxCtx && hs % 32 == 0 && kv_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {
+        const int nsl = hs / kValSlice;
+        RK_LAUNCH(att_values_reg_kernel, dim3(heads * nsl, ctl ? 1 : bt.tokens), dim3(kVrThreads),
+                  att_values_reg_lds(ctx), s, att, att_stride, vals, out, ctl, bt, heads / kv_heads, hs, kv_dim, nsl,
+                  (ctx + 3) & ~3, qx, xs, xsum);
+        return;
+    }
+    const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice, ctl ? 1 : bt.tokens);
     const int ctx_pad = (ctx + 3) & ~3;
     if (hs % 4 == 0 && kv_dim % 4 == 0)
         RK_LAUNCH(att_values_kernel<true>, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals, out,

@@ -156,15 +156,6 @@ __device__ void norm_quant_rt(const float4 *xv, const float4 *wv, int n, int nt,
     }
 }
 
-// The LDS address space form of a pointer into the kernel's LDS.
-__device__ __forceinline__ __attribute__((address_space(3))) void *lds_ptr(void *p) {
-    return (__attribute__((address_space(3))) void *)p;
-}
-
-// s_waitcnt operand (gfx9) waiting for vector memory operations until at
-// most n remain outstanding, and for nothing else.
-constexpr int vmcnt_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-
 // LDS of the transposed x of norm_quant_rt for n values.
 size_t stream_norm_lds(int n) { return (size_t)32 * ((((n >> 5) + 3) & ~3) + 4) * 4; }
 

@@ -224,6 +224,25 @@ def test_generation_real_shapes_one_layer(dev, name):
     check_generation(dev, m, [11, 7000, 123, 99], 12, 64)
 
 
+@pytest.mark.parametrize("case", ["kv2_ctx1024", "kv2_ctx1100", "kv8_gqa_ctx1000"])
+def test_generation_long_context(dev, case):
+    """Decode at positions up to the end of a long context, every logit
+    bitwise: contexts up to 1024 keep all of a value slice's positions in
+    LDS (several product chunks), 1100 takes the chunked values kernel;
+    8 value heads of 32 (two query heads each) put each value slice's
+    workgroups on one XCD."""
+    if case.startswith("kv2"):
+        ctx = int(case.split("ctx")[1])
+        c = Config(**{**CONFIGS[1].__dict__, "dtype": "q8_0", "seq_len": ctx})
+    else:
+        ctx = 1000
+        c = Config(dim=128, hidden=192, layers=2, heads=16, kv_heads=8, vocab=50, seq_len=ctx, head_dim=32,
+                   dtype="q8_0")
+    m = Model(c, random_model(c, 6))
+    prompt = [int(t) for t in np.random.default_rng(3).integers(0, c.vocab, ctx - 10)]
+    check_generation(dev, m, prompt, 10, ctx)
+
+
 def forward_one_by_one(st, xs, pos0):
     return np.stack([st.forward(xs[t], pos0 + t)[0] for t in range(len(xs))])
 
