@@ -599,20 +599,22 @@ struct StreamTune {
     int fmt, pro, epi, rows, cols, k, u, w, nbatch;
 };
 const StreamTune kStreamTune[] = {
-    {kFmtQ8, kProQuant, kEpStore, 4096, 4096, 1, 4, 8, 2},         // config 2
-    {kFmtQ8, kProQuant, kEpStore, 14336, 4096, 1, 4, 8, 4},        // config 2
+    {kFmtQ8, kProQuant, kEpStore, 4096, 4096, 2, 8, 8, 1},         // config 2
+    {kFmtQ8, kProQuant, kEpStore, 14336, 4096, 1, 4, 8, 7},        // config 2
     {kFmtQ8, kProQuant, kEpStore, 4096, 14336, 1, 7, 16, 1},       // config 2
+    {kFmtQ8, kProGlobal, kEpStore, 4096, 4096, 2, 4, 4, 1},
+    {kFmtQ8, kProGlobal, kEpStore, 14336, 4096, 2, 4, 7, 4},
     {kFmtQ8, kProGlobal, kEpStore, 4096, 14336, 1, 7, 8, 1},
-    {kFmtQ8, kProNorm, kEpQKV, 6144, 4096, 2, 4, 16, 1},           // 8B-shape layer
+    {kFmtQ8, kProNorm, kEpQKV, 6144, 4096, 2, 4, 12, 1},           // 8B-shape layer
     {kFmtQ8, kProGlobal, kEpAdd, 4096, 4096, 2, 4, 4, 1},
     {kFmtQ8, kProNorm, kEpSilu, 28672, 4096, 4, 8, 8, 2},
     {kFmtQ8, kProGlobal, kEpAddCanon, 4096, 14336, 1, 7, 8, 1},
-    {kFmtQ8, kProNorm, kEpLogits, 128256, 4096, 2, 8, 8, 16},
+    {kFmtQ8, kProNorm, kEpLogits, 128256, 4096, 2, 4, 8, 38},
     {kFmtQ4, kProNorm, kEpQKV, 4608, 3584, 2, 4, 9, 1},            // Qwen-7B-shape layer
-    {kFmtQ4, kProGlobal, kEpAdd, 3584, 3584, 2, 4, 4, 1},
+    {kFmtQ4, kProGlobal, kEpAdd, 3584, 3584, 2, 4, 7, 1},
     {kFmtQ4, kProNorm, kEpSilu, 37888, 3584, 4, 4, 16, 3},
     {kFmtQ4, kProGlobal, kEpAddCanon, 3584, 18944, 1, 5, 8, 1},
-    {kFmtQ8, kProNorm, kEpLogits, 152064, 3584, 2, 4, 8, 8},
+    {kFmtQ8, kProNorm, kEpLogits, 152064, 3584, 2, 4, 8, 41},
 };
 
 constexpr int kStreamLdsMax = 160 * 1024;
