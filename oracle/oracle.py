@@ -190,6 +190,16 @@ def dot32(a, b):
     return np.float32(lib().rko_dot32(ptr(a), ptr(b), a.size))
 
 
+def dot_bf16(w, x):
+    w, x = _c(w, np.uint16), _c(x, np.float32)
+    return np.float32(lib().rko_dot_bf16(ptr(w), ptr(x), w.size))
+
+
+def to_bf16(v):
+    v = _c(v, np.float32)
+    return np.array([lib().rko_to_bf16(np.float32(t)) for t in v], np.uint16)
+
+
 def rmsnorm(x, w, eps):
     x, w = _c(x, np.float32), _c(w, np.float32)
     out = np.empty_like(x)

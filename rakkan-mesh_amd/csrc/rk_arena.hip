@@ -252,16 +252,20 @@ int rk_batch_matvecs(rk_batch *b, int32_t n, rk_matrix *const *ms, const int64_t
     if (!ms || !out_offs) return latch(b, fail(d, RK_ERR_ARGS, "rk_batch_matvecs: null arguments"));
     const int64_t cols = ms[0] ? ms[0]->cols : 0;
     std::vector<float *> outs(n);
+    bool quantized = false;
     for (int i = 0; i < n; i++) {
         rk_matrix *m = ms[i];
         if (!m || m->d != d) return latch(b, fail(d, RK_ERR_ARGS, "gpu: matrix on another device"));
         if (m->cols != cols) return latch(b, fail(d, RK_ERR_ARGS, "gpu: products of one input need one width"));
-        if (m->kind != RK_Q8 && m->kind != RK_Q4)
+        if (m->kind != RK_Q8 && m->kind != RK_Q4 && m->kind != RK_F32 && m->kind != RK_BF16)
             return latch(b, fail(d, RK_ERR_UNSUPPORTED, "rk_batch_matvecs: format %d has no kernel in this build",
                                  m->kind));
         if (!(outs[i] = span(b, out_offs[i], m->rows, "product output"))) return b->err;
+        quantized = quantized || m->kind == RK_Q8 || m->kind == RK_Q4;
     }
-    if (a->qx_off < 0) return latch(b, fail(d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
+    // internal/gpu/batch.go:240-245: only a quantized product needs the scratch
+    if (quantized && a->qx_off < 0)
+        return latch(b, fail(d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
     const float *x = span(b, in_off, cols, "product input");
     if (!x) return b->err;
     int rc = enqueue_matvecs(d, n, ms, outs.data(), x, cols, QScratch{a->qx, a->xs, a->xsum}, d->stream);

@@ -66,6 +66,11 @@ __device__ __forceinline__ float lds_sum_fixed(const float *p, float acc) {
     return acc;
 }
 
+// Buffer descriptor word 3 of an untyped 32-bit raw buffer (gfx9 family),
+// and the cache policy of a streamed weight load (non-temporal).
+constexpr int kRsrcWord3 = 0x00020000;
+constexpr int kAuxStream = 2;
+
 // The LDS address space form of a pointer into the kernel's LDS (the
 // destination operand of a direct-to-LDS load).
 __device__ __forceinline__ __attribute__((address_space(3))) void *lds_ptr(void *p) {

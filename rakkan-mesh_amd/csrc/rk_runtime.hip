@@ -5,6 +5,7 @@
 #include "rk_mm.h"
 #include "rk_runtime.h"
 
+#include "rk_dense.h"
 #include "rk_fused.h"
 
 #include <cstdarg>
@@ -145,6 +146,13 @@ int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const 
         int rc = flush();
         if (rc) return rc;
     }
+    // float32 / bfloat16 matrices take x as it is (internal/gpu/batch.go:
+    // 263-264: no quantized input), one launch each
+    for (int i = 0; i < n; i++) {
+        if (ms[i]->kind != RK_F32 && ms[i]->kind != RK_BF16) continue;
+        ProfScope p(d, s, ms[i]->kind == RK_BF16 ? "matvec_bf16" : "matvec_f32");
+        launch_dense_matvec(ms[i]->kind == RK_BF16, ms[i]->w, ms[i]->rows, cols, x, outs[i], s);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(d, e, "matvec launch");
     return RK_OK;
@@ -159,7 +167,7 @@ int check_products(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, 
         if (m->cols != cols)
             return fail(d, RK_ERR_ARGS, "gpu: %lld×%lld matrix times %lld", (long long)m->rows, (long long)m->cols,
                         (long long)cols);
-        if (m->kind != RK_Q8 && m->kind != RK_Q4)
+        if (m->kind != RK_Q8 && m->kind != RK_Q4 && m->kind != RK_F32 && m->kind != RK_BF16)
             return fail(d, RK_ERR_UNSUPPORTED, "rk_matvecs: format %d has no kernel in this build", m->kind);
         *total += m->rows;
     }
@@ -248,10 +256,50 @@ int enqueue_matmuls(rk_device *d, int32_t n, rk_matrix *const *ms, float *const 
 static int check_matmul(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, int32_t tokens, int64_t *total) {
     int rc = check_products(d, n, ms, cols, total);
     if (rc) return rc;
+    for (int i = 0; i < n; i++)
+        if (ms[i]->kind != RK_Q8 && ms[i]->kind != RK_Q4)
+            return fail(d, RK_ERR_UNSUPPORTED, "rk_matmul_t: format %d has no batched kernel in this build",
+                        ms[i]->kind);
     if (tokens < 0) return fail(d, RK_ERR_ARGS, "rk_matmul_t: %d tokens", tokens);
     if ((int64_t)tokens * cols > ((int64_t)1 << 31) - 32 || (int64_t)tokens * *total > ((int64_t)1 << 31))
         return fail(d, RK_ERR_ARGS, "rk_matmul_t: %d tokens of %lld columns is too large for one call", tokens,
                     (long long)cols);
+    return RK_OK;
+}
+
+// internal/gpu/device.go:587-597, 619-621 Upload of float32 / bfloat16
+// rows (bfloat16 rows need an even width). Each row is stored padded with
+// zeros to dense_row_elems(cols) elements (the products' layout).
+static int upload_dense(rk_device *d, int32_t kind, int64_t rows, int64_t cols, const void *w, rk_matrix **out) {
+    if (kind == RK_BF16 && cols % 2 != 0) return fail(d, RK_ERR_ARGS, "gpu: bfloat16 rows need an even width");
+    const size_t es = kind == RK_BF16 ? 2 : 4;
+    const int64_t pitch = dense_row_elems(cols) * (int64_t)es;
+    const int64_t wbytes = rows * pitch;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    rk_matrix *m = new rk_matrix();
+    m->d = d;
+    m->kind = kind;
+    m->rows = rows;
+    m->cols = cols;
+    int rc = dev_alloc(d, (void **)&m->w, (size_t)wbytes, "matrix");
+    if (rc) {
+        delete m;
+        return rc;
+    }
+    hipError_t e = hipMemsetAsync(m->w, 0, (size_t)wbytes, d->stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(m->w, (size_t)pitch, w, (size_t)cols * es, (size_t)cols * es, (size_t)rows,
+                             hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(m->w);
+        delete m;
+        return hip_fail(d, e, "matrix upload");
+    }
+    m->bytes = wbytes;
+    add_used(d, m->bytes);
+    *out = m;
     return RK_OK;
 }
 
@@ -376,7 +424,7 @@ int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, con
     case RK_Q8: wbytes = rows * cols; break;
     case RK_Q4: wbytes = rows * cols / 2; break;
     case RK_F32:
-    case RK_BF16: return fail(d, RK_ERR_UNSUPPORTED, "rk_matrix_upload: format %d has no kernel in this build", kind);
+    case RK_BF16: return upload_dense(d, kind, rows, cols, w, out);
     default: return fail(d, RK_ERR_ARGS, "rk_matrix_upload: unknown format %d", kind);
     }
     if (cols % 32 != 0 || !scales) return fail(d, RK_ERR_ARGS, "gpu: quantized matrix of the wrong shape");

@@ -40,10 +40,6 @@ struct Row {
     __amdgpu_buffer_rsrc_t w, s;
 };
 
-// Buffer descriptor word 3 of an untyped 32-bit raw buffer (gfx9 family),
-// and the cache policy of a streamed weight load (non-temporal).
-constexpr int kRsrcWord3 = 0x00020000;
-constexpr int kAuxStream = 2;
 
 // Codes and scales of logical row l: up to three matrices concatenated, or
 // (kEpSilu) W1 and W3 interleaved row by row. l is wave-uniform, so this

@@ -343,3 +343,76 @@ def test_activation_quantize_equals_weight_quantize():
                            oracle.ptr(sums))
         want = _qrow(sums, s[r * 3:(r + 1) * 3], xs)
         assert bits(oracle.matvec_q8(q[r * cols:(r + 1) * cols], s[r * 3:(r + 1) * 3], x, 1, cols)[0]) == bits(want)
+
+
+def test_dot32_order_closed_forms():
+    """Dot32 (internal/num/matvec.go:32-67): each input pins one part of the
+    order, because the plausible alternative gives another float32.
+    * a running sum adds its elements in order: 1e8 + 1 rounds back to 1e8,
+      so s0 = ((1e8 + 1) - 1e8) is 0 (another order gives 1);
+    * e_j = (s_j + s_j+8) + (s_j+16 + s_j+24): with s0 = 1e8, s8 = -1e8,
+      s16 = 1 it is 1 ((s0 + s16) + (s8 + s24) gives 0);
+    * ((e0+e1)+(e2+e3))+((e4+e5)+(e6+e7)): with e0 = 1, e2 = 1e8,
+      e3 = -1e8 it is 1 (a left fold gives 0), and with e4 = 1e8,
+      e5 = -1e8, e6 = 1 likewise;
+    * each product is rounded before it is added (no fused multiply-add):
+      (1+2^-12)^2 rounds to 1+2^-11, so adding -(1+2^-11) gives 0 (2^-24
+      with a fused multiply-add)."""
+    def d(a, b=None):
+        a = np.asarray(a, np.float32)
+        return oracle.dot32(a, np.ones_like(a) if b is None else np.asarray(b, np.float32))
+
+    a = np.zeros(96, np.float32)
+    a[0], a[32], a[64] = 1e8, 1, -1e8
+    assert d(a) == 0.0
+    a = np.zeros(32, np.float32)
+    a[0], a[8], a[16] = 1e8, -1e8, 1
+    assert d(a) == 1.0
+    a = np.zeros(32, np.float32)
+    a[0], a[2], a[3] = 1, 1e8, -1e8
+    assert d(a) == 1.0
+    a = np.zeros(32, np.float32)
+    a[4], a[5], a[6] = 1e8, -1e8, 1
+    assert d(a) == 1.0
+    u = np.float32(1 + 2.0 ** -12)
+    a = np.zeros(64, np.float32)
+    b = np.ones(64, np.float32)
+    a[0], b[0], a[32] = u, u, -np.float32(1 + 2.0 ** -11)
+    assert d(a, b) == 0.0
+    # all partial sums exact: the integer dot product, any length (tails too)
+    rng = np.random.default_rng(11)
+    for n in (1, 31, 33, 100, 4097):
+        ai = rng.integers(-50, 51, n)
+        bi = rng.integers(-50, 51, n)
+        assert d(ai.astype(np.float32), bi.astype(np.float32)) == float(np.dot(ai, bi))
+
+
+def test_dot_bf16_equals_dot32_and_error_bound():
+    """internal/num/num_test.go:83-105 (TestDot8AndBF16): DotBF16 equals
+    Dot32 on the converted weights bit for bit, and Dot32 is within
+    1e-4·sqrt(n) + 1e-6 of the exact product."""
+    rng = np.random.default_rng(2)
+    for n in (0, 1, 7, 8, 9, 63, 896, 4865):
+        w16 = oracle.to_bf16(rng.normal(0, 1, n).astype(np.float32))
+        w = (w16.astype(np.uint32) << 16).view(np.float32)  # BF16: the upper half of a float32
+        x = rng.normal(0, 1, n).astype(np.float32)
+        a, b = oracle.dot32(w, x), oracle.dot_bf16(w16, x)
+        assert bits(a) == bits(b), n
+        exact = float(np.dot(w.astype(np.float64), x.astype(np.float64)))
+        assert abs(float(a) - exact) <= 1e-4 * math.sqrt(n) + 1e-6, n
+
+
+def test_matvec32_rows_are_dot32():
+    """MatVec32 / MatVecBF16 (internal/num/matvec.go:106-123): row i is
+    Dot32 of row i, whatever the split over workers."""
+    rng = np.random.default_rng(5)
+    rows, cols = 37, 300
+    w = rng.normal(0, 1, rows * cols).astype(np.float32)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    got = oracle.matvec32(w, x, rows, cols)
+    for i in range(rows):
+        assert bits(got[i]) == bits(oracle.dot32(w[i * cols:(i + 1) * cols], x))
+    w16 = oracle.to_bf16(w)
+    got = oracle.matvec_bf16(w16, x, rows, cols)
+    for i in range(rows):
+        assert bits(got[i]) == bits(oracle.dot_bf16(w16[i * cols:(i + 1) * cols], x))
