@@ -184,6 +184,104 @@ def matvec_bench(dev, rkhip, args):
     return out, (q_all, s_all, xs, gpu_outs)
 
 
+def measure_speed_weights(rows, cols):
+    """MeasureSpeed's weights (internal/llm/speed.go:20-25): an LCG seed
+    s = s·1664525 + 1013904223 per element, w = ToBF16(float32(int32(s>>8) -
+    2^23) / 2^30), computed in closed form (s_k = a^k·s_0 + c·(1 + a + ... +
+    a^(k-1)) mod 2^32); x_i = float32(i mod 17) / 17."""
+    n = rows * cols
+    a = np.full(n, 1664525, np.uint64)
+    ak = np.cumprod(a)                                    # a^k, k = 1..n (mod 2^64)
+    geo = np.cumsum(np.concatenate(([np.uint64(1)], ak[:-1])))  # 1 + a + ... + a^(k-1)
+    seed = ((ak * np.uint64(1) + np.uint64(1013904223) * geo) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+    v = ((seed >> 8).astype(np.int32) - (1 << 23)).astype(np.float32) / np.float32(1 << 30)
+    b = v.view(np.uint32).astype(np.uint64)
+    w16 = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    x = (np.arange(cols) % 17).astype(np.float32) / np.float32(17)
+    return w16, x
+
+
+def dense_bench(dev, rkhip, args):
+    """The planner's speed probe (internal/llm/speed.go:16-47 MeasureSpeed):
+    products with a 4096x4096 bfloat16 matrix, reported as GB of weights per
+    second. Device-resident products rotated over copies past the MALL
+    (graph replays), each launch's duration by HIP events for the roofline,
+    and the reference's own measure (median of 7 host round trips, input and
+    output copies included). A float32 matrix of the same shape beside it."""
+    rows = cols = 4096
+    w16, x = measure_speed_weights(rows, cols)
+    w32 = (w16.astype(np.uint32) << 16).view(np.float32)
+    out = {}
+    L = rkhip.lib()
+    P = ctypes.c_void_p
+    for name, kind, w, es in (("bf16", rkhip.BF16, w16, 2), ("f32", rkhip.F32, w32, 4)):
+        wbytes = rows * cols * es
+        copies = max(2, int(600e6 // wbytes) + 1)
+        ms = [dev.upload(kind, rows, cols, w) for _ in range(copies)]
+        arena = dev.arena(cols + rows, cols)
+        b = arena.begin()
+        b.write(0, x)
+        b.submit()
+        xp, op = P(arena.device_ptr(0)), (P * 1)(arena.device_ptr(cols))
+        hs = [(P * 1)(m.h) for m in ms]
+
+        def run(n, start=0):
+            for k in range(start, start + n):
+                rc = L.rk_matvecs_device(dev.h, 1, hs[k % copies], op, xp, cols, None)
+                if rc:
+                    raise rkhip.RKError(rc, L.rk_last_error(dev.h).decode())
+
+        run(copies)
+        arena.begin().submit()
+        dev.graph_begin()
+        run(copies)
+        g = dev.graph_end()
+        g.launch(2)
+        reps = max(1, 400 // copies)
+        t0 = time.perf_counter()
+        g.launch(reps)
+        t1 = time.perf_counter()
+        per = (t1 - t0) / (reps * copies)
+        dev.profile_start()
+        run(200)
+        arena.begin().submit()
+        prof = dev.profile_stop()
+        calls, ms_tot = prof.get("matvec_" + name, (0, 0.0))
+        launch_us = ms_tot / max(calls, 1) * 1e3
+        alg = wbytes + 4 * cols + 4 * rows
+        rt = []
+        for _ in range(8):
+            s0 = time.perf_counter()
+            dev.matvec(ms[0], x)
+            rt.append(time.perf_counter() - s0)
+        rt = sorted(rt[1:])
+        got = dev.matvec(ms[0], x)
+        g.free()
+        arena.free()
+        for m in ms:
+            m.free()
+        out[name] = {"weights_GB_s": round(wbytes / per / 1e9, 1), "us_per_product": round(per * 1e6, 3),
+                     "avg_launch_us": round(launch_us, 3),
+                     "roofline_frac": round(alg / (launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "round_trip_GB_s": round(2 * rows * cols / rt[len(rt) // 2] / 1e9, 1),
+                     "copies": copies}
+        if name == "bf16" and not args.no_cpu:
+            from oracle import oracle
+
+            want = oracle.matvec_bf16(w16, x, rows, cols)
+            n, c0 = 0, time.perf_counter()
+            while time.perf_counter() - c0 < min(3.0, args.cpu_seconds):
+                oracle.matvec_bf16(w16, x, rows, cols)
+                n += 1
+            el = time.perf_counter() - c0
+            out[name]["bit_exact_vs_cpu"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+            out[name]["cpu_baseline"] = {"weights_GB_s": round(n * 2 * rows * cols / el / 1e9, 2), "cores": 1,
+                                         "kind": "port", "sample": f"{n} products in {el:.1f} s (scalar C "
+                                         "restatement of MatVecBF16, one thread)"}
+    return {"measure_speed": {"config": "MeasureSpeed: 4096x4096 bfloat16 (LCG weights as speed.go), f32 input "
+                              "i%17/17; float32 matrix of the same values beside it", **out}}
+
+
 PMC_COPY_WORDS = 1 << 26  # the calibration copy: 256 MiB read, 256 MiB written
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "q8_matvec_config2_pmc.md")
 
@@ -540,6 +638,7 @@ def main():
                     help="only the launches the PMC runs count (config-2 products and a calibration copy)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--moe-layers", type=int, default=4)
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--prefill-layers", type=int, default=28)
@@ -588,6 +687,9 @@ def main():
     if not args.no_moe:
         log("moe bench (config 5)")
         result.update(moe_bench(dev, rkhip, args))
+    if not args.no_dense:
+        log("dense bench (MeasureSpeed)")
+        result.update(dense_bench(dev, rkhip, args))
     result["device"] = {"name": info.name.decode(), "arch": info.arch.decode(), "cu": info.compute_units}
     if not args.no_cpu:
         log("cpu baseline")

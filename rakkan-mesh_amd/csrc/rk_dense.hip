@@ -14,16 +14,16 @@
 // never become -0 (x + y is -0 only when both are), so s + (+0) == s, NaN
 // payloads included.
 //
-// Work layout: eight lanes per row; lane q of a row keeps the running sums
-// 4q..4q+3 and at row step m (32 elements) reads elements 32m+4q..+3 (16
-// bytes of float32 or 8 of bfloat16), so a row step is one 128- or 64-byte
-// segment and a wave reads eight rows' segments per instruction. U steps
-// of every row are in flight (a register ring): a wave keeps U·1 KiB
-// (float32) in flight. The row's loads are buffer loads at a wave-uniform
-// step offset; past the row's last step they repeat that step (cache hits)
-// and those steps add +0, so every step issues the same loads and
-// additions and the waits are fixed counts. The input is staged in LDS
-// (zero-padded), in segments of kDenseMaxLdsElems for wider rows.
+// Work layout: 32/SL lanes per row; lane l of a row keeps the running sums
+// SL·l .. SL·l+SL-1 and at row step m (32 elements) reads elements
+// 32m+SL·l .. +SL-1, so a row step is one contiguous 128-byte (float32) or
+// 64-byte (bfloat16) segment. U steps of every row are in flight (a
+// register ring). The row's loads are buffer loads at a wave-uniform step
+// offset; past the row's last step they repeat that step (cache hits) and
+// those steps add +0, so every step issues the same loads and additions and
+// the waits are fixed counts. The input is staged in LDS (zero-padded), in
+// segments of kDenseMaxLdsElems for wider rows, and read a block of U steps
+// at a time.
 #include <algorithm>
 #include <mutex>
 
@@ -35,114 +35,191 @@ namespace rk {
 
 namespace {
 
-constexpr int kDenseU = 32;                 // row steps in flight per lane
+// Running sums per lane (32/SL lanes a row) and row steps in flight, the
+// fastest measured on MI355X: float32 one sum a lane (4-byte loads, two
+// rows a wave), bfloat16 two (one 4-byte word, four rows a wave).
+constexpr int kDenseSlF32 = 1;
+constexpr int kDenseSlBf16 = 2;
+constexpr int kDenseU = 16;
 constexpr int kDenseMaxLdsElems = 32768;    // input staged in LDS up to this width (128 KiB)
 constexpr int64_t kDenseLaunchBytes = 1 << 30;  // a launch's matrix bytes (one buffer resource)
 
 typedef int rk_v2i __attribute__((ext_vector_type(2)));
 
-template <bool BF>
-struct DenseStep {
-    typedef rk_v4i type;
+// Lanes per row 32/SL: lane l of a row keeps running sums SL·l .. SL·l+SL-1
+// and reads SL elements per row step. U row steps in flight (U <= 63, the
+// vector memory counter's range).
+template <bool BF, int SL>
+struct DenseLoad;
+template <>
+struct DenseLoad<false, 1> {
+    typedef int type;
+    static __device__ type load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, kAuxStream);
+    }
 };
 template <>
-struct DenseStep<true> {
+struct DenseLoad<false, 2> {
     typedef rk_v2i type;
+    static __device__ type load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, v, s, kAuxStream);
+    }
+};
+template <>
+struct DenseLoad<false, 4> {
+    typedef rk_v4i type;
+    static __device__ type load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, kAuxStream);
+    }
+};
+template <>
+struct DenseLoad<true, 2> {
+    typedef int type;
+    static __device__ type load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, kAuxStream);
+    }
+};
+template <>
+struct DenseLoad<true, 4> {
+    typedef rk_v2i type;
+    static __device__ type load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, v, s, kAuxStream);
+    }
 };
 
-template <bool BF>
+// Element k (< SL) of a loaded step as float32.
+template <bool BF, int SL, typename V>
+__device__ __forceinline__ float dense_elem(const V &v, int k) {
+    if constexpr (!BF) {
+        if constexpr (SL == 1)
+            return __int_as_float(v);
+        else
+            return __int_as_float(v[k]);
+    } else {
+        int word;
+        if constexpr (SL == 2)
+            word = v;
+        else
+            word = v[k >> 1];
+        return __int_as_float((k & 1) ? (word & (int)0xFFFF0000u) : (word << 16));
+    }
+}
+
+template <bool BF, int SL, int U>
 __global__ __launch_bounds__(512) void dense_matvec_kernel(const void *w, int64_t rows, int row_elems,
                                                             const float *x, int cols, float *out) {
-    typedef typename DenseStep<BF>::type V;
-    extern __shared__ __align__(16) float sx[];
+    typedef DenseLoad<BF, SL> LD;
+    typedef typename LD::type V;
+    constexpr int LPR = 32 / SL;    // lanes per row
+    constexpr int RPW = 64 / LPR;   // rows per wave
     constexpr int ES = BF ? 2 : 4;  // bytes per element
     constexpr int SB = 32 * ES;     // bytes per row step
-    const int tid = threadIdx.x, lane = tid & 63, q = lane & 7;
+    extern __shared__ __align__(16) float sx[];
+    const int tid = threadIdx.x, lane = tid & 63, l = lane % LPR;
     const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (tid >> 6);
-    const int64_t row = wave * 8 + (lane >> 3);
+    const int64_t row = wave * RPW + lane / LPR;
     // groups past the end repeat the last row (never stored) and take part
     // in the workgroup's barriers
     const int64_t r = row < rows ? row : rows - 1;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(w), 0, (int)(rows * row_elems * ES), kRsrcWord3);
-    const int vo = (int)(r * row_elems * ES) + q * 4 * ES;
-    float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+    const int vo = (int)(r * row_elems * ES) + l * SL * ES;
+    float acc[SL];
+#pragma unroll
+    for (int k = 0; k < SL; k++) acc[k] = 0.0f;
     // segments of the row whose input fits the LDS (one for widths up to
     // kDenseMaxLdsElems)
     for (int c0 = 0; c0 < row_elems; c0 += kDenseMaxLdsElems) {  // uniform
         const int ce = min(kDenseMaxLdsElems, row_elems - c0);
         const int nsteps = ce >> 5, mb = c0 >> 5;
-        auto load = [&](int m) -> V {
-            const int mm = mb + (m < nsteps ? m : nsteps - 1);
-            if constexpr (BF)
-                return __builtin_amdgcn_raw_buffer_load_b64(rs, vo, mm * SB, kAuxStream);
-            else
-                return __builtin_amdgcn_raw_buffer_load_b128(rs, vo, mm * SB, kAuxStream);
-        };
+        auto load = [&](int m) -> V { return LD::load(rs, vo, (mb + (m < nsteps ? m : nsteps - 1)) * SB); };
         // the segment's first U steps, oldest first (the ring's waits count
         // on that order), then its input into LDS, zero past cols
-        V wb[kDenseU];
+        V wb[U];
 #pragma unroll
-        for (int u = 0; u < kDenseU; u++) {
+        for (int u = 0; u < U; u++) {
             wb[u] = load(u);
             __builtin_amdgcn_sched_barrier(0);
         }
         if (c0 > 0) __syncthreads();  // every wave is done with the previous segment's input
         for (int i = tid; i < ce; i += blockDim.x) sx[i] = c0 + i < cols ? x[c0 + i] : 0.0f;
         __syncthreads();
-        for (int m0 = 0; m0 < nsteps; m0 += kDenseU) {
+        for (int m0 = 0; m0 < nsteps; m0 += U) {
+            // the block's U input steps from LDS first (one LDS latency a
+            // block, not a step)
+            float xv[U][SL];
 #pragma unroll
-            for (int u = 0; u < kDenseU; u++) {
+            for (int u = 0; u < U; u++) {
+                const int m = m0 + u;
+                const float *xp = sx + (m < nsteps ? m : nsteps - 1) * 32 + l * SL;
+                if constexpr (SL == 4) {
+                    const float4 t = *reinterpret_cast<const float4 *>(xp);
+                    xv[u][0] = t.x, xv[u][1] = t.y, xv[u][2] = t.z, xv[u][3] = t.w;
+                } else if constexpr (SL == 2) {
+                    const float2 t = *reinterpret_cast<const float2 *>(xp);
+                    xv[u][0] = t.x, xv[u][1] = t.y;
+                } else {
+                    xv[u][0] = xp[0];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; u++) {
                 // every step adds (no branch, so no load is left in flight
                 // under a register it is about to reload); a step past the
                 // segment adds +0, which leaves the sum as it is
                 const int m = m0 + u;
                 const bool live = m < nsteps;  // uniform
-                const float4 xv = reinterpret_cast<const float4 *>(sx)[(live ? m : nsteps - 1) * 8 + q];
-                float4 wv;
-                if constexpr (BF) {
-                    const rk_v2i b = wb[u];
-                    wv = make_float4(__int_as_float(b.x << 16), __int_as_float(b.x & (int)0xFFFF0000u),
-                                     __int_as_float(b.y << 16), __int_as_float(b.y & (int)0xFFFF0000u));
-                } else {
-                    const rk_v4i b = wb[u];
-                    wv = make_float4(__int_as_float(b.x), __int_as_float(b.y), __int_as_float(b.z),
-                                     __int_as_float(b.w));
-                }
-                s0 += live ? wv.x * xv.x : 0.0f;
-                s1 += live ? wv.y * xv.y : 0.0f;
-                s2 += live ? wv.z * xv.z : 0.0f;
-                s3 += live ? wv.w * xv.w : 0.0f;
-                wb[u] = load(m + kDenseU);
+#pragma unroll
+                for (int k = 0; k < SL; k++)
+                    acc[k] += live ? dense_elem<BF, SL>(wb[u], k) * xv[u][k] : 0.0f;
+                wb[u] = load(m + U);
             }
         }
     }
-    // combine: lane q holds s_4q..s_4q+3; a = s_j + s_j+8 (lanes 0, 1) and
-    // s_j+16 + s_j+24 (lanes 4, 5); e_j in lanes 0 (j < 4) and 1 (j >= 4)
-    float a0 = s0 + __shfl_down(s0, 2, 8), a1 = s1 + __shfl_down(s1, 2, 8);
-    float a2 = s2 + __shfl_down(s2, 2, 8), a3 = s3 + __shfl_down(s3, 2, 8);
-    const float e0 = a0 + __shfl_down(a0, 4, 8), e1 = a1 + __shfl_down(a1, 4, 8);
-    const float e2 = a2 + __shfl_down(a2, 4, 8), e3 = a3 + __shfl_down(a3, 4, 8);
-    const float hsum = (e0 + e1) + (e2 + e3);
-    const float res = hsum + __shfl_down(hsum, 1, 8);
-    if (q == 0 && row < rows) out[row] = res;
+    // Dot32's combine: s_j sits in lane j/SL of the row, element j mod SL.
+    // a = s_j + s_j+8 (lanes of j < 8), then + (s_j+16 + s_j+24) gives e_j;
+    // then ((e0+e1)+(e2+e3))+((e4+e5)+(e6+e7)).
+    float e[SL];
+#pragma unroll
+    for (int k = 0; k < SL; k++) {
+        const float a = acc[k] + __shfl_down(acc[k], 8 / SL, LPR);
+        e[k] = a + __shfl_down(a, 16 / SL, LPR);
+    }
+    // lanes 0 .. 8/SL-1 hold e_j (j = SL·l + k)
+    float res;
+    if constexpr (SL == 4) {
+        const float h = (e[0] + e[1]) + (e[2] + e[3]);  // lane 0: e0..e3; lane 1: e4..e7
+        res = h + __shfl_down(h, 1, LPR);
+    } else if constexpr (SL == 2) {
+        const float p = e[0] + e[1];                    // lane l: e_2l + e_2l+1
+        const float t = p + __shfl_down(p, 1, LPR);     // lanes 0, 2
+        res = t + __shfl_down(t, 2, LPR);
+    } else {
+        const float p = e[0] + __shfl_down(e[0], 1, LPR);  // lanes 0, 2, 4, 6
+        const float t = p + __shfl_down(p, 2, LPR);        // lanes 0, 4
+        res = t + __shfl_down(t, 4, LPR);
+    }
+    if (l == 0 && row < rows) out[row] = res;
 }
 
-template <bool BF>
+template <bool BF, int SL, int U>
 void launch_dense_t(const void *w, int64_t rows, int row_elems, const float *x, int cols, float *out,
-                    hipStream_t s) {
+                    hipStream_t s, int waves_per_wg = 0) {
+    constexpr int RPW = 2 * SL;
     const size_t lds = (size_t)std::min(row_elems, kDenseMaxLdsElems) * 4;
     static std::once_flag once;
     std::call_once(once, [] {
-        (void)hipFuncSetAttribute((const void *)dense_matvec_kernel<BF>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  kDenseMaxLdsElems * 4);
+        (void)hipFuncSetAttribute((const void *)dense_matvec_kernel<BF, SL, U>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kDenseMaxLdsElems * 4);
     });
-    const int64_t waves = (rows + 7) / 8;
-    // up to 8 waves (two a SIMD: the ring's registers allow no more)
-    const int64_t W = std::min<int64_t>(8, std::max<int64_t>(1, (waves + 255) / 256));
+    const int64_t waves = (rows + RPW - 1) / RPW;
+    // four waves a workgroup once there are enough (measured best on
+    // MI355X for 4096- and 14336-row products)
+    const int64_t W = waves_per_wg > 0 ? waves_per_wg : std::min<int64_t>(4, std::max<int64_t>(1, waves / 256));
     const int64_t grid = (waves + W - 1) / W;
-    RK_LAUNCH((dense_matvec_kernel<BF>), dim3((unsigned)grid), dim3((unsigned)(64 * W)), lds, s, w, rows, row_elems,
-              x, cols, out);
+    RK_LAUNCH((dense_matvec_kernel<BF, SL, U>), dim3((unsigned)grid), dim3((unsigned)(64 * W)), lds, s, w, rows,
+              row_elems, x, cols, out);
 }
 
 }  // namespace
@@ -158,9 +235,9 @@ void launch_dense_matvec(bool bf16, const void *w, int64_t rows, int64_t cols, c
         const int64_t n = std::min(per, rows - r0);
         const void *wr = static_cast<const uint8_t *>(w) + r0 * rb;
         if (bf16)
-            launch_dense_t<true>(wr, n, row_elems, x, (int)cols, out + r0, s);
+            launch_dense_t<true, kDenseSlBf16, kDenseU>(wr, n, row_elems, x, (int)cols, out + r0, s);
         else
-            launch_dense_t<false>(wr, n, row_elems, x, (int)cols, out + r0, s);
+            launch_dense_t<false, kDenseSlF32, kDenseU>(wr, n, row_elems, x, (int)cols, out + r0, s);
     }
 }
 
