@@ -152,7 +152,8 @@ class Model:
         self.c = c
         d, q, kv, h = c.dim, c.q_dim(), c.kv_dim(), c.hidden
         self.embed = Mat(c.vocab, d, raw["embed"], c.embed_type())
-        self.wcls = self.embed  # shared classifier
+        # a separate classifier when raw has one, else the shared embedding
+        self.wcls = Mat(c.vocab, d, raw["wcls"], c.embed_type()) if raw.get("wcls") is not None else self.embed
         self.rms_final = raw["rms_final"]
         self.layers = []
         shapes = {"wq": (q, d, False), "wk": (kv, d, False), "wv": (kv, d, True), "wo": (d, q, False),
