@@ -6,6 +6,9 @@ model.go:269-279, 390-400 matBytes, LayerBytes), and the weight quantizers
 Quantize calls (internal/num/quant.go:25-126 QuantizeQ8 / QuantizeQ4,
 recip.go:16-67 Recip32, matvec.go:22-29 ToBF16), restated with the same
 float32 / float64 roundings so the codes are the reference's bit for bit.
+Hugging Face models (internal/llm/hf.go: safetensors, float16/bfloat16
+weights, the rotary row permutation, config.json's mapping) import to the
+same parts.
 
 `stage_from_checkpoint` uploads a quantized checkpoint's layers to a device
 as an rkhip.Stage and its head, the way internal/llm moves layers to a GPU
@@ -471,6 +474,319 @@ def load_head(c: Config, data: bytes, embed: Matrix):
         h.wcls = d.mat(c.vocab_size * c.dim, c.embed_type())
     d.done()
     return h
+
+
+# --- Hugging Face models (internal/llm/hf.go) ---------------------------------
+
+HF_MODEL_TYPES = ("llama", "mistral", "qwen2", "qwen3")
+_ST_HEADER_MAX = 100 << 20  # hf.go:84
+
+
+class _Bytes:
+    """A file read in pieces (hf.go:39-43 SizedReaderAt) over bytes in memory."""
+
+    def __init__(self, b):
+        self.b = memoryview(b)
+        self.size = len(b)
+
+    def read_at(self, off, n):
+        return bytes(self.b[off:off + n])
+
+
+class _File:
+    """A file read in pieces from disk, one tensor at a time."""
+
+    def __init__(self, path):
+        self.path = path
+        import os
+        self.size = os.path.getsize(path)
+
+    def read_at(self, off, n):
+        with open(self.path, "rb") as f:
+            f.seek(off)
+            b = f.read(n)
+        if len(b) != n:
+            raise ValueError("unexpected EOF")
+        return b
+
+
+def _reader(f):
+    if isinstance(f, (bytes, bytearray, memoryview)):
+        return _Bytes(f)
+    if isinstance(f, str):
+        return _File(f)
+    return f  # anything with read_at(off, n) and size
+
+
+@dataclass
+class STTensor:
+    """hf.go:67-75 stTensor: a tensor's type, shape and byte range in a
+    safetensors file."""
+    dtype: str
+    shape: list
+    offsets: tuple
+    file: object = None
+    base: int = 0
+
+    def elems(self):
+        n = 1
+        for d in self.shape:
+            n *= d
+        return n
+
+    def raw(self, name, want):
+        """hf.go:117-137 raw: the tensor's bytes, checking its type and
+        element count. Returns (bytes, element size)."""
+        size = {"BF16": 2, "F16": 2, "F32": 4}.get(self.dtype)
+        if size is None:
+            raise ValueError(f"tensor {name}: type {self.dtype} not supported")
+        if self.elems() != want or want * size != self.offsets[1] - self.offsets[0]:
+            raise ValueError(f"tensor {name}: shape {self.shape}, want {want} elements")
+        return self.file.read_at(self.base + self.offsets[0], want * size), size
+
+
+def read_safetensors(f, into: dict):
+    """hf.go:77-115 readSafetensors: an 8-byte little-endian header size, a
+    JSON header naming each tensor's type, shape and byte range, then the
+    data. Adds the file's tensors to `into` (name -> STTensor); f is a path,
+    bytes, or an object with read_at(off, n) and size. The header is parsed
+    as JSON only; no tensor data is read here."""
+    import json
+
+    r = _reader(f)
+    if r.size < 8:
+        raise ValueError("safetensors: unexpected EOF")
+    n = int(np.frombuffer(r.read_at(0, 8), "<u8")[0])
+    if n > _ST_HEADER_MAX or n + 8 > r.size:
+        raise ValueError(f"safetensors: header of {n} bytes")
+    try:
+        h = json.loads(r.read_at(8, n))
+    except ValueError as e:
+        raise ValueError(f"safetensors header: {e}") from None
+    if not isinstance(h, dict):
+        raise ValueError("safetensors header: not an object")
+    base = 8 + n
+    for name, v in h.items():
+        if name == "__metadata__":
+            continue
+        try:
+            off = v.get("data_offsets") or [0, 0]
+            t = STTensor(str(v.get("dtype", "")), [int(d) for d in v.get("shape") or []],
+                         (int(off[0]), int(off[1])), r, base)
+        except (AttributeError, TypeError, ValueError, IndexError) as e:
+            raise ValueError(f"safetensors tensor {name}: {e}") from None
+        if t.offsets[0] < 0 or t.offsets[1] < t.offsets[0] or base + t.offsets[1] > r.size:
+            raise ValueError(f"safetensors tensor {name}: data outside the file")
+        if name in into:
+            raise ValueError(f"safetensors: tensor {name} in two files")
+        into[name] = t
+
+
+def f16_to_f32(h):
+    """hf.go:139-155 f16ToF32 over an array of IEEE half bit patterns:
+    exact, subnormals normalized, infinities and NaNs keep their payload
+    (shifted up 13 bits, the quiet bit as it was)."""
+    h = np.asarray(h, np.uint16).astype(np.uint32)
+    sign = (h >> 15) << 31
+    exp = (h >> 10) & 0x1F
+    frac = h & 0x3FF
+    out = sign | ((exp + (127 - 15)) << 23) | (frac << 13)  # normal numbers
+    out = np.where(exp == 0x1F, sign | 0x7F800000 | (frac << 13), out)
+    # subnormals: shift the fraction up until its leading bit reaches 0x400
+    sub = (exp == 0) & (frac != 0)
+    e = np.full(h.shape, -14, np.int64)
+    f = frac.copy()
+    for _ in range(10):
+        m = sub & ((f & 0x400) == 0)
+        f = np.where(m, f << 1, f)
+        e = np.where(m, e - 1, e)
+    out = np.where(sub, sign | ((e + 127).astype(np.uint32) << 23) | ((f & 0x3FF) << 13), out)
+    out = np.where((exp == 0) & (frac == 0), sign, out)
+    return out.astype(np.uint32).view(F32)
+
+
+def permute_rows(w, rows, head):
+    """hf.go:235-249 permuteRows: each head's rows from Hugging Face's
+    rotary layout (dimension j turns with j + head/2) to the engine's
+    (adjacent pairs turn together): row 2j takes row j, row 2j+1 takes row
+    j + head/2. Returns the permuted array (w is not changed)."""
+    w = np.asarray(w)
+    n = w.size // rows
+    half = head // 2
+    src = np.empty(head, np.int64)
+    src[0::2] = np.arange(half)
+    src[1::2] = np.arange(half) + half
+    blocks = w.reshape(rows // head, head, n)
+    return np.ascontiguousarray(blocks[:, src, :]).reshape(w.shape)
+
+
+def permute_vec(v, head):
+    """hf.go:251 permuteVec."""
+    return permute_rows(v, len(v), head)
+
+
+def _cfg_int(hc, key):
+    v = hc.get(key)
+    if v is None:
+        return 0
+    if isinstance(v, bool) or not isinstance(v, (int, float)) or (isinstance(v, float) and not v.is_integer()):
+        raise ValueError(f"config.json: {key} is not an integer")
+    return int(v)
+
+
+def _cfg_float(hc, key):
+    v = hc.get(key)
+    if v is None:
+        return 0.0
+    if isinstance(v, bool) or not isinstance(v, (int, float)):
+        raise ValueError(f"config.json: {key} is not a number")
+    return float(v)
+
+
+def hf_config_of(hc: dict, weights: dict) -> Config:
+    """hf.go:253-307 hfConfigOf: config.json (parsed) and the tensor table
+    to a Config, refusing what the engine would run differently from the
+    model's definition. Raises ValueError with the reference's messages."""
+    import json
+
+    mt = hc.get("model_type") or ""
+    if mt not in HF_MODEL_TYPES:
+        raise ValueError(f'model type "{mt}" is not supported (llama, mistral, qwen2, qwen3)')
+    act = hc.get("hidden_act") or ""
+    if act not in ("", "silu"):
+        raise ValueError(f'activation "{act}" is not supported')
+    if hc.get("rope_scaling") is not None:
+        raise ValueError(f"rope scaling {json.dumps(hc['rope_scaling'], separators=(',', ':'))} is not supported")
+    c = Config(dim=_cfg_int(hc, "hidden_size"), hidden_dim=_cfg_int(hc, "intermediate_size"),
+               n_layers=_cfg_int(hc, "num_hidden_layers"), n_heads=_cfg_int(hc, "num_attention_heads"),
+               n_kv_heads=_cfg_int(hc, "num_key_value_heads"), vocab_size=_cfg_int(hc, "vocab_size"),
+               seq_len=_cfg_int(hc, "max_position_embeddings"), rope_theta=_cfg_float(hc, "rope_theta"),
+               norm_eps=_cfg_float(hc, "rms_norm_eps"), shared_classifier=bool(hc.get("tie_word_embeddings")))
+    if c.n_kv_heads == 0:
+        c.n_kv_heads = c.n_heads
+    hd = _cfg_int(hc, "head_dim")
+    if hd > 0 and (c.n_heads == 0 or hd != c.dim // c.n_heads):
+        c.head_dim = hd
+    if c.rope_theta == 0:
+        c.rope_theta = 10000.0
+    if c.norm_eps == 0:
+        c.norm_eps = 1e-6
+    # within a sliding window attention is ordinary attention: the context
+    # is capped to the window rather than masked
+    win, use = hc.get("sliding_window"), hc.get("use_sliding_window")
+    if isinstance(win, int) and not isinstance(win, bool) and 0 < win < c.seq_len and (use is None or use):
+        c.seq_len = win
+    if "lm_head.weight" not in weights:
+        c.shared_classifier = True
+    c.qkv_bias = "model.layers.0.self_attn.q_proj.bias" in weights
+    c.qk_norm = "model.layers.0.self_attn.q_norm.weight" in weights
+    et = weights.get("model.embed_tokens.weight")
+    c.dtype = "bf16" if et is not None and et.dtype == "BF16" else "f32"
+    if "model.layers.0.self_attn.o_proj.bias" in weights:
+        raise ValueError("output projection biases are not supported")
+    c.validate()
+    return c
+
+
+class HFModel:
+    """hf.go:158-233 hfModel: tensors read by name in the target config's
+    types, one at a time."""
+
+    def __init__(self, c: Config, tensors_: dict):
+        self.c, self.tensors = c, tensors_
+
+    def _get(self, name):
+        t = self.tensors.get(name)
+        if t is None:
+            raise ValueError(f"tensor {name} missing")
+        return t
+
+    def vec(self, name, n):
+        """hf.go:164-187 vec: float32, bfloat16 or float16 to float32."""
+        t = self._get(name)
+        b, size = t.raw(name, n)
+        if size == 4:
+            return np.frombuffer(b, "<f4").astype(F32)
+        u = np.frombuffer(b, "<u2").astype(np.uint16)
+        if t.dtype == "BF16":
+            return (u.astype(np.uint32) << 16).view(F32)
+        return f16_to_f32(u)
+
+    def mat(self, name, n, dtype):
+        """hf.go:189-232 mat: a matrix stored as dtype; bfloat16 tensors
+        stay as they are for a bfloat16 target, other types round to it."""
+        if dtype in ("q8_0", "q4_0"):
+            return Matrix(f32=self.vec(name, n)).convert(dtype)
+        if dtype == "bf16":
+            t = self._get(name)
+            if t.dtype == "BF16":
+                b, _ = t.raw(name, n)
+                return Matrix(bf16=np.frombuffer(b, "<u2").astype(np.uint16))
+            return Matrix(bf16=to_bf16(self.vec(name, n)))
+        return Matrix(f32=self.vec(name, n))
+
+    def layer(self, i):
+        """hf.go:382-440 layer: query and key rows (and their biases and
+        head norms) permuted to the engine's rotary layout before they are
+        converted to the stored type."""
+        c = self.c
+        p = f"model.layers.{i}."
+        d, q, kv, h, hs = c.dim, c.q_dim(), c.kv_dim(), c.hidden_dim, c.head_size()
+        ly = Layer()
+        ly.rms_att = self.vec(p + "input_layernorm.weight", d)
+        wq = self.mat(p + "self_attn.q_proj.weight", q * d, "f32")
+        wk = self.mat(p + "self_attn.k_proj.weight", kv * d, "f32")
+        ly.wv = self.mat(p + "self_attn.v_proj.weight", kv * d, c.mat_type(True))
+        ly.wo = self.mat(p + "self_attn.o_proj.weight", d * q, c.mat_type(False))
+        ly.rms_ffn = self.vec(p + "post_attention_layernorm.weight", d)
+        ly.w1 = self.mat(p + "mlp.gate_proj.weight", h * d, c.mat_type(False))
+        ly.w2 = self.mat(p + "mlp.down_proj.weight", d * h, c.mat_type(True))
+        ly.w3 = self.mat(p + "mlp.up_proj.weight", h * d, c.mat_type(False))
+        if c.qkv_bias:
+            ly.bq = self.vec(p + "self_attn.q_proj.bias", q)
+            ly.bk = self.vec(p + "self_attn.k_proj.bias", kv)
+            ly.bv = self.vec(p + "self_attn.v_proj.bias", kv)
+        if c.qk_norm:
+            ly.q_norm = self.vec(p + "self_attn.q_norm.weight", hs)
+            ly.k_norm = self.vec(p + "self_attn.k_norm.weight", hs)
+        ly.wq = Matrix(f32=permute_rows(wq.f32, q, hs)).convert(c.mat_type(False))
+        ly.wk = Matrix(f32=permute_rows(wk.f32, kv, hs)).convert(c.mat_type(False))
+        if c.qkv_bias:
+            ly.bq, ly.bk = permute_vec(ly.bq, hs), permute_vec(ly.bk, hs)
+        if c.qk_norm:
+            ly.q_norm, ly.k_norm = permute_vec(ly.q_norm, hs), permute_vec(ly.k_norm, hs)
+        return ly
+
+
+def import_hf(config_json, weights, quant="") -> Checkpoint:
+    """hf.go:310-380 ImportHF, without the store: config.json (bytes or
+    str) and the safetensors files (paths, bytes, or readers; all shards in
+    any order) to a Checkpoint of the model's parts in their stored types
+    (encode_layer / encode_head / append_matrix give a node's bytes).
+    quant, if set, stores the matrices as "bf16", "q8_0", "q4_0" or "q4_m"
+    instead of the type they come in. The tokenizer, stop tokens and chat
+    format (hf.go:331-335, 442-483) are not read here."""
+    import json
+
+    try:
+        hc = json.loads(config_json)
+    except ValueError as e:
+        raise ValueError(f"config.json: {e}") from None
+    if not isinstance(hc, dict):
+        raise ValueError("config.json: not an object")
+    ts = {}
+    for f in weights:
+        read_safetensors(f, ts)
+    c = hf_config_of(hc, ts)
+    if quant:
+        c.dtype = quant
+        c.validate()
+    hm = HFModel(c, ts)
+    embed = hm.mat("model.embed_tokens.weight", c.vocab_size * c.dim, c.embed_type())
+    head = Head(rms_final=hm.vec("model.norm.weight", c.dim), wcls=embed)
+    if not c.shared_classifier:
+        head.wcls = hm.mat("lm_head.weight", c.vocab_size * c.dim, c.embed_type())
+    return Checkpoint(c, embed, [hm.layer(i) for i in range(c.n_layers)], head)
 
 
 # --- onto a device -----------------------------------------------------------
