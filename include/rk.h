@@ -45,6 +45,8 @@ enum {
     RK_BF16 = 1,
     RK_Q8 = 2, /* int8 codes [rows][cols], float32 scales [rows][cols/32] */
     RK_Q4 = 3, /* nibbles [rows][cols/2] (low: j, high: j+16 of a block), scales as Q8 */
+    RK_FP8 = 4, /* E4M3 codes [rows][cols], E8M0 scale bytes [ceil(rows/32)][cols/32] */
+    RK_FP4 = 5, /* E2M1 codes [rows][cols/2] (low nibble: even element), E8M0 bytes [rows][cols/32] */
 };
 
 typedef struct rk_device rk_device;
@@ -82,6 +84,22 @@ const char *rk_last_error(rk_device *dev);
  * device layout is this build's own (the reference layout is repacked). */
 int rk_matrix_upload(rk_device *dev, int32_t kind, int64_t rows, int64_t cols, const void *w, const float *scales,
                      rk_matrix **out);
+
+/* internal/gpu/device.go:562-585, 587-700 Upload of Format{FP8 | FP4, E8M0}
+ * (DeepSeek-V4.1's block-scaled matrices): kind RK_FP8 or RK_FP4, codes and
+ * E8M0 scale bytes laid out as the enum above says. E4M3 NaN codes (0x7f,
+ * 0xff) are refused ("gpu: NaN in E4M3 weights"), as num.ValidE4M3 is
+ * checked there. Their products (rk_matvecs, rk_matvecs_device,
+ * rk_batch_matvecs) quantize the input to E4M3 with a power-of-two scale
+ * per 32 (num.QuantizeActFP8) and return num.MatVecFP8 / MatVecFP4 bit for
+ * bit, rounded to bfloat16 (internal/num/mx.go:282-334). */
+int rk_matrix_upload_mx(rk_device *dev, int32_t kind, int64_t rows, int64_t cols, const uint8_t *w,
+                        const uint8_t *e8m0, rk_matrix **out);
+
+/* internal/gpu/device.go:548 Matrix.unrounded: raw != 0 leaves an E4M3 /
+ * E2M1 matrix's products in float32 (num.MatVecFP8Unrounded), for checks
+ * where bfloat16 would hide the last bits. */
+int rk_matrix_set_raw(rk_matrix *m, int32_t raw);
 
 /* internal/gpu/device.go:733-738 Matrix.Free. */
 int rk_matrix_free(rk_matrix *m);
@@ -158,6 +176,11 @@ int rk_batch_read(rk_batch *b, int64_t off, float *dst, int64_t n);
 int rk_batch_matvecs(rk_batch *b, int32_t n, rk_matrix *const *ms, const int64_t *out_offs, int64_t in_off);
 /* internal/gpu/batch.go:277-280 Quantize: n floats at in into the scratch. */
 int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n);
+/* internal/gpu/batch.go:271-275 QuantizeFP8: n floats at word `in` to E4M3
+ * codes and block scales in the arena's quantize scratch (codes at qx_off,
+ * scales at xs_off), as num.QuantizeActFP8. */
+int rk_batch_quantize_fp8(rk_batch *b, int64_t in, int64_t n);
+
 /* internal/gpu/batch.go:282-287 RMSNorm: segs segments of n floats at in
  * (stride apart) into out: out = w·(Rsqrt32(Dot32(x,x)·recip_n + eps)·x). */
 int rk_batch_rmsnorm(rk_batch *b, rk_vectors *vecs, int64_t in, int64_t out, int64_t w, int32_t n, int32_t segs,

@@ -68,6 +68,13 @@ def _declare(L):
         "rko_tensor_matmul_f32": (None, [P, P, P, I64, I64, I64, ctypes.c_int]),
         "rko_tensor_matmul_i8": (None, [P, P, P, I64, I64, I64, ctypes.c_int]),
         "rko_tensor_quantize": (None, [P, P, I64, F32]), "rko_tensor_scale_i32": (None, [P, P, I64, F32]),
+        "rko_e4m3_value": (F64, [ctypes.c_uint8]), "rko_encode_e4m3_n": (None, [P, I64, P]),
+        "rko_decode_e8m0": (F32, [ctypes.c_uint8]), "rko_decode_e2m1": (F32, [ctypes.c_uint8]),
+        "rko_encode_e2m1": (ctypes.c_uint8, [F32]), "rko_pow2ceil": (F32, [F32]),
+        "rko_act_fp8": (None, [P, I64, P, P]), "rko_act_quant_inplace": (None, [P, I64]),
+        "rko_matvec_fp8": (None, [P, P, P, P, P, I64, I64, ctypes.c_int]),
+        "rko_matvec_fp4": (None, [P, P, P, P, P, I64, I64, ctypes.c_int]),
+        "rko_quantize_fp4": (None, [P, I64, ctypes.c_int, P, P]), "rko_dequant_fp4": (None, [P, I64, ctypes.c_int, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -290,3 +297,69 @@ class PCG:
 
     def intn(self, n):
         return lib().rko_rand_intn(ctypes.cast(self._st, P), n)
+
+
+# ---- internal/num/mx.go: DeepSeek-V4.1 block-scaled formats ------------------
+
+def e4m3_values():
+    """The 256 E4M3 codes' values (float64; NaN for 0x7f and 0xff)."""
+    L = lib()
+    return np.array([L.rko_e4m3_value(c) for c in range(256)], np.float64)
+
+
+def encode_e4m3(v):
+    v = _c(v, np.float32).ravel()
+    out = np.empty(v.size, np.uint8)
+    lib().rko_encode_e4m3_n(ptr(v), v.size, ptr(out))
+    return out
+
+
+def act_fp8(x):
+    """QuantizeActFP8: (E4M3 codes, float32 block scales)."""
+    x = _c(x, np.float32).ravel()
+    codes = np.empty(x.size, np.uint8)
+    scales = np.empty(x.size // 32, np.float32)
+    lib().rko_act_fp8(ptr(x), x.size, ptr(codes), ptr(scales))
+    return codes, scales
+
+
+def act_quant_inplace(x):
+    x = _c(x, np.float32).ravel().copy()
+    lib().rko_act_quant_inplace(ptr(x), x.size)
+    return x
+
+
+def matvec_fp8(w, ws, x, rows, cols, bf16=True):
+    """MatVecFP8 (bf16) / MatVecFP8Unrounded of float32 input x."""
+    codes, xs = act_fp8(x)
+    w, ws = _c(w, np.uint8), _c(ws, np.uint8)
+    out = np.empty(rows, np.float32)
+    lib().rko_matvec_fp8(ptr(out), ptr(w), ptr(ws), ptr(codes), ptr(xs), rows, cols, int(bf16))
+    return out
+
+
+def matvec_fp4(w, ws, x, rows, cols, bf16=True):
+    """MatVecFP4 (bf16) / MatVecFP4Unrounded of float32 input x."""
+    codes, xs = act_fp8(x)
+    w, ws = _c(w, np.uint8), _c(ws, np.uint8)
+    out = np.empty(rows, np.float32)
+    lib().rko_matvec_fp4(ptr(out), ptr(w), ptr(ws), ptr(codes), ptr(xs), rows, cols, int(bf16))
+    return out
+
+
+def quantize_fp4(x, e4m3):
+    """QuantizeFP4: (packed codes, scale bytes); blocks of 16 with E4M3
+    scales if e4m3, else of 32 with E8M0 scales."""
+    x = _c(x, np.float32).ravel()
+    blk = 16 if e4m3 else 32
+    packed = np.zeros(x.size // 2, np.uint8)
+    scales = np.empty(x.size // blk, np.uint8)
+    lib().rko_quantize_fp4(ptr(x), x.size, int(e4m3), ptr(packed), ptr(scales))
+    return packed, scales
+
+
+def dequant_fp4(packed, scales, n, e4m3):
+    packed, scales = _c(packed, np.uint8), _c(scales, np.uint8)
+    x = np.empty(n, np.float32)
+    lib().rko_dequant_fp4(ptr(x), n, int(e4m3), ptr(packed), ptr(scales))
+    return x

@@ -21,6 +21,23 @@
 extern "C" {
 #endif
 
+/* ---- internal/num/mx.go: DeepSeek-V4.1 block-scaled formats (rk_oracle_mx.c) ---- */
+double rko_e4m3_value(uint8_t c);
+uint8_t rko_encode_e4m3(float v);
+void rko_encode_e4m3_n(const float *v, int64_t n, uint8_t *out);
+float rko_decode_e8m0(uint8_t c);
+float rko_decode_e2m1(uint8_t c);
+uint8_t rko_encode_e2m1(float v);
+float rko_pow2ceil(float t);
+void rko_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales);
+void rko_act_quant_inplace(float *x, int64_t n);
+void rko_matvec_fp8(float *out, const uint8_t *w, const uint8_t *ws, const uint8_t *xc, const float *xs, int64_t rows,
+                    int64_t cols, int bf16);
+void rko_matvec_fp4(float *out, const uint8_t *w, const uint8_t *ws, const uint8_t *xc, const float *xs, int64_t rows,
+                    int64_t cols, int bf16);
+void rko_quantize_fp4(const float *x, int64_t n, int e4m3, uint8_t *packed, uint8_t *scales);
+void rko_dequant_fp4(float *x, int64_t n, int e4m3, const uint8_t *packed, const uint8_t *scales);
+
 /* ---- internal/num scalar functions ---- */
 float rko_canonical(float v);
 float rko_pow2(int k);

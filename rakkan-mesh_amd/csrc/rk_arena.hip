@@ -7,6 +7,7 @@
 #include <cstring>
 
 #include "rk_layer.h"
+#include "rk_mx.h"
 #include "rk_runtime.h"
 
 // internal/gpu/batch.go:12-20 Arena.
@@ -231,8 +232,18 @@ int rk_batch_read(rk_batch *b, int64_t off, float *dst, int64_t n) {
     rk_arena *a = b->a;
     if (b->staged + n > a->staging_words)
         return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: batch moves more than its staging holds"));
-    float *src = span(b, off, n, "read");
-    if (!src) return b->err;
+    // the quantized input, which the reference keeps in the arena at qx_off
+    // (codes, four a word) and xs_off (scales), is read from the scratch
+    // that holds it here (internal/gpu/mx_test.go:98-127 reads it back)
+    // (the scales' window first: it is the smaller, and a caller lays the
+    // codes out before it)
+    float *src = nullptr;
+    if (a->xs_off >= 0 && off >= a->xs_off && off + n <= a->xs_off + kMaxCols / 32)
+        src = a->xs + (off - a->xs_off);
+    else if (a->qx_off >= 0 && off >= a->qx_off && off + n <= a->qx_off + kMaxCols / 4)
+        src = reinterpret_cast<float *>(a->qx) + (off - a->qx_off);
+    else if (!(src = span(b, off, n, "read")))
+        return b->err;
     float *st = a->staging + b->staged;
     hipError_t e = hipMemcpyAsync(st, src, (size_t)n * 4, hipMemcpyDeviceToHost, a->d->stream);
     if (e != hipSuccess) return latch(b, hip_fail(a->d, e, "batch read"));
@@ -257,12 +268,13 @@ int rk_batch_matvecs(rk_batch *b, int32_t n, rk_matrix *const *ms, const int64_t
         rk_matrix *m = ms[i];
         if (!m || m->d != d) return latch(b, fail(d, RK_ERR_ARGS, "gpu: matrix on another device"));
         if (m->cols != cols) return latch(b, fail(d, RK_ERR_ARGS, "gpu: products of one input need one width"));
-        if (m->kind != RK_Q8 && m->kind != RK_Q4 && m->kind != RK_F32 && m->kind != RK_BF16)
+        if (m->kind < RK_F32 || m->kind > RK_FP4)
             return latch(b, fail(d, RK_ERR_UNSUPPORTED, "rk_batch_matvecs: format %d has no kernel in this build",
                                  m->kind));
         if (!(outs[i] = span(b, out_offs[i], m->rows, "product output"))) return b->err;
-        quantized = quantized || m->kind == RK_Q8 || m->kind == RK_Q4;
+        quantized = quantized || (m->kind != RK_F32 && m->kind != RK_BF16);
     }
+    if (int rc = mixed_inputs(d, n, ms)) return latch(b, rc);
     // internal/gpu/batch.go:240-245: only a quantized product needs the scratch
     if (quantized && a->qx_off < 0)
         return latch(b, fail(d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
@@ -283,6 +295,21 @@ int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n) {
     if (!x) return b->err;
     ProfScope p(a->d, a->d->stream, "quantize_acts");
     launch_quantize_acts(x, n, a->qx, a->xs, a->xsum, a->d->stream);
+    return launched(b, "quantize");
+}
+
+// internal/gpu/batch.go:271-275 QuantizeFP8: E4M3 codes and block scales
+// into the arena's quantize scratch (codes at qx, scales at xs).
+int rk_batch_quantize_fp8(rk_batch *b, int64_t in, int64_t n) {
+    if (!b) return RK_ERR_ARGS;
+    if (b->err) return b->err;
+    rk_arena *a = b->a;
+    if (a->qx_off < 0) return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
+    if (n % 32 != 0 || n > kMaxCols) return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: quantize of %lld floats", (long long)n));
+    const float *x = span(b, in, n, "quantize input");
+    if (!x) return b->err;
+    ProfScope p(a->d, a->d->stream, "act_fp8");
+    launch_act_fp8(x, n, reinterpret_cast<uint8_t *>(a->qx), a->xs, a->d->stream);
     return launched(b, "quantize");
 }
 

@@ -1,0 +1,21 @@
+// rk_mx.h — DeepSeek-V4.1 block-scaled products (E4M3 and E2M1 weights
+// with E8M0 scales) and their input quantization, for gfx950.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rk {
+
+// internal/num/mx.go:185-203 QuantizeActFP8: n floats (a multiple of 32) to
+// E4M3 codes and one power-of-two float32 scale per 32.
+void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s);
+
+// internal/num/mx.go:282-334 MatVecFP8 / MatVecFP4 of an input quantized by
+// launch_act_fp8: out[r] for rows rows; w E4M3 [rows][cols] with E8M0 scales
+// [ceil(rows/32)][cols/32] (fp4 = false), or E2M1 packed [rows][cols/2]
+// with E8M0 scales [rows][cols/32] (fp4 = true). raw leaves the sums in
+// float32 instead of rounding them to bfloat16.
+void launch_mx_matvec(bool fp4, const uint8_t *w, const uint8_t *ws, int64_t rows, int64_t cols, const uint8_t *xc,
+                      const float *xs, float *out, bool raw, hipStream_t s);
+
+}  // namespace rk

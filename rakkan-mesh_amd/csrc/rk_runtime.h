@@ -114,6 +114,11 @@ struct rk_matrix {
     int64_t rows = 0, cols = 0;
     uint8_t *w = nullptr;    // codes, [rows][row bytes]
     float *scales = nullptr; // [rows][cols/32]
+    // E4M3 / E2M1 matrices: E8M0 scale bytes, [ceil(rows/32)][cols/32]
+    // (RK_FP8) or [rows][cols/32] (RK_FP4); raw leaves their products in
+    // float32 rather than bfloat16 (device.go:548 unrounded).
+    uint8_t *e8m0 = nullptr;
+    int32_t raw = 0;
     int64_t bytes = 0;
 };
 
@@ -130,6 +135,8 @@ int fail(rk_device *d, int code, const char *fmt, ...);
 int hip_fail(rk_device *d, hipError_t e, const char *what);
 int dev_alloc(rk_device *d, void **p, size_t bytes, const char *what);
 int scratch_acquire(rk_device *d, hipStream_t s);
+// internal/gpu/batch.go:221-238: Q8_0 and E4M3 inputs are not mixed in one call.
+int mixed_inputs(rk_device *d, int32_t n, rk_matrix *const *ms);
 int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
                     const QScratch &q, hipStream_t s);
 void add_used(rk_device *d, int64_t bytes);

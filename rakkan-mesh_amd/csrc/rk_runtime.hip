@@ -6,6 +6,7 @@
 #include "rk_runtime.h"
 
 #include "rk_dense.h"
+#include "rk_mx.h"
 #include "rk_fused.h"
 
 #include <cstdarg>
@@ -146,6 +147,21 @@ int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const 
         int rc = flush();
         if (rc) return rc;
     }
+    // E4M3 / E2M1 matrices: the input quantized once to E4M3 with block
+    // scales into the scratch (internal/gpu/batch.go:221-233 QuantizeFP8),
+    // then one launch each
+    bool mx_quantized = false;
+    for (int i = 0; i < n; i++) {
+        if (ms[i]->kind != RK_FP8 && ms[i]->kind != RK_FP4) continue;
+        if (!mx_quantized) {
+            ProfScope p(d, s, "act_fp8");
+            launch_act_fp8(x, cols, reinterpret_cast<uint8_t *>(q.qx), q.xs, s);
+            mx_quantized = true;
+        }
+        ProfScope p(d, s, ms[i]->kind == RK_FP8 ? "matvec_fp8" : "matvec_fp4");
+        launch_mx_matvec(ms[i]->kind == RK_FP4, ms[i]->w, ms[i]->e8m0, ms[i]->rows, cols,
+                         reinterpret_cast<const uint8_t *>(q.qx), q.xs, outs[i], ms[i]->raw != 0, s);
+    }
     // float32 / bfloat16 matrices take x as it is (internal/gpu/batch.go:
     // 263-264: no quantized input), one launch each
     for (int i = 0; i < n; i++) {
@@ -158,6 +174,17 @@ int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const 
     return RK_OK;
 }
 
+// internal/gpu/batch.go:221-238: one input is quantized either to Q8_0 or
+// to E4M3, not both.
+int mixed_inputs(rk_device *d, int32_t n, rk_matrix *const *ms) {
+    bool q8 = false, fp8 = false;
+    for (int i = 0; i < n; i++) {
+        q8 = q8 || ms[i]->kind == RK_Q8 || ms[i]->kind == RK_Q4;
+        fp8 = fp8 || ms[i]->kind == RK_FP8 || ms[i]->kind == RK_FP4;
+    }
+    return q8 && fp8 ? fail(d, RK_ERR_ARGS, "gpu: Q8_0 and FP8 products of one input") : RK_OK;
+}
+
 int check_products(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, int64_t *total) {
     if (!d || n < 0 || (n > 0 && !ms)) return fail(d, RK_ERR_ARGS, "rk_matvecs: bad arguments");
     *total = 0;
@@ -167,11 +194,11 @@ int check_products(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, 
         if (m->cols != cols)
             return fail(d, RK_ERR_ARGS, "gpu: %lld×%lld matrix times %lld", (long long)m->rows, (long long)m->cols,
                         (long long)cols);
-        if (m->kind != RK_Q8 && m->kind != RK_Q4 && m->kind != RK_F32 && m->kind != RK_BF16)
+        if (m->kind < RK_F32 || m->kind > RK_FP4)
             return fail(d, RK_ERR_UNSUPPORTED, "rk_matvecs: format %d has no kernel in this build", m->kind);
         *total += m->rows;
     }
-    return RK_OK;
+    return mixed_inputs(d, n, ms);
 }
 
 // Grows a device buffer to `need` elements of `elem` bytes (contents not
@@ -425,6 +452,8 @@ int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, con
     case RK_Q4: wbytes = rows * cols / 2; break;
     case RK_F32:
     case RK_BF16: return upload_dense(d, kind, rows, cols, w, out);
+    case RK_FP8:
+    case RK_FP4: return fail(d, RK_ERR_ARGS, "rk_matrix_upload: E4M3 / E2M1 matrices go through rk_matrix_upload_mx");
     default: return fail(d, RK_ERR_ARGS, "rk_matrix_upload: unknown format %d", kind);
     }
     if (cols % 32 != 0 || !scales) return fail(d, RK_ERR_ARGS, "gpu: quantized matrix of the wrong shape");
@@ -458,6 +487,60 @@ int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, con
     return RK_OK;
 }
 
+// internal/gpu/device.go:587-700 Upload of Format{FP8 | FP4, E8M0}: codes
+// [rows][row bytes] and their scale bytes as given.
+int rk_matrix_upload_mx(rk_device *d, int32_t kind, int64_t rows, int64_t cols, const uint8_t *w,
+                        const uint8_t *e8m0, rk_matrix **out) {
+    if (!d || !out || !w || !e8m0) return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: null argument");
+    *out = nullptr;
+    if (kind != RK_FP8 && kind != RK_FP4) return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: format %d", kind);
+    if (rows <= 0 || cols <= 0 || cols > kMaxCols || rows > (int64_t)1 << 24)
+        return fail(d, RK_ERR_ARGS, "gpu: matrix %lld×%lld out of range", (long long)rows, (long long)cols);
+    if (cols % 32 != 0) return fail(d, RK_ERR_ARGS, "gpu: block-scaled matrix of the wrong shape");
+    const int64_t nb = cols / 32;
+    const int64_t wbytes = kind == RK_FP8 ? rows * cols : rows * cols / 2;
+    const int64_t sbytes = kind == RK_FP8 ? (rows + 31) / 32 * nb : rows * nb;
+    if (kind == RK_FP8) {  // num.ValidE4M3: the NaN codes are refused
+        for (int64_t i = 0; i < wbytes; i++)
+            if ((w[i] & 0x7f) == 0x7f) return fail(d, RK_ERR_ARGS, "gpu: NaN in E4M3 weights");
+    }
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    rk_matrix *m = new rk_matrix();
+    m->d = d;
+    m->kind = kind;
+    m->rows = rows;
+    m->cols = cols;
+    int rc;
+    if ((rc = dev_alloc(d, (void **)&m->w, (size_t)wbytes, "matrix")) ||
+        (rc = dev_alloc(d, (void **)&m->e8m0, (size_t)sbytes, "matrix scales"))) {
+        (void)hipFree(m->w);
+        delete m;
+        return rc;
+    }
+    hipError_t e = hipMemcpyAsync(m->w, w, (size_t)wbytes, hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(m->e8m0, e8m0, (size_t)sbytes, hipMemcpyHostToDevice, d->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(m->w);
+        (void)hipFree(m->e8m0);
+        delete m;
+        return hip_fail(d, e, "matrix upload");
+    }
+    m->bytes = wbytes + sbytes;
+    add_used(d, m->bytes);
+    *out = m;
+    return RK_OK;
+}
+
+int rk_matrix_set_raw(rk_matrix *m, int32_t raw) {
+    if (!m) return RK_ERR_ARGS;
+    if (m->kind != RK_FP8 && m->kind != RK_FP4)
+        return fail(m->d, RK_ERR_ARGS, "rk_matrix_set_raw: only E4M3 / E2M1 products round to bfloat16");
+    m->raw = raw != 0;
+    return RK_OK;
+}
+
 int rk_matrix_free(rk_matrix *m) {
     if (!m) return RK_ERR_ARGS;
     rk_device *d = m->d;
@@ -466,6 +549,7 @@ int rk_matrix_free(rk_matrix *m) {
     (void)hipStreamSynchronize(d->stream);
     (void)hipFree(m->w);
     (void)hipFree(m->scales);
+    (void)hipFree(m->e8m0);
     add_used(d, -m->bytes);
     delete m;
     return RK_OK;

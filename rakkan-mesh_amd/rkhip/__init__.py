@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(PKG_DIR, "librkhip.so")
 HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "rk.h")
 
 RK_OK, RK_ERR_ARGS, RK_ERR_OOM, RK_ERR_HIP, RK_ERR_UNSUPPORTED, RK_ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5
-F32, BF16, Q8, Q4 = 0, 1, 2, 3
+F32, BF16, Q8, Q4, FP8, FP4 = 0, 1, 2, 3, 4, 5
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
@@ -45,6 +45,9 @@ SIGNATURES = {
     "rk_last_error": (ctypes.c_char_p, [P]),
     "rk_matrix_upload": (ctypes.c_int, [P, I32, I64, I64, P, P, P]),
     "rk_matrix_free": (ctypes.c_int, [P]),
+    "rk_matrix_upload_mx": (ctypes.c_int, [P, I32, I64, I64, P, P, P]),
+    "rk_matrix_set_raw": (ctypes.c_int, [P, I32]),
+    "rk_batch_quantize_fp8": (ctypes.c_int, [P, I64, I64]),
     "rk_matrix_bytes": (I64, [P]),
     "rk_matvecs": (ctypes.c_int, [P, I32, P, P, P, I64]),
     "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
@@ -159,6 +162,10 @@ class Matrix:
     def bytes(self):
         return lib().rk_matrix_bytes(self.h)
 
+    def set_raw(self, raw):
+        """E4M3 / E2M1 products left in float32 (internal/gpu Matrix.unrounded)."""
+        self.dev._check(lib().rk_matrix_set_raw(self.h, int(bool(raw))))
+
     def free(self):
         if self.h:
             self.dev._check(lib().rk_matrix_free(self.h))
@@ -235,6 +242,9 @@ class Batch:
     def quantize(self, inp, n):
         return lib().rk_batch_quantize(self.h, inp, n)
 
+    def quantize_fp8(self, inp, n):
+        return lib().rk_batch_quantize_fp8(self.h, inp, n)
+
     def rmsnorm(self, vecs, inp, out, w, n, segs, stride, recip_n, eps):
         return lib().rk_batch_rmsnorm(self.h, vecs.h, inp, out, w, n, segs, stride, float(recip_n), float(eps))
 
@@ -302,6 +312,15 @@ class Device:
             sp = _ptr(scales)
         h = P()
         self._check(lib().rk_matrix_upload(self.h, kind, rows, cols, _ptr(w), sp, ctypes.byref(h)))
+        return Matrix(self, h, kind, rows, cols)
+
+    def upload_mx(self, kind, rows, cols, w, e8m0):
+        """An E4M3 (FP8) or packed E2M1 (FP4) matrix with its E8M0 scale
+        bytes (internal/gpu Upload of Format{FP8 | FP4, E8M0})."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        e8m0 = np.ascontiguousarray(e8m0, dtype=np.uint8)
+        h = P()
+        self._check(lib().rk_matrix_upload_mx(self.h, kind, rows, cols, _ptr(w), _ptr(e8m0), ctypes.byref(h)))
         return Matrix(self, h, kind, rows, cols)
 
     def upload_q8(self, q, s, rows, cols):
