@@ -282,6 +282,99 @@ def dense_bench(dev, rkhip, args):
                               "i%17/17; float32 matrix of the same values beside it", **out}}
 
 
+MX_SHAPES = [  # DeepSeek-V4.1's decode products (dim 5120, q_lora 1280, 64x512 heads, 2304-wide experts)
+    ("fp8", 32768, 1280, "wq_b: q_lora 1280 -> 64 heads x 512"),
+    ("fp8", 5120, 8192, "wo_b: 8 x 1024 -> dim"),
+    ("fp4", 13824, 5120, "6 routed experts' gate rows stacked (6 x 2304)"),
+    ("fp4", 5120, 2304, "one expert's down projection"),
+]
+
+
+def mx_bench(dev, rkhip, args):
+    """DeepSeek-V4.1 block-scaled products (internal/num/mx.go MatVecFP8 /
+    MatVecFP4 through internal/gpu): E4M3 / E2M1 weights with E8M0 scales,
+    the input quantized on the device each call. Device-resident products
+    rotated over copies past the MALL (graph replays); each kernel's average
+    launch by HIP events for the roofline (weights + scales + input codes
+    and scales + output per product). One product per format checked bit
+    for bit against the CPU oracle, which is also timed (one thread)."""
+    L = rkhip.lib()
+    P = ctypes.c_void_p
+    rng = np.random.default_rng(41)
+    out = []
+    for kind, rows, cols, what in MX_SHAPES:
+        x = rng.normal(0, 1, cols).astype(np.float32)
+        nb = cols // 32
+        if kind == "fp8":
+            w = rng.integers(0, 0x7E, rows * cols, dtype=np.uint8) | (rng.integers(0, 2, rows * cols, dtype=np.uint8) << 7)
+            sc = rng.integers(118, 128, (rows + 31) // 32 * nb).astype(np.uint8)
+            fmt, wbytes = rkhip.FP8, rows * cols
+        else:
+            w = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+            sc = rng.integers(118, 128, rows * nb).astype(np.uint8)
+            fmt, wbytes = rkhip.FP4, rows * cols // 2
+        alg = wbytes + sc.size + cols + 4 * nb + 4 * rows
+        copies = max(2, int(600e6 // wbytes) + 1)
+        ms = [dev.upload_mx(fmt, rows, cols, w, sc) for _ in range(copies)]
+        arena = dev.arena(cols + rows, cols)
+        b = arena.begin()
+        b.write(0, x)
+        b.submit()
+        xp, op = P(arena.device_ptr(0)), (P * 1)(arena.device_ptr(cols))
+        hs = [(P * 1)(m.h) for m in ms]
+
+        def run(n):
+            for k in range(n):
+                rc = L.rk_matvecs_device(dev.h, 1, hs[k % copies], op, xp, cols, None)
+                if rc:
+                    raise rkhip.RKError(rc, L.rk_last_error(dev.h).decode())
+
+        run(copies)
+        arena.begin().submit()
+        dev.graph_begin()
+        run(copies)
+        g = dev.graph_end()
+        g.launch(2)
+        reps = max(1, 400 // copies)
+        t0 = time.perf_counter()
+        g.launch(reps)
+        per = (time.perf_counter() - t0) / (reps * copies)
+        dev.profile_start()
+        run(200)
+        arena.begin().submit()
+        prof = dev.profile_stop()
+        kc, kms = prof.get("matvec_" + kind, (0, 0.0))
+        qc, qms = prof.get("act_fp8", (0, 0.0))
+        launch_us = kms / max(kc, 1) * 1e3
+        got = dev.matvecs([ms[0]], x)[0]
+        g.free()
+        arena.free()
+        for m in ms:
+            m.free()
+        r = {"format": kind, "shape": f"{rows}x{cols}", "matrix": what, "weights_MB": round((wbytes + sc.size) / 1e6, 1),
+             "us_per_product": round(per * 1e6, 3), "weights_GB_s": round((wbytes + sc.size) / per / 1e9, 1),
+             "avg_launch_us": round(launch_us, 3), "act_fp8_avg_launch_us": round(qms / max(qc, 1) * 1e3, 3),
+             "roofline_frac": round(alg / (launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
+        if not args.no_cpu and (rows, cols) in ((5120, 8192), (5120, 2304)):
+            from oracle import oracle
+
+            mv = oracle.matvec_fp8 if kind == "fp8" else oracle.matvec_fp4
+            want = mv(w, sc, x, rows, cols)
+            n, c0 = 0, time.perf_counter()
+            while time.perf_counter() - c0 < min(3.0, args.cpu_seconds):
+                mv(w, sc, x, rows, cols)
+                n += 1
+            el = time.perf_counter() - c0
+            r["bit_exact_vs_cpu"] = bool(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+            r["cpu_baseline"] = {"weights_GB_s": round(n * (wbytes + sc.size) / el / 1e9, 3), "cores": 1,
+                                 "kind": "port", "sample": f"{n} products in {el:.1f} s (scalar C restatement of "
+                                 f"MatVec{kind.upper()}, one thread)"}
+        log(f"  {kind} {rows}x{cols}: {r['us_per_product']} us/product, {r['weights_GB_s']} GB/s, "
+            f"launch {r['avg_launch_us']} us (frac {r['roofline_frac']})")
+        out.append(r)
+    return {"deepseek_mx": out}
+
+
 PMC_COPY_WORDS = 1 << 26  # the calibration copy: 256 MiB read, 256 MiB written
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "q8_matvec_config2_pmc.md")
 
@@ -639,6 +732,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-mx", action="store_true")
     ap.add_argument("--moe-layers", type=int, default=4)
     ap.add_argument("--moe-reps", type=int, default=20)
     ap.add_argument("--prefill-layers", type=int, default=28)
@@ -690,6 +784,9 @@ def main():
     if not args.no_dense:
         log("dense bench (MeasureSpeed)")
         result.update(dense_bench(dev, rkhip, args))
+    if not args.no_mx:
+        log("DeepSeek-V4.1 block-scaled products")
+        result.update(mx_bench(dev, rkhip, args))
     result["device"] = {"name": info.name.decode(), "arch": info.arch.decode(), "cu": info.compute_units}
     if not args.no_cpu:
         log("cpu baseline")

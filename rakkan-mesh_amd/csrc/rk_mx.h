@@ -10,11 +10,19 @@ namespace rk {
 // E4M3 codes and one power-of-two float32 scale per 32.
 void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s);
 
+// The device layout of E2M1 scales: a workgroup tile's rows side by side,
+// each lane's row steps together (bytes ((t·G + g)·nb + b)·RT + r for row
+// t·RT·G + r·G + g, block b; zero past the last row). Its size, and the
+// repacking of the reference layout [rows][cols/32] into it.
+int64_t mx_fp4_scale_bytes(int64_t rows, int64_t cols);
+void mx_fp4_pack_scales(const uint8_t *e8m0, int64_t rows, int64_t cols, uint8_t *dst);
+
 // internal/num/mx.go:282-334 MatVecFP8 / MatVecFP4 of an input quantized by
-// launch_act_fp8: out[r] for rows rows; w E4M3 [rows][cols] with E8M0 scales
-// [ceil(rows/32)][cols/32] (fp4 = false), or E2M1 packed [rows][cols/2]
-// with E8M0 scales [rows][cols/32] (fp4 = true). raw leaves the sums in
-// float32 instead of rounding them to bfloat16.
+// launch_act_fp8 (codes xc, scales xs): out[r] for rows rows; w E4M3
+// [rows][cols] with E8M0 scales [ceil(rows/32)][cols/32] (fp4 = false), or
+// E2M1 packed [rows][cols/2] with E8M0 scales in mx_fp4_pack_scales's
+// layout (fp4 = true). raw leaves the sums in float32 instead of rounding
+// them to bfloat16.
 void launch_mx_matvec(bool fp4, const uint8_t *w, const uint8_t *ws, int64_t rows, int64_t cols, const uint8_t *xc,
                       const float *xs, float *out, bool raw, hipStream_t s);
 

@@ -24,13 +24,16 @@
 // times the input's scale, times the weight's, the blocks added in order,
 // NaN canonical, rounded to bfloat16 (unless raw).
 //
-// Work layout: a workgroup takes RT rows; lane groups of LB lanes take one
-// 32-weight block each (lane p of a group 32/LB consecutive weights), so a
-// row's weights are read as one contiguous run by the workgroup, and each
-// lane keeps its input slice in registers for all RT rows. The terms go to
-// LDS, [row][block], and RT lanes of wave 0 add their rows' terms in block
-// order (a sequential float32 chain, lds_chain_sum). Rows wider than the
-// workgroup's blocks take several chunks, the chain carried across them.
+// Work layout: lane groups of LB lanes take one 32-weight block each (lane
+// p of a group 32/LB consecutive weights: 16-byte loads), so a row's
+// weights are read as one contiguous run, and each lane keeps its input
+// slice in registers for all the workgroup's rows. A workgroup takes RT
+// steps of G consecutive rows side by side (G > 1 for narrow rows, whose
+// G rows are one contiguous run), all RT loads issued before the first is
+// used. The terms go to LDS, [row][block], and one lane per row adds them
+// in block order (a sequential float32 chain, lds_chain_sum). Rows wider
+// than the workgroup's lanes take several chunks, the chain carried across
+// them.
 #include <algorithm>
 #include <mutex>
 
@@ -105,7 +108,15 @@ __global__ __launch_bounds__(256) void act_fp8_kernel(const float *x, int64_t n,
 #pragma unroll
     for (int o = 1; o < 32; o <<= 1) m = gomax(m, __shfl_xor(m, o, 32));  // absMax (NaN if any)
     const float s = pow2ceil(gomax(m, kActFloor) * kInv448);
-    const float q = __fdiv_rn(v, s);
+    // v / s: v times 1/s where s is a normal power of two (one rounding
+    // either way); a division for the scales of blocks with infinities or
+    // NaNs (+inf, -0)
+    const uint32_t e = f2u(s) >> 23;  // 256 for -0
+    float q;
+    if (e >= 1 && e <= 253)
+        q = v * u2f((254u - e) << 23);
+    else
+        q = __fdiv_rn(v, s);
     const uint32_t c = encode_e4m3(gomin(gomax(q, -448.0f), 448.0f));
     if (in) {
         codes[i] = (uint8_t)c;
@@ -113,144 +124,252 @@ __global__ __launch_bounds__(256) void act_fp8_kernel(const float *x, int64_t n,
     }
 }
 
-// E bytes a lane loads per row: 16, 8 or 4.
+// E bytes a lane loads per row (16, 8 or 4): buffer loads, so that a row
+// past the matrix's end reads zeros (the hardware's range check) and the
+// row's offset is a scalar added to the lane's fixed offset.
+typedef int rk_v2i __attribute__((ext_vector_type(2)));
 template <int E>
 struct Chunk;
 template <>
 struct Chunk<16> {
-    typedef uint4 T;
-    static __device__ uint32_t word(const T &v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }
+    typedef rk_v4i T;
+    static __device__ T load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, kAuxStream);
+    }
+    static __device__ uint32_t word(const T &v, int k) { return (uint32_t)v[k]; }
 };
 template <>
 struct Chunk<8> {
-    typedef uint2 T;
-    static __device__ uint32_t word(const T &v, int k) { return k == 0 ? v.x : v.y; }
+    typedef rk_v2i T;
+    static __device__ T load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b64(r, v, s, kAuxStream);
+    }
+    static __device__ uint32_t word(const T &v, int k) { return (uint32_t)v[k]; }
 };
 template <>
 struct Chunk<4> {
-    typedef uint32_t T;
-    static __device__ uint32_t word(const T &v, int) { return v; }
+    typedef int T;
+    static __device__ T load(__amdgpu_buffer_rsrc_t r, int v, int s) {
+        return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, kAuxStream);
+    }
+    static __device__ uint32_t word(const T &v, int) { return (uint32_t)v; }
 };
 
-// Terms per row in LDS: the workgroup's blocks, padded to keep rows 16-byte
-// aligned and spread over the banks.
-__device__ __host__ constexpr int term_stride(int cb) { return cb + 4; }
+// Row steps a workgroup loads at once (every lane holds RT weight chunks in
+// registers; the fastest measured on MI355X, from 4 to 16 and with a
+// persistent double-buffered variant, which was slower). For E4M3, RT
+// divides 32: a tile's rows then share one row of 32x32-block scales.
+constexpr int kMxStepsFp8 = 8;
+constexpr int kMxStepsFp4 = 8;
 
-template <bool FP4, int LB, int RT>
+// Terms per row in LDS: the row's blocks, padded to keep rows 16-byte
+// aligned and spread over the banks.
+__device__ __host__ constexpr int term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
+
+// The lane's input slice, converted once: float64 values (E4M3 weights),
+// or float16 pairs with the NaN codes' positions (E2M1 weights).
+template <bool FP4, int NE>
+struct XSlice;
+template <int NE>
+struct XSlice<false, NE> {
+    double v[NE];
+    __device__ void init(const uint32_t (&xw)[NE / 4]) {
+#pragma unroll
+        for (int k = 0; k < NE / 4; k++) {
+            const rk_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(xw[k], false);
+            const rk_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(xw[k], true);
+            v[4 * k] = lo.x, v[4 * k + 1] = lo.y, v[4 * k + 2] = hi.x, v[4 * k + 3] = hi.y;
+        }
+    }
+};
+template <int NE>
+struct XSlice<true, NE> {
+    rk_h2 h[NE / 2];
+    uint32_t nanmask;
+    __device__ void init(const uint32_t (&xw)[NE / 4]) {
+        nanmask = 0;
+#pragma unroll
+        for (int k = 0; k < NE / 4; k++) {
+            uint32_t u = xw[k];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (((u >> (8 * j)) & 0x7f) == 0x7f) {  // NaN code: 0 here, its position kept
+                    nanmask |= 1u << (4 * k + j);
+                    u &= ~(0xffu << (8 * j));
+                }
+            h[2 * k] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u, 1.0f, false);
+            h[2 * k + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u, 1.0f, true);
+        }
+    }
+};
+
+// Where a lane's loads go: G rows side by side, each lane one block of row
+// gl of each step.
+struct MxLane {
+    __amdgpu_buffer_rsrc_t rw, rsc;
+    int vo;       // the lane's byte offset in a step
+    int gl, b, nb, G;
+    int64_t rb;   // weight bytes a row
+};
+
+// Tile t's loads: RT steps of G rows (weights, then scale bytes), issued
+// unconditionally; rows past the part read zeros (buffer range check).
+template <bool FP4, bool SIDE, int LB, int RT, typename WT>
+__device__ __forceinline__ void mx_load_tile(const MxLane &L, int64_t t, WT (&wv)[RT], uint32_t (&wsv)[RT]) {
+    typedef Chunk<FP4 ? 16 / LB : 32 / LB> WC;
+    const int64_t row0 = t * RT * L.G;
+#pragma unroll
+    for (int r = 0; r < RT; r++) wv[r] = WC::load(L.rw, L.vo, (int)((row0 + (int64_t)r * L.G) * L.rb));
+    if constexpr (FP4) {
+        // the lane's RT scale bytes, stored together (tile-major layout)
+        const typename Chunk<RT>::T sb = Chunk<RT>::load(L.rsc, (L.gl * L.nb + L.b) * RT, (int)(t * L.G * L.nb * RT));
+#pragma unroll
+        for (int r = 0; r < RT; r++) wsv[r] = (Chunk<RT>::word(sb, r >> 2) >> (8 * (r & 3))) & 0xffu;
+    } else if constexpr (!SIDE) {
+        // RT divides 32: the tile's rows share one row of 32x32-block scales
+        const uint32_t s1 = __builtin_amdgcn_raw_buffer_load_b8(L.rsc, L.b, (int)((row0 >> 5) * L.nb), 0);
+#pragma unroll
+        for (int r = 0; r < RT; r++) wsv[r] = s1;
+    } else {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+            wsv[r] = __builtin_amdgcn_raw_buffer_load_b8(L.rsc, (int)((row0 + (int64_t)r * L.G + L.gl) >> 5) * L.nb + L.b,
+                                                         0, 0);
+    }
+}
+
+// One tile's terms into LDS, terms[(r·G + g)·ts + block]: the exact block
+// sums, combined over the block's LB lanes, rounded to float32, times the
+// input's scale, times the weight's.
+template <bool FP4, int LB, int RT, typename WT>
+__device__ __forceinline__ void mx_tile_terms(const WT (&wv)[RT], const uint32_t (&wsv)[RT],
+                                              const XSlice<FP4, 32 / LB> &x, float xsb, bool write, int G, int g,
+                                              int bi, int ts, float *terms) {
+    constexpr int NE = 32 / LB;
+    constexpr int WB = FP4 ? NE / 2 : NE;
+    typedef Chunk<WB> WC;
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        float t;
+        if constexpr (!FP4) {
+            double s0 = 0.0, s1 = 0.0;
+#pragma unroll
+            for (int k = 0; k < NE / 4; k++) {
+                const uint32_t u = WC::word(wv[r], k);
+                const rk_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(u, false);
+                const rk_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(u, true);
+                s0 = __builtin_fma((double)lo.x, x.v[4 * k], s0);
+                s1 = __builtin_fma((double)lo.y, x.v[4 * k + 1], s1);
+                s0 = __builtin_fma((double)hi.x, x.v[4 * k + 2], s0);
+                s1 = __builtin_fma((double)hi.y, x.v[4 * k + 3], s1);
+            }
+            double d = s0 + s1;  // exact: every partial sum is
+#pragma unroll
+            for (int o = 1; o < LB; o <<= 1) d += __shfl_xor(d, o);
+            t = (float)d;
+        } else {
+            uint32_t isum = 0;
+#pragma unroll
+            for (int k = 0; k < WB / 4; k++) {
+                const uint32_t u = WC::word(wv[r], k);  // 8 weights
+                const rk_h2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 0);
+                const rk_h2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 1);
+                const rk_h2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 2);
+                const rk_h2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 3);
+                const float f0 =
+                    __builtin_amdgcn_fdot2(w1, x.h[4 * k + 1], __builtin_amdgcn_fdot2(w0, x.h[4 * k], 0.0f, false), false);
+                const float f1 =
+                    __builtin_amdgcn_fdot2(w3, x.h[4 * k + 3], __builtin_amdgcn_fdot2(w2, x.h[4 * k + 2], 0.0f, false), false);
+                isum += (uint32_t)(int32_t)f0 + (uint32_t)(int32_t)f1;
+            }
+            if (x.nanmask) {  // rare: an infinite or NaN input in the block
+                uint32_t odd = 0;
+#pragma unroll
+                for (int i = 0; i < NE; i++) {
+                    const uint32_t nib = (WC::word(wv[r], i >> 3) >> (4 * (i & 7))) & 15u;
+                    odd ^= ((x.nanmask >> i) & 1u) & (((nib & 5u) == 1u) ? 1u : 0u);
+                }
+                isum += odd << 31;
+            }
+#pragma unroll
+            for (int o = 1; o < LB; o <<= 1) isum += (uint32_t)__shfl_xor((int)isum, o);
+            t = (float)(int32_t)isum * 0.0009765625f;  // float32(sum / 1024): one rounding
+        }
+        if (write) {
+            t = t * xsb;
+            t = t * e8m0(wsv[r]);
+            terms[(r * G + g) * ts + bi] = t;
+        }
+    }
+}
+
+template <bool FP4, int LB>
+__device__ __forceinline__ MxLane mx_lane(const uint8_t *w, const uint8_t *ws, int64_t rows, int nb, int G, int RT,
+                                          int g, bool live, int b, int p) {
+    constexpr int NE = 32 / LB, WB = FP4 ? NE / 2 : NE;
+    MxLane L;
+    L.rb = FP4 ? (int64_t)nb * 16 : (int64_t)nb * 32;
+    const int64_t tiles = (rows + RT * G - 1) / (RT * G);
+    // the part's weights and scales (under 2^31 bytes: launches are split)
+    L.rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, (int)(rows * L.rb), kRsrcWord3);
+    L.rsc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ws), 0,
+                                              (int)(FP4 ? tiles * G * nb * RT : (rows + 31) / 32 * nb), kRsrcWord3);
+    L.gl = live ? g : 0;
+    L.b = b;
+    L.nb = nb;
+    L.G = G;
+    L.vo = L.gl * (int)L.rb + b * (FP4 ? 16 : 32) + p * WB;
+    return L;
+}
+
+// A workgroup takes RT·G rows: G consecutive rows side by side (rows are
+// contiguous, so G rows of a narrow matrix read as one long run) and RT
+// such steps. Lane group lg (LB lanes) takes block lg mod nb of row lg / nb
+// within the step; rows wider than the workgroup's lanes take chunks of cb
+// blocks (G = 1), the chains carried across them.
+template <bool FP4, bool SIDE, int LB, int RT>
 __global__ __launch_bounds__(512) void mx_matvec_kernel(const uint8_t *__restrict__ w, const uint8_t *__restrict__ ws,
-                                                        int64_t rows, int cols, const uint8_t *__restrict__ xc,
+                                                        int64_t rows, int cols, int G, const uint8_t *__restrict__ xc,
                                                         const float *__restrict__ xs, float *__restrict__ out,
                                                         int raw) {
-    constexpr int NE = 32 / LB;               // weights (and inputs) per lane per row
-    constexpr int WB = FP4 ? NE / 2 : NE;     // weight bytes per lane per row
-    typedef Chunk<WB> WC;
-    typedef typename WC::T WT;
+    constexpr int NE = 32 / LB;
+    typedef typename Chunk<FP4 ? NE / 2 : NE>::T WT;
     extern __shared__ __align__(16) float terms[];
-    const int tid = threadIdx.x, p = tid % LB, bl = tid / LB;
-    const int cb = blockDim.x / LB, ts = term_stride(cb);
+    const int tid = threadIdx.x, p = tid % LB, lg = tid / LB;
     const int nb = cols >> 5;
-    const int64_t row0 = (int64_t)blockIdx.x * RT;
-    const int64_t rb = FP4 ? cols / 2 : cols;  // weight bytes per row
-    float acc = 0.0f;                          // the chain of row row0 + tid (tid < RT)
-    for (int c0 = 0; c0 < nb; c0 += cb) {       // uniform
-        const int b = min(c0 + bl, nb - 1);     // past the last block: repeat it (its terms are not added)
-        // the lane's input slice
+    const int groups = blockDim.x / LB;           // lane groups
+    const int cb = SIDE ? nb : groups;            // blocks of a row per chunk
+    const int g = SIDE ? lg / nb : 0;             // row within the step
+    const bool live = SIDE ? g < G : true;        // idle groups past G·nb
+    const int ts = term_stride(SIDE ? nb : cb);
+    const int64_t row0 = (int64_t)blockIdx.x * RT * G;
+    float acc = 0.0f;  // chain of row row0 + tid (tid < RT, G = 1)
+    for (int c0 = 0; c0 < nb; c0 += cb) {  // uniform (one pass when SIDE)
+        const int bi = SIDE ? lg % nb : lg;
+        const int b = min(c0 + bi, nb - 1);  // past the last block: repeat it (its terms are not added)
+        const MxLane L = mx_lane<FP4, LB>(w, ws, rows, nb, G, RT, g, live, b, p);
+        // the input slice first (loads complete in issue order: it is then
+        // ready while the weights are still on their way)
         uint32_t xw[NE / 4];
 #pragma unroll
         for (int k = 0; k < NE / 4; k++) xw[k] = *reinterpret_cast<const uint32_t *>(xc + b * 32 + p * NE + 4 * k);
         const float xsb = xs[b];
-        // the rows' weights: all RT loads first, consumed in order
         WT wv[RT];
-        uint32_t wsv[FP4 ? RT : 1];
-#pragma unroll
-        for (int r = 0; r < RT; r++) {
-            const int64_t rr = min(row0 + r, rows - 1);
-            wv[r] = *reinterpret_cast<const WT *>(w + rr * rb + (int64_t)b * (FP4 ? 16 : 32) + p * WB);
-            if constexpr (FP4) wsv[r] = ws[rr * nb + b];
-        }
-        float wsf = 0.0f;
-        if constexpr (!FP4) wsf = e8m0(ws[(row0 >> 5) * nb + b]);  // RT divides 32: one scale row a tile
-        if constexpr (!FP4) {
-            double xv[NE];
-#pragma unroll
-            for (int k = 0; k < NE / 4; k++) {
-                const rk_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(xw[k], false);
-                const rk_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(xw[k], true);
-                xv[4 * k] = lo.x, xv[4 * k + 1] = lo.y, xv[4 * k + 2] = hi.x, xv[4 * k + 3] = hi.y;
-            }
-#pragma unroll
-            for (int r = 0; r < RT; r++) {
-                double s0 = 0.0, s1 = 0.0;
-#pragma unroll
-                for (int k = 0; k < NE / 4; k++) {
-                    const uint32_t u = WC::word(wv[r], k);
-                    const rk_f2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(u, false);
-                    const rk_f2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(u, true);
-                    s0 = __builtin_fma((double)lo.x, xv[4 * k], s0);
-                    s1 = __builtin_fma((double)lo.y, xv[4 * k + 1], s1);
-                    s0 = __builtin_fma((double)hi.x, xv[4 * k + 2], s0);
-                    s1 = __builtin_fma((double)hi.y, xv[4 * k + 3], s1);
-                }
-                double d = s0 + s1;  // exact: every partial sum is
-#pragma unroll
-                for (int o = 1; o < LB; o <<= 1) d += __shfl_xor(d, o);
-                if (p == 0) {
-                    float t = (float)d;
-                    t = t * xsb;
-                    t = t * wsf;
-                    terms[r * ts + bl] = t;
-                }
-            }
-        } else {
-            // the input as float16 pairs; NaN codes as 0, their positions kept
-            rk_h2 xh[NE / 2];
-            uint32_t nanmask = 0;
-#pragma unroll
-            for (int k = 0; k < NE / 4; k++) {
-                uint32_t u = xw[k];
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (((u >> (8 * j)) & 0x7f) == 0x7f) {
-                        nanmask |= 1u << (4 * k + j);
-                        u &= ~(0xffu << (8 * j));
-                    }
-                xh[2 * k] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u, 1.0f, false);
-                xh[2 * k + 1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u, 1.0f, true);
-            }
-#pragma unroll
-            for (int r = 0; r < RT; r++) {
-                uint32_t isum = 0;
-#pragma unroll
-                for (int k = 0; k < WB / 4; k++) {
-                    const uint32_t u = WC::word(wv[r], k);  // 8 weights
-                    const rk_h2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 0);
-                    const rk_h2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 1);
-                    const rk_h2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 2);
-                    const rk_h2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(u, 1024.0f, 3);
-                    const float f0 = __builtin_amdgcn_fdot2(w1, xh[4 * k + 1], __builtin_amdgcn_fdot2(w0, xh[4 * k], 0.0f, false), false);
-                    const float f1 = __builtin_amdgcn_fdot2(w3, xh[4 * k + 3], __builtin_amdgcn_fdot2(w2, xh[4 * k + 2], 0.0f, false), false);
-                    isum += (uint32_t)(int32_t)f0 + (uint32_t)(int32_t)f1;
-                }
-                if (nanmask) {  // rare: an infinite or NaN input in the block
-                    uint32_t odd = 0;
-#pragma unroll
-                    for (int i = 0; i < NE; i++) {
-                        const uint32_t nib = (WC::word(wv[r], i >> 3) >> (4 * (i & 7))) & 15u;
-                        odd ^= ((nanmask >> i) & 1u) & (((nib & 5u) == 1u) ? 1u : 0u);
-                    }
-                    isum += odd << 31;
-                }
-#pragma unroll
-                for (int o = 1; o < LB; o <<= 1) isum += (uint32_t)__shfl_xor((int)isum, o);
-                if (p == 0) {
-                    float t = (float)(int32_t)isum * 0.0009765625f;  // float32(sum / 1024): one rounding
-                    t = t * xsb;
-                    t = t * e8m0(wsv[r]);
-                    terms[r * ts + bl] = t;
-                }
-            }
-        }
+        uint32_t wsv[RT];
+        mx_load_tile<FP4, SIDE, LB, RT>(L, blockIdx.x, wv, wsv);
+        XSlice<FP4, NE> x;
+        x.init(xw);
+        mx_tile_terms<FP4, LB, RT>(wv, wsv, x, xsb, p == 0 && live, G, g, bi, ts, terms);
         __syncthreads();
+        if constexpr (SIDE) {
+            // one chunk: every row's chain at once, rows strided over the threads
+            for (int rl = tid; rl < RT * G; rl += blockDim.x) {
+                if (row0 + rl >= rows) break;
+                const float v = canonical(lds_chain_sum(terms + rl * ts, nb, 0.0f));
+                out[row0 + rl] = raw ? v : round_bf16(v);
+            }
+            return;
+        }
         if (tid < RT) acc = lds_chain_sum(terms + tid * ts, min(cb, nb - c0), acc);
         __syncthreads();  // the terms are read before the next chunk writes them
     }
@@ -260,47 +379,74 @@ __global__ __launch_bounds__(512) void mx_matvec_kernel(const uint8_t *__restric
     }
 }
 
-constexpr int kMxRows = 16;  // rows a workgroup (divides 32, the E4M3 scale rows)
-
-template <bool FP4, int LB>
-void launch_mx_t(const uint8_t *w, const uint8_t *ws, int64_t rows, int cols, const uint8_t *xc, const float *xs,
-                 float *out, bool raw, int waves, hipStream_t s) {
-    static std::once_flag once;
-    std::call_once(once, [] {
-        (void)hipFuncSetAttribute((const void *)mx_matvec_kernel<FP4, LB, kMxRows>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    });
-    const int cb = 64 * waves / LB;
-    const size_t lds = (size_t)kMxRows * term_stride(cb) * 4;
-    const int64_t grid = (rows + kMxRows - 1) / kMxRows;
-    RK_LAUNCH((mx_matvec_kernel<FP4, LB, kMxRows>), dim3((unsigned)grid), dim3((unsigned)(64 * waves)), lds, s, w, ws,
-              rows, cols, xc, xs, out, raw ? 1 : 0);
-}
-
-// Lanes per block and waves per workgroup for nb blocks: the fewest idle
-// lanes over the row's chunks, then the fewest chunks, then the widest
-// loads.
-void mx_shape(bool fp4, int nb, int *lb, int *waves) {
-    const int cands8[3] = {2, 4, 8}, cands4[3] = {1, 2, 4};
-    const int *c = fp4 ? cands4 : cands8;
-    int64_t best = -1;
-    for (int i = 0; i < 3; i++) {
-        const int64_t lanes = (int64_t)nb * c[i];
-        for (int W = 1; W <= 8; W++) {
-            const int64_t per = 64 * W, chunks = (lanes + per - 1) / per;
-            if (chunks * per - lanes >= per) continue;  // a whole idle wave
-            const int64_t waste = chunks * per - lanes;
-            const int64_t key = waste * 4096 + chunks * 16 + i;
-            if (best < 0 || key < best) {
-                best = key;
-                *lb = c[i];
-                *waves = W;
-            }
+// Launch shape for nb blocks a row: lanes per block LB (the widest load
+// first: 16 bytes), rows side by side G and waves W, for the fewest idle
+// lanes; rows wider than 8 waves' lanes take chunks (G = 1).
+struct MxShape {
+    int lb, g, waves;
+};
+MxShape mx_shape(bool fp4, int nb) {
+    const int lb = fp4 ? 1 : 2;  // 16-byte loads
+    const int64_t lanes = (int64_t)nb * lb;
+    MxShape best{lb, 1, 8};
+    int64_t best_key = -1;
+    for (int W = 1; W <= 8; W++) {
+        const int64_t per = 64 * W;
+        int64_t G = std::min<int64_t>(per / lanes, 16), waste, chunks = 1;
+        if (G >= 1) {
+            waste = per - G * lanes;
+        } else {
+            G = 1;
+            chunks = (lanes + per - 1) / per;
+            waste = chunks * per - lanes;
+        }
+        if (waste >= 64) continue;  // a whole idle wave
+        // the fewest idle lanes, then the fewest chunks, then the most
+        // rows side by side
+        const int64_t key = waste * 65536 + chunks * 256 + (16 - G);  // G <= 16
+        if (best_key < 0 || key < best_key) {
+            best_key = key;
+            best = MxShape{lb, (int)G, W};
         }
     }
+    return best;
+}
+
+template <bool FP4, bool SIDE, int LB, int RT>
+void launch_mx_t(const uint8_t *w, const uint8_t *ws, int64_t rows, int cols, const uint8_t *xc, const float *xs,
+                 float *out, bool raw, int G, int waves, hipStream_t s) {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute((const void *)mx_matvec_kernel<FP4, SIDE, LB, RT>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    });
+    const int nb = cols / 32, cb = SIDE ? nb : 64 * waves / LB;
+    const size_t lds = (size_t)RT * G * term_stride(cb) * 4;
+    const int64_t per = (int64_t)RT * G;
+    const int64_t tiles = (rows + per - 1) / per;
+    RK_LAUNCH((mx_matvec_kernel<FP4, SIDE, LB, RT>), dim3((unsigned)tiles), dim3((unsigned)(64 * waves)), lds, s, w,
+              ws, rows, cols, G, xc, xs, out, raw ? 1 : 0);
 }
 
 }  // namespace
+
+int64_t mx_fp4_scale_bytes(int64_t rows, int64_t cols) {
+    const MxShape sh = mx_shape(true, (int)(cols / 32));
+    const int64_t tile = (int64_t)kMxStepsFp4 * sh.g;
+    return (rows + tile - 1) / tile * tile * (cols / 32);
+}
+
+void mx_fp4_pack_scales(const uint8_t *e8m0, int64_t rows, int64_t cols, uint8_t *dst) {
+    const MxShape sh = mx_shape(true, (int)(cols / 32));
+    const int64_t RT = kMxStepsFp4, G = sh.g, nb = cols / 32, tile = RT * G;
+    const int64_t total = mx_fp4_scale_bytes(rows, cols);
+    for (int64_t i = 0; i < total; i++) {
+        // i = ((t·G + g)·nb + b)·RT + r holds row t·tile + r·G + g, block b
+        const int64_t r = i % RT, b = (i / RT) % nb, tg = i / (RT * nb), g = tg % G, t = tg / G;
+        const int64_t row = t * tile + r * G + g;
+        dst[i] = row < rows ? e8m0[row * nb + b] : 0;
+    }
+}
 
 void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s) {
     if (n <= 0) return;
@@ -309,16 +455,24 @@ void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hi
 
 void launch_mx_matvec(bool fp4, const uint8_t *w, const uint8_t *ws, int64_t rows, int64_t cols, const uint8_t *xc,
                       const float *xs, float *out, bool raw, hipStream_t s) {
-    int lb = 2, waves = 1;
-    mx_shape(fp4, (int)(cols / 32), &lb, &waves);
-    if (fp4) {
-        if (lb == 1) launch_mx_t<true, 1>(w, ws, rows, (int)cols, xc, xs, out, raw, waves, s);
-        else if (lb == 2) launch_mx_t<true, 2>(w, ws, rows, (int)cols, xc, xs, out, raw, waves, s);
-        else launch_mx_t<true, 4>(w, ws, rows, (int)cols, xc, xs, out, raw, waves, s);
-    } else {
-        if (lb == 2) launch_mx_t<false, 2>(w, ws, rows, (int)cols, xc, xs, out, raw, waves, s);
-        else if (lb == 4) launch_mx_t<false, 4>(w, ws, rows, (int)cols, xc, xs, out, raw, waves, s);
-        else launch_mx_t<false, 8>(w, ws, rows, (int)cols, xc, xs, out, raw, waves, s);
+    const MxShape sh = mx_shape(fp4, (int)(cols / 32));
+    const int64_t rb = fp4 ? cols / 2 : cols, nb = cols / 32;
+    // parts of at most 1 GiB of weights, whole 32-row scale blocks and
+    // whole workgroup tiles (the E2M1 scales' layout)
+    const int64_t align = fp4 ? (int64_t)kMxStepsFp4 * sh.g : 32;
+    const int64_t per = std::max<int64_t>(align, ((int64_t)1 << 30) / rb / align * align);
+    for (int64_t r0 = 0; r0 < rows; r0 += per) {
+        const int64_t n = std::min(per, rows - r0);
+        const uint8_t *wp = w + r0 * rb;
+        const uint8_t *sp = ws + (fp4 ? r0 * nb : r0 / 32 * nb);  // fp4: r0 is whole tiles of nb bytes a row
+        if (fp4 && sh.g > 1)
+            launch_mx_t<true, true, 1, kMxStepsFp4>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, sh.g, sh.waves, s);
+        else if (fp4)
+            launch_mx_t<true, false, 1, kMxStepsFp4>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, 1, sh.waves, s);
+        else if (sh.g > 1)
+            launch_mx_t<false, true, 2, kMxStepsFp8>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, sh.g, sh.waves, s);
+        else
+            launch_mx_t<false, false, 2, kMxStepsFp8>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, 1, sh.waves, s);
     }
 }
 

@@ -149,7 +149,8 @@ int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const 
     }
     // E4M3 / E2M1 matrices: the input quantized once to E4M3 with block
     // scales into the scratch (internal/gpu/batch.go:221-233 QuantizeFP8),
-    // then one launch each
+    // then one launch each. (Quantizing inside the products was measured
+    // slower: every workgroup of a few rows quantizes the whole input.)
     bool mx_quantized = false;
     for (int i = 0; i < n; i++) {
         if (ms[i]->kind != RK_FP8 && ms[i]->kind != RK_FP4) continue;
@@ -499,7 +500,14 @@ int rk_matrix_upload_mx(rk_device *d, int32_t kind, int64_t rows, int64_t cols, 
     if (cols % 32 != 0) return fail(d, RK_ERR_ARGS, "gpu: block-scaled matrix of the wrong shape");
     const int64_t nb = cols / 32;
     const int64_t wbytes = kind == RK_FP8 ? rows * cols : rows * cols / 2;
-    const int64_t sbytes = kind == RK_FP8 ? (rows + 31) / 32 * nb : rows * nb;
+    // E2M1 scales are repacked into the products' tile layout
+    const int64_t sbytes = kind == RK_FP8 ? (rows + 31) / 32 * nb : mx_fp4_scale_bytes(rows, cols);
+    std::vector<uint8_t> packed;
+    if (kind == RK_FP4) {
+        packed.resize((size_t)sbytes);
+        mx_fp4_pack_scales(e8m0, rows, cols, packed.data());
+        e8m0 = packed.data();
+    }
     if (kind == RK_FP8) {  // num.ValidE4M3: the NaN codes are refused
         for (int64_t i = 0; i < wbytes; i++)
             if ((w[i] & 0x7f) == 0x7f) return fail(d, RK_ERR_ARGS, "gpu: NaN in E4M3 weights");

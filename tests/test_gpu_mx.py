@@ -317,3 +317,32 @@ def test_mx_errors(dev):
         m8.free()
         mq.free()
     assert dev.used == 0
+
+
+def test_batch_input_at_any_word(dev):
+    """Products of an input at arena words 3 and 4 (unaligned and aligned
+    to 16 bytes): the CPU's bits either way."""
+    rng = np.random.default_rng(8)
+    cols, r8, r4 = 2304, 70, 50
+    x = mx_input(rng, cols, specials=True)
+    w8, s8 = random_fp8(rng, r8, cols)
+    w4 = rng.integers(0, 256, r4 * cols // 2).astype(np.uint8)
+    s4 = random_scales(rng, r4 * cols // 32)
+    ms = [dev.upload_mx(rkhip.FP8, r8, cols, w8, s8), dev.upload_mx(rkhip.FP4, r4, cols, w4, s4)]
+    base = cols + 8
+    arena = dev.arena(base + r8 + r4 + cols, 2 * cols)
+    arena.set_quant_scratch(base + r8 + r4, base + r8 + r4 + cols // 4)
+    try:
+        for off in (3, 4):
+            b = arena.begin()
+            b.write(off, x)
+            b.matvecs(ms, [base, base + r8], off)
+            got = np.asarray(b.read(base, r8 + r4))
+            b.submit()
+            same_bits(got[:r8], oracle.matvec_fp8(w8, s8, x, r8, cols), f"fp8, input at word {off}")
+            same_bits(got[r8:], oracle.matvec_fp4(w4, s4, x, r4, cols), f"fp4, input at word {off}")
+    finally:
+        arena.free()
+        for m in ms:
+            m.free()
+    assert dev.used == 0
