@@ -176,6 +176,16 @@ int rk_batch_read(rk_batch *b, int64_t off, float *dst, int64_t n);
 int rk_batch_matvecs(rk_batch *b, int32_t n, rk_matrix *const *ms, const int64_t *out_offs, int64_t in_off);
 /* internal/gpu/batch.go:277-280 Quantize: n floats at in into the scratch. */
 int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n);
+/* internal/gpu/dsbatch.go:142-172 ExpertMatVecs: m holds E2M1 experts of
+ * per_expert rows each (a multiple of 8 here; RK_ERR_UNSUPPORTED otherwise);
+ * slot k (of slots) multiplies expert ids[k] (uint32 words at arena word
+ * `ids`; an id past the last expert is skipped) by input k / div (div 0:
+ * one input for all) at word in + (k/div)·in_stride into out + k·out_stride.
+ * The inputs are quantized into the arena's quantize scratch, which must be
+ * set and hold them (inputs·cols <= 2^18). */
+int rk_batch_expert_matvecs(rk_batch *b, rk_matrix *m, int64_t per_expert, int64_t ids, int32_t slots, int64_t in,
+                            int64_t in_stride, int32_t div, int64_t out, int64_t out_stride);
+
 /* internal/gpu/batch.go:271-275 QuantizeFP8: n floats at word `in` to E4M3
  * codes and block scales in the arena's quantize scratch (codes at qx_off,
  * scales at xs_off), as num.QuantizeActFP8. */

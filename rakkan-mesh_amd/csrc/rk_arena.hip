@@ -313,6 +313,48 @@ int rk_batch_quantize_fp8(rk_batch *b, int64_t in, int64_t n) {
     return launched(b, "quantize");
 }
 
+// internal/gpu/dsbatch.go:142-172 ExpertMatVecs: the inputs quantized into
+// the arena's quantize scratch (input k at k·cols codes), then one launch
+// over the slots.
+int rk_batch_expert_matvecs(rk_batch *b, rk_matrix *m, int64_t per_expert, int64_t ids, int32_t slots, int64_t in,
+                            int64_t in_stride, int32_t div, int64_t out, int64_t out_stride) {
+    if (!b) return RK_ERR_ARGS;
+    if (b->err) return b->err;
+    rk_arena *a = b->a;
+    rk_device *d = a->d;
+    if (!m || m->d != d || m->kind != RK_FP4 || per_expert <= 0 || m->rows % per_expert != 0)
+        return latch(b, fail(d, RK_ERR_ARGS, "gpu: not a matrix of E2M1 experts"));
+    if (per_expert % 8 != 0)
+        return latch(b, fail(d, RK_ERR_UNSUPPORTED, "gpu: experts of %lld rows (this build takes multiples of 8)",
+                             (long long)per_expert));
+    if (slots <= 0) return RK_OK;
+    if (div < 0) return latch(b, fail(d, RK_ERR_ARGS, "rk_batch_expert_matvecs: negative div"));
+    if (div == 0) div = slots;
+    if (a->qx_off < 0) return latch(b, fail(d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
+    const int64_t cols = m->cols, inputs = (slots + div - 1) / div;
+    if (inputs * cols > kMaxCols)
+        return latch(b, fail(d, RK_ERR_ARGS, "gpu: %lld inputs of %lld floats exceed the quantize scratch",
+                             (long long)inputs, (long long)cols));
+    const float *idw = span(b, ids, slots, "expert ids");
+    if (!idw) return b->err;
+    for (int32_t k = 0; k < slots; k++)
+        if (!span(b, out + k * out_stride, per_expert, "expert output")) return b->err;
+    float *o = a->buf + out;
+    hipStream_t s = d->stream;
+    {
+        ProfScope p(d, s, "act_fp8");
+        for (int64_t k = 0; k < inputs; k++) {
+            const float *x = span(b, in + k * in_stride, cols, "expert input");
+            if (!x) return b->err;
+            launch_act_fp8(x, cols, reinterpret_cast<uint8_t *>(a->qx) + k * cols, a->xs + k * (cols / 32), s);
+        }
+    }
+    ProfScope p(d, s, "matvec_fp4_experts");
+    launch_mx_experts(m->w, m->e8m0, m->rows / per_expert, per_expert, cols, reinterpret_cast<const uint32_t *>(idw),
+                      slots, div, reinterpret_cast<const uint8_t *>(a->qx), a->xs, o, out_stride, m->raw != 0, s);
+    return launched(b, "expert products");
+}
+
 // internal/gpu/batch.go:282-287 RMSNorm.
 int rk_batch_rmsnorm(rk_batch *b, rk_vectors *vecs, int64_t in, int64_t out, int64_t w, int32_t n, int32_t segs,
                      int64_t stride, float recip_n, float eps) {

@@ -10,10 +10,10 @@ namespace rk {
 // E4M3 codes and one power-of-two float32 scale per 32.
 void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s);
 
-// The device layout of E2M1 scales: a workgroup tile's rows side by side,
-// each lane's row steps together (bytes ((t·G + g)·nb + b)·RT + r for row
-// t·RT·G + r·G + g, block b; zero past the last row). Its size, and the
-// repacking of the reference layout [rows][cols/32] into it.
+// The device layout of E2M1 scales: blocks of RT = 8 rows, a lane's rows
+// together (byte (k·nb + b)·8 + r for row 8k + r, block b; zero past the
+// last row). Its size, and the repacking of the reference layout
+// [rows][cols/32] into it.
 int64_t mx_fp4_scale_bytes(int64_t rows, int64_t cols);
 void mx_fp4_pack_scales(const uint8_t *e8m0, int64_t rows, int64_t cols, uint8_t *dst);
 
@@ -25,5 +25,14 @@ void mx_fp4_pack_scales(const uint8_t *e8m0, int64_t rows, int64_t cols, uint8_t
 // them to bfloat16.
 void launch_mx_matvec(bool fp4, const uint8_t *w, const uint8_t *ws, int64_t rows, int64_t cols, const uint8_t *xc,
                       const float *xs, float *out, bool raw, hipStream_t s);
+
+// internal/gpu/dsbatch.go:142-172 ExpertMatVecs: E2M1 experts of per_expert
+// rows stacked in w (experts of them; per_expert a multiple of 8); slot y
+// (of slots) multiplies expert ids[y] (device memory; ids not below experts
+// are skipped) by input y / div (codes xc + (y/div)·cols, scales
+// xs + (y/div)·cols/32) into out + y·out_stride.
+void launch_mx_experts(const uint8_t *w, const uint8_t *ws, int64_t experts, int64_t per_expert, int64_t cols,
+                       const uint32_t *ids, int slots, int div, const uint8_t *xc, const float *xs, float *out,
+                       int64_t out_stride, bool raw, hipStream_t s);
 
 }  // namespace rk

@@ -166,6 +166,15 @@ constexpr int kMxStepsFp4 = 8;
 // aligned and spread over the banks.
 __device__ __host__ constexpr int term_stride(int nb) { return ((nb + 3) & ~3) + 4; }
 
+// Selected experts (internal/gpu/dsbatch.go:142-172 ExpertMatVecs): slot y
+// of the launch multiplies expert ids[y] - e0 (if below experts) of S.per
+// rows by input y / div into out + y·out_stride. ids null: one product.
+struct MxSlots {
+    const uint32_t *ids;
+    int64_t per, out_stride;
+    int32_t e0, experts, div;
+};
+
 // The lane's input slice, converted once: float64 values (E4M3 weights),
 // or float16 pairs with the NaN codes' positions (E2M1 weights).
 template <bool FP4, int NE>
@@ -212,17 +221,18 @@ struct MxLane {
     int64_t rb;   // weight bytes a row
 };
 
-// Tile t's loads: RT steps of G rows (weights, then scale bytes), issued
+// Tile t's loads: RT steps, step r taking row g·RT + r of the tile for each
+// of the G rows side by side (weights, then scale bytes), issued
 // unconditionally; rows past the part read zeros (buffer range check).
 template <bool FP4, bool SIDE, int LB, int RT, typename WT>
 __device__ __forceinline__ void mx_load_tile(const MxLane &L, int64_t t, WT (&wv)[RT], uint32_t (&wsv)[RT]) {
     typedef Chunk<FP4 ? 16 / LB : 32 / LB> WC;
     const int64_t row0 = t * RT * L.G;
 #pragma unroll
-    for (int r = 0; r < RT; r++) wv[r] = WC::load(L.rw, L.vo, (int)((row0 + (int64_t)r * L.G) * L.rb));
+    for (int r = 0; r < RT; r++) wv[r] = WC::load(L.rw, L.vo, (int)((row0 + r) * L.rb));
     if constexpr (FP4) {
-        // the lane's RT scale bytes, stored together (tile-major layout)
-        const typename Chunk<RT>::T sb = Chunk<RT>::load(L.rsc, (L.gl * L.nb + L.b) * RT, (int)(t * L.G * L.nb * RT));
+        // the lane's RT rows' scale bytes, stored together (blocks of RT rows)
+        const typename Chunk<RT>::T sb = Chunk<RT>::load(L.rsc, (L.gl * L.nb + L.b) * RT, (int)(row0 * L.nb));
 #pragma unroll
         for (int r = 0; r < RT; r++) wsv[r] = (Chunk<RT>::word(sb, r >> 2) >> (8 * (r & 3))) & 0xffu;
     } else if constexpr (!SIDE) {
@@ -233,12 +243,11 @@ __device__ __forceinline__ void mx_load_tile(const MxLane &L, int64_t t, WT (&wv
     } else {
 #pragma unroll
         for (int r = 0; r < RT; r++)
-            wsv[r] = __builtin_amdgcn_raw_buffer_load_b8(L.rsc, (int)((row0 + (int64_t)r * L.G + L.gl) >> 5) * L.nb + L.b,
-                                                         0, 0);
+            wsv[r] = __builtin_amdgcn_raw_buffer_load_b8(L.rsc, (int)((row0 + L.gl * RT + r) >> 5) * L.nb + L.b, 0, 0);
     }
 }
 
-// One tile's terms into LDS, terms[(r·G + g)·ts + block]: the exact block
+// One tile's terms into LDS, terms[(g·RT + r)·ts + block]: the exact block
 // sums, combined over the block's LB lanes, rounded to float32, times the
 // input's scale, times the weight's.
 template <bool FP4, int LB, int RT, typename WT>
@@ -298,7 +307,7 @@ __device__ __forceinline__ void mx_tile_terms(const WT (&wv)[RT], const uint32_t
         if (write) {
             t = t * xsb;
             t = t * e8m0(wsv[r]);
-            terms[(r * G + g) * ts + bi] = t;
+            terms[(g * RT + r) * ts + bi] = t;
         }
     }
 }
@@ -309,29 +318,44 @@ __device__ __forceinline__ MxLane mx_lane(const uint8_t *w, const uint8_t *ws, i
     constexpr int NE = 32 / LB, WB = FP4 ? NE / 2 : NE;
     MxLane L;
     L.rb = FP4 ? (int64_t)nb * 16 : (int64_t)nb * 32;
-    const int64_t tiles = (rows + RT * G - 1) / (RT * G);
     // the part's weights and scales (under 2^31 bytes: launches are split)
     L.rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(w), 0, (int)(rows * L.rb), kRsrcWord3);
     L.rsc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(ws), 0,
-                                              (int)(FP4 ? tiles * G * nb * RT : (rows + 31) / 32 * nb), kRsrcWord3);
+                                              (int)(FP4 ? (rows + RT - 1) / RT * RT * nb : (rows + 31) / 32 * nb),
+                                              kRsrcWord3);
     L.gl = live ? g : 0;
     L.b = b;
     L.nb = nb;
     L.G = G;
-    L.vo = L.gl * (int)L.rb + b * (FP4 ? 16 : 32) + p * WB;
+    L.vo = L.gl * RT * (int)L.rb + b * (FP4 ? 16 : 32) + p * WB;
     return L;
 }
 
-// A workgroup takes RT·G rows: G consecutive rows side by side (rows are
-// contiguous, so G rows of a narrow matrix read as one long run) and RT
-// such steps. Lane group lg (LB lanes) takes block lg mod nb of row lg / nb
+// A workgroup takes RT·G rows: G runs of RT consecutive rows side by side
+// (a step reads G rows at once; rows are contiguous, so a narrow matrix's
+// rows read as long runs), RT steps. Lane group lg (LB lanes) takes block lg mod nb of row lg / nb
 // within the step; rows wider than the workgroup's lanes take chunks of cb
 // blocks (G = 1), the chains carried across them.
 template <bool FP4, bool SIDE, int LB, int RT>
 __global__ __launch_bounds__(512) void mx_matvec_kernel(const uint8_t *__restrict__ w, const uint8_t *__restrict__ ws,
                                                         int64_t rows, int cols, int G, const uint8_t *__restrict__ xc,
                                                         const float *__restrict__ xs, float *__restrict__ out,
-                                                        int raw) {
+                                                        int raw, MxSlots S) {
+    if (S.ids) {
+        // slot blockIdx.y: the expert its id names (rows experts of S.per
+        // rows from w), its input, its output; ids outside the part are
+        // another launch's (uniform per workgroup)
+        const uint32_t e = S.ids[blockIdx.y] - (uint32_t)S.e0;
+        if (e >= (uint32_t)S.experts) return;
+        const int64_t nb = cols >> 5;
+        w += (int64_t)e * S.per * (FP4 ? cols / 2 : cols);
+        ws += FP4 ? (int64_t)e * S.per * nb : (int64_t)e * S.per / 32 * nb;
+        rows = S.per;
+        const int inp = blockIdx.y / S.div;
+        xc += (int64_t)inp * cols;
+        xs += (int64_t)inp * nb;
+        out += blockIdx.y * S.out_stride;
+    }
     constexpr int NE = 32 / LB;
     typedef typename Chunk<FP4 ? NE / 2 : NE>::T WT;
     extern __shared__ __align__(16) float terms[];
@@ -414,7 +438,7 @@ MxShape mx_shape(bool fp4, int nb) {
 
 template <bool FP4, bool SIDE, int LB, int RT>
 void launch_mx_t(const uint8_t *w, const uint8_t *ws, int64_t rows, int cols, const uint8_t *xc, const float *xs,
-                 float *out, bool raw, int G, int waves, hipStream_t s) {
+                 float *out, bool raw, int G, int waves, const MxSlots &S, int slots, hipStream_t s) {
     static std::once_flag once;
     std::call_once(once, [] {
         (void)hipFuncSetAttribute((const void *)mx_matvec_kernel<FP4, SIDE, LB, RT>,
@@ -424,26 +448,34 @@ void launch_mx_t(const uint8_t *w, const uint8_t *ws, int64_t rows, int cols, co
     const size_t lds = (size_t)RT * G * term_stride(cb) * 4;
     const int64_t per = (int64_t)RT * G;
     const int64_t tiles = (rows + per - 1) / per;
-    RK_LAUNCH((mx_matvec_kernel<FP4, SIDE, LB, RT>), dim3((unsigned)tiles), dim3((unsigned)(64 * waves)), lds, s, w,
-              ws, rows, cols, G, xc, xs, out, raw ? 1 : 0);
+    RK_LAUNCH((mx_matvec_kernel<FP4, SIDE, LB, RT>), dim3((unsigned)tiles, (unsigned)slots), dim3((unsigned)(64 * waves)),
+              lds, s, w, ws, rows, cols, G, xc, xs, out, raw ? 1 : 0, S);
+}
+
+void launch_mx_any(bool fp4, const MxShape &sh, const uint8_t *w, const uint8_t *ws, int64_t rows, int cols,
+                   const uint8_t *xc, const float *xs, float *out, bool raw, const MxSlots &S, int slots,
+                   hipStream_t s) {
+    if (fp4 && sh.g > 1)
+        launch_mx_t<true, true, 1, kMxStepsFp4>(w, ws, rows, cols, xc, xs, out, raw, sh.g, sh.waves, S, slots, s);
+    else if (fp4)
+        launch_mx_t<true, false, 1, kMxStepsFp4>(w, ws, rows, cols, xc, xs, out, raw, 1, sh.waves, S, slots, s);
+    else if (sh.g > 1)
+        launch_mx_t<false, true, 2, kMxStepsFp8>(w, ws, rows, cols, xc, xs, out, raw, sh.g, sh.waves, S, slots, s);
+    else
+        launch_mx_t<false, false, 2, kMxStepsFp8>(w, ws, rows, cols, xc, xs, out, raw, 1, sh.waves, S, slots, s);
 }
 
 }  // namespace
 
 int64_t mx_fp4_scale_bytes(int64_t rows, int64_t cols) {
-    const MxShape sh = mx_shape(true, (int)(cols / 32));
-    const int64_t tile = (int64_t)kMxStepsFp4 * sh.g;
-    return (rows + tile - 1) / tile * tile * (cols / 32);
+    return (rows + kMxStepsFp4 - 1) / kMxStepsFp4 * kMxStepsFp4 * (cols / 32);
 }
 
 void mx_fp4_pack_scales(const uint8_t *e8m0, int64_t rows, int64_t cols, uint8_t *dst) {
-    const MxShape sh = mx_shape(true, (int)(cols / 32));
-    const int64_t RT = kMxStepsFp4, G = sh.g, nb = cols / 32, tile = RT * G;
-    const int64_t total = mx_fp4_scale_bytes(rows, cols);
+    const int64_t RT = kMxStepsFp4, nb = cols / 32, total = mx_fp4_scale_bytes(rows, cols);
     for (int64_t i = 0; i < total; i++) {
-        // i = ((t·G + g)·nb + b)·RT + r holds row t·tile + r·G + g, block b
-        const int64_t r = i % RT, b = (i / RT) % nb, tg = i / (RT * nb), g = tg % G, t = tg / G;
-        const int64_t row = t * tile + r * G + g;
+        // i = (k·nb + b)·RT + r holds row k·RT + r, block b
+        const int64_t r = i % RT, b = (i / RT) % nb, row = i / (RT * nb) * RT + r;
         dst[i] = row < rows ? e8m0[row * nb + b] : 0;
     }
 }
@@ -457,22 +489,30 @@ void launch_mx_matvec(bool fp4, const uint8_t *w, const uint8_t *ws, int64_t row
                       const float *xs, float *out, bool raw, hipStream_t s) {
     const MxShape sh = mx_shape(fp4, (int)(cols / 32));
     const int64_t rb = fp4 ? cols / 2 : cols, nb = cols / 32;
-    // parts of at most 1 GiB of weights, whole 32-row scale blocks and
-    // whole workgroup tiles (the E2M1 scales' layout)
-    const int64_t align = fp4 ? (int64_t)kMxStepsFp4 * sh.g : 32;
+    // parts of at most 1 GiB of weights, whole 32-row scale blocks (and so
+    // whole blocks of the E2M1 scales' RT rows)
+    const int64_t align = 32;
     const int64_t per = std::max<int64_t>(align, ((int64_t)1 << 30) / rb / align * align);
+    const MxSlots none{nullptr, 0, 0, 0, 0, 1};
     for (int64_t r0 = 0; r0 < rows; r0 += per) {
         const int64_t n = std::min(per, rows - r0);
-        const uint8_t *wp = w + r0 * rb;
-        const uint8_t *sp = ws + (fp4 ? r0 * nb : r0 / 32 * nb);  // fp4: r0 is whole tiles of nb bytes a row
-        if (fp4 && sh.g > 1)
-            launch_mx_t<true, true, 1, kMxStepsFp4>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, sh.g, sh.waves, s);
-        else if (fp4)
-            launch_mx_t<true, false, 1, kMxStepsFp4>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, 1, sh.waves, s);
-        else if (sh.g > 1)
-            launch_mx_t<false, true, 2, kMxStepsFp8>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, sh.g, sh.waves, s);
-        else
-            launch_mx_t<false, false, 2, kMxStepsFp8>(wp, sp, n, (int)cols, xc, xs, out + r0, raw, 1, sh.waves, s);
+        launch_mx_any(fp4, sh, w + r0 * rb, ws + (fp4 ? r0 * nb : r0 / 32 * nb), n, (int)cols, xc, xs, out + r0, raw,
+                      none, 1, s);
+    }
+}
+
+void launch_mx_experts(const uint8_t *w, const uint8_t *ws, int64_t experts, int64_t per_expert, int64_t cols,
+                       const uint32_t *ids, int slots, int div, const uint8_t *xc, const float *xs, float *out,
+                       int64_t out_stride, bool raw, hipStream_t s) {
+    const MxShape sh = mx_shape(true, (int)(cols / 32));
+    const int64_t rb = cols / 2, nb = cols / 32;
+    // parts of whole experts, at most 1 GiB of weights each
+    const int64_t per = std::max<int64_t>(1, ((int64_t)1 << 30) / rb / per_expert);
+    for (int64_t e0 = 0; e0 < experts; e0 += per) {
+        const int64_t ne = std::min(per, experts - e0);
+        const MxSlots S{ids, per_expert, out_stride, (int32_t)e0, (int32_t)ne, div};
+        launch_mx_any(true, sh, w + e0 * per_expert * rb, ws + e0 * per_expert * nb, per_expert, (int)cols, xc, xs, out,
+                      raw, S, slots, s);
     }
 }
 

@@ -48,6 +48,7 @@ SIGNATURES = {
     "rk_matrix_upload_mx": (ctypes.c_int, [P, I32, I64, I64, P, P, P]),
     "rk_matrix_set_raw": (ctypes.c_int, [P, I32]),
     "rk_batch_quantize_fp8": (ctypes.c_int, [P, I64, I64]),
+    "rk_batch_expert_matvecs": (ctypes.c_int, [P, P, I64, I64, I32, I64, I64, I32, I64, I64]),
     "rk_matrix_bytes": (I64, [P]),
     "rk_matvecs": (ctypes.c_int, [P, I32, P, P, P, I64]),
     "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
@@ -244,6 +245,11 @@ class Batch:
 
     def quantize_fp8(self, inp, n):
         return lib().rk_batch_quantize_fp8(self.h, inp, n)
+
+    def expert_matvecs(self, m, per_expert, ids, slots, inp, in_stride, div, out, out_stride):
+        """internal/gpu Batch.ExpertMatVecs (ids: arena word of uint32 expert ids)."""
+        return lib().rk_batch_expert_matvecs(self.h, m.h, per_expert, ids, slots, inp, in_stride, div, out,
+                                             out_stride)
 
     def rmsnorm(self, vecs, inp, out, w, n, segs, stride, recip_n, eps):
         return lib().rk_batch_rmsnorm(self.h, vecs.h, inp, out, w, n, segs, stride, float(recip_n), float(eps))

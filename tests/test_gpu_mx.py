@@ -346,3 +346,46 @@ def test_batch_input_at_any_word(dev):
         for m in ms:
             m.free()
     assert dev.used == 0
+
+
+@pytest.mark.parametrize("cols,div", [(2304, 0), (2304, 1), (5120, 2)])
+def test_expert_matvecs(dev, cols, div):
+    """internal/gpu/dsbatch.go:142-172 ExpertMatVecs: selected E2M1 experts
+    (ids in arena words, repeats allowed, an id past the last expert
+    skipped) times inputs shared by all slots (div 0), one a slot (div 1) or
+    one per two slots, each slot's output the CPU's product of its expert
+    and input; the skipped slot's output is left as it was."""
+    rng = np.random.default_rng(cols + div)
+    E, P = 5, 40
+    ids = np.array([3, 0, 3, 7, 1, 4], np.uint32)
+    slots = ids.size
+    w = rng.integers(0, 256, E * P * cols // 2).astype(np.uint8)
+    s = random_scales(rng, E * P * cols // 32)
+    d = slots if div == 0 else div
+    inputs = (slots + d - 1) // d
+    xs = [mx_input(rng, cols, specials=True) for _ in range(inputs)]
+    m = dev.upload_mx(rkhip.FP4, E * P, cols, w, s)
+    in0, idw, out0 = 0, inputs * cols, inputs * cols + 8
+    words = out0 + slots * P + 64
+    arena = dev.arena(words + cols, 2 * words)
+    arena.set_quant_scratch(words, words + cols // 4)
+    try:
+        b = arena.begin()
+        for k, x in enumerate(xs):
+            b.write(in0 + k * cols, x)
+        b.write(idw, ids.view(np.float32))
+        b.write(out0, np.full(slots * P, 7.0, np.float32))
+        assert b.expert_matvecs(m, P, idw, slots, in0, cols, div, out0, P) == 0
+        got = np.asarray(b.read(out0, slots * P)).reshape(slots, P)
+        b.submit()
+        for k, e in enumerate(ids):
+            if e >= E:
+                assert np.all(got[k] == 7.0), "skipped slot written"
+                continue
+            want = oracle.matvec_fp4(w[e * P * cols // 2:(e + 1) * P * cols // 2], s[e * P * cols // 32:(e + 1) * P * cols // 32],
+                                     xs[k // d], P, cols)
+            same_bits(got[k], want, f"slot {k} expert {e}")
+    finally:
+        arena.free()
+        m.free()
+    assert dev.used == 0
