@@ -372,6 +372,59 @@ def mx_bench(dev, rkhip, args):
         log(f"  {kind} {rows}x{cols}: {r['us_per_product']} us/product, {r['weights_GB_s']} GB/s, "
             f"launch {r['avg_launch_us']} us (frac {r['roofline_frac']})")
         out.append(r)
+    # selected experts (ExpertMatVecs): 6 of 64 E2M1 experts of 2304 rows a
+    # call, the ids rotated over 10 sets (60 experts, past the MALL)
+    E, P, cols, slots = 64, 2304, 5120, 6
+    nb = cols // 32
+    w = rng.integers(0, 256, E * P * cols // 2, dtype=np.uint8)
+    sc = rng.integers(118, 128, E * P * nb).astype(np.uint8)
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    m = dev.upload_mx(rkhip.FP4, E * P, cols, w, sc)
+    sets = [np.arange(slots, dtype=np.uint32) * 10 + k for k in range(10)]
+    idw, outw = cols, cols + 64
+    qx = outw + slots * P
+    arena = dev.arena(qx + 2 * cols, 2 * cols + slots * P)
+    arena.set_quant_scratch(qx, qx + cols // 4)
+    b = arena.begin()
+    b.write(0, x)
+    for k, ids in enumerate(sets):
+        b.write(idw + 6 * k, ids.view(np.float32))
+    b.submit()
+
+    def call(k):
+        bb = arena.begin()
+        bb.expert_matvecs(m, P, idw + 6 * (k % 10), slots, 0, cols, 0, outw, P)
+        bb.submit()
+
+    for k in range(10):
+        call(k)
+    dev.profile_start()
+    for k in range(200):
+        call(k)
+    prof = dev.profile_stop()
+    kc, kms = prof.get("matvec_fp4_experts", (0, 0.0))
+    launch_us = kms / max(kc, 1) * 1e3
+    ebytes = slots * (P * cols // 2 + P * nb)
+    alg = ebytes + cols + 4 * nb + 4 * slots * P
+    b = arena.begin()
+    b.expert_matvecs(m, P, idw, slots, 0, cols, 0, outw, P)
+    got = np.asarray(b.read(outw, slots * P)).reshape(slots, P)
+    b.submit()
+    r = {"format": "fp4", "shape": f"{slots} of {E} experts, {P}x{cols} each", "matrix": "ExpertMatVecs: one token's "
+         "routed experts' gate rows", "weights_MB": round(ebytes / 1e6, 1), "avg_launch_us": round(launch_us, 3),
+         "weights_GB_s_in_launch": round(ebytes / (launch_us * 1e-6) / 1e9, 1),
+         "roofline_frac": round(alg / (launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    if not args.no_cpu:
+        from oracle import oracle
+
+        e = int(sets[0][2])
+        want = oracle.matvec_fp4(w[e * P * cols // 2:(e + 1) * P * cols // 2], sc[e * P * nb:(e + 1) * P * nb], x, P,
+                                 cols)
+        r["bit_exact_vs_cpu"] = bool(np.array_equal(got[2].view(np.uint32), want.view(np.uint32)))
+    log(f"  fp4 experts {slots}x{P}x{cols}: launch {r['avg_launch_us']} us (frac {r['roofline_frac']})")
+    out.append(r)
+    arena.free()
+    m.free()
     return {"deepseek_mx": out}
 
 
