@@ -186,6 +186,14 @@ int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n);
 int rk_batch_expert_matvecs(rk_batch *b, rk_matrix *m, int64_t per_expert, int64_t ids, int32_t slots, int64_t in,
                             int64_t in_stride, int32_t div, int64_t out, int64_t out_stride);
 
+/* internal/gpu/dsbatch.go:174-210 MatVecsBatch: m times n inputs at words
+ * in + j·in_stride into out + j·out_stride, each output MatVecs' bits. An
+ * E4M3 matrix is read once for up to 16 inputs (the inputs quantized into
+ * the arena's quantize scratch, which must be set); other matrices take one
+ * product an input. */
+int rk_batch_matvecs_batch(rk_batch *b, rk_matrix *m, int64_t out, int64_t out_stride, int64_t in, int64_t in_stride,
+                           int32_t n);
+
 /* internal/gpu/batch.go:271-275 QuantizeFP8: n floats at word `in` to E4M3
  * codes and block scales in the arena's quantize scratch (codes at qx_off,
  * scales at xs_off), as num.QuantizeActFP8. */

@@ -49,6 +49,7 @@ SIGNATURES = {
     "rk_matrix_set_raw": (ctypes.c_int, [P, I32]),
     "rk_batch_quantize_fp8": (ctypes.c_int, [P, I64, I64]),
     "rk_batch_expert_matvecs": (ctypes.c_int, [P, P, I64, I64, I32, I64, I64, I32, I64, I64]),
+    "rk_batch_matvecs_batch": (ctypes.c_int, [P, P, I64, I64, I64, I64, I32]),
     "rk_matrix_bytes": (I64, [P]),
     "rk_matvecs": (ctypes.c_int, [P, I32, P, P, P, I64]),
     "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
@@ -245,6 +246,10 @@ class Batch:
 
     def quantize_fp8(self, inp, n):
         return lib().rk_batch_quantize_fp8(self.h, inp, n)
+
+    def matvecs_batch(self, m, out, out_stride, inp, in_stride, n):
+        """internal/gpu Batch.MatVecsBatch."""
+        return lib().rk_batch_matvecs_batch(self.h, m.h, out, out_stride, inp, in_stride, n)
 
     def expert_matvecs(self, m, per_expert, ids, slots, inp, in_stride, div, out, out_stride):
         """internal/gpu Batch.ExpertMatVecs (ids: arena word of uint32 expert ids)."""

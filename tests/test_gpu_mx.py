@@ -389,3 +389,36 @@ def test_expert_matvecs(dev, cols, div):
         arena.free()
         m.free()
     assert dev.used == 0
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 32), (300, 896), (1000, 1280), (40, 5120), (33, 9216)])
+def test_matvecs_batch(dev, rows, cols):
+    """internal/gpu/mx_test.go:371-420 MatVecsBatch: an E4M3 matrix times
+    1, 3, 8, 11 and 17 inputs (two launches past 16; 9216 columns: one
+    product an input), rounded and raw, each output the CPU's product."""
+    rng = np.random.default_rng(rows + cols)
+    w, s = random_fp8(rng, rows, cols)
+    m = dev.upload_mx(rkhip.FP8, rows, cols, w, s)
+    nmax = 17
+    words = nmax * cols + nmax * rows + 64
+    arena = dev.arena(words + cols, nmax * (cols + rows) + 64)
+    arena.set_quant_scratch(words, words + cols // 4)
+    try:
+        for raw in (False, True):
+            m.set_raw(raw)
+            for n in (1, 3, 8, 11, 17):
+                xs = [mx_input(rng, cols) for _ in range(n)]
+                b = arena.begin()
+                for j in range(n):
+                    b.write(j * cols, xs[j])
+                out = n * cols
+                assert b.matvecs_batch(m, out, rows, 0, cols, n) == 0
+                got = np.asarray(b.read(out, n * rows)).reshape(n, rows)
+                b.submit()
+                for j in range(n):
+                    same_bits(got[j], oracle.matvec_fp8(w, s, xs[j], rows, cols, bf16=not raw),
+                              f"{rows}x{cols} input {j} of {n} raw {raw}")
+    finally:
+        arena.free()
+        m.free()
+    assert dev.used == 0
