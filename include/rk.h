@@ -187,10 +187,8 @@ int rk_batch_expert_matvecs(rk_batch *b, rk_matrix *m, int64_t per_expert, int64
                             int64_t in_stride, int32_t div, int64_t out, int64_t out_stride);
 
 /* internal/gpu/dsbatch.go:174-210 MatVecsBatch: m times n inputs at words
- * in + j·in_stride into out + j·out_stride, each output MatVecs' bits. An
- * E4M3 matrix is read once for up to 16 inputs (the inputs quantized into
- * the arena's quantize scratch, which must be set); other matrices take one
- * product an input. */
+ * in + j·in_stride into out + j·out_stride, each output MatVecs' bits (one
+ * product an input here; the weights are read once an input). */
 int rk_batch_matvecs_batch(rk_batch *b, rk_matrix *m, int64_t out, int64_t out_stride, int64_t in, int64_t in_stride,
                            int32_t n);
 

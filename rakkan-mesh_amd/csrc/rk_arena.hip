@@ -356,46 +356,23 @@ int rk_batch_expert_matvecs(rk_batch *b, rk_matrix *m, int64_t per_expert, int64
     return launched(b, "expert products");
 }
 
-// internal/gpu/dsbatch.go:174-210 MatVecsBatch: an E4M3 matrix times n
-// inputs, the weights read once per launch of up to 16 inputs (as many as
-// the quantize scratch and LDS hold); other matrices, and rows too wide for
-// one chunk, one product an input (as the reference does for them).
+// internal/gpu/dsbatch.go:174-210 MatVecsBatch: m times n inputs, one
+// product an input (each input quantized once). A kernel reading an E4M3
+// matrix once for several inputs measured slower on MI355X than the
+// products one by one (its float64 block sums per input make it
+// compute-bound: 14.5 µs an input against about 10 µs a product at
+// 5120x8192), so the weights are read once an input.
 int rk_batch_matvecs_batch(rk_batch *b, rk_matrix *m, int64_t out, int64_t out_stride, int64_t in, int64_t in_stride,
                            int32_t n) {
     if (!b) return RK_ERR_ARGS;
     if (b->err) return b->err;
-    rk_arena *a = b->a;
-    rk_device *d = a->d;
-    if (!m || m->d != d) return latch(b, fail(d, RK_ERR_ARGS, "gpu: matrix on another device"));
-    if (n <= 0) return RK_OK;
-    const int64_t cols = m->cols;
-    const int most = m->kind == RK_FP8 ? std::min<int64_t>(mx_batch_inputs_max(cols), kMaxCols / cols) : 0;
-    if (most <= 0) {
-        for (int32_t j = 0; j < n; j++) {
-            const int64_t o = out + j * out_stride;
-            int rc = rk_batch_matvecs(b, 1, &m, &o, in + j * in_stride);
-            if (rc) return rc;
-        }
-        return RK_OK;
+    if (!m || m->d != b->a->d) return latch(b, fail(b->a->d, RK_ERR_ARGS, "gpu: matrix on another device"));
+    for (int32_t j = 0; j < n; j++) {
+        const int64_t o = out + j * out_stride;
+        int rc = rk_batch_matvecs(b, 1, &m, &o, in + j * in_stride);
+        if (rc) return rc;
     }
-    if (a->qx_off < 0) return latch(b, fail(d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
-    for (int32_t j = 0; j < n; j++)
-        if (!span(b, out + j * out_stride, m->rows, "product output") || !span(b, in + j * in_stride, cols, "product input"))
-            return b->err;
-    hipStream_t s = d->stream;
-    for (int32_t j0 = 0; j0 < n; j0 += most) {
-        const int nj = std::min<int32_t>(most, n - j0);
-        {
-            ProfScope p(d, s, "act_fp8");
-            for (int k = 0; k < nj; k++)
-                launch_act_fp8(a->buf + in + (int64_t)(j0 + k) * in_stride, cols,
-                               reinterpret_cast<uint8_t *>(a->qx) + k * cols, a->xs + k * (cols / 32), s);
-        }
-        ProfScope p(d, s, "matvec_fp8_batch");
-        launch_mx_batch(m->w, m->e8m0, m->rows, cols, reinterpret_cast<const uint8_t *>(a->qx), a->xs, nj,
-                        a->buf + out + (int64_t)j0 * out_stride, out_stride, m->raw != 0, s);
-    }
-    return launched(b, "batched products");
+    return RK_OK;
 }
 
 // internal/gpu/batch.go:282-287 RMSNorm.

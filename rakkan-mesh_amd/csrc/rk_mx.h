@@ -35,14 +35,4 @@ void launch_mx_experts(const uint8_t *w, const uint8_t *ws, int64_t experts, int
                        const uint32_t *ids, int slots, int div, const uint8_t *xc, const float *xs, float *out,
                        int64_t out_stride, bool raw, hipStream_t s);
 
-// internal/gpu/dsbatch.go:174-210 MatVecsBatch for an E4M3 matrix: ni
-// inputs quantized by launch_act_fp8 (input j's codes at xc + j·cols,
-// scales at xs + j·cols/32), out + j·out_stride the product of input j,
-// the weights read once for all. mx_batch_inputs_max gives the most inputs
-// one launch takes for the width (0: none; each input is then a product of
-// its own).
-int mx_batch_inputs_max(int64_t cols);
-void launch_mx_batch(const uint8_t *w, const uint8_t *ws, int64_t rows, int64_t cols, const uint8_t *xc,
-                     const float *xs, int ni, float *out, int64_t out_stride, bool raw, hipStream_t s);
-
 }  // namespace rk

@@ -162,6 +162,7 @@ struct Chunk<4> {
 constexpr int kMxStepsFp8 = 8;
 constexpr int kMxStepsFp4 = 8;
 constexpr int RT_BATCH = kMxStepsFp8;  // row steps of the several-input kernel (divides 32)
+constexpr int kMxBatchGroup = 4;       // inputs a pass of the several-input kernel
 
 // Terms per row in LDS: the row's blocks, padded to keep rows 16-byte
 // aligned and spread over the banks.
@@ -437,49 +438,6 @@ MxShape mx_shape(bool fp4, int nb) {
     return best;
 }
 
-// internal/gpu/dsbatch.go:174-210 MatVecsBatch (mxBatchKernel): an E4M3
-// matrix times ni inputs (codes xc + j·cols, scales xs + j·cols/32), each
-// tile's weights read once from HBM into registers and used for every
-// input; rows of one chunk only (nb·2 lanes fit the workgroup). Terms per
-// input in LDS, then one chain per (input, row), strided over the threads.
-template <bool SIDE, int RT>
-__global__ __launch_bounds__(512) void mx_batch_kernel(const uint8_t *__restrict__ w, const uint8_t *__restrict__ ws,
-                                                       int64_t rows, int cols, int G, const uint8_t *__restrict__ xc,
-                                                       const float *__restrict__ xs, int ni, float *__restrict__ out,
-                                                       int64_t out_stride, int raw) {
-    constexpr int LB = 2, NE = 16;
-    typedef typename Chunk<NE>::T WT;
-    extern __shared__ __align__(16) float terms[];
-    const int tid = threadIdx.x, p = tid % LB, lg = tid / LB;
-    const int nb = cols >> 5;
-    const int g = SIDE ? lg / nb : (lg < nb ? 0 : 1);
-    const bool live = g < G;
-    const int bi = SIDE ? lg % nb : min(lg, nb - 1), b = bi;
-    const int ts = term_stride(nb), n = RT * G;
-    const int64_t row0 = (int64_t)blockIdx.x * n;
-    const MxLane L = mx_lane<false, LB>(w, ws, rows, nb, G, RT, g, live, b, p);
-    WT wv[RT];
-    uint32_t wsv[RT];
-    mx_load_tile<false, SIDE, LB, RT>(L, blockIdx.x, wv, wsv);
-    for (int j = 0; j < ni; j++) {  // uniform
-        uint32_t xw[NE / 4];
-#pragma unroll
-        for (int k = 0; k < NE / 4; k++)
-            xw[k] = *reinterpret_cast<const uint32_t *>(xc + (int64_t)j * cols + b * 32 + p * NE + 4 * k);
-        XSlice<false, NE> x;
-        x.init(xw);
-        mx_tile_terms<false, LB, RT>(wv, wsv, x, xs[(int64_t)j * nb + b], p == 0 && live, G, g, bi, ts,
-                                     terms + (int64_t)j * n * ts);
-    }
-    __syncthreads();
-    for (int q = tid; q < ni * n; q += blockDim.x) {
-        const int j = q / n, rl = q % n;
-        if (row0 + rl >= rows) continue;
-        const float v = canonical(lds_chain_sum(terms + (j * n + rl) * ts, nb, 0.0f));
-        out[j * out_stride + row0 + rl] = raw ? v : round_bf16(v);
-    }
-}
-
 template <bool FP4, bool SIDE, int LB, int RT>
 void launch_mx_t(const uint8_t *w, const uint8_t *ws, int64_t rows, int cols, const uint8_t *xc, const float *xs,
                  float *out, bool raw, int G, int waves, const MxSlots &S, int slots, hipStream_t s) {
@@ -542,40 +500,6 @@ void launch_mx_matvec(bool fp4, const uint8_t *w, const uint8_t *ws, int64_t row
         const int64_t n = std::min(per, rows - r0);
         launch_mx_any(fp4, sh, w + r0 * rb, ws + (fp4 ? r0 * nb : r0 / 32 * nb), n, (int)cols, xc, xs, out + r0, raw,
                       none, 1, s);
-    }
-}
-
-int mx_batch_inputs_max(int64_t cols) {
-    const MxShape sh = mx_shape(false, (int)(cols / 32));
-    if (cols / 32 * 2 > 64 * sh.waves) return 0;  // rows of several chunks: one product an input
-    const int64_t tile = (int64_t)RT_BATCH * sh.g * term_stride((int)(cols / 32)) * 4;
-    return (int)std::min<int64_t>(16, (150 * 1024) / tile);
-}
-
-void launch_mx_batch(const uint8_t *w, const uint8_t *ws, int64_t rows, int64_t cols, const uint8_t *xc,
-                     const float *xs, int ni, float *out, int64_t out_stride, bool raw, hipStream_t s) {
-    const MxShape sh = mx_shape(false, (int)(cols / 32));
-    const int nb = (int)(cols / 32);
-    const size_t lds = (size_t)ni * RT_BATCH * sh.g * term_stride(nb) * 4;
-    const int64_t per = std::max<int64_t>(32, ((int64_t)1 << 30) / cols / 32 * 32);
-    static std::once_flag once;
-    std::call_once(once, [] {
-        (void)hipFuncSetAttribute((const void *)mx_batch_kernel<true, RT_BATCH>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        (void)hipFuncSetAttribute((const void *)mx_batch_kernel<false, RT_BATCH>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    });
-    for (int64_t r0 = 0; r0 < rows; r0 += per) {
-        const int64_t n = std::min(per, rows - r0);
-        const int64_t tiles = (n + (int64_t)RT_BATCH * sh.g - 1) / ((int64_t)RT_BATCH * sh.g);
-        if (sh.g > 1)
-            RK_LAUNCH((mx_batch_kernel<true, RT_BATCH>), dim3((unsigned)tiles), dim3((unsigned)(64 * sh.waves)), lds, s,
-                      w + r0 * cols, ws + r0 / 32 * (cols / 32), n, (int)cols, sh.g, xc, xs, ni, out + r0, out_stride,
-                      raw ? 1 : 0);
-        else
-            RK_LAUNCH((mx_batch_kernel<false, RT_BATCH>), dim3((unsigned)tiles), dim3((unsigned)(64 * sh.waves)), lds,
-                      s, w + r0 * cols, ws + r0 / 32 * (cols / 32), n, (int)cols, 1, xc, xs, ni, out + r0, out_stride,
-                      raw ? 1 : 0);
     }
 }
 

@@ -394,8 +394,8 @@ def test_expert_matvecs(dev, cols, div):
 @pytest.mark.parametrize("rows,cols", [(7, 32), (300, 896), (1000, 1280), (40, 5120), (33, 9216)])
 def test_matvecs_batch(dev, rows, cols):
     """internal/gpu/mx_test.go:371-420 MatVecsBatch: an E4M3 matrix times
-    1, 3, 8, 11 and 17 inputs (two launches past 16; 9216 columns: one
-    product an input), rounded and raw, each output the CPU's product."""
+    1, 3, 8, 11 and 17 inputs, rounded and raw, each output the CPU's
+    product."""
     rng = np.random.default_rng(rows + cols)
     w, s = random_fp8(rng, rows, cols)
     m = dev.upload_mx(rkhip.FP8, rows, cols, w, s)
