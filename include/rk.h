@@ -59,6 +59,7 @@ typedef struct {
     int64_t memory;      /* device-local bytes */
     int32_t compute_units;
     int32_t exact;       /* 1: IEEE f32 with denormals kept, round to nearest even */
+    int32_t integrated;  /* 1: an integrated GPU (device.go Info.Type "integrated"), 0: discrete */
 } rk_device_info;
 
 /* internal/gpu/device.go:125-183 Devices (count, then rk_device_info per index). */

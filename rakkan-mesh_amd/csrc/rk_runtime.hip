@@ -367,6 +367,7 @@ int rk_device_info_get(int32_t index, rk_device_info *info) {
     // The kernels are built for gfx950 with f32 denormals kept and
     // round-to-nearest-even: exact there, and nowhere else.
     info->exact = strncmp(p.gcnArchName, "gfx950", 6) == 0;
+    info->integrated = p.integrated != 0;
     return RK_OK;
 }
 

@@ -32,7 +32,7 @@ class RKError(RuntimeError):
 
 class DeviceInfo(ctypes.Structure):
     _fields_ = [("index", I32), ("name", ctypes.c_char * 64), ("arch", ctypes.c_char * 32), ("memory", I64),
-                ("compute_units", I32), ("exact", I32)]
+                ("compute_units", I32), ("exact", I32), ("integrated", I32)]
 
 
 # name -> (restype, argtypes); the exported C-ABI, kept in step with rk.h.
@@ -142,6 +142,31 @@ def device_count():
     n = I32()
     lib().rk_device_count(ctypes.byref(n))
     return n.value
+
+
+def devices():
+    """internal/gpu/device.go:125-183 Devices: every device's info."""
+    return [device_info(i) for i in range(device_count())]
+
+
+def best(infos):
+    """internal/gpu/device.go:185-201 Best: among devices computing exactly,
+    the discrete one with the most memory, else an integrated one; None if
+    none is exact."""
+    pick = None
+    for d in infos:
+        if not d.exact:
+            continue
+        rank = 2 if d.integrated else 3
+        if pick is None or rank > pick[0] or (rank == pick[0] and d.memory > pick[1].memory):
+            pick = (rank, d)
+    return pick[1] if pick else None
+
+
+def device_bytes_budget(info):
+    """internal/llm/service.go:210-212: the default budget of a node's GPU
+    layers, 85 % of the device's memory (memory / 100 * 85 in integers)."""
+    return int(info.memory) // 100 * 85
 
 
 def device_info(index=0):
