@@ -193,6 +193,14 @@ int rk_batch_expert_matvecs(rk_batch *b, rk_matrix *m, int64_t per_expert, int64
 int rk_batch_matvecs_batch(rk_batch *b, rk_matrix *m, int64_t out, int64_t out_stride, int64_t in, int64_t in_stride,
                            int32_t n);
 
+/* internal/gpu/dsbatch.go:60-74 ActQuantInPlace (num.ActQuantInPlace: each
+ * value its E4M3 rounding times its block's power-of-two scale, in
+ * bfloat16; n a multiple of 32) and FP4QuantInPlace (num.FP4QuantInPlace:
+ * E2M1 codes with E4M3 scales per 16 if e4m3, else E8M0 per 32, dequantized
+ * to bfloat16) of n floats at word off, in place. */
+int rk_batch_act_quant_inplace(rk_batch *b, int64_t off, int64_t n);
+int rk_batch_fp4_quant_inplace(rk_batch *b, int64_t off, int64_t n, int32_t e4m3);
+
 /* internal/gpu/batch.go:271-275 QuantizeFP8: n floats at word `in` to E4M3
  * codes and block scales in the arena's quantize scratch (codes at qx_off,
  * scales at xs_off), as num.QuantizeActFP8. */

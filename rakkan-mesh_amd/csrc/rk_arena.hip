@@ -375,6 +375,30 @@ int rk_batch_matvecs_batch(rk_batch *b, rk_matrix *m, int64_t out, int64_t out_s
     return RK_OK;
 }
 
+// internal/gpu/dsbatch.go:60-74 ActQuantInPlace and FP4QuantInPlace.
+int rk_batch_act_quant_inplace(rk_batch *b, int64_t off, int64_t n) {
+    if (!b) return RK_ERR_ARGS;
+    if (b->err) return b->err;
+    if (n < 0 || n % 32 != 0) return latch(b, fail(b->a->d, RK_ERR_ARGS, "gpu: act quant of %lld floats", (long long)n));
+    float *x = span(b, off, n, "act quant");
+    if (!x) return b->err;
+    ProfScope p(b->a->d, b->a->d->stream, "act_quant_inplace");
+    launch_act_quant_inplace(x, n, b->a->d->stream);
+    return launched(b, "act quant");
+}
+
+int rk_batch_fp4_quant_inplace(rk_batch *b, int64_t off, int64_t n, int32_t e4m3) {
+    if (!b) return RK_ERR_ARGS;
+    if (b->err) return b->err;
+    if (n < 0 || n % (e4m3 ? 16 : 32) != 0)
+        return latch(b, fail(b->a->d, RK_ERR_ARGS, "gpu: fp4 quant of %lld floats", (long long)n));
+    float *x = span(b, off, n, "fp4 quant");
+    if (!x) return b->err;
+    ProfScope p(b->a->d, b->a->d->stream, "fp4_quant_inplace");
+    launch_fp4_quant_inplace(x, n, e4m3 != 0, b->a->d->stream);
+    return launched(b, "fp4 quant");
+}
+
 // internal/gpu/batch.go:282-287 RMSNorm.
 int rk_batch_rmsnorm(rk_batch *b, rk_vectors *vecs, int64_t in, int64_t out, int64_t w, int32_t n, int32_t segs,
                      int64_t stride, float recip_n, float eps) {

@@ -10,6 +10,11 @@ namespace rk {
 // E4M3 codes and one power-of-two float32 scale per 32.
 void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s);
 
+// mx.go:205-214 ActQuantInPlace and 268-290 FP4QuantInPlace of n floats
+// (n a multiple of the block: 32, or 16 for E4M3 scales) in place.
+void launch_act_quant_inplace(float *x, int64_t n, hipStream_t s);
+void launch_fp4_quant_inplace(float *x, int64_t n, bool e4m3, hipStream_t s);
+
 // The device layout of E2M1 scales: blocks of RT = 8 rows, a lane's rows
 // together (byte (k·nb + b)·8 + r for row 8k + r, block b; zero past the
 // last row). Its size, and the repacking of the reference layout

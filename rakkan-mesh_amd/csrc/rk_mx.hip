@@ -124,6 +124,62 @@ __global__ __launch_bounds__(256) void act_fp8_kernel(const float *x, int64_t n,
     }
 }
 
+// mx.go:205-214 ActQuantInPlace: each value its E4M3 rounding (as
+// act_fp8_kernel) times the block scale, rounded to bfloat16.
+__global__ __launch_bounds__(256) void act_quant_inplace_kernel(float *x, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool in = i < n;
+    const float v = in ? x[i] : 0.0f;
+    float m = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) m = gomax(m, __shfl_xor(m, o, 32));
+    const float s = pow2ceil(gomax(m, kActFloor) * kInv448);
+    const uint32_t c = encode_e4m3(gomin(gomax(__fdiv_rn(v, s), -448.0f), 448.0f));
+    const float q = __builtin_amdgcn_cvt_pk_f32_fp8(c, false)[0];  // the code's value, exact
+    if (in) x[i] = round_bf16(q * s);
+}
+
+// mx.go:128-145 EncodeE2M1: the nearest of 0, .5, 1, 1.5, 2, 3, 4, 6, ties
+// to the even code; the sign kept (NaN: code 0 and its sign).
+__device__ __forceinline__ uint32_t encode_e2m1(float v) {
+    const float a = fabsf(v);
+    const float mid[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
+    uint32_t code = 0;
+#pragma unroll
+    for (int k = 0; k < 7; k++)
+        if (a > mid[k] || (a == mid[k] && ((k + 1) & 1) == 0)) code = (uint32_t)(k + 1);
+    return code | ((f2u(v) >> 31) << 3);
+}
+
+// mx.go:234-280 QuantizeFP4 then DequantFP4 (FP4QuantInPlace): blocks of 16
+// with an E4M3 scale of amax/6 (E4M3 = true), or of 32 with the power of
+// two pow2Ceil(amax/6) stored as its exponent byte; each value becomes its
+// E2M1 code's value times the stored scale, rounded to bfloat16.
+template <bool E4M3>
+__global__ __launch_bounds__(256) void fp4_quant_inplace_kernel(float *x, int64_t n) {
+    constexpr int BS = E4M3 ? 16 : 32;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool in = i < n;
+    const float v = in ? x[i] : 0.0f;
+    float m = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < BS; o <<= 1) m = gomax(m, __shfl_xor(m, o, BS));
+    float s, stored;
+    if constexpr (E4M3) {
+        m = gomax(m, 0.01171875f);  // 6/512: an all-zero group keeps a nonzero scale
+        const uint32_t sc = encode_e4m3(__fdiv_rn(m, 6.0f));
+        s = stored = __builtin_amdgcn_cvt_pk_f32_fp8(sc, false)[0];
+    } else {
+        m = gomax(m, u2f(0x00C00000u));  // float32(6·2^-126)
+        s = pow2ceil(m * (float)(1.0 / 6));
+        stored = e8m0((f2u(s) >> 23) & 0xffu);  // the scale byte, as DequantFP4 reads it
+    }
+    const uint32_t c = encode_e2m1(gomin(gomax(__fdiv_rn(v, s), -6.0f), 6.0f));
+    const float grid[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};  // mx.go:45 fp4Grid
+    const float fv = (c & 8) ? -grid[c & 7] : grid[c & 7];
+    if (in) x[i] = round_bf16(fv * stored);
+}
+
 // E bytes a lane loads per row (16, 8 or 4): buffer loads, so that a row
 // past the matrix's end reads zeros (the hardware's range check) and the
 // row's offset is a scalar added to the lane's fixed offset.
@@ -485,6 +541,19 @@ void mx_fp4_pack_scales(const uint8_t *e8m0, int64_t rows, int64_t cols, uint8_t
 void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s) {
     if (n <= 0) return;
     RK_LAUNCH(act_fp8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, codes, scales);
+}
+
+void launch_act_quant_inplace(float *x, int64_t n, hipStream_t s) {
+    if (n <= 0) return;
+    RK_LAUNCH(act_quant_inplace_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n);
+}
+
+void launch_fp4_quant_inplace(float *x, int64_t n, bool e4m3, hipStream_t s) {
+    if (n <= 0) return;
+    if (e4m3)
+        RK_LAUNCH(fp4_quant_inplace_kernel<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n);
+    else
+        RK_LAUNCH(fp4_quant_inplace_kernel<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n);
 }
 
 void launch_mx_matvec(bool fp4, const uint8_t *w, const uint8_t *ws, int64_t rows, int64_t cols, const uint8_t *xc,

@@ -50,6 +50,8 @@ SIGNATURES = {
     "rk_batch_quantize_fp8": (ctypes.c_int, [P, I64, I64]),
     "rk_batch_expert_matvecs": (ctypes.c_int, [P, P, I64, I64, I32, I64, I64, I32, I64, I64]),
     "rk_batch_matvecs_batch": (ctypes.c_int, [P, P, I64, I64, I64, I64, I32]),
+    "rk_batch_act_quant_inplace": (ctypes.c_int, [P, I64, I64]),
+    "rk_batch_fp4_quant_inplace": (ctypes.c_int, [P, I64, I64, I32]),
     "rk_matrix_bytes": (I64, [P]),
     "rk_matvecs": (ctypes.c_int, [P, I32, P, P, P, I64]),
     "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
@@ -271,6 +273,12 @@ class Batch:
 
     def quantize_fp8(self, inp, n):
         return lib().rk_batch_quantize_fp8(self.h, inp, n)
+
+    def act_quant_inplace(self, off, n):
+        return lib().rk_batch_act_quant_inplace(self.h, off, n)
+
+    def fp4_quant_inplace(self, off, n, e4m3):
+        return lib().rk_batch_fp4_quant_inplace(self.h, off, n, int(bool(e4m3)))
 
     def matvecs_batch(self, m, out, out_stride, inp, in_stride, n):
         """internal/gpu Batch.MatVecsBatch."""

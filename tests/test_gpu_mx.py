@@ -422,3 +422,37 @@ def test_matvecs_batch(dev, rows, cols):
         arena.free()
         m.free()
     assert dev.used == 0
+
+
+def test_in_place_quantizers(dev):
+    """internal/gpu/dsbatch.go:60-74 ActQuantInPlace and FP4QuantInPlace
+    (both scale kinds) against the oracle, which equals the reference
+    kernels' act_quant / fp4_act_quant vectors (test_oracle_mx.py): the
+    reference's own inputs, then random blocks (zero, huge, tiny, ties,
+    denormals, signed zeros). Inputs with infinities are left out of the
+    E2M1 case: the sign of the NaN they make there is not pinned."""
+    with gzip.open(GOLDEN, "rt") as f:
+        vec = json.load(f)
+    rng = np.random.default_rng(13)
+    cases = [bf16s(c["x"]) for c in vec["act_quant"]] + [mx_input(rng, 4096), mx_input(rng, 96)]
+    fcases = [bf16s(c["x"]) for c in vec["fp4_quant"]] + [mx_input(rng, 4096), mx_input(rng, 64)]
+    arena = dev.arena(8192, 16384)
+    try:
+        for x in cases:
+            b = arena.begin()
+            b.write(0, x)
+            assert b.act_quant_inplace(0, x.size) == 0
+            got = np.asarray(b.read(0, x.size))
+            b.submit()
+            same_bits(got, oracle.act_quant_inplace(x), f"act quant of {x.size}")
+        for x in fcases:
+            for e4m3 in (False, True):
+                b = arena.begin()
+                b.write(0, x)
+                assert b.fp4_quant_inplace(0, x.size, e4m3) == 0
+                got = np.asarray(b.read(0, x.size))
+                b.submit()
+                p_, s_ = oracle.quantize_fp4(x, e4m3)
+                same_bits(got, oracle.dequant_fp4(p_, s_, x.size, e4m3), f"fp4 quant of {x.size} e4m3={e4m3}")
+    finally:
+        arena.free()
