@@ -27,13 +27,15 @@
 // Work layout: lane groups of LB lanes take one 32-weight block each (lane
 // p of a group 32/LB consecutive weights: 16-byte loads), so a row's
 // weights are read as one contiguous run, and each lane keeps its input
-// slice in registers for all the workgroup's rows. A workgroup takes RT
-// steps of G consecutive rows side by side (G > 1 for narrow rows, whose
-// G rows are one contiguous run), all RT loads issued before the first is
-// used. The terms go to LDS, [row][block], and one lane per row adds them
-// in block order (a sequential float32 chain, lds_chain_sum). Rows wider
-// than the workgroup's lanes take several chunks, the chain carried across
-// them.
+// slice in registers for all the workgroup's rows. A workgroup takes RT = 8
+// row steps; narrow rows go G side by side (G runs of 8 consecutive rows,
+// a step reading one row of each run), all RT loads issued before the first
+// is used. The terms go to LDS, [row][block], and one lane per row adds
+// them in block order (a sequential float32 chain, lds_chain_sum). Rows
+// wider than the workgroup's lanes take several chunks, the chain carried
+// across them. With a slot table the grid's second dimension runs selected
+// experts (ExpertMatVecs). Also here: the in-place E4M3 / E2M1 quantizers
+// of the DeepSeek batch (ActQuantInPlace, FP4QuantInPlace).
 #include <algorithm>
 #include <mutex>
 
