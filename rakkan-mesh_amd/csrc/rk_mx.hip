@@ -301,9 +301,12 @@ __device__ __forceinline__ void mx_load_tile(const MxLane &L, int64_t t, WT (&wv
 #pragma unroll
         for (int r = 0; r < RT; r++) wsv[r] = s1;
     } else {
+        // the lane's RT rows are consecutive from a multiple of RT (which
+        // divides 32): one row of 32x32-block scales too
+        const uint32_t s1 =
+            __builtin_amdgcn_raw_buffer_load_b8(L.rsc, (int)((row0 + L.gl * RT) >> 5) * L.nb + L.b, 0, 0);
 #pragma unroll
-        for (int r = 0; r < RT; r++)
-            wsv[r] = __builtin_amdgcn_raw_buffer_load_b8(L.rsc, (int)((row0 + L.gl * RT + r) >> 5) * L.nb + L.b, 0, 0);
+        for (int r = 0; r < RT; r++) wsv[r] = s1;
     }
 }
 
