@@ -18,6 +18,9 @@ struct rk_arena {
     float *buf = nullptr;       // device words
     float *staging = nullptr;   // pinned host words
     int64_t qx_off = -1, xs_off = -1;
+    // codes the last quantize op wrote (Quantize / QuantizeFP8), which
+    // reads at qx_off / xs_off return from the scratch
+    int64_t q_codes = 0;
     // The quantized input of products (kept here, 16-byte aligned, rather
     // than in the reserved words: the kernels read it as 128-bit vectors).
     int8_t *qx = nullptr;
@@ -236,12 +239,12 @@ int rk_batch_read(rk_batch *b, int64_t off, float *dst, int64_t n) {
     // the quantized input, which the reference keeps in the arena at qx_off
     // (codes, four a word) and xs_off (scales), is read from the scratch
     // that holds it here (internal/gpu/mx_test.go:98-127 reads it back)
-    // (the scales' window first: it is the smaller, and a caller lays the
-    // codes out before it)
+    // (the words the last Quantize / QuantizeFP8 wrote; the scales' window
+    // first: a caller lays the codes out before it)
     float *src = nullptr;
-    if (a->xs_off >= 0 && off >= a->xs_off && off + n <= a->xs_off + kMaxCols / 32)
+    if (a->xs_off >= 0 && off >= a->xs_off && off + n <= a->xs_off + a->q_codes / 32)
         src = a->xs + (off - a->xs_off);
-    else if (a->qx_off >= 0 && off >= a->qx_off && off + n <= a->qx_off + kMaxCols / 4)
+    else if (a->qx_off >= 0 && off >= a->qx_off && off + n <= a->qx_off + (a->q_codes + 3) / 4)
         src = reinterpret_cast<float *>(a->qx) + (off - a->qx_off);
     else if (!(src = span(b, off, n, "read")))
         return b->err;
@@ -296,6 +299,7 @@ int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n) {
     if (!x) return b->err;
     ProfScope p(a->d, a->d->stream, "quantize_acts");
     launch_quantize_acts(x, n, a->qx, a->xs, a->xsum, a->d->stream);
+    a->q_codes = n;
     return launched(b, "quantize");
 }
 
@@ -311,6 +315,7 @@ int rk_batch_quantize_fp8(rk_batch *b, int64_t in, int64_t n) {
     if (!x) return b->err;
     ProfScope p(a->d, a->d->stream, "act_fp8");
     launch_act_fp8(x, n, reinterpret_cast<uint8_t *>(a->qx), a->xs, a->d->stream);
+    a->q_codes = n;
     return launched(b, "quantize");
 }
 

@@ -456,3 +456,30 @@ def test_in_place_quantizers(dev):
                 same_bits(got, oracle.dequant_fp4(p_, s_, x.size, e4m3), f"fp4 quant of {x.size} e4m3={e4m3}")
     finally:
         arena.free()
+
+
+def test_words_past_the_quantized_input_read_from_the_arena(dev):
+    """Reads at the quantize scratch's offsets return what QuantizeFP8 wrote
+    there, and only that: words beyond its codes and scales are the
+    arena's own."""
+    rng = np.random.default_rng(21)
+    cols = 256
+    x = mx_input(rng, cols)
+    qx, xs = 1024, 1024 + cols // 4
+    arena = dev.arena(4096, 8192)
+    arena.set_quant_scratch(qx, xs)
+    try:
+        b = arena.begin()
+        b.write(0, x)
+        b.write(xs + cols // 32, np.arange(64, dtype=np.float32))  # after the scales
+        assert b.quantize_fp8(0, cols) == 0
+        codes = np.asarray(b.read(qx, cols // 4))
+        scales = np.asarray(b.read(xs, cols // 32))
+        after = np.asarray(b.read(xs + cols // 32, 64))
+        b.submit()
+        want_c, want_s = oracle.act_fp8(x)
+        assert np.array_equal(codes.view(np.uint8), want_c)
+        assert np.array_equal(bits(scales), bits(want_s))
+        assert np.array_equal(after, np.arange(64, dtype=np.float32))
+    finally:
+        arena.free()
