@@ -146,10 +146,13 @@ typedef struct rk_batch rk_batch;
 /* internal/gpu/batch.go:22-49 NewArena: `words` of device memory and pinned
  * staging for `staging_words` moved per submission. */
 int rk_arena_new(rk_device *dev, int64_t words, int64_t staging_words, rk_arena **out);
-/* internal/gpu/batch.go:51-55 SetQuantScratch: reserves room for a product's
- * quantized input (qx_off: cols/4 words, xs_off: cols/32 words). The
- * quantized form itself is kept in the arena's own 16-byte-aligned scratch,
- * which products read as 128-bit vectors; the reserved words are not written. */
+/* internal/gpu/batch.go:51-55 SetQuantScratch: reserves room for a quantized
+ * input: at qx_off cols/4 words (Q8_0 codes, four a word) or cols words
+ * (E4M3 values), at xs_off cols/32 words (block scales). Products keep their
+ * quantized input in the arena's own 16-byte-aligned scratch (read as
+ * 128-bit vectors) and leave the reserved words as they were; rk_batch_quantize
+ * and rk_batch_quantize_fp8 write their result there, in the reference's
+ * layout. */
 int rk_arena_set_quant_scratch(rk_arena *a, int64_t qx_off, int64_t xs_off);
 /* internal/gpu/batch.go:57-58 Bytes. */
 int64_t rk_arena_bytes(const rk_arena *a);
@@ -175,7 +178,8 @@ int rk_batch_read(rk_batch *b, int64_t off, float *dst, int64_t n);
 /* internal/gpu/batch.go:212-269 MatVecs: ms[i]·x into word out_offs[i], x
  * at in_off, quantized once (Q8/Q4 need the arena's quant scratch). */
 int rk_batch_matvecs(rk_batch *b, int32_t n, rk_matrix *const *ms, const int64_t *out_offs, int64_t in_off);
-/* internal/gpu/batch.go:277-280 Quantize: n floats at in into the scratch. */
+/* internal/gpu/batch.go:277-280 Quantize: n floats at in to Q8_0: codes four
+ * a word (code j in byte j) at qx_off, block scales at xs_off. */
 int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n);
 /* internal/gpu/dsbatch.go:142-172 ExpertMatVecs: m holds E2M1 experts of
  * per_expert rows each (a multiple of 8 here; RK_ERR_UNSUPPORTED otherwise);
@@ -202,8 +206,10 @@ int rk_batch_act_quant_inplace(rk_batch *b, int64_t off, int64_t n);
 int rk_batch_fp4_quant_inplace(rk_batch *b, int64_t off, int64_t n, int32_t e4m3);
 
 /* internal/gpu/batch.go:271-275 QuantizeFP8: n floats at word `in` to E4M3
- * codes and block scales in the arena's quantize scratch (codes at qx_off,
- * scales at xs_off), as num.QuantizeActFP8. */
+ * with block scales, as num.QuantizeActFP8: the codes' values, unscaled, as n
+ * float32 words at qx_off (internal/gpu/mx.go:146-172), the scales at
+ * xs_off. A NaN code (an input block holding an infinity or NaN) reads as
+ * NaN, num.ActFP8.Vals' value; the reference's Vulkan kernel gives ±480. */
 int rk_batch_quantize_fp8(rk_batch *b, int64_t in, int64_t n);
 
 /* internal/gpu/batch.go:282-287 RMSNorm: segs segments of n floats at in

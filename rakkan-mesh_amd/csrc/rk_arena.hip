@@ -18,11 +18,10 @@ struct rk_arena {
     float *buf = nullptr;       // device words
     float *staging = nullptr;   // pinned host words
     int64_t qx_off = -1, xs_off = -1;
-    // codes the last quantize op wrote (Quantize / QuantizeFP8), which
-    // reads at qx_off / xs_off return from the scratch
-    int64_t q_codes = 0;
     // The quantized input of products (kept here, 16-byte aligned, rather
     // than in the reserved words: the kernels read it as 128-bit vectors).
+    // Quantize and QuantizeFP8 also leave their result in the reserved
+    // words, in the reference's layout, for callers that read it back.
     int8_t *qx = nullptr;
     float *xs = nullptr;
     int32_t *xsum = nullptr;
@@ -236,18 +235,8 @@ int rk_batch_read(rk_batch *b, int64_t off, float *dst, int64_t n) {
     rk_arena *a = b->a;
     if (b->staged + n > a->staging_words)
         return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: batch moves more than its staging holds"));
-    // the quantized input, which the reference keeps in the arena at qx_off
-    // (codes, four a word) and xs_off (scales), is read from the scratch
-    // that holds it here (internal/gpu/mx_test.go:98-127 reads it back)
-    // (the words the last Quantize / QuantizeFP8 wrote; the scales' window
-    // first: a caller lays the codes out before it)
-    float *src = nullptr;
-    if (a->xs_off >= 0 && off >= a->xs_off && off + n <= a->xs_off + a->q_codes / 32)
-        src = a->xs + (off - a->xs_off);
-    else if (a->qx_off >= 0 && off >= a->qx_off && off + n <= a->qx_off + (a->q_codes + 3) / 4)
-        src = reinterpret_cast<float *>(a->qx) + (off - a->qx_off);
-    else if (!(src = span(b, off, n, "read")))
-        return b->err;
+    const float *src = span(b, off, n, "read");
+    if (!src) return b->err;
     float *st = a->staging + b->staged;
     hipError_t e = hipMemcpyAsync(st, src, (size_t)n * 4, hipMemcpyDeviceToHost, a->d->stream);
     if (e != hipSuccess) return latch(b, hip_fail(a->d, e, "batch read"));
@@ -288,7 +277,10 @@ int rk_batch_matvecs(rk_batch *b, int32_t n, rk_matrix *const *ms, const int64_t
     return rc ? latch(b, rc) : RK_OK;
 }
 
-// internal/gpu/batch.go:277-280 Quantize.
+// internal/gpu/batch.go:277-280 Quantize: the input's Q8_0 form into the
+// products' scratch, and, as the reference leaves it in the arena, its
+// codes four a word (little-endian, code j in byte j) at qx_off and its
+// block scales at xs_off (internal/gpu/kernels.go:323-353).
 int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n) {
     if (!b) return RK_ERR_ARGS;
     if (b->err) return b->err;
@@ -296,15 +288,26 @@ int rk_batch_quantize(rk_batch *b, int64_t in, int64_t n) {
     if (a->qx_off < 0) return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
     if (n % 32 != 0 || n > kMaxCols) return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: quantize of %lld floats", (long long)n));
     const float *x = span(b, in, n, "quantize input");
-    if (!x) return b->err;
-    ProfScope p(a->d, a->d->stream, "quantize_acts");
-    launch_quantize_acts(x, n, a->qx, a->xs, a->xsum, a->d->stream);
-    a->q_codes = n;
+    float *qw = x ? span(b, a->qx_off, n / 4, "quantized codes") : nullptr;
+    float *sw = qw ? span(b, a->xs_off, n / 32, "quantized scales") : nullptr;
+    if (!sw) return b->err;
+    hipStream_t s = a->d->stream;
+    {
+        ProfScope p(a->d, s, "quantize_acts");
+        launch_quantize_acts(x, n, a->qx, a->xs, a->xsum, s);
+    }
+    hipError_t e = hipMemcpyAsync(qw, a->qx, (size_t)n, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(sw, a->xs, (size_t)(n / 32) * 4, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return latch(b, hip_fail(a->d, e, "quantize"));
     return launched(b, "quantize");
 }
 
 // internal/gpu/batch.go:271-275 QuantizeFP8: E4M3 codes and block scales
-// into the arena's quantize scratch (codes at qx, scales at xs).
+// into the products' scratch, and, as the reference leaves them in the
+// arena (internal/gpu/mx.go:146-172), the codes' values, unscaled, as n
+// float32 words at qx_off and the block scales at xs_off. (A NaN code, from
+// an input block holding an infinity or NaN, reads as NaN, the CPU path's
+// value in num.ActFP8.Vals; the reference's Vulkan kernel gives ±480 there.)
 int rk_batch_quantize_fp8(rk_batch *b, int64_t in, int64_t n) {
     if (!b) return RK_ERR_ARGS;
     if (b->err) return b->err;
@@ -312,10 +315,20 @@ int rk_batch_quantize_fp8(rk_batch *b, int64_t in, int64_t n) {
     if (a->qx_off < 0) return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: arena has no scratch for quantized inputs"));
     if (n % 32 != 0 || n > kMaxCols) return latch(b, fail(a->d, RK_ERR_ARGS, "gpu: quantize of %lld floats", (long long)n));
     const float *x = span(b, in, n, "quantize input");
-    if (!x) return b->err;
-    ProfScope p(a->d, a->d->stream, "act_fp8");
-    launch_act_fp8(x, n, reinterpret_cast<uint8_t *>(a->qx), a->xs, a->d->stream);
-    a->q_codes = n;
+    float *vw = x ? span(b, a->qx_off, n, "quantized values") : nullptr;
+    float *sw = vw ? span(b, a->xs_off, n / 32, "quantized scales") : nullptr;
+    if (!sw) return b->err;
+    hipStream_t s = a->d->stream;
+    {
+        ProfScope p(a->d, s, "act_fp8");
+        launch_act_fp8(x, n, reinterpret_cast<uint8_t *>(a->qx), a->xs, s);
+    }
+    {
+        ProfScope p(a->d, s, "e4m3_values");
+        launch_e4m3_values(reinterpret_cast<const uint8_t *>(a->qx), n, vw, s);
+    }
+    hipError_t e = hipMemcpyAsync(sw, a->xs, (size_t)(n / 32) * 4, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return latch(b, hip_fail(a->d, e, "quantize"));
     return launched(b, "quantize");
 }
 

@@ -10,6 +10,10 @@ namespace rk {
 // E4M3 codes and one power-of-two float32 scale per 32.
 void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s);
 
+// The value of each of n E4M3 codes, unscaled, as float32 (the layout the
+// reference's QuantizeFP8 leaves in the arena, internal/gpu/mx.go:146-172).
+void launch_e4m3_values(const uint8_t *codes, int64_t n, float *out, hipStream_t s);
+
 // mx.go:205-214 ActQuantInPlace and 268-290 FP4QuantInPlace of n floats
 // (n a multiple of the block: 32, or 16 for E4M3 scales) in place.
 void launch_act_quant_inplace(float *x, int64_t n, hipStream_t s);

@@ -126,6 +126,14 @@ __global__ __launch_bounds__(256) void act_fp8_kernel(const float *x, int64_t n,
     }
 }
 
+// internal/gpu/mx.go:146-172 actFP8Kernel's arena form of the codes: each
+// code's value, unscaled, as a float32 word (exact: E4M3 values are
+// float32 values).
+__global__ __launch_bounds__(256) void e4m3_values_kernel(const uint8_t *codes, int64_t n, float *out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)codes[i], false)[0];
+}
+
 // mx.go:205-214 ActQuantInPlace: each value its E4M3 rounding (as
 // act_fp8_kernel) times the block scale, rounded to bfloat16.
 __global__ __launch_bounds__(256) void act_quant_inplace_kernel(float *x, int64_t n) {
@@ -172,7 +180,7 @@ __global__ __launch_bounds__(256) void fp4_quant_inplace_kernel(float *x, int64_
         const uint32_t sc = encode_e4m3(__fdiv_rn(m, 6.0f));
         s = stored = __builtin_amdgcn_cvt_pk_f32_fp8(sc, false)[0];
     } else {
-        m = gomax(m, u2f(0x00C00000u));  // float32(6·2^-126)
+        m = gomax(m, u2f(0x01C00000u));  // float32(6·2^-126) = 1.5·2^-124
         s = pow2ceil(m * (float)(1.0 / 6));
         stored = e8m0((f2u(s) >> 23) & 0xffu);  // the scale byte, as DequantFP4 reads it
     }
@@ -219,8 +227,6 @@ struct Chunk<4> {
 // divides 32: a tile's rows then share one row of 32x32-block scales.
 constexpr int kMxStepsFp8 = 8;
 constexpr int kMxStepsFp4 = 8;
-constexpr int RT_BATCH = kMxStepsFp8;  // row steps of the several-input kernel (divides 32)
-constexpr int kMxBatchGroup = 4;       // inputs a pass of the several-input kernel
 
 // Terms per row in LDS: the row's blocks, padded to keep rows 16-byte
 // aligned and spread over the banks.
@@ -559,6 +565,11 @@ void mx_fp4_pack_scales(const uint8_t *e8m0, int64_t rows, int64_t cols, uint8_t
 void launch_act_fp8(const float *x, int64_t n, uint8_t *codes, float *scales, hipStream_t s) {
     if (n <= 0) return;
     RK_LAUNCH(act_fp8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n, codes, scales);
+}
+
+void launch_e4m3_values(const uint8_t *codes, int64_t n, float *out, hipStream_t s) {
+    if (n <= 0) return;
+    RK_LAUNCH(e4m3_values_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, codes, n, out);
 }
 
 void launch_act_quant_inplace(float *x, int64_t n, hipStream_t s) {

@@ -125,6 +125,49 @@ def test_zero_and_tiny_inputs(dev):
     m.free()
 
 
+@pytest.mark.parametrize("n", [32, 288, 4096])
+def test_batch_quantize_leaves_codes_in_the_arena(dev, n):
+    """internal/gpu/batch.go:277-280 Quantize through an arena: the Q8_0
+    codes four a word (code j in byte j, kernels.go:340-349) at qxOff and
+    the block scales at xsOff, as num.QuantizeActs gives them; the word
+    after the scales is the arena's own, and a product afterwards (which
+    quantizes into its own scratch) leaves the reserved words as they were."""
+    rng = np.random.default_rng(n)
+    x = awkward(rng, n, 1.0)
+    x[:32] = 0.0  # an all-zero block: scale 0, codes 0
+    want_q, want_s = oracle.quantize8(x)
+    qx, xs = 2 * n, 2 * n + n // 4
+    arena = dev.arena(xs + n // 32 + 1 + 64, 4 * n + 64)
+    arena.set_quant_scratch(qx, xs)
+    rows = 64
+    q8, s8 = oracle.quantize8(rng.normal(0, 0.05, rows * n).astype(np.float32))
+    m = dev.upload_q8(q8, s8, rows, n)
+    try:
+        b = arena.begin()
+        b.write(0, x)
+        b.write(xs + n // 32, np.array([1.5], np.float32))
+        assert b.quantize(0, n) == 0
+        codes = b.read(qx, n // 4)
+        scales = b.read(xs, n // 32)
+        after = b.read(xs + n // 32, 1)
+        b.submit()
+        assert np.array_equal(np.asarray(codes).view(np.int8), want_q)
+        same_bits(np.asarray(scales), want_s, "Quantize scales")
+        assert after[0] == 1.5
+        b = arena.begin()
+        b.write(n, -x)
+        b.matvecs([m], [xs + n // 32 + 1], n)
+        again = b.read(qx, n // 4)
+        got = b.read(xs + n // 32 + 1, rows)
+        b.submit()
+        assert np.array_equal(np.asarray(again).view(np.int8), want_q)
+        same_bits(np.asarray(got), oracle.matvec_q8(q8, s8, -x, rows, n), "product after Quantize")
+    finally:
+        arena.free()
+        m.free()
+    assert dev.used == 0
+
+
 def test_shape_errors(dev):
     rng = np.random.default_rng(23)
     q = rng.integers(-127, 128, 64 * 64, dtype=np.int8)
@@ -136,6 +179,34 @@ def test_shape_errors(dev):
     with pytest.raises(rkhip.RKError) as e:
         dev.matvecs([m], np.zeros(32, np.float32))
     assert e.value.code == rkhip.RK_ERR_ARGS
+    m.free()
+    assert dev.used == 0
+
+
+def test_out_of_memory_is_an_error_and_the_device_stays_usable(dev):
+    """The failure internal/llm/model.go:168-188 falls back from: a request
+    for more device memory than the GPU has (an arena of 400 GB on a 288 GB
+    MI355X; hipMalloc refuses it before anything else happens) returns
+    RK_ERR_OOM with its text, does not abort, leaves Used() as it was, and
+    the next products on the device still give the CPU's bits, as does a
+    product call that fails (a submission of more rows than one call takes)."""
+    rng = np.random.default_rng(26)
+    rows, cols = 512, 4096
+    q = rng.integers(-127, 128, rows * cols, dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-2, rows * cols // 32).astype(np.float32)
+    m = dev.upload_q8(q, s, rows, cols)
+    used = dev.used
+    x = rng.normal(0, 1, cols).astype(np.float32)
+    with pytest.raises(rkhip.RKError) as e:
+        dev.arena(100_000_000_000, 16)  # 400 GB of words
+    assert e.value.code == rkhip.RK_ERR_OOM
+    assert "arena" in str(e.value) and "memory" in str(e.value).lower(), str(e.value)
+    assert dev.used == used
+    same_bits(dev.matvec(m, x), oracle.matvec_q8(q, s, x, rows, cols), "product after the failed allocation")
+    with pytest.raises(rkhip.RKError) as e:
+        dev.matvecs([m] * 2049, x)  # 2049 · 512 rows > 2^20 in one submission
+    assert e.value.code == rkhip.RK_ERR_ARGS
+    same_bits(dev.matvec(m, x), oracle.matvec_q8(q, s, x, rows, cols), "product after the failed call")
     m.free()
     assert dev.used == 0
 

@@ -267,17 +267,17 @@ def test_quantize_fp8_and_batch_products(dev):
     wf = rng.normal(0, 1, 16 * cols).astype(np.float32)
     ms = [dev.upload_mx(rkhip.FP8, 96, cols, w8, s8), dev.upload_mx(rkhip.FP4, 80, cols, w4, s4),
           dev.upload(rkhip.F32, 16, cols, wf)]
-    qx, xs = cols + 192, cols + 192 + cols // 4
-    arena = dev.arena(xs + cols // 32, 2 * cols)
+    qx, xs = cols + 192, cols + 192 + cols  # E4M3 values take cols words
+    arena = dev.arena(xs + cols // 32, 3 * cols)
     arena.set_quant_scratch(qx, xs)
     try:
         b = arena.begin()
         b.write(0, x)
         assert b.quantize_fp8(0, cols) == 0
-        codes = b.read(qx, cols // 4)
+        vals = b.read(qx, cols)
         scales = b.read(xs, cols // 32)
         b.submit()
-        assert np.array_equal(np.asarray(codes).view(np.uint8), want_c)
+        same_values(np.asarray(vals), e4m3_f32(want_c), "QuantizeFP8 values")
         assert np.array_equal(bits(scales), bits(want_s))
         b = arena.begin()
         b.write(0, x)
@@ -429,13 +429,18 @@ def test_in_place_quantizers(dev):
     (both scale kinds) against the oracle, which equals the reference
     kernels' act_quant / fp4_act_quant vectors (test_oracle_mx.py): the
     reference's own inputs, then random blocks (zero, huge, tiny, ties,
-    denormals, signed zeros). Inputs with infinities are left out of the
-    E2M1 case: the sign of the NaN they make there is not pinned."""
+    denormals, signed zeros), then blocks holding an infinity or a NaN.
+    Those make NaNs (0·inf, 0/-0): they must sit at the oracle's positions
+    and every other value must match bit for bit, but a NaN's sign is not
+    pinned (the CPU path's x86 multiply gives the negative default NaN, the
+    GPU a positive one), so NaNs match any NaN."""
     with gzip.open(GOLDEN, "rt") as f:
         vec = json.load(f)
     rng = np.random.default_rng(13)
-    cases = [bf16s(c["x"]) for c in vec["act_quant"]] + [mx_input(rng, 4096), mx_input(rng, 96)]
-    fcases = [bf16s(c["x"]) for c in vec["fp4_quant"]] + [mx_input(rng, 4096), mx_input(rng, 64)]
+    cases = [bf16s(c["x"]) for c in vec["act_quant"]] + [mx_input(rng, 4096), mx_input(rng, 96),
+                                                        mx_input(rng, 4096, specials=True)]
+    fcases = [bf16s(c["x"]) for c in vec["fp4_quant"]] + [mx_input(rng, 4096), mx_input(rng, 64),
+                                                         mx_input(rng, 4096, specials=True)]
     arena = dev.arena(8192, 16384)
     try:
         for x in cases:
@@ -444,7 +449,7 @@ def test_in_place_quantizers(dev):
             assert b.act_quant_inplace(0, x.size) == 0
             got = np.asarray(b.read(0, x.size))
             b.submit()
-            same_bits(got, oracle.act_quant_inplace(x), f"act quant of {x.size}")
+            same_values(got, oracle.act_quant_inplace(x), f"act quant of {x.size}")
         for x in fcases:
             for e4m3 in (False, True):
                 b = arena.begin()
@@ -453,33 +458,60 @@ def test_in_place_quantizers(dev):
                 got = np.asarray(b.read(0, x.size))
                 b.submit()
                 p_, s_ = oracle.quantize_fp4(x, e4m3)
-                same_bits(got, oracle.dequant_fp4(p_, s_, x.size, e4m3), f"fp4 quant of {x.size} e4m3={e4m3}")
+                same_values(got, oracle.dequant_fp4(p_, s_, x.size, e4m3), f"fp4 quant of {x.size} e4m3={e4m3}")
     finally:
         arena.free()
 
 
 def test_words_past_the_quantized_input_read_from_the_arena(dev):
-    """Reads at the quantize scratch's offsets return what QuantizeFP8 wrote
-    there, and only that: words beyond its codes and scales are the
-    arena's own."""
+    """internal/gpu/mx_test.go:98-127: after QuantizeFP8 of n floats, n words
+    at qxOff hold the E4M3 values, unscaled, and n/32 at xsOff the scales;
+    words beyond them are the arena's own. A product afterwards leaves those
+    words as they were."""
     rng = np.random.default_rng(21)
     cols = 256
     x = mx_input(rng, cols)
-    qx, xs = 1024, 1024 + cols // 4
+    qx, xs = 1024, 1024 + cols
     arena = dev.arena(4096, 8192)
     arena.set_quant_scratch(qx, xs)
+    w8, s8 = random_fp8(rng, 40, cols)
+    m = dev.upload_mx(rkhip.FP8, 40, cols, w8, s8)
     try:
         b = arena.begin()
         b.write(0, x)
         b.write(xs + cols // 32, np.arange(64, dtype=np.float32))  # after the scales
         assert b.quantize_fp8(0, cols) == 0
-        codes = np.asarray(b.read(qx, cols // 4))
+        vals = np.asarray(b.read(qx, cols))
         scales = np.asarray(b.read(xs, cols // 32))
         after = np.asarray(b.read(xs + cols // 32, 64))
         b.submit()
         want_c, want_s = oracle.act_fp8(x)
-        assert np.array_equal(codes.view(np.uint8), want_c)
+        same_values(vals, e4m3_f32(want_c), "QuantizeFP8 values")
         assert np.array_equal(bits(scales), bits(want_s))
         assert np.array_equal(after, np.arange(64, dtype=np.float32))
+        # a product of another input: the reserved words keep the values
+        b = arena.begin()
+        b.write(0, -x)
+        b.matvecs([m], [2048], 0)
+        again = np.asarray(b.read(qx, cols))
+        got = np.asarray(b.read(2048, 40))
+        b.submit()
+        same_values(again, vals, "reserved words after a product")
+        same_bits(got, oracle.matvec_fp8(w8, s8, -x, 40, cols), "product after QuantizeFP8")
     finally:
         arena.free()
+        m.free()
+
+
+def e4m3_f32(codes):
+    """The E4M3 codes' values as float32 (NaN for the NaN codes)."""
+    return oracle.e4m3_values()[np.asarray(codes)].astype(np.float32)
+
+
+def same_values(got, want, what):
+    """Bit-equal, except that a NaN matches any NaN (the NaN codes' values
+    carry no pinned payload)."""
+    g, w = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    nan = np.isnan(w)
+    assert np.array_equal(np.isnan(g), nan), f"{what}: NaN positions differ"
+    same_bits(g[~nan], w[~nan], what)
