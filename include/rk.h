@@ -133,6 +133,18 @@ int rk_matmul_t(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *o
  * ([tokens][rows_i]), enqueued on `stream` (NULL: the device's own). */
 int rk_matmul_t_device(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *d_outs, const float *d_x,
                        int64_t cols, int32_t tokens, void *stream);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): rk_matmul_t_device's products, bit for bit, with the tokens'
+ * quantized inputs in a static device array of the library (about 20 MiB
+ * per GPU, held until the process ends) instead of a scratch grown with
+ * hipMalloc. It allocates nothing. tokens·cols must not pass 2^24 (16,777,216
+ * codes, e.g. 512 tokens of 32768 columns); a larger call returns
+ * RK_ERR_ARGS before enqueuing anything. Every call on a device shares the
+ * array: calls that overlap on one device (on streams without an order
+ * between them) race on it, so the caller orders them. */
+int rk_matmul_t_device_noalloc(rk_device *dev, int32_t n, rk_matrix *const *ms, float *const *d_outs,
+                               const float *d_x, int64_t cols, int32_t tokens, void *stream);
 
 /* ---- Arenas, vectors and batches (internal/gpu/batch.go) ----
  * An arena is device memory of 32-bit words holding a computation's

@@ -87,6 +87,9 @@ struct rk_device {
     int64_t bq_cap = 0;  // codes
     float *bx = nullptr, *bout = nullptr;
     int64_t bx_cap = 0, bout_cap = 0;  // floats
+    // Device address of rk_noalloc.hip's static scratch on this device
+    // (looked up at open; rk_matmul_t_device_noalloc's quantized inputs).
+    void *noalloc = nullptr;
     hipEvent_t scratch_free = nullptr;
     hipStream_t scratch_stream = nullptr;  // the last stream that used the scratch
     bool scratch_stream_set = false;
@@ -140,6 +143,15 @@ int mixed_inputs(rk_device *d, int32_t n, rk_matrix *const *ms);
 int enqueue_matvecs(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
                     const QScratch &q, hipStream_t s);
 void add_used(rk_device *d, int64_t bytes);
+// Batched products (rk_matmul_t*): the checks, and the enqueue with the
+// tokens' quantized inputs in q ([tokens][cols] codes, [tokens][cols/32]
+// scales and code sums).
+int check_matmul(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, int32_t tokens, int64_t *total);
+int enqueue_matmuls(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
+                    int32_t tokens, const QScratch &q, hipStream_t s);
+// Looks up the static scratch's device address on the current device
+// (rk_noalloc.hip); called by rk_device_open.
+int noalloc_setup(rk_device *d);
 
 // Times the one kernel launched in its scope when the device is profiling.
 class ProfScope {

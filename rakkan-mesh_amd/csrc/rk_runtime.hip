@@ -242,17 +242,17 @@ static int batch_scratch(rk_device *d, int64_t codes) {
 // Batched products: quantize the tokens' inputs once, then one MFMA launch
 // per format (up to three matrices each).
 int enqueue_matmuls(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *outs, const float *x, int64_t cols,
-                    int32_t tokens, hipStream_t s) {
+                    int32_t tokens, const QScratch &q, hipStream_t s) {
     {
         ProfScope p(d, s, "quantize_acts");
-        launch_quantize_acts(x, cols * tokens, d->bqx, d->bxs, d->bxsum, s);
+        launch_quantize_acts(x, cols * tokens, q.qx, q.xs, q.xsum, s);
     }
     for (int kind : {RK_Q8, RK_Q4}) {
         MmArgs a{};
         a.cols = (int32_t)cols;
         a.tokens = tokens;
-        a.qx = d->bqx;
-        a.xs = d->bxs;
+        a.qx = q.qx;
+        a.xs = q.xs;
         auto flush = [&]() -> int {
             if (a.nseg == 0) return RK_OK;
             bool ok;
@@ -281,7 +281,7 @@ int enqueue_matmuls(rk_device *d, int32_t n, rk_matrix *const *ms, float *const 
     return RK_OK;
 }
 
-static int check_matmul(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, int32_t tokens, int64_t *total) {
+int check_matmul(rk_device *d, int32_t n, rk_matrix *const *ms, int64_t cols, int32_t tokens, int64_t *total) {
     int rc = check_products(d, n, ms, cols, total);
     if (rc) return rc;
     for (int i = 0; i < n; i++)
@@ -402,6 +402,7 @@ int rk_device_open(int32_t index, rk_device **out) {
         return bail(rc);
     if ((e = hipHostMalloc((void **)&d->h_stage, 4 * (kMaxCols + kMaxRows), hipHostMallocDefault)) != hipSuccess)
         return bail(hip_fail(d, e, "pinned staging"));
+    if ((rc = noalloc_setup(d))) return bail(rc);
     *out = d;
     return RK_OK;
 }
@@ -641,7 +642,8 @@ int rk_matmul_t(rk_device *d, int32_t n, rk_matrix *const *ms, float *const *out
         douts[i] = d->bout + at;
         at += ms[i]->rows * tokens;
     }
-    if ((rc = enqueue_matmuls(d, n, ms, douts.data(), d->bx, cols, tokens, s))) return rc;
+    if ((rc = enqueue_matmuls(d, n, ms, douts.data(), d->bx, cols, tokens, QScratch{d->bqx, d->bxs, d->bxsum}, s)))
+        return rc;
     at = 0;
     for (int i = 0; i < n; i++) {
         HIP_TRY(d, hipMemcpyAsync(outs[i], d->bout + at, (size_t)(ms[i]->rows * tokens) * 4, hipMemcpyDeviceToHost, s),
@@ -668,7 +670,7 @@ int rk_matmul_t_device(rk_device *d, int32_t n, rk_matrix *const *ms, float *con
         return fail(d, RK_ERR_ARGS, "while recording a graph, work goes on the device's stream");
     if ((rc = scratch_acquire(d, s))) return rc;
     if ((rc = batch_scratch(d, cols * tokens))) return rc;
-    return enqueue_matmuls(d, n, ms, d_outs, d_x, cols, tokens, s);
+    return enqueue_matmuls(d, n, ms, d_outs, d_x, cols, tokens, QScratch{d->bqx, d->bxs, d->bxsum}, s);
 }
 
 int rk_graph_begin(rk_device *d) {

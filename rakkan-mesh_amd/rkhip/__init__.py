@@ -57,6 +57,7 @@ SIGNATURES = {
     "rk_matvecs_device": (ctypes.c_int, [P, I32, P, P, P, I64, P]),
     "rk_matmul_t": (ctypes.c_int, [P, I32, P, P, P, I64, I32]),
     "rk_matmul_t_device": (ctypes.c_int, [P, I32, P, P, P, I64, I32, P]),
+    "rk_matmul_t_device_noalloc": (ctypes.c_int, [P, I32, P, P, P, I64, I32, P]),
     "rk_arena_new": (ctypes.c_int, [P, I64, I64, P]),
     "rk_arena_set_quant_scratch": (ctypes.c_int, [P, I64, I64]),
     "rk_arena_bytes": (I64, [P]),
@@ -402,6 +403,14 @@ class Device:
         ops = (P * len(ms))(*d_outs)
         self._check(lib().rk_matmul_t_device(self.h, len(ms), hs, ops, P(d_x), cols, tokens,
                                              P(stream) if stream else None))
+
+    def matmul_t_device_noalloc(self, ms, d_outs, d_x, cols, tokens, stream=None):
+        """rk_matmul_t_device_noalloc: the same products with the quantized
+        inputs in the library's static scratch (allocates nothing)."""
+        hs = (P * len(ms))(*[m.h for m in ms])
+        ops = (P * len(ms))(*d_outs)
+        self._check(lib().rk_matmul_t_device_noalloc(self.h, len(ms), hs, ops, P(d_x), cols, tokens,
+                                                     P(stream) if stream else None))
 
     def tensor_matmul(self, a, b, transposed=False):
         """rakkan_tensor_v1 matmul (b [k][n]) / matmul_t (b [n][k]) of 2-D
