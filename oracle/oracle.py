@@ -60,6 +60,7 @@ def _declare(L):
         "rko_transcendental_words": (None, [P, I64]),
         "rko_matvec": (None, [P, P, P]), "rko_rope_table": (None, [P, I32, P, P]),
         "rko_rmsnorm": (None, [P, P, P, I64, F32]), "rko_softmax": (None, [P, I64]), "rko_silu": (F32, [F32]),
+        "rko_attention_head": (None, [P, P, P, I64, ctypes.c_int, ctypes.c_int, F32, P, P]),
         "rko_forward": (None, [P, P, I32, P, P, P, P, I32, P, I32, P]),
         "rko_embed": (None, [P, P, I32, P]), "rko_logits": (None, [P, P, P, P, P]), "rko_argmax": (I32, [P, I64]),
         "rko_num_eval": (None, [ctypes.c_int, P, P, I64]),
@@ -218,6 +219,18 @@ def softmax(x):
     x = _c(x, np.float32).copy()
     lib().rko_softmax(ptr(x), x.size)
     return x
+
+
+def attention_head(q, keys, vals, inv_sqrt):
+    """One head's attention (internal/llm/model.go:570-588): q [hs], keys and
+    vals [positions][hs]; returns (weights [positions], out [hs])."""
+    q, keys, vals = _c(q, np.float32), _c(keys, np.float32), _c(vals, np.float32)
+    positions, hs = keys.shape
+    att = np.empty(positions, np.float32)
+    out = np.empty(hs, np.float32)
+    lib().rko_attention_head(ptr(q), ptr(keys), ptr(vals), hs, hs, positions, np.float32(inv_sqrt), ptr(att),
+                             ptr(out))
+    return att, out
 
 
 def topk(v, k):

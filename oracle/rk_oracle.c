@@ -679,6 +679,22 @@ void rko_softmax(float *x, int64_t n) {
     for (int64_t i = 0; i < n; i++) x[i] = x[i] * inv;
 }
 
+/* internal/llm/model.go:570-588: one head's attention at a position, over
+ * `positions` cached keys and values (kv_stride floats apart, the head's
+ * slice at their start): scores float32(Dot32(q, k_t)·invSqrt), softmax, and
+ * out[i] = Σ_t a_t·v_t[i] added in t order from +0. att holds the scores,
+ * then the weights. */
+void rko_attention_head(const float *qh, const float *keys, const float *vals, int64_t kv_stride, int hs,
+                        int positions, float inv_sqrt, float *att, float *out) {
+    for (int t = 0; t < positions; t++) att[t] = rko_dot32(qh, keys + (int64_t)t * kv_stride, hs) * inv_sqrt;
+    rko_softmax(att, positions);
+    for (int i = 0; i < hs; i++) out[i] = 0.0f;
+    for (int t = 0; t < positions; t++) {
+        const float *vt = vals + (int64_t)t * kv_stride;
+        for (int i = 0; i < hs; i++) out[i] += att[t] * vt[i];
+    }
+}
+
 /* internal/llm/model.go:657 silu */
 float rko_silu(float v) { return v * rko_recip32(1.0f + rko_exp32(-v)); }
 
@@ -733,16 +749,9 @@ void rko_forward(const rko_config *c, const rko_layer *layers, int32_t nlayers, 
         memcpy(keys[li] + (int64_t)pos * kvDim, k, (size_t)kvDim * 4);
         memcpy(vals[li] + (int64_t)pos * kvDim, v, (size_t)kvDim * 4);
         for (int h = 0; h < c->heads; h++) {
-            const float *qh = q + h * hs;
             int off = (h / kvMul) * hs;
-            for (int t = 0; t <= pos; t++) att[t] = rko_dot32(qh, keys[li] + (int64_t)t * kvDim + off, hs) * invSqrt;
-            rko_softmax(att, pos + 1);
-            float *out = attOut + h * hs;
-            for (int i = 0; i < hs; i++) out[i] = 0.0f;
-            for (int t = 0; t <= pos; t++) {
-                const float *vt = vals[li] + (int64_t)t * kvDim + off;
-                for (int i = 0; i < hs; i++) out[i] += att[t] * vt[i];
-            }
+            rko_attention_head(q + h * hs, keys[li] + off, vals[li] + off, kvDim, hs, pos + 1, invSqrt, att,
+                               attOut + h * hs);
         }
         rko_matvec(&l->wo, xb2, attOut);
         for (int i = 0; i < dim; i++) x[i] += xb2[i];

@@ -118,6 +118,8 @@ void rko_matvec(const rko_mat *m, float *out, const float *x);
 void rko_rope_table(const rko_config *c, int32_t n, float *cos_t, float *sin_t);
 void rko_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps);
 void rko_softmax(float *x, int64_t n);
+void rko_attention_head(const float *qh, const float *keys, const float *vals, int64_t kv_stride, int hs,
+                        int positions, float inv_sqrt, float *att, float *out);
 float rko_silu(float v);
 void rko_num_eval(int fn, const float *in, float *out, int64_t n);
 /* One token through layers [0, nlayers) at position pos, x in place.

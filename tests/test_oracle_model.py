@@ -119,3 +119,76 @@ def test_quantized_models_stay_close_to_float():
         worst[dtype] = w
         assert w <= 0.5, (dtype, w)
     assert worst["q8_0"] < worst["q4_0"]
+
+
+# --- closed forms for the order of the layer's float sums -------------------
+# Each input makes the reference's order give one float32 and every other
+# plausible order (pairwise, reversed, a plain dot product) another.
+
+def _b(v):
+    return np.asarray(v, np.float32).view(np.uint32)
+
+
+def test_softmax_sums_in_one_sequential_chain():
+    """internal/llm/model.go:640-654: sum += e_i for i ascending. With
+    e = 1, Exp32(-17), Exp32(-17), each small term is below half an ulp of 1
+    (2^-24), so 1 + e1 + e2 stays 1 and p0 = 1 exactly; added as
+    1 + (e1 + e2) or from the end, the two terms pass half an ulp and the
+    sum is 1 + 2^-23, so p0 = Recip32(1 + 2^-23) < 1."""
+    from oracle import oracle
+
+    e = np.float32(oracle.exp32(-17.0))
+    assert 2.0 ** -25 < e <= 2.0 ** -24
+    assert np.float32(np.float32(1) + np.float32(e + e)) == np.float32(1 + 2.0 ** -23)
+    for x in ([0.0, -17.0, -17.0], [5.0, -12.0, -12.0]):  # the maximum subtracted first
+        p = oracle.softmax(np.array(x, np.float32))
+        assert _b(p[0]) == _b(1.0), p
+        assert _b(p[1]) == _b(e) and _b(p[2]) == _b(e)
+
+
+def test_attention_adds_positions_in_order():
+    """internal/llm/model.go:580-586: out[i] += a_t·v_t[i] for t ascending,
+    from +0. A zero query gives equal scores, weights Recip32(4) = 0.25
+    exactly, and exact products. Element 0's products 1e8, 1, -1e8, 1 sum
+    to 1 in order ((1e8 + 1) rounds to 1e8) but to 0 reversed or pairwise;
+    element 1's 1, 1e8, -1e8, 0 sum to 0 in order but to 1 reversed."""
+    from oracle import oracle
+
+    hs = 32
+    keys = np.random.default_rng(1).normal(0, 1, (4, hs)).astype(np.float32)
+    vals = np.zeros((4, hs), np.float32)
+    vals[:, 0] = np.array([1e8, 1, -1e8, 1], np.float32) * 4
+    vals[:, 1] = np.array([1, 1e8, -1e8, 0], np.float32) * 4
+    vals[:, 2] = 4.0
+    att, out = oracle.attention_head(np.zeros(hs, np.float32), keys, vals, 1 / math.sqrt(hs))
+    assert np.all(_b(att) == _b(0.25))
+    assert _b(out[0]) == _b(1.0) and _b(out[1]) == _b(0.0) and _b(out[2]) == _b(4.0)
+    assert not out[3:].any()
+
+
+def test_rmsnorm_uses_dot32():
+    """internal/llm/model.go:632-638: ss = Dot32(x, x)·Recip32(n) + eps.
+    x = 4096 then 31 ones: Dot32's running sum 0 holds 2^24, its combine
+    adds the ones in groups (e_0 = (2^24 + 1) + (1 + 1) = 2^24 + 2, the other
+    seven 4 each), giving 2^24 + 30; a sequential Dot loses every one
+    (2^24 + 1 is a tie that rounds back to 2^24). The output is
+    w·float32(Rsqrt32(ss)·x) from the Dot32 sum, not from the other."""
+    from oracle import oracle
+
+    x = np.ones(32, np.float32)
+    x[0] = 4096
+    assert oracle.dot32(x, x) == np.float32(2 ** 24 + 30)
+    assert np.float32(oracle.lib().rko_dot(oracle.ptr(x), oracle.ptr(x), 32)) == np.float32(2 ** 24)
+    w = np.linspace(0.5, 1.5, 32).astype(np.float32)
+    eps = np.float32(1e-5)
+    rn = np.float32(oracle.recip32(32.0))
+    assert rn == np.float32(1 / 32)
+
+    def norm_from(total):
+        ss = np.float32(np.float32(np.float32(total) * rn) + eps)
+        r = np.float32(oracle.rsqrt32(ss))
+        return (w * (r * x).astype(np.float32)).astype(np.float32)
+
+    got = oracle.rmsnorm(x, w, eps)
+    assert np.array_equal(_b(got), _b(norm_from(2 ** 24 + 30)))
+    assert not np.array_equal(_b(got), _b(norm_from(2 ** 24)))

@@ -32,6 +32,12 @@ def test_topk_is_a_stable_descending_sort():
 
 
 def test_moe_composition():
+    """The contract's three order choices, each on inputs where the
+    plausible alternative gives other bits (checked in the test, so a
+    planted slip in the oracle fails it): experts added in ascending index
+    (not selection order), each weight applied to the expert's hidden
+    activation before W2 (not to its output), and the weights' normalising
+    sum taken in selection order (not ascending)."""
     rng = np.random.default_rng(2)
     dim, hidden, experts, k = 96, 64, 12, 3
     q8 = lambda r, c: Mat(r, c, (rng.normal(0, 0.2, r * c)).astype(np.float32), "q8_0")  # noqa: E731
@@ -39,6 +45,7 @@ def test_moe_composition():
     w1 = [q8(hidden, dim) for _ in range(experts)]
     w3 = [q8(hidden, dim) for _ in range(experts)]
     w2 = [q8(dim, hidden) for _ in range(experts)]
+    differs = {"selection-order sum": 0, "weight on the output": 0, "ascending weight sum": 0}
     for t in range(20):
         xn = rng.normal(0, 1, dim).astype(np.float32)
         y, sel, w = oracle.moe_ffn(router, w1, w2, w3, k, xn)
@@ -51,11 +58,29 @@ def test_moe_composition():
         inv = oracle.recip32(tot)
         ww = (p[s] * inv).astype(np.float32)
         assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
-        acc = np.zeros(dim, np.float32)
-        for e in sorted(s):
+        outs, outs_unweighted = {}, {}
+        for e in s:
             g = oracle.matvec_q8(w1[e].q, w1[e].scales, xn, hidden, dim)
             u = oracle.matvec_q8(w3[e].q, w3[e].scales, xn, hidden, dim)
             sg = oracle.num_eval(3, g)  # silu
-            h = (ww[list(s).index(e)] * (sg * u).astype(np.float32)).astype(np.float32)
-            acc = (acc + oracle.matvec_q8(w2[e].q, w2[e].scales, h, dim, hidden)).astype(np.float32)
-        assert np.array_equal(y.view(np.uint32), acc.view(np.uint32))
+            gu = (sg * u).astype(np.float32)
+            h = (ww[list(s).index(e)] * gu).astype(np.float32)
+            outs[e] = oracle.matvec_q8(w2[e].q, w2[e].scales, h, dim, hidden)
+            outs_unweighted[e] = oracle.matvec_q8(w2[e].q, w2[e].scales, gu, dim, hidden)
+
+        def add(order, terms):
+            acc = np.zeros(dim, np.float32)
+            for e in order:
+                acc = (acc + terms[e]).astype(np.float32)
+            return acc.view(np.uint32)
+
+        assert np.array_equal(y.view(np.uint32), add(sorted(s), outs))
+        alt = {e: (ww[list(s).index(e)] * outs_unweighted[e]).astype(np.float32) for e in s}
+        differs["selection-order sum"] += not np.array_equal(y.view(np.uint32), add(list(s), outs))
+        differs["weight on the output"] += not np.array_equal(y.view(np.uint32), add(sorted(s), alt))
+        tot_asc = np.float32(0)
+        for e in sorted(s):
+            tot_asc = np.float32(tot_asc + p[e])
+        differs["ascending weight sum"] += not np.array_equal(ww.view(np.uint32),
+                                                              (p[s] * oracle.recip32(tot_asc)).astype(np.float32).view(np.uint32))
+    assert all(n > 0 for n in differs.values()), differs

@@ -190,6 +190,32 @@ def test_go_float64_functions_close_to_libm():
     assert worst <= 4
 
 
+def test_exp_within_one_ulp_of_correctly_rounded():
+    """internal/num/num.go:101-123 Exp (float64; used for NewRope's
+    frequencies). The reference pins it to 4 ulp of math.Exp (num_test.go:
+    41-47); its Taylor series to r^13 over |r| <= 0.347 keeps it within one
+    ulp of the correctly rounded value (50-digit Decimal), which a dropped
+    ln2Lo term, a missing Taylor term or a wrong factorial would break. Bits
+    beyond that are not pinned. Also its cut-offs (num.go:102-109)."""
+    from decimal import getcontext
+
+    getcontext().prec = 50
+    L = oracle.lib()
+    rng = np.random.default_rng(8)
+    xs = [float(v) for v in np.arange(-700.0, 700.0, 1.37)] + [float(v) for v in rng.uniform(-40, 40, 2000)]
+    xs += [k * math.log(2) for k in range(-60, 60)] + [math.nextafter(0.5 * math.log(2), 1.0)]
+    exact = 0
+    for x in xs:
+        got, cr = L.rko_exp(x), float(Decimal(x).exp())
+        if got != cr:
+            assert abs(got - cr) <= abs(math.nextafter(cr, math.inf) - cr), (x, got, cr)
+        else:
+            exact += 1
+    assert exact > 0.8 * len(xs)
+    assert L.rko_exp(0.0) == 1.0 and math.isinf(L.rko_exp(709.79)) and L.rko_exp(-745.14) == 0.0
+    assert math.isnan(L.rko_exp(math.nan))
+
+
 def test_bf16_rounding():
     """internal/num/num_test.go:104."""
     L = oracle.lib()
@@ -216,6 +242,49 @@ def test_quantize8_closed_forms():
     assert q.min() >= -127 and q.max() <= 127
     deq = q.astype(np.float32) * np.repeat(s, 32)
     assert np.all(np.abs(deq - w) <= s.repeat(32) * 0.5001)
+
+
+def test_quantize8_rounds_half_to_even():
+    """internal/num/quant.go:41-50: codes are RoundToEven(v·id). With a
+    block maximum of 127, d = 127·float32(1/127) is exactly 1 and
+    Recip32(1) = 1, so v·id = v and the halves are ties: ±0.5, ±1.5, ±2.5,
+    3.5 must give 0, ±2, ±2, 4. Rounding half away from zero gives ±1, ±2,
+    ±3, 4; truncation 0, ±1, ±2, 3."""
+    assert np.float32(127) * np.float32(1.0 / 127) == np.float32(1)
+    assert oracle.recip32(1.0) == 1.0
+    blk = np.zeros(32, np.float32)
+    ties = [0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 3.5, 126.5]
+    blk[0] = 127
+    blk[1:1 + len(ties)] = ties
+    q, s = oracle.quantize8(blk)
+    assert bits(s[0]) == bits(1.0)
+    assert q[0] == 127
+    assert list(q[1:1 + len(ties)]) == [0, 0, 2, -2, 2, -2, 4, 126]
+
+
+def test_quantize8_multiplies_by_recip32_not_divides():
+    """internal/num/quant.go:41: id = Recip32(d), then float32(v·id); no
+    division. At d = float32(102.8525·float32(1/127)) = 0.8098622,
+    Recip32(d) (0x3f9e0d35) is one ulp above the correctly rounded 1/d
+    (0x3f9e0d34), and at these three inputs that ulp moves v·id across a
+    rounding point: the exact products, rounded to float32, are 0.50000006,
+    1.5 (a tie, to even: 2) and 2.5000002, giving codes 1, 2, 3; v/d gives
+    0.5, 1.4999999 and 2.5 (codes 0, 1, 2), and v·float32(1/d) the same."""
+    amax = np.uint32(0x42CDB47B).view(np.float32)
+    d = np.float32(amax * np.float32(1.0 / 127))
+    r = np.float32(oracle.recip32(d))
+    assert bits(r) == 0x3F9E0D35 and bits(np.float32(1) / d) == 0x3F9E0D34
+    vs = np.array([0x3ECF5321, 0x3F9B7E58, 0x400193F5], np.uint32).view(np.float32)
+    blk = np.zeros(32, np.float32)
+    blk[0] = amax
+    blk[1:4] = vs
+    blk[4:7] = -vs
+    q, s = oracle.quantize8(blk)
+    assert bits(s[0]) == bits(d)
+    # the products rounded to float32, from exact rationals (not float code)
+    prods = [f32_round(Fraction(float(v)) * Fraction(float(r))) for v in vs]
+    assert prods == [bits(0.50000006), bits(1.5), bits(2.5000002)]
+    assert list(q[1:7]) == [1, 2, 3, -1, -2, -3]
 
 
 def test_quantized_matvec_error_bounds():
