@@ -61,6 +61,7 @@ def _declare(L):
         "rko_matvec": (None, [P, P, P]), "rko_rope_table": (None, [P, I32, P, P]),
         "rko_rmsnorm": (None, [P, P, P, I64, F32]), "rko_softmax": (None, [P, I64]), "rko_silu": (F32, [F32]),
         "rko_attention_head": (None, [P, P, P, I64, ctypes.c_int, ctypes.c_int, F32, P, P]),
+        "rko_set_matvec_threads": (None, [ctypes.c_int]),
         "rko_forward": (None, [P, P, I32, P, P, P, P, I32, P, I32, P]),
         "rko_embed": (None, [P, P, I32, P]), "rko_logits": (None, [P, P, P, P, P]), "rko_argmax": (I32, [P, I64]),
         "rko_num_eval": (None, [ctypes.c_int, P, P, I64]),
@@ -163,6 +164,23 @@ def matmul_q4(w, ws, x, tokens, rows, cols):
     out = np.empty(tokens * rows, np.float32)
     lib().rko_matmul_q4(ptr(out), ptr(w), ptr(ws), ptr(x), tokens, rows, cols)
     return out.reshape(tokens, rows)
+
+
+class matvec_threads:
+    """Within the block, the model forward's Q8 / Q4 products (rko_matvec)
+    run the AVX2 block sums on n threads (the same bits as the portable
+    loops; for model-size checks)."""
+
+    def __init__(self, n):
+        self.n = n
+
+    def __enter__(self):
+        lib().rko_set_matvec_threads(self.n)
+        return self
+
+    def __exit__(self, *exc):
+        lib().rko_set_matvec_threads(0)
+        return False
 
 
 def matvec_q8_avx2(w, ws, x, rows, cols, threads):

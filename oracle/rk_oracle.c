@@ -630,8 +630,23 @@ void rko_transcendental_words(uint64_t *out, int64_t steps) {
 }
 
 /* ------------------------------------------------------------------ */
+/* Threads for the Q8 / Q4 products of rko_matvec (the forward, the head,
+ * MoE): 0 (the default) runs the portable loops; n > 0 runs the AVX2 block
+ * sums with rows over n threads, which give the same bits (the order is
+ * per row, and block sums are exact), for model-size checks that must
+ * finish in seconds. */
+static int g_mv_threads = 0;
+void rko_set_matvec_threads(int n) { g_mv_threads = n > 0 && rko_have_avx2() ? n : 0; }
+
 /* internal/llm/model.go:170-188 Matrix.MulVec by storage type */
 void rko_matvec(const rko_mat *m, float *out, const float *x) {
+    if (g_mv_threads > 0 && (m->kind == RKO_Q8 || m->kind == RKO_Q4)) {
+        if (m->kind == RKO_Q8)
+            rko_matvec_q8_avx2_mt(out, m->q8, m->scales, x, m->rows, m->cols, g_mv_threads);
+        else
+            rko_matvec_q4_avx2_mt(out, m->q4, m->scales, x, m->rows, m->cols, g_mv_threads);
+        return;
+    }
     switch (m->kind) {
     case RKO_Q8: rko_matvec_q8(out, m->q8, m->scales, x, m->rows, m->cols); break;
     case RKO_Q4: rko_matvec_q4(out, m->q4, m->scales, x, m->rows, m->cols); break;

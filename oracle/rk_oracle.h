@@ -115,6 +115,9 @@ typedef struct {
 } rko_config;
 
 void rko_matvec(const rko_mat *m, float *out, const float *x);
+/* n > 0: rko_matvec's Q8 / Q4 products through the AVX2 block sums on n
+ * threads (the same bits); 0: the portable loops. */
+void rko_set_matvec_threads(int n);
 void rko_rope_table(const rko_config *c, int32_t n, float *cos_t, float *sin_t);
 void rko_rmsnorm(float *out, const float *x, const float *w, int64_t n, float eps);
 void rko_softmax(float *x, int64_t n);

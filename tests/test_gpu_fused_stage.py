@@ -182,10 +182,13 @@ def coded_model(c, seed, scale_lo=1e-4, scale_hi=1e-3):
 
     def mat(rows, cols, kind):
         s = rng.uniform(scale_lo, scale_hi, rows * cols // 32).astype(np.float32)
+        # uniform random bytes, from the generator's raw 64-bit words (fast
+        # at model sizes); Q8 codes are never -128 (quantize8 clamps to ±127)
+        n = rows * cols if kind == Q8 else rows * cols // 2
+        q = rng.bit_generator.random_raw((n + 7) // 8).view(np.uint8)[:n].copy()
         if kind == Q8:
-            q = rng.integers(-127, 128, rows * cols, dtype=np.int8)
-        else:
-            q = rng.integers(0, 256, rows * cols // 2, dtype=np.uint8)
+            q = q.view(np.int8)
+            q[q == -128] = -127
         return Mat.from_codes(kind, rows, cols, q, s)
 
     kind = Q4 if c.dtype == "q4_0" else Q8

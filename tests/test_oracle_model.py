@@ -192,3 +192,24 @@ def test_rmsnorm_uses_dot32():
     got = oracle.rmsnorm(x, w, eps)
     assert np.array_equal(_b(got), _b(norm_from(2 ** 24 + 30)))
     assert not np.array_equal(_b(got), _b(norm_from(2 ** 24)))
+
+
+def test_forward_with_threaded_products_gives_the_same_bits():
+    """The forward's products through the AVX2 block sums on several
+    threads (used by the model-size GPU checks) give the portable loops'
+    bits, for Q8 and Q4 layers."""
+    import pytest
+    from oracle import oracle
+
+    if not oracle.lib().rko_have_avx2():
+        pytest.skip("no AVX2 on this host")
+    for dtype in ("q8_0", "q4_m"):
+        c = Config(**{**CONFIGS[0].__dict__, "dtype": dtype})
+        m = Model(c, random_model(c, 11))
+        outs = []
+        for threads in (0, 5):
+            st = Stage(m, 24)
+            with oracle.matvec_threads(threads):
+                xs = [m.logits(st.forward(m.embed_token(t), pos)) for pos, t in enumerate([3, 7, 1, 40, 2])]
+            outs.append(np.stack(xs).view(np.uint32))
+        assert np.array_equal(outs[0], outs[1])
