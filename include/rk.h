@@ -277,6 +277,7 @@ int rk_graph_free(rk_graph *g);
  * HIP graph and replayed at every position. Results are the CPU path's
  * bits (Stage.Forward, internal/llm/model.go:522-613). */
 typedef struct rk_stage rk_stage;
+typedef struct rk_moe rk_moe; /* a mixture-of-experts feed-forward (rk_moe_new, below) */
 
 typedef struct {
     int32_t dim, hidden, heads, kv_heads;
@@ -288,15 +289,20 @@ typedef struct {
     float recip_dim;    /* num.Recip32(float32(dim)) (gpustage.go:124) */
     float recip_head;   /* num.Recip32(float32(head size)) (gpustage.go:125) */
     float inv_sqrt;     /* float32(1/math.Sqrt(float64(head size))) (gpustage.go:126) */
+    int32_t seqs;       /* independent sequences decoded together (rk_stage_seqs_*); 0 or 1: one */
 } rk_stage_config;
 
 /* One layer: its uploaded Q8/Q4 matrices (internal/llm/model.go:150-166
- * Layer) and host copies of its vectors (NULL when the config has none). */
+ * Layer) and host copies of its vectors (NULL when the config has none).
+ * With moe set, the layer's feed-forward is that mixture of experts (the
+ * same RMSNorm before it and residual after it: x = Canonical(x + moe(xn)))
+ * and w1, w2, w3 are not used (they may be NULL). */
 typedef struct {
     rk_matrix *wq, *wk, *wv, *wo, *w1, *w2, *w3;
     const float *rms_att, *rms_ffn; /* dim */
     const float *bq, *bk, *bv;      /* q_dim, kv_dim, kv_dim (qkv_bias) */
     const float *q_norm, *k_norm;   /* head size (qk_norm) */
+    rk_moe *moe;
 } rk_stage_layer;
 
 /* internal/llm/gpustage.go:51-83 newGPUStage: caches for ctx positions and
@@ -335,6 +341,27 @@ int rk_stage_generate_tokens(rk_stage *s, int32_t from, int32_t n, int32_t *out)
 /* start, then run n_prompt+steps-1 positions: steps generated tokens. */
 int rk_stage_generate(rk_stage *s, const int32_t *prompt, int32_t n_prompt, int32_t steps, int32_t *out);
 
+/* Independent sequences decoded together (config.seqs of them; the
+ * coordinator's generations, internal/llm/generate.go:415-522, run side by
+ * side on one device). No reference counterpart as an API: each sequence's
+ * tokens and logits are bit for bit those of its own generation alone
+ * (rk_stage_generate), whatever the others hold. A stage of several
+ * sequences runs only these (the single-sequence calls return RK_ERR_ARGS);
+ * a stage of one runs both. The stage needs a head.
+ *
+ * start: prompts are the sequences' prompts back to back, lens[z] tokens
+ * each (1..ctx); every prompt position but the last goes through the
+ * batched path (each sequence's own caches). */
+int rk_stage_seqs_start(rk_stage *s, const int32_t *prompts, const int32_t *lens);
+/* `steps` decode steps: each sequence at its position (first the last of
+ * its prompt) runs embed, layers and head; its greedy argmax becomes its
+ * next token. logits, if not NULL, receives [steps][seqs][vocab]. Every
+ * sequence's positions must stay within the context. Blocking; each step is
+ * one replay of a recorded graph. */
+int rk_stage_seqs_run(rk_stage *s, int32_t steps, float *logits);
+/* Tokens of sequence `seq` at positions from..from+n-1. */
+int rk_stage_seqs_tokens(rk_stage *s, int32_t seq, int32_t from, int32_t n, int32_t *out);
+
 /* ---- The device's float functions (internal/num), for host callers and
  * tests: out[i] = f(in[i]) computed by the same device code the kernels use.
  * No reference counterpart (the Go CPU path calls package num directly). */
@@ -352,8 +379,8 @@ int rk_num_eval(rk_device *dev, int32_t fn, const float *in, float *out, int64_t
  * y = Σ W2_e·(w_e·(silu(W1_e·xn)·(W3_e·xn))) over the selected experts in
  * ascending index, from +0, in float32. Experts are Q8 W1/W3 [hidden][dim]
  * and W2 [dim][hidden]; the router is Q8 [experts][dim]. The matrices stay
- * the caller's (free them after rk_moe_free). */
-typedef struct rk_moe rk_moe;
+ * the caller's (free them after rk_moe_free, and after any stage that holds
+ * the handle in a layer). */
 int rk_moe_new(rk_device *dev, rk_matrix *router, int32_t experts, rk_matrix *const *w1, rk_matrix *const *w2,
                rk_matrix *const *w3, int32_t topk, rk_moe **out);
 /* xn, y: [tokens][dim] host buffers; sel, wsel (either may be NULL):

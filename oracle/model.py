@@ -22,7 +22,9 @@ class RkoMat(ctypes.Structure):
 
 class RkoLayer(ctypes.Structure):
     _fields_ = [(n, P) for n in ("rms_att", "rms_ffn", "bq", "bk", "bv", "q_norm", "k_norm")] + \
-               [(n, RkoMat) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")]
+               [(n, RkoMat) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3")] + \
+               [("experts", ctypes.c_int32), ("topk", ctypes.c_int32), ("router", RkoMat),
+                ("ew1", P), ("ew2", P), ("ew3", P)]
 
 
 class RkoConfig(ctypes.Structure):
@@ -111,6 +113,18 @@ class Mat:
                       a(self.q) if self.kind == Q8 else None, a(self.q) if self.kind == Q4 else None, a(self.scales))
 
 
+class Moe:
+    """A mixture-of-experts feed-forward (the build's contract, rko_moe_ffn):
+    a router Mat [experts][dim] and per expert W1/W3 [hidden][dim] and W2
+    [dim][hidden] Mats, top `topk`."""
+
+    def __init__(self, router, w1, w2, w3, topk):
+        self.router, self.w1, self.w2, self.w3, self.topk = router, list(w1), list(w2), list(w3), topk
+        n = len(self.w1)
+        arr = lambda ms: (RkoMat * n)(*[m.ctype() for m in ms])  # noqa: E731
+        self._c = (arr(self.w1), arr(self.w2), arr(self.w3))  # kept alive with the layer
+
+
 class Layer:
     VECS = ("rms_att", "rms_ffn", "bq", "bk", "bv", "q_norm", "k_norm")
     MATS = ("wq", "wk", "wv", "wo", "w1", "w2", "w3")
@@ -118,11 +132,17 @@ class Layer:
     def __init__(self):
         for n in self.VECS + self.MATS:
             setattr(self, n, None)
+        self.moe = None  # a Moe in place of w1/w2/w3
 
     def ctype(self):
         v = {n: (getattr(self, n).ctypes.data if getattr(self, n) is not None else None) for n in self.VECS}
-        m = {n: getattr(self, n).ctype() for n in self.MATS}
-        return RkoLayer(**v, **m)
+        if self.moe is None:
+            m = {n: getattr(self, n).ctype() for n in self.MATS}
+            return RkoLayer(**v, **m)
+        m = {n: (getattr(self, n).ctype() if getattr(self, n) is not None else RkoMat()) for n in self.MATS}
+        a1, a2, a3 = self.moe._c
+        return RkoLayer(**v, **m, experts=len(self.moe.w1), topk=self.moe.topk, router=self.moe.router.ctype(),
+                        ew1=ctypes.addressof(a1), ew2=ctypes.addressof(a2), ew3=ctypes.addressof(a3))
 
 
 def random_model(c: Config, seed: int, wscale=0.1):

@@ -771,6 +771,13 @@ void rko_forward(const rko_config *c, const rko_layer *layers, int32_t nlayers, 
         rko_matvec(&l->wo, xb2, attOut);
         for (int i = 0; i < dim; i++) x[i] += xb2[i];
         rko_rmsnorm(xb, x, l->rms_ffn, dim, eps);
+        if (l->experts > 0) {
+            /* the MoE feed-forward in place of SwiGLU, the same residual
+             * (model.go:608-610): x = Canonical(x + y) */
+            rko_moe_ffn(&l->router, l->ew1, l->ew2, l->ew3, l->experts, l->topk, xb, xb2, NULL, NULL);
+            for (int i = 0; i < dim; i++) x[i] = rko_canonical(x[i] + xb2[i]);
+            continue;
+        }
         rko_matvec(&l->w1, hb, xb);
         rko_matvec(&l->w3, hb2, xb);
         for (int i = 0; i < hidden; i++) hb[i] = rko_silu(hb[i]) * hb2[i];

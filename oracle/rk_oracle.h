@@ -106,6 +106,12 @@ typedef struct {
 typedef struct {
     const float *rms_att, *rms_ffn, *bq, *bk, *bv, *q_norm, *k_norm;
     rko_mat wq, wk, wv, wo, w1, w2, w3;
+    /* A mixture-of-experts feed-forward in place of w1/w2/w3 when experts
+     * > 0: the router [experts][dim] and each expert's W1/W3 [hidden][dim]
+     * and W2 [dim][hidden] (rko_moe_ffn), top `topk`. */
+    int32_t experts, topk;
+    rko_mat router;
+    const rko_mat *ew1, *ew2, *ew3;
 } rko_layer;
 
 typedef struct {

@@ -219,7 +219,8 @@ __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const floa
 }
 
 bool att_group_fits(const AttBatch &bt, int hs, int kv_dim) {
-    return bt.pos0 + bt.tokens <= kGrpMaxT && hs % 32 == 0 && kv_dim % 4 == 0;
+    // (consecutive positions of one sequence only)
+    return !bt.pos && bt.pos0 + bt.tokens <= kGrpMaxT && hs % 32 == 0 && kv_dim % 4 == 0;
 }
 
 void launch_att_scores_group(const float *q, const float *keys, float *att, int32_t att_stride, const AttBatch &bt,

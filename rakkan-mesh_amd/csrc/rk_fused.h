@@ -104,10 +104,21 @@ bool stream_has(int fmt, int pro, int epi, int cols);
 // A batch of consecutive positions for the attention kernels: token z sits
 // at pos0 + z and attends to positions 0..pos0+z; its rows are z·stride
 // floats into the q, scores and output buffers. Used when ctl is null.
+// Independent sequences: with `pos` set, token z is sequence z, at position
+// pos[z] (device memory), attending to its own cache, cache_stride floats
+// after sequence z-1's.
 struct AttBatch {
     int32_t pos0 = 0, tokens = 1;
     int64_t q_stride = 0, att_stride = 0, out_stride = 0;
+    const int32_t *pos = nullptr;
+    int64_t cache_stride = 0;
 };
+
+// Position of token z of an attention launch: the stage's (ctl), the
+// sequence's own (bt.pos), or z after the batch's first.
+__device__ __forceinline__ int att_position(const int32_t *ctl, const AttBatch &bt, int z) {
+    return ctl ? ctl[kCtlPos] : (bt.pos ? bt.pos[z] : bt.pos0 + z);
+}
 
 // Attention of one position over a stage's cache (internal/llm/model.go:
 // 575-591), position and length read from ctl (or, ctl null, a batch):
@@ -129,11 +140,12 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx,
                        float *xs, int32_t *xsum, hipStream_t s);
 // QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches, at
-// the position in ctl (or, ctl null, for `tokens` rows at pos0, pos0+1, ...).
+// the position in ctl (or, ctl null, for `tokens` rows at pos0, pos0+1, ...;
+// or, seq_pos set, row z at seq_pos[z] in caches cache_stride floats apart).
 void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                         float recip_hs, float eps, const float *cos_t, const float *sin_t, const int32_t *ctl,
                         int32_t pos0, int tokens, float *kcache, float *vcache, int heads, int kv_heads, int hs,
-                        hipStream_t s);
+                        hipStream_t s, const int32_t *seq_pos = nullptr, int64_t cache_stride = 0);
 // x = the embedding row of tokens[ctl[kCtlPos]] (Q8_0 or Q4_0 table), and
 // RMSNorm(x) with norm_w quantized into qx/xs/xsum (one workgroup;
 // dim <= kMaxNormCols).
@@ -141,9 +153,16 @@ void launch_embed_norm(const uint8_t *w, const float *scales, bool q4, const int
                        int dim, float *x, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
                        int32_t *xsum, hipStream_t s);
 // Embedding rows of tokens[pos0..pos0+n) (Q8_0 or Q4_0 table) into x
-// [n][dim], as embed_norm gives them one position at a time.
+// [n][dim], as embed_norm gives them one position at a time; with seq_pos,
+// row z is sequence z's token at its position, tokens[z·tok_stride +
+// seq_pos[z]].
 void launch_embed_rows(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, int32_t pos0, int n,
-                       int dim, float *x, hipStream_t s);
+                       int dim, float *x, hipStream_t s, int64_t tok_stride = 0, const int32_t *seq_pos = nullptr);
+// Independent sequences' greedy step: the argmax of each of `seqs` logits
+// rows ([seqs][vocab]) becomes that sequence's token at pos[z]+1 (past its
+// prompt), and pos[z] advances.
+void launch_seqs_advance(const float *logits, int64_t vocab, int seqs, int32_t *pos, const int32_t *prompt,
+                         int32_t *tokens, int64_t tok_stride, int32_t tokens_len, hipStream_t s);
 // RMSNorm(x) with norm_w quantized into qx/xs/xsum (one workgroup; n <=
 // kMaxNormCols).
 // The greedy argmax's end (internal/llm/sample.go:45-53): folds the

@@ -619,9 +619,10 @@ __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const f
                                                          int kv_mul, int hs_rt, int kv_dim, float inv_sqrt) {
     const int hs = HS ? HS : hs_rt;
     const int z = blockIdx.z;  // token of a batch (0 when the position comes from ctl)
-    const int T = (ctl ? ctl[kCtlPos] : bt.pos0 + z) + 1;
+    const int T = att_position(ctl, bt, z) + 1;
     q += (int64_t)z * bt.q_stride;
     att += (int64_t)z * bt.att_stride;
+    keys += (int64_t)z * bt.cache_stride;
     const int t0 = blockIdx.y * kScoreTile;
     if (t0 >= T) return;
     const int h = blockIdx.x, g = h / kv_mul;
@@ -671,8 +672,9 @@ void launch_att_scores(const float *q, const float *keys, float *att, int32_t at
         launch_att_scores_group(q, keys, att, att_stride, bt, heads, kv_heads, kv_dim, inv_sqrt, s);
         return;
     }
-    // decode: positions up to ctx; a batch: up to its last token's
-    const int npos = ctl ? ctx : bt.pos0 + bt.tokens;
+    // decode and independent sequences: positions up to ctx (tiles past a
+    // token's position exit); a batch: up to its last token's
+    const int npos = ctl || bt.pos ? ctx : bt.pos0 + bt.tokens;
     const dim3 grid(heads, (npos + kScoreTile - 1) / kScoreTile, ctl ? 1 : bt.tokens);
     if (hs == 128)
         RK_LAUNCH(att_scores_kernel<128>, grid, dim3(256), 0, s, q, keys, att, att_stride, ctl, bt, heads / kv_heads,
@@ -717,9 +719,10 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
     float *sa = smem;            // [ctx_pad] scores -> weights
     float *sp = smem + ctx_pad;  // [2][kValSlice][kValPitch] product tiles of two chunks
     const int z = blockIdx.z;  // token of a batch (0 when the position comes from ctl)
-    const int T = (ctl ? ctl[kCtlPos] : bt.pos0 + z) + 1;
+    const int T = att_position(ctl, bt, z) + 1;
     att += (int64_t)z * bt.att_stride;
     out += (int64_t)z * bt.out_stride;
+    vals += (int64_t)z * bt.cache_stride;
     if (qx) {
         qx += (int64_t)z * bt.out_stride;
         xs += (int64_t)z * (bt.out_stride >> 5);
@@ -920,10 +923,11 @@ __global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float 
     float *sa = smem;               // [ctx_pad] scores -> e_t
     float *tiles = smem + ctx_pad;  // [2][32][kVrChunk] products, swizzled rows
     const int z = blockIdx.y;       // token of a batch (0 when the position comes from ctl)
-    const int T = (ctl ? ctl[kCtlPos] : bt.pos0 + z) + 1;
+    const int T = att_position(ctl, bt, z) + 1;
     const int nch = (T + kVrChunk - 1) / kVrChunk;
     att += (int64_t)z * bt.att_stride;
     out += (int64_t)z * bt.out_stride;
+    vals += (int64_t)z * bt.cache_stride;
     if (qx) {
         qx += (int64_t)z * bt.out_stride;
         xs += (int64_t)z * (bt.out_stride >> 5);
@@ -1085,13 +1089,17 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
 __global__ __launch_bounds__(64) void qknorm_rope_kernel(float *q, const float *k, const float *v,
                                                          const float *q_norm, const float *k_norm, float recip_hs,
                                                          float eps, const float *cos_t, const float *sin_t,
-                                                         const int32_t *ctl, int32_t pos0, float *kcache,
-                                                         float *vcache, int heads, int hs, int kv_dim) {
+                                                         const int32_t *ctl, int32_t pos0, const int32_t *seq_pos,
+                                                         int64_t cache_stride, float *kcache, float *vcache,
+                                                         int heads, int hs, int kv_dim) {
     extern __shared__ float sy[];  // [hs]
-    // a batch: token blockIdx.y at pos0 + blockIdx.y, rows [tokens][heads·hs]
-    // and [tokens][kv_dim]
+    // a batch: token blockIdx.y at pos0 + blockIdx.y (or, independent
+    // sequences, at seq_pos[blockIdx.y] in its own caches), rows
+    // [tokens][heads·hs] and [tokens][kv_dim]
     const int z = blockIdx.y;
-    const int pos = ctl ? ctl[kCtlPos] : pos0 + z;
+    const int pos = ctl ? ctl[kCtlPos] : seq_pos ? seq_pos[z] : pos0 + z;
+    kcache += (int64_t)z * cache_stride;
+    vcache += (int64_t)z * cache_stride;
     q += (int64_t)z * heads * hs;
     k += (int64_t)z * kv_dim;
     v += (int64_t)z * kv_dim;
@@ -1122,9 +1130,10 @@ __global__ __launch_bounds__(64) void qknorm_rope_kernel(float *q, const float *
 void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
                         float recip_hs, float eps, const float *cos_t, const float *sin_t, const int32_t *ctl,
                         int32_t pos0, int tokens, float *kcache, float *vcache, int heads, int kv_heads, int hs,
-                        hipStream_t s) {
+                        hipStream_t s, const int32_t *seq_pos, int64_t cache_stride) {
     RK_LAUNCH(qknorm_rope_kernel, dim3(heads + kv_heads, ctl ? 1 : tokens), dim3(64), (size_t)hs * 4, s, q, k, v,
-              q_norm, k_norm, recip_hs, eps, cos_t, sin_t, ctl, pos0, kcache, vcache, heads, hs, kv_heads * hs);
+              q_norm, k_norm, recip_hs, eps, cos_t, sin_t, ctl, pos0, seq_pos, cache_stride, kcache, vcache, heads,
+              hs, kv_heads * hs);
 }
 
 // Embedding row of the token at the position (internal/llm/model.go:216-231
@@ -1182,8 +1191,12 @@ void launch_embed_norm(const uint8_t *w, const float *scales, bool q4, const int
 // embed_norm_kernel gives one position): workgroup per row, four elements a
 // thread.
 __global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t *w, const float *scales, int q4,
-                                                         const int32_t *tokens, int32_t pos0, int dim, float *x) {
-    const int64_t tok = tokens[pos0 + blockIdx.x];
+                                                         const int32_t *tokens, int32_t pos0, int dim, float *x,
+                                                         int64_t tok_stride, const int32_t *seq_pos) {
+    // row z: tokens[pos0 + z], or (independent sequences) sequence z's token
+    // at its position, tokens[z·tok_stride + seq_pos[z]]
+    const int z = blockIdx.x;
+    const int64_t tok = seq_pos ? tokens[(int64_t)z * tok_stride + seq_pos[z]] : tokens[pos0 + z];
     const int nb = dim >> 5, ng = dim >> 2;
     float *xr = x + (int64_t)blockIdx.x * dim;
     for (int g = threadIdx.x; g < ng; g += 256) {
@@ -1203,8 +1216,56 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t *w, const
 }
 
 void launch_embed_rows(const uint8_t *w, const float *scales, bool q4, const int32_t *tokens, int32_t pos0, int n,
-                       int dim, float *x, hipStream_t s) {
-    RK_LAUNCH(embed_rows_kernel, dim3(n), dim3(256), 0, s, w, scales, q4 ? 1 : 0, tokens, pos0, dim, x);
+                       int dim, float *x, hipStream_t s, int64_t tok_stride, const int32_t *seq_pos) {
+    RK_LAUNCH(embed_rows_kernel, dim3(n), dim3(256), 0, s, w, scales, q4 ? 1 : 0, tokens, pos0, dim, x, tok_stride,
+              seq_pos);
+}
+
+// Independent sequences' greedy step (internal/llm/sample.go:45-53 per
+// sequence): workgroup z takes the argmax of logits row z (the first index
+// holding the largest value; NaNs are never candidates, and a NaN first
+// logit keeps index 0, as the reference's `>` scan does), writes it as the
+// token at pos[z]+1 when that position is past the prompt, and advances
+// pos[z].
+__global__ __launch_bounds__(256) void seqs_advance_kernel(const float *logits, int64_t vocab, int32_t *pos,
+                                                           const int32_t *prompt, int32_t *tokens, int64_t tok_stride,
+                                                           int32_t tokens_len) {
+    __shared__ float s_v[4];
+    __shared__ int s_i[4];
+    const int z = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float *row = logits + (int64_t)z * vocab;
+    float bv = 0.0f;
+    int bi = -1;
+    for (int64_t i = threadIdx.x; i < vocab; i += 256) {
+        const float v = row[i];
+        if (v == v) argmax_merge(bv, bi, v, (int)i);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_down(bv, off);
+        const int oi = __shfl_down(bi, off);
+        argmax_merge(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        s_v[wave] = bv;
+        s_i[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = 0.0f;
+        int i = -1;
+        for (int w = 0; w < 4; w++) argmax_merge(v, i, s_v[w], s_i[w]);
+        if (row[0] != row[0] || i < 0) i = 0;  // a NaN first logit, or every logit NaN
+        const int p = pos[z];
+        if (p + 1 >= prompt[z] && p + 1 < tokens_len) tokens[(int64_t)z * tok_stride + p + 1] = i;
+        pos[z] = p + 1;
+    }
+}
+
+void launch_seqs_advance(const float *logits, int64_t vocab, int seqs, int32_t *pos, const int32_t *prompt,
+                         int32_t *tokens, int64_t tok_stride, int32_t tokens_len, hipStream_t s) {
+    RK_LAUNCH(seqs_advance_kernel, dim3(seqs), dim3(256), 0, s, logits, vocab, pos, prompt, tokens, tok_stride,
+              tokens_len);
 }
 
 __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(const float *x, int n, const float *norm_w,

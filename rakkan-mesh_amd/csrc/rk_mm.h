@@ -27,6 +27,8 @@ struct MmArgs {
     int32_t ldx;
     int32_t row_base;            // kEpQKV: logical q/k/v row (and bias index) of row 0
     int32_t pos0;                // kEpQKV: position of token 0
+    const int32_t *seq_pos;      // kEpQKV, independent sequences: token t at seq_pos[t] (device), not pos0 + t,
+    int64_t cache_stride;        //   in caches cache_stride floats after token t-1's
     int32_t hs, qdim, kvdim;     // kEpQKV: head size, q rows, k rows (= v rows)
     const float *cos_t, *sin_t;  // kEpQKV: rotary table [ctx][hs/2]
     float *q;                    // kEpQKV: [tokens][qdim]

@@ -296,7 +296,8 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
         for (int ti = 0; ti < TI; ti++) {
             const int gb = row0 + rb(ti) + 4 * lq;  // the lane's first row
             if (EPI == kEpQKV) {
-                const int pos = a.pos0 + t, half = a.hs >> 1;
+                const int pos = a.seq_pos ? a.seq_pos[t] : a.pos0 + t, half = a.hs >> 1;
+                const int64_t cache0 = (int64_t)t * a.cache_stride;  // token t's sequence's caches
 #pragma unroll
                 for (int pr = 0; pr < 2; pr++) {
                     const int g0 = gb + 2 * pr;  // an even row: a rotary pair with g0 + 1
@@ -321,8 +322,8 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
                         const int l = l0 + h;
                         float *dst = l < a.qdim ? a.q + (int64_t)t * a.qdim + l
                                      : l < a.qdim + a.kvdim
-                                         ? a.kcache + (int64_t)pos * a.kvdim + (l - a.qdim)
-                                         : a.vcache + (int64_t)pos * a.kvdim + (l - a.qdim - a.kvdim);
+                                         ? a.kcache + cache0 + (int64_t)pos * a.kvdim + (l - a.qdim)
+                                         : a.vcache + cache0 + (int64_t)pos * a.kvdim + (l - a.qdim - a.kvdim);
                         *dst = h ? v1 : v0;
                     }
                 }

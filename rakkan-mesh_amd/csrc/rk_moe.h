@@ -1,0 +1,63 @@
+// rk_moe.h — the mixture-of-experts feed-forward's internals, shared by the
+// standalone rk_moe_* entry points and the stages that hold MoE layers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rk_runtime.h"
+
+namespace rk {
+
+// Device scratch of one MoE feed-forward over up to `cap` tokens (a stage
+// shares one among its MoE layers, which run one after another).
+struct MoeScratch {
+    int cap = 0;
+    int gcap = 0;                  // groups the layout holds: min(experts, cap·topk)
+    float *logits = nullptr;       // [cap][experts]
+    int32_t *sel = nullptr;        // [cap][topk] selected experts, selection order
+    float *wsel = nullptr;         // [cap][topk] their weights
+    int32_t *grp = nullptr;        // groups: count, expert[gcap], start[gcap], pairs[gcap], pair list[cap·topk]
+    int8_t *hq = nullptr;          // [cap·topk][hidden] each (token, slot)'s h, quantized
+    float *hs = nullptr;
+    int32_t *hsum = nullptr;
+    float *o = nullptr;            // [cap·topk][dim] each (token, slot)'s W2·h
+};
+
+}  // namespace rk
+
+// One MoE feed-forward's weights: the router and each expert's W1, W3, W2
+// (caller-owned matrices), with device tables of their codes and scales.
+struct rk_moe {
+    rk_device *d = nullptr;
+    rk_matrix *router = nullptr;
+    int32_t experts = 0, topk = 0, dim = 0, hidden = 0;
+    const uint8_t **w1 = nullptr, **w3 = nullptr, **w2 = nullptr;
+    const float **s1 = nullptr, **s3 = nullptr, **s2 = nullptr;
+    void *tables = nullptr;
+    // scratch of the standalone calls (rk_moe_ffn*), grown to the largest
+    // batch: the input, its quantized form, the output, and a MoeScratch
+    void *mem = nullptr;
+    int64_t bytes = 0;
+    int cap = 0;
+    float *x = nullptr, *y = nullptr;
+    int8_t *qx = nullptr;
+    float *xs = nullptr;
+    int32_t *xsum = nullptr;
+    rk::MoeScratch sc;
+};
+
+namespace rk {
+
+// Bytes of a MoeScratch for `cap` tokens of m; with mem, also lays it out
+// there (256-byte aligned pieces). A stage sizes one for the largest of its
+// MoE layers.
+int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc);
+
+// The feed-forward of `tokens` inputs already quantized (qx [tokens][dim]
+// codes, xs/xsum [tokens][dim/32]): out = y, or (residual) out =
+// Canonical(out + y), rows [tokens][dim]. Enqueue only; it allocates
+// nothing, so it may be recorded into a graph.
+int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, const int32_t *xsum,
+                  int tokens, float *out, bool residual, hipStream_t s);
+
+}  // namespace rk

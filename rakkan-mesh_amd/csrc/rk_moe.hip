@@ -12,13 +12,16 @@
 //   h = float32(w·float32(silu(W1·xn)·(W3·xn)))  per selected expert
 //   y = Σ W2·h over the selected experts in ascending index, from +0
 //
-// Launches: the input quantized once; the router's product; the routing
-// (one workgroup per token); the selected experts' W1/W3 rows with the
-// gate and weight, h quantized in the same workgroup; their W2 rows; the
-// ascending-order sum.
-// Every expert product is a row dot of MatVecQ8 (integer block sums, the
-// eight ordered running sums), so each token's bits do not depend on the
-// batch.
+// Launches: the router's product (on the quantized input); the routing
+// (one wave per token); the grouping of the (token, slot) pairs by expert;
+// each selected expert's W1/W3 rows for all the tokens that chose it, with
+// the gate, the weight and h's quantization; each selected expert's W2 rows
+// for those tokens; the ascending-order sum (optionally into a residual).
+// An expert's rows are read from memory once per call however many tokens
+// chose it: a wave loads a chunk of its rows and dots it with each of the
+// group's inputs. Every expert product is a row dot of MatVecQ8 (integer
+// block sums, the eight ordered running sums), so each token's bits do not
+// depend on the batch or on the grouping.
 #include <algorithm>
 #include <mutex>
 #include <vector>
@@ -26,26 +29,7 @@
 #include "rk_dev.h"
 #include "rk_fused.h"
 #include "rk_mm.h"
-#include "rk_runtime.h"
-
-struct rk_moe {
-    rk_device *d = nullptr;
-    rk_matrix *router = nullptr;
-    int32_t experts = 0, topk = 0, dim = 0, hidden = 0;
-    // device tables: codes and scales of W1, W3, W2 per expert
-    const uint8_t **w1 = nullptr, **w3 = nullptr, **w2 = nullptr;
-    const float **s1 = nullptr, **s3 = nullptr, **s2 = nullptr;
-    void *tables = nullptr;
-    // scratch for up to `cap` tokens
-    int cap = 0;
-    void *mem = nullptr;
-    float *x = nullptr, *logits = nullptr, *wsel = nullptr, *o = nullptr, *y = nullptr;
-    int32_t *sel = nullptr;
-    int8_t *qx = nullptr, *hq = nullptr;
-    float *xs = nullptr, *hs = nullptr;
-    int32_t *xsum = nullptr, *hsum = nullptr;
-    int64_t bytes = 0;
-};
+#include "rk_moe.h"
 
 namespace rk {
 
@@ -54,23 +38,26 @@ namespace {
 constexpr int kMoeMaxK = 32;        // experts per token
 constexpr int kMoeMaxExperts = 1024;
 constexpr int kMoeMaxCols = 8192;   // widest expert input (chunks of 1 KiB per row)
-constexpr int kMoeRows = 4;         // rows per wave in the expert kernels
+constexpr int kMoePass = 4;         // inputs an expert's rows meet per pass
 
-// NR Q8 rows dotted with one quantized input (MatVecQ8's order per row:
-// exact block sums; block b into running sum b mod 8 in order of b; the
-// fixed tree). Lane 0 returns the results. Every lane of the wave calls it.
-template <int NR>
-__device__ __forceinline__ void wave_rows_q8(const uint8_t *const (&w)[NR], const float *const (&ws)[NR],
-                                             const int8_t *qx, const float *xs, int cols, float (&res)[NR]) {
+// NR Q8 rows dotted with np (<= NP) quantized inputs, each (row, input) in
+// MatVecQ8's order: exact block sums; block b into running sum b mod 8 in
+// order of b; the fixed tree ((0+1)+(2+3))+((4+5)+(6+7)). Each chunk of the
+// rows is loaded once for all the inputs. Lane 0 returns res[j][r]. Every
+// lane of the wave calls it; np is wave-uniform.
+template <int NR, int NP>
+__device__ __forceinline__ void wave_rows_q8_multi(const uint8_t *const (&w)[NR], const float *const (&ws)[NR],
+                                                   const int8_t *const (&qx)[NP], const float *const (&xs)[NP], int np,
+                                                   int cols, float (&res)[NP][NR]) {
     const int lane = threadIdx.x & 63;
     const int nb = cols >> 5, C = (cols + 1023) >> 10;
-    float acc[NR];
+    float acc[NP][NR];
 #pragma unroll
-    for (int r = 0; r < NR; r++) acc[r] = 0.0f;
+    for (int j = 0; j < NP; j++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) acc[j][r] = 0.0f;
     for (int c = 0; c < C; c++) {
         const int o = min(c * 1024 + lane * 16, cols - 16);  // lanes past the row's end: blocks excluded below
-        const int4 xv = *reinterpret_cast<const int4 *>(qx + o);
-        const float sx = xs[o >> 5];
         int4 wv[NR];
         float sw[NR];
 #pragma unroll
@@ -78,28 +65,36 @@ __device__ __forceinline__ void wave_rows_q8(const uint8_t *const (&w)[NR], cons
             wv[r] = load_stream16(w[r] + o);
             sw[r] = ws[r][o >> 5];
         }
+        const int b0 = c * 32 + (lane >> 1);
 #pragma unroll
-        for (int r = 0; r < NR; r++) {
-            const int s = pair_sum(dot16(wv[r], xv, 0));
-            const float t = (float)s * (sw[r] * sx);
-            // block 32c+k is in lanes 2k, 2k+1; running sum L (lane 2L) takes
-            // blocks 32c+L, +8, +16, +24
-            const float t1 = __shfl_down(t, 16), t2 = __shfl_down(t, 32), t3 = __shfl_down(t, 48);
-            if (lane < 16 && (lane & 1) == 0) {
-                const int b0 = c * 32 + (lane >> 1);
-                if (b0 < nb) acc[r] += t;
-                if (b0 + 8 < nb) acc[r] += t1;
-                if (b0 + 16 < nb) acc[r] += t2;
-                if (b0 + 24 < nb) acc[r] += t3;
+        for (int j = 0; j < NP; j++) {
+            if (j >= np) break;  // uniform
+            const int4 xv = *reinterpret_cast<const int4 *>(qx[j] + o);
+            const float sx = xs[j][o >> 5];
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const int s = pair_sum(dot16(wv[r], xv, 0));
+                const float t = (float)s * (sw[r] * sx);
+                // block 32c+k is in lanes 2k, 2k+1; running sum L (lane 2L)
+                // takes blocks 32c+L, +8, +16, +24
+                const float t1 = __shfl_down(t, 16), t2 = __shfl_down(t, 32), t3 = __shfl_down(t, 48);
+                if (lane < 16 && (lane & 1) == 0) {
+                    if (b0 < nb) acc[j][r] += t;
+                    if (b0 + 8 < nb) acc[j][r] += t1;
+                    if (b0 + 16 < nb) acc[j][r] += t2;
+                    if (b0 + 24 < nb) acc[j][r] += t3;
+                }
             }
         }
     }
 #pragma unroll
-    for (int r = 0; r < NR; r++) {
-        const float p2 = acc[r] + __shfl_down(acc[r], 2);
-        const float q4 = p2 + __shfl_down(p2, 4);
-        res[r] = q4 + __shfl_down(q4, 8);
-    }
+    for (int j = 0; j < NP; j++)
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const float p2 = acc[j][r] + __shfl_down(acc[j][r], 2);
+            const float q4 = p2 + __shfl_down(p2, 4);
+            res[j][r] = q4 + __shfl_down(q4, 8);
+        }
 }
 
 // 64-bit key of probability v at expert e for a max-reduction that picks
@@ -200,24 +195,62 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
     }
 }
 
-// W1 and W3 rows of each (token, slot)'s expert: h = w·(silu(W1·xn)·(W3·xn)),
-// then h's Q8_0 block. Workgroup (pair, block of 32 hidden rows), eight
-// waves of four hidden rows (W1 and W3 of each: eight row dots).
-constexpr int kUpRows = 8;
+// The (token, slot) pairs grouped by expert: grp[0] = the number of experts
+// selected, then at grp + 1 + g, + gcap, + 2·gcap their index (ascending),
+// first entry in the pair list and count, and the pair list from
+// grp + 1 + 3·gcap (each group's pairs in ascending order). One workgroup;
+// thread e counts expert e's pairs.
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, int npairs, int experts, int gcap,
+                                                         int32_t *grp) {
+    __shared__ int s_cnt[1024], s_any[1024];
+    const int e = threadIdx.x;
+    int cnt = 0;
+    if (e < experts)
+        for (int p = 0; p < npairs; p++) cnt += sel[p] == e;
+    s_cnt[e] = cnt;
+    s_any[e] = cnt > 0;
+    __syncthreads();
+    // inclusive scans (Hillis-Steele) of the counts and of the group marks
+    for (int d = 1; d < 1024; d <<= 1) {
+        const int c = e >= d ? s_cnt[e - d] : 0, a = e >= d ? s_any[e - d] : 0;
+        __syncthreads();
+        s_cnt[e] += c;
+        s_any[e] += a;
+        __syncthreads();
+    }
+    int32_t *gexp = grp + 1, *gstart = grp + 1 + gcap, *gcount = grp + 1 + 2 * gcap, *list = grp + 1 + 3 * gcap;
+    if (cnt > 0) {
+        const int g = s_any[e] - 1, start = s_cnt[e] - cnt;
+        gexp[g] = e;
+        gstart[g] = start;
+        gcount[g] = cnt;
+        int k = 0;
+        for (int p = 0; p < npairs; p++)
+            if (sel[p] == e) list[start + k++] = p;
+    }
+    if (e == 1023) grp[0] = s_any[1023];
+}
+
+// W1 and W3 rows of a selected expert for every pair that chose it:
+// h = w·(silu(W1·xn)·(W3·xn)), then h's Q8_0 block. Workgroup (group, block
+// of 32 hidden rows), eight waves of four hidden rows (W1 and W3 of each:
+// eight row dots), the group's pairs kMoePass at a time. Groups past the
+// count exit.
 __global__ __launch_bounds__(512) void moe_up_kernel(const uint8_t *const *w1, const float *const *s1,
                                                      const uint8_t *const *w3, const float *const *s3,
-                                                     const int32_t *sel, const float *wsel, int k, const int8_t *qx,
-                                                     const float *xs, int dim, int hidden, int8_t *hq, float *hs,
-                                                     int32_t *hsum) {
-    __shared__ __align__(16) float sh[32];
-    const int pr = blockIdx.x, t = pr / k;
-    const int e = sel[pr];
-    const float wt = wsel[pr];
+                                                     const int32_t *grp, int gcap, const float *wsel, int k,
+                                                     const int8_t *qx, const float *xs, int dim, int hidden,
+                                                     int8_t *hq, float *hs, int32_t *hsum) {
+    __shared__ __align__(16) float sh[kMoePass][32];
+    const int g = blockIdx.x;
+    if (g >= grp[0]) return;  // uniform
+    const int e = grp[1 + g], start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
+    const int32_t *list = grp + 1 + 3 * gcap + start;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int j0 = blockIdx.y * 32 + 4 * wave;  // hidden rows j0 .. j0+3
     const int nb = dim >> 5;
-    const uint8_t *w[kUpRows];
-    const float *ws[kUpRows];
+    const uint8_t *w[8];
+    const float *ws[8];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int j = j0 + q;  // hidden is a multiple of 32
@@ -226,60 +259,103 @@ __global__ __launch_bounds__(512) void moe_up_kernel(const uint8_t *const *w1, c
         w[2 * q + 1] = w3[e] + (int64_t)j * dim;
         ws[2 * q + 1] = s3[e] + (int64_t)j * nb;
     }
-    float res[kUpRows];
-    wave_rows_q8<kUpRows>(w, ws, qx + (int64_t)t * dim, xs + (int64_t)t * nb, dim, res);
-    if (lane == 0) {
+    for (int p0 = 0; p0 < count; p0 += kMoePass) {
+        const int np = min(kMoePass, count - p0);
+        int pr[kMoePass];
+        const int8_t *xq[kMoePass];
+        const float *xsp[kMoePass];
 #pragma unroll
-        for (int q = 0; q < 4; q++) sh[4 * wave + q] = wt * silu_mul(res[2 * q], res[2 * q + 1]);
+        for (int j = 0; j < kMoePass; j++) {
+            pr[j] = list[p0 + min(j, np - 1)];
+            const int t = pr[j] / k;
+            xq[j] = qx + (int64_t)t * dim;
+            xsp[j] = xs + (int64_t)t * nb;
+        }
+        float res[kMoePass][8];
+        wave_rows_q8_multi<8, kMoePass>(w, ws, xq, xsp, np, dim, res);
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < kMoePass; j++) {
+                if (j >= np) break;
+                const float wt = wsel[pr[j]];
+#pragma unroll
+                for (int q = 0; q < 4; q++) sh[j][4 * wave + q] = wt * silu_mul(res[j][2 * q], res[j][2 * q + 1]);
+            }
+        }
+        __syncthreads();
+        if (wave < np) {  // pair `wave`'s block of h: lanes 0-7, four values each
+            const int gi = min(lane, 7);
+            const float4 v4 = reinterpret_cast<const float4 *>(sh[wave])[gi];
+            float d;
+            int cs;
+            const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
+            int p = pr[0];
+#pragma unroll
+            for (int j = 1; j < kMoePass; j++)
+                if (j == wave) p = pr[j];
+            const int64_t base = (int64_t)p * hidden + blockIdx.y * 32;
+            if (lane < 8) {
+                reinterpret_cast<uint32_t *>(hq + base)[lane] = pk;
+                if (lane == 0) {
+                    hs[base >> 5] = d;
+                    hsum[base >> 5] = cs;
+                }
+            }
+        }
+        __syncthreads();
     }
-    __syncthreads();
-    if (wave == 0) {  // the block of h: lanes 0-7, four values each
-        const int g = min(lane, 7);
-        const float4 v4 = reinterpret_cast<const float4 *>(sh)[g];
-        float d;
-        int cs;
-        const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
-        const int64_t base = (int64_t)pr * hidden + blockIdx.y * 32;
-        if (lane < 8) {
-            reinterpret_cast<uint32_t *>(hq + base)[lane] = pk;
-            if (lane == 0) {
-                hs[base >> 5] = d;
-                hsum[base >> 5] = cs;
+}
+
+// W2 rows of a selected expert on the quantized h of every pair that chose
+// it. Workgroup (group, block of 16 output rows), four rows a wave.
+constexpr int kDownRows = 4;
+__global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t *const *w2, const float *const *s2,
+                                                       const int32_t *grp, int gcap, const int8_t *hq, const float *hs,
+                                                       int dim, int hidden, float *o) {
+    const int g = blockIdx.x;
+    if (g >= grp[0]) return;  // uniform
+    const int e = grp[1 + g], start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
+    const int32_t *list = grp + 1 + 3 * gcap + start;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i0 = blockIdx.y * 16 + kDownRows * wave;
+    const int nb = hidden >> 5;
+    const uint8_t *w[kDownRows];
+    const float *ws[kDownRows];
+#pragma unroll
+    for (int r = 0; r < kDownRows; r++) {
+        const int i = min(i0 + r, dim - 1);
+        w[r] = w2[e] + (int64_t)i * hidden;
+        ws[r] = s2[e] + (int64_t)i * nb;
+    }
+    for (int p0 = 0; p0 < count; p0 += kMoePass) {
+        const int np = min(kMoePass, count - p0);
+        int pr[kMoePass];
+        const int8_t *xq[kMoePass];
+        const float *xsp[kMoePass];
+#pragma unroll
+        for (int j = 0; j < kMoePass; j++) {
+            pr[j] = list[p0 + min(j, np - 1)];
+            xq[j] = hq + (int64_t)pr[j] * hidden;
+            xsp[j] = hs + (int64_t)pr[j] * nb;
+        }
+        float res[kMoePass][kDownRows];
+        wave_rows_q8_multi<kDownRows, kMoePass>(w, ws, xq, xsp, np, hidden, res);
+        if (lane == 0) {
+#pragma unroll
+            for (int j = 0; j < kMoePass; j++) {
+                if (j >= np) break;
+#pragma unroll
+                for (int r = 0; r < kDownRows; r++)
+                    if (i0 + r < dim) o[(int64_t)pr[j] * dim + i0 + r] = res[j][r];
             }
         }
     }
 }
 
-// W2 rows of each (token, slot)'s expert on its quantized h. Workgroup
-// (pair, block of 16 output rows), four rows a wave.
-__global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t *const *w2, const float *const *s2,
-                                                       const int32_t *sel, const int8_t *hq, const float *hs,
-                                                       int dim, int hidden, float *o) {
-    const int pr = blockIdx.x;
-    const int e = sel[pr];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int i0 = blockIdx.y * 16 + kMoeRows * wave;
-    const int nb = hidden >> 5;
-    const uint8_t *w[kMoeRows];
-    const float *ws[kMoeRows];
-#pragma unroll
-    for (int r = 0; r < kMoeRows; r++) {
-        const int i = min(i0 + r, dim - 1);
-        w[r] = w2[e] + (int64_t)i * hidden;
-        ws[r] = s2[e] + (int64_t)i * nb;
-    }
-    float res[kMoeRows];
-    wave_rows_q8<kMoeRows>(w, ws, hq + (int64_t)pr * hidden, hs + (int64_t)pr * nb, hidden, res);
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < kMoeRows; r++)
-            if (i0 + r < dim) o[(int64_t)pr * dim + i0 + r] = res[r];
-    }
-}
-
-// y_t = Σ o over the token's experts in ascending index, from +0.
+// y_t = Σ o over the token's experts in ascending index, from +0; out_t = y_t,
+// or Canonical(out_t + y_t) (the layer's residual, model.go:608-610).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, int k, const float *o, int dim,
-                                                          float *y) {
+                                                          float *out, int residual) {
     __shared__ int order[kMoeMaxK];  // the token's slots by ascending expert
     const int t = blockIdx.x;
     if (threadIdx.x == 0) {
@@ -296,12 +372,100 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, in
     if (i >= dim) return;
     float acc = 0.0f;
     for (int s = 0; s < k; s++) acc += o[((int64_t)t * k + order[s]) * dim + i];
-    y[(int64_t)t * dim + i] = acc;
+    float *dst = out + (int64_t)t * dim + i;
+    *dst = residual ? canonical(*dst + acc) : acc;
 }
 
 }  // namespace
 
-static int moe_scratch(rk_moe *m, int tokens) {
+int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc) {
+    const int64_t T = cap, K = m->topk, E = m->experts, D = m->dim, H = m->hidden;
+    const int64_t G = std::min<int64_t>(E, T * K);
+    int64_t at = 0;
+    auto take = [&](int64_t bytes) {
+        const int64_t here = at;
+        at += (bytes + 255) & ~(int64_t)255;
+        return mem ? mem + here : nullptr;
+    };
+    MoeScratch s;
+    s.cap = cap;
+    s.gcap = (int)G;
+    s.logits = reinterpret_cast<float *>(take(4 * T * E));
+    s.sel = reinterpret_cast<int32_t *>(take(4 * T * K));
+    s.wsel = reinterpret_cast<float *>(take(4 * T * K));
+    s.grp = reinterpret_cast<int32_t *>(take(4 * (1 + 3 * G + T * K)));
+    s.hq = reinterpret_cast<int8_t *>(take(T * K * H));
+    s.hs = reinterpret_cast<float *>(take(4 * T * K * (H / 32)));
+    s.hsum = reinterpret_cast<int32_t *>(take(4 * T * K * (H / 32)));
+    s.o = reinterpret_cast<float *>(take(4 * T * K * D));
+    if (sc) *sc = s;
+    return at;
+}
+
+int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, const int32_t *xsum, int tokens,
+                  float *out, bool residual, hipStream_t s) {
+    rk_device *d = m->d;
+    const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
+    if (tokens <= 0) return RK_OK;
+    if (tokens > sc.cap) return fail(d, RK_ERR_ARGS, "moe: %d tokens beyond the scratch's %d", tokens, sc.cap);
+    bool ok;
+    if (tokens == 1) {
+        FusedArgs a{};
+        a.seg[0] = MatSeg{m->router->w, m->router->scales, sc.logits, m->router->rows};
+        a.nseg = 1;
+        a.cols = D;
+        a.rows = E;
+        a.qx = qx;
+        a.xs = xs;
+        a.xsum = xsum;
+        ProfScope p(d, s, "moe_router");
+        ok = launch_fused(kFmtQ8, kProGlobal, kEpStore, a, d->cu, s);
+    } else {
+        MmArgs a{};
+        a.seg[0] = MatSeg{m->router->w, m->router->scales, sc.logits, m->router->rows};
+        a.nseg = 1;
+        a.cols = D;
+        a.rows = E;
+        a.tokens = tokens;
+        a.qx = qx;
+        a.xs = xs;
+        ProfScope p(d, s, "moe_router");
+        ok = launch_mm(kFmtQ8, kEpStore, a, s);
+    }
+    if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
+    {
+        ProfScope p(d, s, "moe_route");
+        RK_LAUNCH(moe_route_kernel, dim3(tokens), dim3(64), (size_t)E * 4, s, sc.logits, E, K, sc.sel, sc.wsel);
+    }
+    const int npairs = tokens * K;
+    const int groups = std::min(E, npairs);  // launched; those past the selected count exit
+    {
+        ProfScope p(d, s, "moe_group");
+        RK_LAUNCH(moe_group_kernel, dim3(1), dim3(1024), 0, s, sc.sel, npairs, E, sc.gcap, sc.grp);
+    }
+    {
+        ProfScope p(d, s, "moe_up");
+        RK_LAUNCH(moe_up_kernel, dim3((unsigned)groups, (unsigned)(H / 32)), dim3(512), 0, s, m->w1, m->s1, m->w3,
+                  m->s3, sc.grp, sc.gcap, sc.wsel, K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
+    }
+    {
+        ProfScope p(d, s, "moe_down");
+        RK_LAUNCH(moe_down_kernel, dim3((unsigned)groups, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2, m->s2,
+                  sc.grp, sc.gcap, sc.hq, sc.hs, D, H, sc.o);
+    }
+    {
+        ProfScope p(d, s, "moe_combine");
+        RK_LAUNCH(moe_combine_kernel, dim3((unsigned)tokens, (unsigned)((D + 255) / 256)), dim3(256), 0, s, sc.sel, K,
+                  sc.o, D, out, residual ? 1 : 0);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(d, e, "moe launch");
+    return RK_OK;
+}
+
+// The standalone calls' scratch for up to `tokens` inputs (grown: a call
+// that must grow it cannot be recorded).
+static int moe_own_scratch(rk_moe *m, int tokens) {
     if (tokens <= m->cap) return RK_OK;
     rk_device *d = m->d;
     if (d->capturing) return fail(d, RK_ERR_ARGS, "rk_moe: scratch must grow, which cannot be recorded");
@@ -311,87 +475,38 @@ static int moe_scratch(rk_moe *m, int tokens) {
     add_used(d, -m->bytes);
     m->bytes = 0;
     m->cap = 0;
-    const int64_t T = std::max(tokens, 16), K = m->topk, E = m->experts, D = m->dim, H = m->hidden;
-    std::vector<std::pair<void **, int64_t>> plan = {
-        {(void **)&m->x, 4 * T * D},          {(void **)&m->qx, T * D},
-        {(void **)&m->xs, 4 * T * (D / 32)},  {(void **)&m->xsum, 4 * T * (D / 32)},
-        {(void **)&m->logits, 4 * T * E},     {(void **)&m->sel, 4 * T * K},
-        {(void **)&m->wsel, 4 * T * K},
-        {(void **)&m->hq, T * K * H},         {(void **)&m->hs, 4 * T * K * (H / 32)},
-        {(void **)&m->hsum, 4 * T * K * (H / 32)}, {(void **)&m->o, 4 * T * K * D},
-        {(void **)&m->y, 4 * T * D}};
-    int64_t at = 0;
-    for (auto &p : plan) at += (p.second + 255) & ~(int64_t)255;
-    int rc = dev_alloc(d, &m->mem, (size_t)at, "moe scratch");
+    const int64_t T = std::max(tokens, 16), D = m->dim;
+    auto al = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+    const int64_t own = 2 * al(4 * T * D) + al(T * D) + 2 * al(4 * T * (D / 32));
+    const int64_t total = own + moe_scratch_layout(m, (int)T, nullptr, nullptr);
+    int rc = dev_alloc(d, &m->mem, (size_t)total, "moe scratch");
     if (rc) return rc;
-    at = 0;
-    for (auto &p : plan) {
-        *p.first = static_cast<char *>(m->mem) + at;
-        at += (p.second + 255) & ~(int64_t)255;
-    }
-    m->bytes = at;
+    char *p = static_cast<char *>(m->mem);
+    m->x = reinterpret_cast<float *>(p);
+    p += al(4 * T * D);
+    m->y = reinterpret_cast<float *>(p);
+    p += al(4 * T * D);
+    m->qx = reinterpret_cast<int8_t *>(p);
+    p += al(T * D);
+    m->xs = reinterpret_cast<float *>(p);
+    p += al(4 * T * (D / 32));
+    m->xsum = reinterpret_cast<int32_t *>(p);
+    p += al(4 * T * (D / 32));
+    moe_scratch_layout(m, (int)T, p, &m->sc);
+    m->bytes = total;
     m->cap = (int)T;
     add_used(d, m->bytes);
     return RK_OK;
 }
 
-// The launches of one MoE feed-forward over `tokens` inputs at d_xn; the
-// result to d_y ([tokens][dim]).
+// A standalone call: the input quantized into the handle's scratch, then
+// the feed-forward into d_y.
 static int enqueue_moe(rk_moe *m, const float *d_xn, int tokens, float *d_y, hipStream_t s) {
-    rk_device *d = m->d;
-    const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
     {
-        ProfScope p(d, s, "quantize_acts");
-        launch_quantize_acts(d_xn, (int64_t)tokens * D, m->qx, m->xs, m->xsum, s);
+        ProfScope p(m->d, s, "quantize_acts");
+        launch_quantize_acts(d_xn, (int64_t)tokens * m->dim, m->qx, m->xs, m->xsum, s);
     }
-    bool ok;
-    if (tokens == 1) {
-        FusedArgs a{};
-        a.seg[0] = MatSeg{m->router->w, m->router->scales, m->logits, m->router->rows};
-        a.nseg = 1;
-        a.cols = D;
-        a.rows = E;
-        a.qx = m->qx;
-        a.xs = m->xs;
-        a.xsum = m->xsum;
-        ProfScope p(d, s, "moe_router");
-        ok = launch_fused(kFmtQ8, kProGlobal, kEpStore, a, d->cu, s);
-    } else {
-        MmArgs a{};
-        a.seg[0] = MatSeg{m->router->w, m->router->scales, m->logits, m->router->rows};
-        a.nseg = 1;
-        a.cols = D;
-        a.rows = E;
-        a.tokens = tokens;
-        a.qx = m->qx;
-        a.xs = m->xs;
-        ProfScope p(d, s, "moe_router");
-        ok = launch_mm(kFmtQ8, kEpStore, a, s);
-    }
-    if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
-    {
-        ProfScope p(d, s, "moe_route");
-        RK_LAUNCH(moe_route_kernel, dim3(tokens), dim3(64), (size_t)E * 4, s, m->logits, E, K, m->sel, m->wsel);
-    }
-    const unsigned pairs = (unsigned)(tokens * K);
-    {
-        ProfScope p(d, s, "moe_up");
-        RK_LAUNCH(moe_up_kernel, dim3(pairs, (unsigned)(H / 32)), dim3(512), 0, s, m->w1, m->s1, m->w3, m->s3, m->sel,
-                  m->wsel, K, m->qx, m->xs, D, H, m->hq, m->hs, m->hsum);
-    }
-    {
-        ProfScope p(d, s, "moe_down");
-        RK_LAUNCH(moe_down_kernel, dim3(pairs, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2, m->s2, m->sel,
-                  m->hq, m->hs, D, H, m->o);
-    }
-    {
-        ProfScope p(d, s, "moe_combine");
-        RK_LAUNCH(moe_combine_kernel, dim3((unsigned)tokens, (unsigned)((D + 255) / 256)), dim3(256), 0, s, m->sel, K,
-                  m->o, D, d_y);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(d, e, "moe launch");
-    return RK_OK;
+    return enqueue_moe_q(m, m->sc, m->qx, m->xs, m->xsum, tokens, d_y, false, s);
 }
 
 }  // namespace rk
@@ -467,7 +582,7 @@ int rk_moe_ffn(rk_moe *m, const float *xn, int32_t tokens, float *y, int32_t *se
     Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
     if (d->capturing) return fail(d, RK_ERR_ARGS, "rk_moe_ffn waits for its results: it cannot be recorded");
-    int rc = moe_scratch(m, tokens);
+    int rc = moe_own_scratch(m, tokens);
     if (rc) return rc;
     hipStream_t s = d->stream;
     const size_t xb = (size_t)tokens * m->dim * 4;
@@ -475,9 +590,9 @@ int rk_moe_ffn(rk_moe *m, const float *xn, int32_t tokens, float *y, int32_t *se
     if ((rc = enqueue_moe(m, m->x, tokens, m->y, s))) return rc;
     HIP_TRY(d, hipMemcpyAsync(y, m->y, xb, hipMemcpyDeviceToHost, s), "moe output");
     if (sel)
-        HIP_TRY(d, hipMemcpyAsync(sel, m->sel, (size_t)tokens * m->topk * 4, hipMemcpyDeviceToHost, s), "moe sel");
+        HIP_TRY(d, hipMemcpyAsync(sel, m->sc.sel, (size_t)tokens * m->topk * 4, hipMemcpyDeviceToHost, s), "moe sel");
     if (wsel)
-        HIP_TRY(d, hipMemcpyAsync(wsel, m->wsel, (size_t)tokens * m->topk * 4, hipMemcpyDeviceToHost, s), "moe w");
+        HIP_TRY(d, hipMemcpyAsync(wsel, m->sc.wsel, (size_t)tokens * m->topk * 4, hipMemcpyDeviceToHost, s), "moe w");
     HIP_TRY(d, hipStreamSynchronize(s), "moe");
     return RK_OK;
 }
@@ -492,7 +607,7 @@ int rk_moe_ffn_device(rk_moe *m, const float *d_xn, int32_t tokens, float *d_y, 
     hipStream_t s = stream ? (hipStream_t)stream : d->stream;
     if (d->capturing && s != d->stream)
         return fail(d, RK_ERR_ARGS, "while recording a graph, work goes on the device's stream");
-    int rc = moe_scratch(m, tokens);
+    int rc = moe_own_scratch(m, tokens);
     if (rc) return rc;
     return enqueue_moe(m, d_xn, tokens, d_y, s);
 }

@@ -24,6 +24,7 @@
 #include "rk_fused.h"
 #include "rk_layer.h"
 #include "rk_mm.h"
+#include "rk_moe.h"
 #include "rk_runtime.h"
 
 // internal/llm/gpustage.go:23-32 gpuStage.
@@ -36,6 +37,7 @@ struct rk_stage {
     int64_t bytes = 0;
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *att_out = nullptr;
     float *h = nullptr, *cos_t = nullptr, *sin_t = nullptr, *logits = nullptr, *rms_final = nullptr;
+    int64_t logits_n = 0;  // floats of logits (and of its pinned staging)
     int32_t *ctl = nullptr, *tokens = nullptr;
     unsigned long long *amax = nullptr;  // the classifier's argmax keys
     int8_t *qx = nullptr;  // the fallback quantize's output
@@ -67,6 +69,21 @@ struct rk_stage {
     int64_t bbytes = 0;
     float *bx = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr, *batt = nullptr, *batt_out = nullptr;
     rk::QScratch bqa{}, bqb{};
+    // Independent sequences (rk_stage_seqs_*): each has its own caches
+    // (sequence z's at z·ctx·kv_dim in every layer's), position, prompt
+    // length and tokens [ctx+1] on the device; the host keeps a copy of the
+    // positions for the context bound.
+    int seqs = 1;
+    int32_t *seq_pos = nullptr, *seq_prompt = nullptr, *seq_tokens = nullptr;
+    int32_t *h_seq = nullptr;
+    std::vector<int32_t> seq_at;
+    bool seqs_started = false;
+    hipGraph_t g_seqs = nullptr;
+    hipGraphExec_t x_seqs = nullptr;
+    // Mixture-of-experts layers share one scratch (they run one after
+    // another), laid out per layer for moe_cap tokens.
+    char *moe_mem = nullptr;
+    int moe_cap = 0;
 };
 
 namespace rk {
@@ -197,6 +214,17 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
     float *xo[1] = {s->x};
     if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, nullptr, &L.wo, 1, xo, kEpAdd, base)))
         return rc;
+    if (L.moe) {
+        // a mixture of experts: its input RMSNorm_ffn(x) quantized into qb;
+        // the experts' sum goes into the residual, x = Canonical(x + y)
+        {
+            ProfScope p(d, st, "norm_quant");
+            launch_norm_quant(s->x, c.dim, D.rms_ffn, c.recip_dim, c.norm_eps, s->qb.qx, s->qb.xs, s->qb.xsum, st);
+        }
+        MoeScratch sc;
+        moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
+        return enqueue_moe_q(L.moe, sc, s->qb.qx, s->qb.xs, s->qb.xsum, 1, s->x, true, st);
+    }
     // W1 row r and W3 row r interleaved (logical rows); h leaves quantized in qa.
     rk_matrix *w13[2] = {L.w1, L.w3};
     float *ho[2] = {s->h, nullptr};
@@ -246,15 +274,21 @@ static int enqueue_token(rk_stage *s, hipStream_t st) {
     return RK_OK;
 }
 
-// Records `which` (layers or a whole token) into a graph, once.
-static int record(rk_stage *s, bool token) {
+// What a stage records: its layers (Stage.ForwardMany), a whole generation
+// step, or a decode step of every sequence.
+enum Rec { kRecLayers, kRecToken, kRecSeqs };
+
+static int enqueue_rec(rk_stage *s, Rec which, hipStream_t st);
+
+// Records `which` into a graph, once.
+static int record(rk_stage *s, Rec which) {
     rk_device *d = s->d;
-    hipGraph_t &g = token ? s->g_token : s->g_layers;
-    hipGraphExec_t &x = token ? s->x_token : s->x_layers;
+    hipGraph_t &g = which == kRecToken ? s->g_token : which == kRecSeqs ? s->g_seqs : s->g_layers;
+    hipGraphExec_t &x = which == kRecToken ? s->x_token : which == kRecSeqs ? s->x_seqs : s->x_layers;
     if (x) return RK_OK;
     HIP_TRY(d, hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal), "stage capture");
     d->capturing = true;
-    int rc = token ? enqueue_token(s, d->stream) : enqueue_forward(s, d->stream);
+    int rc = enqueue_rec(s, which, d->stream);
     d->capturing = false;
     hipGraph_t gr = nullptr;
     hipError_t e = hipStreamEndCapture(d->stream, &gr);
@@ -277,14 +311,15 @@ static int record(rk_stage *s, bool token) {
     return RK_OK;
 }
 
-// Runs the recorded layers / token once on the device stream; while the
-// device profiles, the launches run one by one instead, each timed.
-static int run_once(rk_stage *s, bool token) {
+// Runs the recorded `which` once on the device stream; while the device
+// profiles, the launches run one by one instead, each timed.
+static int run_once(rk_stage *s, Rec which) {
     rk_device *d = s->d;
-    if (d->profiling) return token ? enqueue_token(s, d->stream) : enqueue_forward(s, d->stream);
-    int rc = record(s, token);
+    if (d->profiling) return enqueue_rec(s, which, d->stream);
+    int rc = record(s, which);
     if (rc) return rc;
-    HIP_TRY(d, hipGraphLaunch(token ? s->x_token : s->x_layers, d->stream), "stage replay");
+    HIP_TRY(d, hipGraphLaunch(which == kRecToken ? s->x_token : which == kRecSeqs ? s->x_seqs : s->x_layers, d->stream),
+            "stage replay");
     return RK_OK;
 }
 
@@ -295,19 +330,30 @@ static int run_once(rk_stage *s, bool token) {
 // token's results are those of its own decode-path forward, bit for bit.
 
 // Largest batch the buffers take: 256 tokens, fewer when the scores of a
-// batch ([tokens][heads][ctx] floats) would pass 512 MiB.
-static int batch_cap(const rk_stage_config &c) {
+// batch ([tokens][heads][ctx] floats) would pass 512 MiB, and never fewer
+// than the stage's sequences (one row each in a decode step).
+static int batch_cap(const rk_stage_config &c, int seqs) {
     const int64_t per = (int64_t)4 * c.heads * c.ctx;
     int64_t cap = ((int64_t)512 << 20) / std::max<int64_t>(per, 1);
     cap = std::min<int64_t>(cap, 256);
-    return (int)std::max<int64_t>(cap, 1);
+    return (int)std::max<int64_t>(std::max<int64_t>(cap, 1), seqs);
 }
+
+// Where a batch's tokens sit: consecutive positions pos0, pos0+1, ... of
+// one sequence whose caches start cache0 floats into each layer's (a
+// prompt), or one token per sequence, token z at seq_pos[z] in caches
+// cache_stride floats apart (the sequences' decode step).
+struct BatchPos {
+    int32_t pos0 = 0;
+    const int32_t *seq_pos = nullptr;
+    int64_t cache0 = 0, cache_stride = 0;
+};
 
 static int batch_alloc(rk_stage *s) {
     if (s->bmem) return RK_OK;
     rk_device *d = s->d;
     const rk_stage_config &c = s->c;
-    const int64_t B = batch_cap(c);
+    const int64_t B = batch_cap(c, s->seqs);
     const int64_t widest = std::max<int64_t>(std::max<int64_t>(c.dim, s->qdim), c.hidden);
     std::vector<std::pair<void **, int64_t>> plan;
     auto take = [&](void **p, int64_t n) { plan.push_back({p, n}); };
@@ -368,8 +414,10 @@ static void batch_norm(rk_stage *s, hipStream_t st, const float *w, int n) {
     launch_norm_quant(s->bx, s->c.dim, w, s->c.recip_dim, s->c.norm_eps, s->bqb.qx, s->bqb.xs, s->bqb.xsum, st, n);
 }
 
-// One layer for n tokens; on entry bqb holds their RMSNorm_att(x) quantized.
-static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, int pos0, const float *next_norm) {
+// One layer for n tokens placed as bp says; on entry bqb holds their
+// RMSNorm_att(x) quantized.
+static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, const BatchPos &bp,
+                               const float *next_norm) {
     rk_device *d = s->d;
     const rk_stage_config &c = s->c;
     const rk_stage_layer &L = s->layers[li];
@@ -388,15 +436,17 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, int p
         if (!c.qk_norm) {
             a.row_base = row;
             a.bias = D.bias;
-            a.pos0 = pos0;
+            a.pos0 = bp.pos0;
+            a.seq_pos = bp.seq_pos;
+            a.cache_stride = bp.cache_stride;
             a.hs = s->hs;
             a.qdim = s->qdim;
             a.kvdim = s->kvdim;
             a.cos_t = s->cos_t;
             a.sin_t = s->sin_t;
             a.q = s->bq;
-            a.kcache = D.keys;
-            a.vcache = D.vals;
+            a.kcache = D.keys + bp.cache0;
+            a.vcache = D.vals + bp.cache0;
             if ((rc = batch_product(s, st, "qkv", qkv + i, j - i, kEpQKV, a))) return rc;
         } else {
             float *outs[3] = {s->bq, s->bk, s->bv};
@@ -410,26 +460,29 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, int p
     if (c.qk_norm) {
         ProfScope p(d, st, "qknorm_rope");
         launch_qknorm_rope(s->bq, s->bk, s->bv, D.q_norm, D.k_norm, c.recip_head, c.norm_eps, s->cos_t, s->sin_t,
-                           nullptr, pos0, n, D.keys, D.vals, c.heads, c.kv_heads, s->hs, st);
+                           nullptr, bp.pos0, n, D.keys + bp.cache0, D.vals + bp.cache0, c.heads, c.kv_heads, s->hs, st,
+                           bp.seq_pos, bp.cache_stride);
     }
     AttBatch bt;
-    bt.pos0 = pos0;
+    bt.pos0 = bp.pos0;
     bt.tokens = n;
     bt.q_stride = s->qdim;
     bt.att_stride = (int64_t)c.heads * c.ctx;
     bt.out_stride = s->qdim;
+    bt.pos = bp.seq_pos;
+    bt.cache_stride = bp.cache_stride;
     {
         ProfScope p(d, st, "att_scores");
-        launch_att_scores(s->bq, D.keys, s->batt, c.ctx, nullptr, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim,
-                          c.inv_sqrt, st);
+        launch_att_scores(s->bq, D.keys + bp.cache0, s->batt, c.ctx, nullptr, bt, c.ctx, c.heads, c.kv_heads, s->hs,
+                          s->kvdim, c.inv_sqrt, st);
     }
     // the attention output comes quantized when its Q8 blocks fall within
     // heads; else it is quantized by a launch of its own
     const bool att_q = s->hs % 32 == 0;
     {
         ProfScope p(d, st, "att_values");
-        launch_att_values(s->batt, c.ctx, D.vals, s->batt_out, nullptr, bt, c.ctx, c.heads, c.kv_heads, s->hs,
-                          s->kvdim, att_q ? s->bqa.qx : nullptr, s->bqa.xs, s->bqa.xsum, st);
+        launch_att_values(s->batt, c.ctx, D.vals + bp.cache0, s->batt_out, nullptr, bt, c.ctx, c.heads, c.kv_heads,
+                          s->hs, s->kvdim, att_q ? s->bqa.qx : nullptr, s->bqa.xs, s->bqa.xsum, st);
     }
     if (!att_q) {
         ProfScope p(d, st, "quantize_acts");
@@ -442,6 +495,14 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, int p
     a.ldx = c.dim;
     if ((rc = batch_product(s, st, "wo", &L.wo, 1, kEpAdd, a))) return rc;
     batch_norm(s, st, D.rms_ffn, n);
+    if (L.moe) {  // the experts' sums into the residual rows, x = Canonical(x + y)
+        MoeScratch sc;
+        moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
+        if ((rc = enqueue_moe_q(L.moe, sc, s->bqb.qx, s->bqb.xs, s->bqb.xsum, n, s->bx, true, st))) return rc;
+        batch_norm(s, st, next_norm, n);
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? RK_OK : hip_fail(d, e, "stage launch");
+    }
     rk_matrix *w13[2] = {L.w1, L.w3};
     a = base;
     a.qx_out = s->bqa.qx;
@@ -461,20 +522,77 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, int p
 }
 
 // Every layer over n tokens whose activations are in bx.
-static int enqueue_forward_batch(rk_stage *s, hipStream_t st, int n, int pos0) {
+static int enqueue_forward_batch(rk_stage *s, hipStream_t st, int n, const BatchPos &bp) {
     batch_norm(s, st, s->ld[0].rms_att, n);
     const int nl = (int)s->layers.size();
     for (int li = 0; li < nl; li++) {
-        int rc = enqueue_layer_batch(s, li, st, n, pos0, li + 1 < nl ? s->ld[li + 1].rms_att : nullptr);
+        int rc = enqueue_layer_batch(s, li, st, n, bp, li + 1 < nl ? s->ld[li + 1].rms_att : nullptr);
         if (rc) return rc;
     }
     return RK_OK;
+}
+
+static BatchPos at_pos(int32_t pos0) {
+    BatchPos bp;
+    bp.pos0 = pos0;
+    return bp;
+}
+
+// One decode step of every sequence (rk_stage_seqs_run): sequence z's token
+// at seq_pos[z] embedded into row z, the layers (each row attends to its
+// own sequence's caches), the head's RMSNorm and classifier for every row,
+// and the greedy step that writes each sequence's next token and advances
+// its position. Every position is read on the device, so the step is
+// recorded once and replayed.
+static int enqueue_seqs_step(rk_stage *s, hipStream_t st) {
+    rk_device *d = s->d;
+    const rk_stage_config &c = s->c;
+    const int S = s->seqs;
+    const int64_t ctx = c.ctx;
+    {
+        ProfScope p(d, st, "embed");
+        launch_embed_rows(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->seq_tokens, 0, S, c.dim, s->bx,
+                          st, ctx + 1, s->seq_pos);
+    }
+    BatchPos bp;
+    bp.seq_pos = s->seq_pos;
+    bp.cache_stride = ctx * s->kvdim;
+    int rc = enqueue_forward_batch(s, st, S, bp);
+    if (rc) return rc;
+    batch_norm(s, st, s->rms_final, S);
+    MmArgs a{};
+    a.seg[0] = MatSeg{s->wcls->w, s->wcls->scales, s->logits, s->wcls->rows};
+    a.tokens = S;
+    a.qx = s->bqb.qx;
+    a.xs = s->bqb.xs;
+    if ((rc = batch_product(s, st, "logits", &s->wcls, 1, kEpStore, a))) return rc;
+    {
+        ProfScope p(d, st, "advance");
+        launch_seqs_advance(s->logits, s->wcls->rows, S, s->seq_pos, s->seq_prompt, s->seq_tokens, ctx + 1,
+                            (int32_t)(ctx + 1), st);
+    }
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? RK_OK : hip_fail(d, e, "stage launch");
+}
+
+static int enqueue_rec(rk_stage *s, Rec which, hipStream_t st) {
+    switch (which) {
+    case kRecToken: return enqueue_token(s, st);
+    case kRecSeqs: return enqueue_seqs_step(s, st);
+    default: return enqueue_forward(s, st);
+    }
 }
 
 __global__ void set_ctl_kernel(int32_t *ctl, unsigned long long *amax, int32_t pos, int32_t prompt) {
     ctl[kCtlPos] = pos;
     ctl[kCtlPrompt] = prompt;
     for (int i = 0; i < kArgmaxSlots; i++) amax[i] = 0ull;
+}
+
+// The single-sequence entry points run on a stage of one sequence.
+static int one_sequence(rk_stage *s, const char *what) {
+    if (s->seqs == 1) return RK_OK;
+    return fail(s->d, RK_ERR_ARGS, "%s: the stage decodes %d sequences (rk_stage_seqs_*)", what, s->seqs);
 }
 
 static bool valid_mat(const rk_matrix *m, rk_device *d, int64_t rows, int64_t cols) {
@@ -502,15 +620,23 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
     if (c->ctx > att_values_max_ctx())
         return fail(d, RK_ERR_UNSUPPORTED, "rk_stage_new: ctx %d beyond %d", c->ctx, att_values_max_ctx());
     const int qdim = c->heads * hs, kvdim = c->kv_heads * hs;
+    const int seqs = std::max(1, c->seqs);
+    if (seqs > 256) return fail(d, RK_ERR_ARGS, "rk_stage_new: %d sequences (at most 256)", seqs);
+    bool any_moe = false;
     for (int i = 0; i < n_layers; i++) {
         const rk_stage_layer &L = layers[i];
+        const bool moe = L.moe != nullptr;
+        any_moe = any_moe || moe;
         if (!valid_mat(L.wq, d, qdim, c->dim) || !valid_mat(L.wk, d, kvdim, c->dim) ||
             !valid_mat(L.wv, d, kvdim, c->dim) || !valid_mat(L.wo, d, c->dim, qdim) ||
-            !valid_mat(L.w1, d, c->hidden, c->dim) || !valid_mat(L.w3, d, c->hidden, c->dim) ||
-            !valid_mat(L.w2, d, c->dim, c->hidden))
+            (!moe && (!valid_mat(L.w1, d, c->hidden, c->dim) || !valid_mat(L.w3, d, c->hidden, c->dim) ||
+                      !valid_mat(L.w2, d, c->dim, c->hidden))))
             return fail(d, RK_ERR_ARGS, "rk_stage_new: layer %d: a matrix is missing, of another shape or device, "
                                         "or not Q8/Q4", i);
-        if (L.w1->kind != L.w3->kind)
+        if (moe && (L.moe->d != d || L.moe->dim != c->dim))
+            return fail(d, RK_ERR_ARGS, "rk_stage_new: layer %d: its experts take %d values on another device or width",
+                        i, (int)L.moe->dim);
+        if (!moe && L.w1->kind != L.w3->kind)
             return fail(d, RK_ERR_UNSUPPORTED, "rk_stage_new: layer %d: W1 and W3 differ in format", i);
         if (!L.rms_att || !L.rms_ffn || (c->qkv_bias && (!L.bq || !L.bk || !L.bv)) ||
             (c->qk_norm && (!L.q_norm || !L.k_norm)))
@@ -525,6 +651,7 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
     s->qdim = qdim;
     s->kvdim = kvdim;
     s->half = hs / 2;
+    s->seqs = seqs;
     s->layers.assign(layers, layers + n_layers);
     // Layout: sizes in bytes, each 256-byte aligned.
     const int64_t ctx = c->ctx;
@@ -554,6 +681,17 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
         take((void **)&q->xsum, 4 * (widest / 32));
     }
     take((void **)&s->rms_final, 4 * c->dim);
+    take((void **)&s->seq_pos, 4 * seqs);
+    take((void **)&s->seq_prompt, 4 * seqs);
+    take((void **)&s->seq_tokens, 4 * seqs * (ctx + 1));
+    // the MoE layers' shared scratch, for the largest batch the stage runs
+    if (any_moe) {
+        s->moe_cap = batch_cap(*c, seqs);
+        int64_t mb = 0;
+        for (int i = 0; i < n_layers; i++)
+            if (layers[i].moe) mb = std::max(mb, moe_scratch_layout(layers[i].moe, s->moe_cap, nullptr, nullptr));
+        take((void **)&s->moe_mem, mb);
+    }
     s->ld.resize(n_layers);
     const int64_t bias_n = c->qkv_bias ? qdim + 2 * kvdim : 0;
     for (int i = 0; i < n_layers; i++) {
@@ -566,8 +704,8 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
             take((void **)&D.q_norm, 4 * hs);
             take((void **)&D.k_norm, 4 * hs);
         }
-        take((void **)&D.keys, 4 * ctx * kvdim);
-        take((void **)&D.vals, 4 * ctx * kvdim);
+        take((void **)&D.keys, 4 * seqs * ctx * kvdim);  // [seqs][ctx][kv_dim]
+        take((void **)&D.vals, 4 * seqs * ctx * kvdim);
     }
     for (auto &pl : plan) at += (pl.second + 255) & ~(int64_t)255;
     int rc = dev_alloc(d, (void **)&s->mem, (size_t)at, "stage");
@@ -585,6 +723,7 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
         (void)hipFree(s->mem);
         if (s->h_x) (void)hipHostFree(s->h_x);
         if (s->h_ctl) (void)hipHostFree(s->h_ctl);
+        if (s->h_seq) (void)hipHostFree(s->h_seq);
         delete s;
         return code;
     };
@@ -617,7 +756,8 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
     if ((e = hipHostMalloc((void **)&s->h_x, (size_t)4 * kForwardBatch * c->dim, hipHostMallocDefault)) !=
             hipSuccess ||
         (e = hipHostMalloc((void **)&s->h_ctl, (size_t)4 * (ctx + 1 + kCtlWords), hipHostMallocDefault)) !=
-            hipSuccess) {
+            hipSuccess ||
+        (e = hipHostMalloc((void **)&s->h_seq, (size_t)4 * seqs * (ctx + 3), hipHostMallocDefault)) != hipSuccess) {
         (void)hipGetLastError();
         return cleanup(hip_fail(d, e, "stage staging"));
     }
@@ -629,6 +769,7 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
 int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens) {
     if (!s) return RK_ERR_ARGS;
     rk_device *d = s->d;
+    if (int rc = one_sequence(s, "rk_stage_forward")) return rc;
     if (tokens < 0 || (tokens > 0 && !xs) || pos < 0 || (int64_t)pos + tokens > s->c.ctx)
         return fail(d, RK_ERR_ARGS, "gpu stage: positions [%d, %d) outside the context of %d", pos, pos + tokens,
                     s->c.ctx);
@@ -644,7 +785,7 @@ int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens) {
             const int n = std::min(s->bcap, tokens - start);
             HIP_TRY(d, hipMemcpyAsync(s->bx, xs + (int64_t)start * dim, (size_t)n * dim * 4, hipMemcpyHostToDevice, st),
                     "stage input");
-            if ((rc = enqueue_forward_batch(s, st, n, pos + start))) return rc;
+            if ((rc = enqueue_forward_batch(s, st, n, at_pos(pos + start)))) return rc;
             HIP_TRY(d, hipMemcpyAsync(xs + (int64_t)start * dim, s->bx, (size_t)n * dim * 4, hipMemcpyDeviceToHost, st),
                     "stage output");
             HIP_TRY(d, hipStreamSynchronize(st), "stage submit");
@@ -658,7 +799,7 @@ int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens) {
             HIP_TRY(d, hipMemcpyAsync(s->x, s->h_x + (int64_t)t * dim, (size_t)dim * 4, hipMemcpyHostToDevice, st),
                     "stage input");
             hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, st, s->ctl, s->amax, pos + start + t, 0);
-            int rc = run_once(s, false);
+            int rc = run_once(s, kRecLayers);
             if (rc) return rc;
             HIP_TRY(d, hipMemcpyAsync(s->h_x + (int64_t)t * dim, s->x, (size_t)dim * 4, hipMemcpyDeviceToHost, st),
                     "stage output");
@@ -681,10 +822,13 @@ int rk_stage_free(rk_stage *s) {
     if (s->g_layers) (void)hipGraphDestroy(s->g_layers);
     if (s->x_token) (void)hipGraphExecDestroy(s->x_token);
     if (s->g_token) (void)hipGraphDestroy(s->g_token);
+    if (s->x_seqs) (void)hipGraphExecDestroy(s->x_seqs);
+    if (s->g_seqs) (void)hipGraphDestroy(s->g_seqs);
     (void)hipFree(s->mem);
     (void)hipFree(s->bmem);
     if (s->h_x) (void)hipHostFree(s->h_x);
     if (s->h_ctl) (void)hipHostFree(s->h_ctl);
+    if (s->h_seq) (void)hipHostFree(s->h_seq);
     if (s->h_logits) (void)hipHostFree(s->h_logits);
     (void)hipGetLastError();
     add_used(d, -s->bytes);
@@ -707,17 +851,36 @@ int rk_stage_set_head(rk_stage *s, rk_matrix *embed, rk_matrix *wcls, const floa
         s->x_token = nullptr;
         s->g_token = nullptr;
     }
+    if (s->x_seqs) {
+        (void)hipGraphExecDestroy(s->x_seqs);
+        (void)hipGraphDestroy(s->g_seqs);
+        s->x_seqs = nullptr;
+        s->g_seqs = nullptr;
+    }
+    // logits of every sequence, [seqs][vocab]
+    const int64_t nl = wcls->rows * s->seqs;
+    if (s->logits && nl > s->logits_n) {
+        HIP_TRY(d, hipStreamSynchronize(d->stream), "logits");
+        (void)hipFree(s->logits);
+        (void)hipHostFree(s->h_logits);
+        s->logits = nullptr;
+        s->h_logits = nullptr;
+        s->bytes -= 4 * s->logits_n;
+        add_used(d, -4 * s->logits_n);
+        s->logits_n = 0;
+    }
     if (!s->logits) {
-        int rc = dev_alloc(d, (void **)&s->logits, (size_t)4 * wcls->rows, "logits");
+        int rc = dev_alloc(d, (void **)&s->logits, (size_t)4 * nl, "logits");
         if (rc) return rc;
-        hipError_t e = hipHostMalloc((void **)&s->h_logits, (size_t)4 * wcls->rows, hipHostMallocDefault);
+        hipError_t e = hipHostMalloc((void **)&s->h_logits, (size_t)4 * nl, hipHostMallocDefault);
         if (e != hipSuccess) {
             (void)hipFree(s->logits);
             s->logits = nullptr;
             return hip_fail(d, e, "logits staging");
         }
-        s->bytes += 4 * wcls->rows;
-        add_used(d, 4 * wcls->rows);
+        s->logits_n = nl;
+        s->bytes += 4 * nl;
+        add_used(d, 4 * nl);
     }
     HIP_TRY(d, hipMemcpyAsync(s->rms_final, rms_final, (size_t)4 * s->c.dim, hipMemcpyHostToDevice, d->stream),
             "head upload");
@@ -730,6 +893,7 @@ int rk_stage_set_head(rk_stage *s, rk_matrix *embed, rk_matrix *wcls, const floa
 int rk_stage_generate_start(rk_stage *s, const int32_t *prompt, int32_t n_prompt) {
     if (!s) return RK_ERR_ARGS;
     rk_device *d = s->d;
+    if (int rc = one_sequence(s, "rk_stage_generate")) return rc;
     if (!s->embed) return fail(d, RK_ERR_ARGS, "rk_stage_generate: the stage has no head");
     if (!prompt || n_prompt <= 0 || n_prompt > s->c.ctx)
         return fail(d, RK_ERR_ARGS, "rk_stage_generate: prompt of %d tokens for a context of %d", n_prompt, s->c.ctx);
@@ -753,6 +917,7 @@ int rk_stage_generate_start(rk_stage *s, const int32_t *prompt, int32_t n_prompt
 int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits) {
     if (!s || positions < 0) return RK_ERR_ARGS;
     rk_device *d = s->d;
+    if (int rc = one_sequence(s, "rk_stage_generate")) return rc;
     if (!s->embed) return fail(d, RK_ERR_ARGS, "rk_stage_generate: the stage has no head");
     Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
@@ -783,7 +948,7 @@ int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits) {
                 launch_embed_rows(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->tokens, pos, n, s->c.dim,
                                   s->bx, st);
             }
-            if ((rc = enqueue_forward_batch(s, st, n, pos))) return rc;
+            if ((rc = enqueue_forward_batch(s, st, n, at_pos(pos)))) return rc;
             pos += n;
             left -= n;
             hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(1), 0, st, s->ctl, s->amax, pos, s->prompt_n);
@@ -791,7 +956,7 @@ int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits) {
         }
     }
     for (int32_t i = 0; i < positions; i++) {
-        int rc = run_once(s, true);
+        int rc = run_once(s, kRecToken);
         if (rc) return rc;
         if (logits) {
             HIP_TRY(d, hipMemcpyAsync(s->h_logits, s->logits, (size_t)vocab * 4, hipMemcpyDeviceToHost, d->stream),
@@ -807,6 +972,7 @@ int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits) {
 int rk_stage_generate_tokens(rk_stage *s, int32_t from, int32_t n, int32_t *out) {
     if (!s || !out || from < 0 || n < 0 || (int64_t)from + n > s->c.ctx + 1) return RK_ERR_ARGS;
     rk_device *d = s->d;
+    if (int rc = one_sequence(s, "rk_stage_generate_tokens")) return rc;
     Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
     HIP_TRY(d, hipStreamSynchronize(d->stream), "tokens");
@@ -821,6 +987,110 @@ int rk_stage_generate(rk_stage *s, const int32_t *prompt, int32_t n_prompt, int3
     if (rc || steps == 0) return rc;
     if ((rc = rk_stage_generate_run(s, n_prompt + steps - 1, nullptr))) return rc;
     return rk_stage_generate_tokens(s, n_prompt, steps, out);
+}
+
+int rk_stage_seqs_start(rk_stage *s, const int32_t *prompts, const int32_t *lens) {
+    if (!s) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    if (!s->embed) return fail(d, RK_ERR_ARGS, "rk_stage_seqs_start: the stage has no head");
+    if (!prompts || !lens) return fail(d, RK_ERR_ARGS, "rk_stage_seqs_start: null argument");
+    const int S = s->seqs;
+    const int64_t ctx = s->c.ctx, vocab = s->embed->rows;
+    int64_t total = 0;
+    for (int z = 0; z < S; z++) {
+        if (lens[z] <= 0 || lens[z] > ctx)
+            return fail(d, RK_ERR_ARGS, "rk_stage_seqs_start: sequence %d: prompt of %d tokens for a context of %lld", z,
+                        lens[z], (long long)ctx);
+        for (int i = 0; i < lens[z]; i++)
+            if (prompts[total + i] < 0 || prompts[total + i] >= vocab)
+                return fail(d, RK_ERR_ARGS, "rk_stage_seqs_start: sequence %d: token %d out of range", z,
+                            prompts[total + i]);
+        total += lens[z];
+    }
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipStream_t st = d->stream;
+    HIP_TRY(d, hipStreamSynchronize(st), "seqs start");
+    int rc = batch_alloc(s);
+    if (rc) return rc;
+    // tokens [S][ctx+1] (each prompt at the start of its row), then the
+    // positions (each prompt's last) and the prompt lengths
+    int32_t *h = s->h_seq;
+    memset(h, 0, (size_t)4 * S * (ctx + 1));
+    int64_t at = 0;
+    for (int z = 0; z < S; z++) {
+        memcpy(h + z * (ctx + 1), prompts + at, (size_t)4 * lens[z]);
+        at += lens[z];
+        h[S * (ctx + 1) + z] = lens[z] - 1;
+        h[S * (ctx + 1) + S + z] = lens[z];
+    }
+    HIP_TRY(d, hipMemcpyAsync(s->seq_tokens, h, (size_t)4 * S * (ctx + 1), hipMemcpyHostToDevice, st), "prompts");
+    HIP_TRY(d, hipMemcpyAsync(s->seq_pos, h + S * (ctx + 1), (size_t)4 * S, hipMemcpyHostToDevice, st), "positions");
+    HIP_TRY(d, hipMemcpyAsync(s->seq_prompt, h + S * (ctx + 1) + S, (size_t)4 * S, hipMemcpyHostToDevice, st),
+            "prompt lengths");
+    // every prompt position but the last: each sequence's batched prefill
+    // into its own caches (the same bits as one position at a time)
+    for (int z = 0; z < S; z++) {
+        for (int start = 0; start < lens[z] - 1; start += s->bcap) {
+            const int n = std::min(s->bcap, lens[z] - 1 - start);
+            {
+                ProfScope p(d, st, "embed");
+                launch_embed_rows(s->embed->w, s->embed->scales, s->embed->kind == RK_Q4, s->seq_tokens + z * (ctx + 1),
+                                  start, n, s->c.dim, s->bx, st);
+            }
+            BatchPos bp;
+            bp.pos0 = start;
+            bp.cache0 = (int64_t)z * ctx * s->kvdim;
+            if ((rc = enqueue_forward_batch(s, st, n, bp))) return rc;
+        }
+    }
+    HIP_TRY(d, hipStreamSynchronize(st), "seqs prefill");
+    s->seq_at.assign(lens, lens + S);
+    for (int32_t &p : s->seq_at) p -= 1;
+    s->seqs_started = true;
+    return RK_OK;
+}
+
+int rk_stage_seqs_run(rk_stage *s, int32_t steps, float *logits) {
+    if (!s || steps < 0) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    if (!s->seqs_started) return fail(d, RK_ERR_ARGS, "rk_stage_seqs_run: no sequences started");
+    const int S = s->seqs;
+    for (int z = 0; z < S; z++)
+        if ((int64_t)s->seq_at[z] + steps > s->c.ctx)
+            return fail(d, RK_ERR_ARGS, "rk_stage_seqs_run: sequence %d: positions [%d, %d) outside the context of %d", z,
+                        s->seq_at[z], s->seq_at[z] + steps, s->c.ctx);
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    const int64_t n = (int64_t)S * s->wcls->rows;
+    for (int32_t i = 0; i < steps; i++) {
+        int rc = run_once(s, kRecSeqs);
+        if (rc) return rc;
+        if (logits) {
+            HIP_TRY(d, hipMemcpyAsync(s->h_logits, s->logits, (size_t)n * 4, hipMemcpyDeviceToHost, d->stream),
+                    "logits");
+            HIP_TRY(d, hipStreamSynchronize(d->stream), "seqs step");
+            memcpy(logits + (int64_t)i * n, s->h_logits, (size_t)n * 4);
+        }
+    }
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "seqs run");
+    for (int32_t &p : s->seq_at) p += steps;
+    return RK_OK;
+}
+
+int rk_stage_seqs_tokens(rk_stage *s, int32_t seq, int32_t from, int32_t n, int32_t *out) {
+    if (!s || !out || seq < 0 || seq >= s->seqs || from < 0 || n < 0 || (int64_t)from + n > s->c.ctx + 1)
+        return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "tokens");
+    HIP_TRY(d,
+            hipMemcpyAsync(out, s->seq_tokens + (int64_t)seq * (s->c.ctx + 1) + from, (size_t)n * 4,
+                           hipMemcpyDeviceToHost, d->stream),
+            "tokens");
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "tokens");
+    return RK_OK;
 }
 
 }  // extern "C"

@@ -93,6 +93,9 @@ SIGNATURES = {
     "rk_stage_generate_run": (ctypes.c_int, [P, I32, P]),
     "rk_stage_generate_tokens": (ctypes.c_int, [P, I32, I32, P]),
     "rk_stage_generate": (ctypes.c_int, [P, P, I32, I32, P]),
+    "rk_stage_seqs_start": (ctypes.c_int, [P, P, P]),
+    "rk_stage_seqs_run": (ctypes.c_int, [P, I32, P]),
+    "rk_stage_seqs_tokens": (ctypes.c_int, [P, I32, I32, I32, P]),
     "rk_num_eval": (ctypes.c_int, [P, I32, P, P, I64]),
     "rk_moe_new": (ctypes.c_int, [P, P, I32, P, P, P, I32, P]),
     "rk_moe_ffn": (ctypes.c_int, [P, P, I32, P, P, P]),
@@ -113,13 +116,13 @@ FN_RECIP32, FN_RSQRT32, FN_EXP32, FN_SILU = 0, 1, 2, 3
 class StageConfig(ctypes.Structure):
     """rk_stage_config (include/rk.h)."""
     _fields_ = [(n, I32) for n in ("dim", "hidden", "heads", "kv_heads", "head_dim", "ctx", "qkv_bias", "qk_norm")] + \
-               [(n, F) for n in ("norm_eps", "recip_dim", "recip_head", "inv_sqrt")]
+               [(n, F) for n in ("norm_eps", "recip_dim", "recip_head", "inv_sqrt")] + [("seqs", I32)]
 
 
 class StageLayer(ctypes.Structure):
     """rk_stage_layer (include/rk.h)."""
     _fields_ = [(n, P) for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3", "rms_att", "rms_ffn", "bq", "bk", "bv",
-                                 "q_norm", "k_norm")]
+                                 "q_norm", "k_norm", "moe")]
 
 
 def lib():
@@ -544,19 +547,22 @@ class Stage:
     (Recip32 of the widths) come from the device's own restatement."""
 
     def __init__(self, dev, dim, hidden, heads, kv_heads, ctx, layers, rope_cos, rope_sin, head_dim=0,
-                 norm_eps=1e-5, qkv_bias=False, qk_norm=False):
+                 norm_eps=1e-5, qkv_bias=False, qk_norm=False, seqs=1):
         hs = head_dim if head_dim > 0 else dim // heads
         rd, rh = dev.num_eval(FN_RECIP32, np.array([dim, hs], np.float32))
         inv_sqrt = np.float32(1.0 / np.sqrt(np.float64(hs)))  # float32(1/math.Sqrt(float64(hs)))
-        self.dev, self.dim, self.ctx, self.hs = dev, dim, ctx, hs
+        self.dev, self.dim, self.ctx, self.hs, self.seqs = dev, dim, ctx, hs, seqs
         self.cfg = StageConfig(dim, hidden, heads, kv_heads, head_dim, ctx, int(qkv_bias), int(qk_norm),
-                               float(np.float32(norm_eps)), float(rd), float(rh), float(inv_sqrt))
+                               float(np.float32(norm_eps)), float(rd), float(rh), float(inv_sqrt), seqs)
         self._keep = []
         arr = (StageLayer * len(layers))()
         for i, L in enumerate(layers):
             vals = {}
+            moe = L.get("moe")  # a Moe in place of w1/w2/w3
+            vals["moe"] = moe.h if moe is not None else None
             for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
-                vals[n] = L[n].h
+                m = L.get(n)
+                vals[n] = m.h if m is not None else None
             for n in ("rms_att", "rms_ffn", "bq", "bk", "bv", "q_norm", "k_norm"):
                 v = L.get(n)
                 if v is not None:
@@ -603,6 +609,24 @@ class Stage:
         p = np.ascontiguousarray(prompt, np.int32)
         out = np.empty(steps, np.int32)
         self.dev._check(lib().rk_stage_generate(self.h, _ptr(p), len(p), steps, _ptr(out)))
+        return out
+
+    def seqs_start(self, prompts):
+        """rk_stage_seqs_start: one prompt (a list of token ids) per sequence."""
+        lens = np.array([len(p) for p in prompts], np.int32)
+        flat = np.ascontiguousarray(np.concatenate([np.asarray(p, np.int32) for p in prompts]), np.int32)
+        self.dev._check(lib().rk_stage_seqs_start(self.h, _ptr(flat), _ptr(lens)))
+
+    def seqs_run(self, steps, want_logits=False):
+        """rk_stage_seqs_run: steps decode steps of every sequence; with
+        want_logits, their logits [steps][seqs][vocab]."""
+        out = np.empty((steps, self.seqs, self.vocab), np.float32) if want_logits else None
+        self.dev._check(lib().rk_stage_seqs_run(self.h, steps, _ptr(out) if want_logits else None))
+        return out
+
+    def seqs_tokens(self, seq, start, n):
+        out = np.empty(n, np.int32)
+        self.dev._check(lib().rk_stage_seqs_tokens(self.h, seq, start, n, _ptr(out)))
         return out
 
     @property
