@@ -55,6 +55,14 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def code_pool(rng, n):
+    """n random Q8 codes in [-127, 127] (uniform bytes from the generator's
+    raw words, -128 moved to -127: fast at model sizes)."""
+    q = rng.bit_generator.random_raw((n + 7) // 8).view(np.int8)[:n].copy()
+    q[q == -128] = -127
+    return q
+
+
 def cpu_baseline(q_all, s_all, xs, threads, budget_s):
     """Times the oracle's AVX2 restatement (internal/num/dot_amd64.s block
     sums, quant.go qrow, rows split as matvec.go:90-104) on the config-2
@@ -77,7 +85,7 @@ def matvec_bench(dev, rkhip, args):
     rng = np.random.default_rng(1)
     q_all, s_all = [], []
     for r, c in SHAPES:
-        q_all.append(rng.integers(-127, 128, r * c, dtype=np.int8))
+        q_all.append(code_pool(rng, r * c))
         s_all.append(rng.uniform(1e-3, 1e-2, r * c // 32).astype(np.float32))
     xs = [rng.normal(0, 1, c).astype(np.float32) for _, c in SHAPES]
     sets = [[dev.upload_q8(q, s, r, c) for (r, c), q, s in zip(SHAPES, q_all, s_all)] for _ in range(args.sets)]
@@ -205,9 +213,10 @@ def dense_bench(dev, rkhip, args):
     """The planner's speed probe (internal/llm/speed.go:16-47 MeasureSpeed):
     products with a 4096x4096 bfloat16 matrix, reported as GB of weights per
     second. Device-resident products rotated over copies past the MALL
-    (graph replays), each launch's duration by HIP events for the roofline,
-    and the reference's own measure (median of 7 host round trips, input and
-    output copies included). A float32 matrix of the same shape beside it."""
+    (graph replays; roofline_frac is a product's bytes over its share of the
+    replay time, launch gaps included), and the reference's own measure
+    (median of 7 host round trips, input and output copies included). A
+    float32 matrix of the same shape beside it."""
     rows = cols = 4096
     w16, x = measure_speed_weights(rows, cols)
     w32 = (w16.astype(np.uint32) << 16).view(np.float32)
@@ -242,12 +251,6 @@ def dense_bench(dev, rkhip, args):
         g.launch(reps)
         t1 = time.perf_counter()
         per = (t1 - t0) / (reps * copies)
-        dev.profile_start()
-        run(200)
-        arena.begin().submit()
-        prof = dev.profile_stop()
-        calls, ms_tot = prof.get("matvec_" + name, (0, 0.0))
-        launch_us = ms_tot / max(calls, 1) * 1e3
         alg = wbytes + 4 * cols + 4 * rows
         rt = []
         for _ in range(8):
@@ -261,8 +264,7 @@ def dense_bench(dev, rkhip, args):
         for m in ms:
             m.free()
         out[name] = {"weights_GB_s": round(wbytes / per / 1e9, 1), "us_per_product": round(per * 1e6, 3),
-                     "avg_launch_us": round(launch_us, 3),
-                     "roofline_frac": round(alg / (launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "roofline_frac": round(alg / per / 1e9 / HBM_PEAK_GBS, 4),
                      "round_trip_GB_s": round(2 * rows * cols / rt[len(rt) // 2] / 1e9, 1),
                      "copies": copies}
         if name == "bf16" and not args.no_cpu:
@@ -294,10 +296,11 @@ def mx_bench(dev, rkhip, args):
     """DeepSeek-V4.1 block-scaled products (internal/num/mx.go MatVecFP8 /
     MatVecFP4 through internal/gpu): E4M3 / E2M1 weights with E8M0 scales,
     the input quantized on the device each call. Device-resident products
-    rotated over copies past the MALL (graph replays); each kernel's average
-    launch by HIP events for the roofline (weights + scales + input codes
-    and scales + output per product). One product per format checked bit
-    for bit against the CPU oracle, which is also timed (one thread)."""
+    rotated over copies past the MALL (graph replays); roofline_frac is a
+    product's bytes (weights + scales + input codes and scales + output)
+    over its share of the replay time, the input's quantize and launch gaps
+    included. One product per format checked bit for bit against the CPU
+    oracle, which is also timed (one thread)."""
     L = rkhip.lib()
     P = ctypes.c_void_p
     rng = np.random.default_rng(41)
@@ -339,13 +342,6 @@ def mx_bench(dev, rkhip, args):
         t0 = time.perf_counter()
         g.launch(reps)
         per = (time.perf_counter() - t0) / (reps * copies)
-        dev.profile_start()
-        run(200)
-        arena.begin().submit()
-        prof = dev.profile_stop()
-        kc, kms = prof.get("matvec_" + kind, (0, 0.0))
-        qc, qms = prof.get("act_fp8", (0, 0.0))
-        launch_us = kms / max(kc, 1) * 1e3
         got = dev.matvecs([ms[0]], x)[0]
         g.free()
         arena.free()
@@ -353,8 +349,7 @@ def mx_bench(dev, rkhip, args):
             m.free()
         r = {"format": kind, "shape": f"{rows}x{cols}", "matrix": what, "weights_MB": round((wbytes + sc.size) / 1e6, 1),
              "us_per_product": round(per * 1e6, 3), "weights_GB_s": round((wbytes + sc.size) / per / 1e9, 1),
-             "avg_launch_us": round(launch_us, 3), "act_fp8_avg_launch_us": round(qms / max(qc, 1) * 1e3, 3),
-             "roofline_frac": round(alg / (launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
+             "roofline_frac": round(alg / per / 1e9 / HBM_PEAK_GBS, 4), "copies": copies}
         if not args.no_cpu and (rows, cols) in ((5120, 8192), (5120, 2304)):
             from oracle import oracle
 
@@ -369,8 +364,8 @@ def mx_bench(dev, rkhip, args):
             r["cpu_baseline"] = {"weights_GB_s": round(n * (wbytes + sc.size) / el / 1e9, 3), "cores": 1,
                                  "kind": "port", "sample": f"{n} products in {el:.1f} s (scalar C restatement of "
                                  f"MatVec{kind.upper()}, one thread)"}
-        log(f"  {kind} {rows}x{cols}: {r['us_per_product']} us/product, {r['weights_GB_s']} GB/s, "
-            f"launch {r['avg_launch_us']} us (frac {r['roofline_frac']})")
+        log(f"  {kind} {rows}x{cols}: {r['us_per_product']} us/product, {r['weights_GB_s']} GB/s "
+            f"(frac {r['roofline_frac']})")
         out.append(r)
     # selected experts (ExpertMatVecs): 6 of 64 E2M1 experts of 2304 rows a
     # call, the ids rotated over 10 sets (60 experts, past the MALL)
@@ -398,22 +393,20 @@ def mx_bench(dev, rkhip, args):
 
     for k in range(10):
         call(k)
-    dev.profile_start()
+    t0 = time.perf_counter()
     for k in range(200):
         call(k)
-    prof = dev.profile_stop()
-    kc, kms = prof.get("matvec_fp4_experts", (0, 0.0))
-    launch_us = kms / max(kc, 1) * 1e3
+    call_us = (time.perf_counter() - t0) / 200 * 1e6
     ebytes = slots * (P * cols // 2 + P * nb)
-    alg = ebytes + cols + 4 * nb + 4 * slots * P
     b = arena.begin()
     b.expert_matvecs(m, P, idw, slots, 0, cols, 0, outw, P)
     got = np.asarray(b.read(outw, slots * P)).reshape(slots, P)
     b.submit()
     r = {"format": "fp4", "shape": f"{slots} of {E} experts, {P}x{cols} each", "matrix": "ExpertMatVecs: one token's "
-         "routed experts' gate rows", "weights_MB": round(ebytes / 1e6, 1), "avg_launch_us": round(launch_us, 3),
-         "weights_GB_s_in_launch": round(ebytes / (launch_us * 1e-6) / 1e9, 1),
-         "roofline_frac": round(alg / (launch_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+         "routed experts' gate rows", "weights_MB": round(ebytes / 1e6, 1),
+         "us_per_batch_call": round(call_us, 3),
+         "timing": "wall time of a Batch (begin, input quantize, products, submit and wait) per call; the "
+                   "kernel's own duration is in the kernel trace"}
     if not args.no_cpu:
         from oracle import oracle
 
@@ -421,7 +414,7 @@ def mx_bench(dev, rkhip, args):
         want = oracle.matvec_fp4(w[e * P * cols // 2:(e + 1) * P * cols // 2], sc[e * P * nb:(e + 1) * P * nb], x, P,
                                  cols)
         r["bit_exact_vs_cpu"] = bool(np.array_equal(got[2].view(np.uint32), want.view(np.uint32)))
-    log(f"  fp4 experts {slots}x{P}x{cols}: launch {r['avg_launch_us']} us (frac {r['roofline_frac']})")
+    log(f"  fp4 experts {slots}x{P}x{cols}: {r['us_per_batch_call']} us a batch call")
     out.append(r)
     arena.free()
     m.free()
@@ -499,7 +492,7 @@ def decode_bench(dev, rkhip, args):
     # Codes come from one random pool at per-matrix offsets (distinct
     # matrices without generating 8 GB on the host); scales keep the
     # activations finite through the layers.
-    pool = rng.integers(-127, 128, vocab * dim + (1 << 20), dtype=np.int8)
+    pool = code_pool(rng, vocab * dim + (1 << 20))
     spool = rng.uniform(2e-5, 2e-4, vocab * dim // 32 + (1 << 16)).astype(np.float32)
     mats = []
 
@@ -590,7 +583,7 @@ def prefill_bench(dev, rkhip, args):
     qdim, kvdim = heads * hs, kv_heads * hs
     rng = np.random.default_rng(4)
     pool = rng.integers(0, 256, hidden * dim // 2 + (1 << 20), dtype=np.uint8)
-    pool8 = rng.integers(-127, 128, vocab * dim + (1 << 20), dtype=np.int8)
+    pool8 = code_pool(rng, vocab * dim + (1 << 20))
     spool = rng.uniform(2e-5, 2e-4, vocab * dim // 32 + (1 << 16)).astype(np.float32)
     mats = []
 
@@ -676,15 +669,21 @@ def prefill_bench(dev, rkhip, args):
 
 
 def moe_bench(dev, rkhip, args):
-    """Config 5's mixture-of-experts feed-forward (Qwen3-MoE shape: dim 2048,
-    128 Q8 experts of ffn 768, Q8 router, top 8) at batch 1 and 16: the
-    time of one layer's FFN, over distinct layers whose experts (604 MB
-    each) stream from HBM."""
-    dim, hidden, experts, topk = 2048, 768, 128, 8
-    nl = args.moe_layers
+    """Config 5: a Qwen3-MoE-shape decoder, 48 layers (dim 2048, 32 q / 4 kv
+    heads of 128 with QK-norm, 128 Q8 experts of ffn 768, Q8 router, top 8,
+    vocab 151936), greedy decode entirely on the device: batch 1 (one
+    sequence, one recorded graph per token) and batch 16 (16 independent
+    sequences, each with its own prompt, position and caches; one recorded
+    graph per step, each selected expert's rows read once per step for all
+    the sequences that chose it). Every layer's matrices are distinct device
+    copies (codes from one random pool at per-matrix offsets)."""
+    dim, heads, kv_heads, hs, experts, ehidden, topk, vocab = 2048, 32, 4, 128, 128, 768, 8, 151936
+    nl, prompt_len, steps = args.moe_layers, args.moe_prompt, args.moe_decode
+    ctx = prompt_len + steps
+    qdim, kvdim = heads * hs, kv_heads * hs
     rng = np.random.default_rng(5)
-    pool = rng.integers(-127, 128, experts * hidden * dim + (1 << 20), dtype=np.int8)
-    spool = rng.uniform(1e-3, 1e-2, experts * hidden * dim // 32 + (1 << 16)).astype(np.float32)
+    pool = code_pool(rng, vocab * dim + (1 << 20))
+    spool = rng.uniform(2e-5, 2e-4, vocab * dim // 32 + (1 << 16)).astype(np.float32)
     mats = []
 
     def mat(rows, cols, lo=1.0):
@@ -696,75 +695,84 @@ def moe_bench(dev, rkhip, args):
         return m
 
     t0 = time.perf_counter()
-    layers = []
+    lay, moes = [], []
     for _ in range(nl):
-        router = mat(experts, dim, 0.3)
-        w1 = [mat(hidden, dim) for _ in range(experts)]
-        w3 = [mat(hidden, dim) for _ in range(experts)]
-        w2 = [mat(dim, hidden, 0.1) for _ in range(experts)]
-        layers.append(rkhip.Moe(dev, router, w1, w2, w3, topk))
-    log(f"moe bench: {nl} layers uploaded in {time.perf_counter() - t0:.1f} s")
-    expert_bytes = 3 * hidden * dim * 33 // 32
-    router_bytes = experts * dim * 33 // 32
+        moe = rkhip.Moe(dev, mat(experts, dim, 10.0), [mat(ehidden, dim) for _ in range(experts)],
+                        [mat(dim, ehidden) for _ in range(experts)], [mat(ehidden, dim) for _ in range(experts)], topk)
+        moes.append(moe)
+        lay.append({"wq": mat(qdim, dim), "wk": mat(kvdim, dim), "wv": mat(kvdim, dim), "wo": mat(dim, qdim),
+                    "moe": moe, "rms_att": rng.normal(1, 0.1, dim).astype(np.float32),
+                    "rms_ffn": rng.normal(1, 0.1, dim).astype(np.float32),
+                    "q_norm": rng.normal(1, 0.1, hs).astype(np.float32),
+                    "k_norm": rng.normal(1, 0.1, hs).astype(np.float32)})
+    embed = mat(vocab, dim)
+    rms_final = rng.normal(1, 0.1, dim).astype(np.float32)
+    log(f"moe bench: {nl} layers ({len(mats)} matrices) uploaded in {time.perf_counter() - t0:.1f} s")
+    cos, sin = rope_table(1000000.0, hs, ctx)
+    q8 = lambda r, c: r * c + r * (c // 32) * 4  # noqa: E731
+    attn_bytes = q8(qdim + 2 * kvdim, dim) + q8(dim, qdim)
+    expert_bytes = 2 * q8(ehidden, dim) + q8(dim, ehidden)
+    router_bytes = q8(experts, dim)
+    cls_bytes = q8(vocab, dim)
+    kv_read = 2 * kvdim * 4 * (prompt_len + steps / 2)  # one sequence's cache reads per layer, average position
     out = {}
     for batch in (1, 16):
-        x = rng.normal(0, 1, (batch, dim)).astype(np.float32)
-        arena = dev.arena(2 * batch * dim, batch * dim)
-        b = arena.begin()
-        b.write(0, x)
-        b.submit()
-        dx, dy = arena.device_ptr(0), arena.device_ptr(batch * dim)
-        # distinct experts a step streams (routing depends on the input only)
-        _, sel, _ = layers[0].ffn(x)
-        distinct = len(set(int(e) for e in sel.ravel()))
-        for m in layers:
-            m.ffn_device(dx, batch, dy)
-        reps = max(1, args.moe_reps)
-        g = None
-        if args.eager:  # launches one by one (for tools that cannot follow graph replays)
-            arena.begin().submit()
-            t0 = time.perf_counter()
-            for _ in range(reps):
-                for m in layers:
-                    m.ffn_device(dx, batch, dy)
-            arena.begin().submit()
-            el = time.perf_counter() - t0
+        st = rkhip.Stage(dev, dim, ehidden, heads, kv_heads, ctx, lay, cos, sin, head_dim=hs, norm_eps=1e-6,
+                         qk_norm=True, seqs=batch)
+        st.set_head(embed, embed, rms_final)
+        prompts = [[int(t) for t in rng.integers(0, vocab, prompt_len)] for _ in range(batch)]
+        if batch == 1:
+            def start():
+                st.generate_start(prompts[0])
+                st.generate_run(prompt_len)  # the prompt (batched) and its last position's token
+
+            def run(n):
+                st.generate_run(n)
         else:
-            dev.graph_begin()
-            for m in layers:
-                m.ffn_device(dx, batch, dy)
-            g = dev.graph_end()
-            g.launch(2)
-            t0 = time.perf_counter()
-            g.launch(reps)
-            el = time.perf_counter() - t0
-        ms_layer = el / (reps * nl) * 1e3
-        step_bytes = distinct * expert_bytes + router_bytes
+            def start():
+                st.seqs_start(prompts)
+
+            def run(n):
+                st.seqs_run(n)
+        start()
+        run(2)  # records the graph, touches every weight
+        start()
+        t0 = time.perf_counter()
+        run(steps - 1)
+        el = time.perf_counter() - t0
+        ms_step = el / (steps - 1) * 1e3
+        start()
         dev.profile_start()
-        for m in layers:
-            m.ffn_device(dx, batch, dy)
-        arena.begin().submit()
+        run(4)
         prof = dev.profile_stop()
+        # distinct experts a step streams per layer: every one of the 8 at
+        # batch 1; at batch 16 the expected count under independent uniform
+        # routing, E·(1 - (1 - k/E)^16)
+        distinct = topk if batch == 1 else experts * (1 - (1 - topk / experts) ** batch)
+        step_bytes = nl * (attn_bytes + router_bytes + distinct * expert_bytes + batch * kv_read) + cls_bytes
         out[f"batch{batch}"] = {
-            "ms_per_layer": round(ms_layer, 4),
-            "ms_per_48_layers": round(ms_layer * 48, 3),
-            "tok_s_48_layer_ffn": round(batch / (ms_layer * 48 / 1e3), 1),
-            "distinct_experts": distinct,
-            "bytes_per_layer": step_bytes,
-            "effective_GB/s": round(step_bytes / (ms_layer / 1e3) / 1e9, 1),
-            "kernels_us_per_layer": {k: round(v[1] / nl * 1e3, 2) for k, v in prof.items()},
+            "tok_s": round(batch / (ms_step / 1e3), 1),
+            "ms_per_step": round(ms_step, 4),
+            "tokens_per_step": batch,
+            "distinct_experts_per_layer": round(distinct, 1),
+            "bytes_per_step": int(step_bytes),
+            "effective_GB/s": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
+            "frac_of_hbm_peak": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernels_us_per_step": {k: round(v[1] / 4 * 1e3, 2) for k, v in prof.items()},
+            "kernel_launches_per_step": {k: v[0] // 4 for k, v in prof.items()},
         }
-        if g:
-            g.free()
-        arena.free()
-    for m in layers:
+        log(f"  batch {batch}: {out[f'batch{batch}']['tok_s']} tok/s, {ms_step:.3f} ms a step")
+        st.free()
+    for m in moes:
         m.free()
     for m in mats:
         m.free()
-    return {"moe": {"config": f"config 5 MoE FFN: dim {dim}, {experts} Q8 experts of ffn {hidden}, Q8 router, top "
-                              f"{topk}; {nl} distinct layers replayed as one graph; router codes scaled so the routing "
-                              f"spreads; the 48-layer figures are {nl}-layer times x 48 (attention not included)",
-                    **out}}
+    return {"moe_decode_tok_s": out["batch1"]["tok_s"], "moe_decode_b16_tok_s": out["batch16"]["tok_s"],
+            "moe": {"config": f"config 5: dim {dim}, {nl} layers, {heads} q / {kv_heads} kv heads of {hs} with "
+                              f"QK-norm, {experts} Q8 experts of ffn {ehidden}, Q8 router, top {topk}, vocab {vocab}, "
+                              f"RoPE theta 1e6, f32 KV; greedy {steps} tokens after {prompt_len}-token seeded "
+                              f"prompts, batch 1 and 16 independent sequences; random Q8 codes, scales U(2e-5, "
+                              f"2e-4) (router x10)", **out}}
 
 
 def main():
@@ -786,8 +794,9 @@ def main():
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-mx", action="store_true")
-    ap.add_argument("--moe-layers", type=int, default=4)
-    ap.add_argument("--moe-reps", type=int, default=20)
+    ap.add_argument("--moe-layers", type=int, default=48)
+    ap.add_argument("--moe-prompt", type=int, default=64)
+    ap.add_argument("--moe-decode", type=int, default=64)
     ap.add_argument("--prefill-layers", type=int, default=28)
     ap.add_argument("--prefill-prompt", type=int, default=512)
     ap.add_argument("--prefill-decode", type=int, default=64)
@@ -843,13 +852,27 @@ def main():
     result["device"] = {"name": info.name.decode(), "arch": info.arch.decode(), "cu": info.compute_units}
     if not args.no_cpu:
         log("cpu baseline")
-        threads = min(16, os.cpu_count() or 1)
+        # every CPU this process may run on, up to the 16 threads a one-GPU
+        # job is allotted on the GPU hosts (nproc and the affinity set are
+        # reported beside it)
+        nproc = os.cpu_count() or 1
+        try:
+            avail = len(os.sched_getaffinity(0))
+        except (AttributeError, OSError):
+            avail = nproc
+        threads = max(1, min(16, avail))
         gbs, reps, el, outs = cpu_baseline(q_all, s_all, xs, threads, args.cpu_seconds)
         exact = all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(outs, gpu_outs))
+        gbs1, reps1, el1, _ = cpu_baseline(q_all, s_all, xs, 1, min(4.0, args.cpu_seconds))
         result["cpu_baseline"] = {"value": round(gbs, 2), "unit": "GB/s", "cores": threads, "kind": "port",
                                   "sample": f"{reps} passes over the three config-2 products in {el:.1f} s "
                                             "(C restatement of the reference CPU path: AVX2 block sums, rows "
                                             "over threads)",
+                                  "host_nproc": nproc, "cpus_available": avail,
+                                  "threads_rule": "all CPUs available to the process, at most the 16 threads a "
+                                                  "one-GPU job is allotted on the GPU host",
+                                  "one_thread": {"value": round(gbs1, 2), "unit": "GB/s", "cores": 1,
+                                                 "sample": f"{reps1} passes in {el1:.1f} s"},
                                   "bit_exact_vs_gpu": bool(exact)}
     dev.close()
     print(json.dumps(result))
