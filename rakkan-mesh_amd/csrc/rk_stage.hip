@@ -144,6 +144,27 @@ static int stage_product(rk_stage *s, hipStream_t st, const char *name, const QS
     return RK_OK;
 }
 
+// The attention of the position in ctl (or of a batch, bt): the scores
+// into att, then the softmax and the weighted values (quantized into qo
+// when given). Two launches: the scores need many workgroups (every score
+// reads a whole key row), the sequential sums few. (One launch computing
+// a head's scores in the workgroups of its value sums measured slower on
+// MI355X: each workgroup then reads all of the head's keys.)
+static void enqueue_attention(rk_stage *s, hipStream_t st, const float *q, const float *keys, const float *vals,
+                              float *att, float *out, const int32_t *ctl, const AttBatch &bt, const QScratch *qo) {
+    rk_device *d = s->d;
+    const rk_stage_config &c = s->c;
+    int8_t *qx = qo ? qo->qx : nullptr;
+    float *xs = qo ? qo->xs : nullptr;
+    int32_t *xsum = qo ? qo->xsum : nullptr;
+    {
+        ProfScope p(d, st, "att_scores");
+        launch_att_scores(q, keys, att, c.ctx, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, c.inv_sqrt, st);
+    }
+    ProfScope p(d, st, "att_values");
+    launch_att_values(att, c.ctx, vals, out, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, qx, xs, xsum, st);
+}
+
 // The launches of one layer (Stage.Forward's body, model.go:530-611). The
 // norms run in the prologues of the products that read them (QKV: the
 // attention norm, unless qb already holds it; W1/W3: the ffn norm).
@@ -198,19 +219,11 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
         launch_qknorm_rope(s->q, s->k, s->v, D.q_norm, D.k_norm, c.recip_head, c.norm_eps, s->cos_t, s->sin_t,
                            s->ctl, 0, 1, D.keys, D.vals, c.heads, c.kv_heads, s->hs, st);
     }
-    {
-        ProfScope p(d, st, "att_scores");
-        launch_att_scores(s->q, D.keys, s->att, c.ctx, s->ctl, AttBatch{}, c.ctx, c.heads, c.kv_heads, s->hs,
-                          s->kvdim, c.inv_sqrt, st);
-    }
     // The attention output comes quantized when its Q8 blocks fall within
     // heads (head size a multiple of 32).
     const bool att_q = s->hs % 32 == 0;
-    {
-        ProfScope p(d, st, "att_values");
-        launch_att_values(s->att, c.ctx, D.vals, s->att_out, s->ctl, AttBatch{}, c.ctx, c.heads, c.kv_heads, s->hs,
-                          s->kvdim, att_q ? s->qa.qx : nullptr, s->qa.xs, s->qa.xsum, st);
-    }
+    enqueue_attention(s, st, s->q, D.keys, D.vals, s->att, s->att_out, s->ctl, AttBatch{},
+                      att_q ? &s->qa : nullptr);
     float *xo[1] = {s->x};
     if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, nullptr, &L.wo, 1, xo, kEpAdd, base)))
         return rc;
@@ -471,19 +484,11 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, const
     bt.out_stride = s->qdim;
     bt.pos = bp.seq_pos;
     bt.cache_stride = bp.cache_stride;
-    {
-        ProfScope p(d, st, "att_scores");
-        launch_att_scores(s->bq, D.keys + bp.cache0, s->batt, c.ctx, nullptr, bt, c.ctx, c.heads, c.kv_heads, s->hs,
-                          s->kvdim, c.inv_sqrt, st);
-    }
     // the attention output comes quantized when its Q8 blocks fall within
     // heads; else it is quantized by a launch of its own
     const bool att_q = s->hs % 32 == 0;
-    {
-        ProfScope p(d, st, "att_values");
-        launch_att_values(s->batt, c.ctx, D.vals + bp.cache0, s->batt_out, nullptr, bt, c.ctx, c.heads, c.kv_heads,
-                          s->hs, s->kvdim, att_q ? s->bqa.qx : nullptr, s->bqa.xs, s->bqa.xsum, st);
-    }
+    enqueue_attention(s, st, s->bq, D.keys + bp.cache0, D.vals + bp.cache0, s->batt, s->batt_out, nullptr, bt,
+                      att_q ? &s->bqa : nullptr);
     if (!att_q) {
         ProfScope p(d, st, "quantize_acts");
         launch_quantize_acts(s->batt_out, (int64_t)n * s->qdim, s->bqa.qx, s->bqa.xs, s->bqa.xsum, st);
