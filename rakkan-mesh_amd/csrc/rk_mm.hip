@@ -224,25 +224,29 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
         }
     };
 
+    // Whole chunks in one loop of one path (a second path inside the loop
+    // makes the compiler copy all 64 running sums at every iteration), then
+    // the short last chunk, if any, after it.
+    const int nfull = nb / kMmKB;
     stage_load(0);
     stage_store(stg[0]);
     __syncthreads();
-    for (int ci = 0; ci < nchunks; ci++) {
-        const int c0 = ci * kMmKB;
+    for (int ci = 0; ci < nfull; ci++) {
         // the next chunk's loads (past the last chunk they re-read it and
         // fill the idle buffer, which nothing reads)
-        stage_load(c0 + kMmKB);
+        stage_load((ci + 1) * kMmKB);
         const MmStage &S = stg[ci & 1];
-        if (c0 + kMmKB <= nb) {
 #pragma unroll
-            for (int k = 0; k < kMmKB; k++) kstep(S, k);
-        } else {
-#pragma unroll
-            for (int k = 0; k < kMmKB; k++)
-                if (c0 + k < nb) kstep(S, k);  // absent blocks are skipped, not added as zeros
-        }
+        for (int k = 0; k < kMmKB; k++) kstep(S, k);
         stage_store(stg[(ci + 1) & 1]);
         __syncthreads();
+    }
+    if (nfull < nchunks) {
+        const MmStage &S = stg[nfull & 1];
+        const int c0 = nfull * kMmKB;
+#pragma unroll
+        for (int k = 0; k < kMmKB; k++)
+            if (c0 + k < nb) kstep(S, k);  // absent blocks are skipped, not added as zeros
     }
 
     // ---- results: the fixed tree of the eight running sums, then the
@@ -260,9 +264,11 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
             }
 
     if (SILU) {
-        // h = silu(W1·x)·(W3·x) into LDS [token][32 rows], then each token's
-        // 32 values (one Q8_0 block of h) quantized by eight lanes
+        // h = silu(W1·x)·(W3·x) into LDS [token][32 rows] (over stage
+        // buffer 0, once every wave is past its last read of it), then each
+        // token's 32 values (one Q8_0 block of h) quantized by eight lanes
         float *hb = reinterpret_cast<float *>(lds);
+        __syncthreads();
         float4 h4;
         h4.x = silu_mul(res[0][0][0], res[1][0][0]);
         h4.y = silu_mul(res[0][0][1], res[1][0][1]);
