@@ -169,6 +169,14 @@ def matvec_bench(dev, rkhip, args):
         us = p["matvec_q8"][1] / p["matvec_q8"][0] * 1e3
         entry["GB/s"] = round(q8_bytes(r, c) / (us / 1e6) / 1e9, 1)
         entry["frac"] = round(q8_bytes(r, c) / (us / 1e6) / 1e9 / HBM_PEAK_GBS, 4)
+        # the floor under a launch that reads these bytes: back-to-back plain
+        # reads of the same size (rotated past the MALL) and empty launches
+        nb16 = q8_bytes(r, c) // 16 * 16
+        empty_us, read_us = dev.launch_floor(nb16, copies=max(2, -(-600_000_000 // nb16)), launches=200)
+        entry["plain_read_us"] = round(read_us, 3)
+        entry["empty_launch_us"] = round(empty_us, 3)
+        entry["plain_read_frac"] = round(q8_bytes(r, c) / (read_us / 1e6) / 1e9 / HBM_PEAK_GBS, 4)
+        entry["frac_of_plain_read"] = round(read_us / us, 4)
         per_shape[f"{r}x{c}"] = entry
 
     out = {

@@ -432,6 +432,16 @@ typedef struct {
 int rk_profile_start(rk_device *dev);
 int rk_profile_stop(rk_device *dev, rk_profile_entry *out, int32_t cap, int32_t *n);
 
+/* ---- Diagnostics (no counterpart in the reference) ----
+ * The floor under one launch on this device, for reading a product's time
+ * against: the time per launch of `launches` back-to-back launches of an
+ * empty kernel (*empty_us) and of a plain streaming read of `bytes` (a
+ * multiple of 16) that stores nothing (*read_us). The reads take `copies`
+ * buffers in turn, so that copies·bytes past the 256 MB MALL come from HBM.
+ * Allocates copies·bytes of device memory for the call. */
+int rk_device_launch_floor(rk_device *dev, int64_t bytes, int32_t copies, int32_t launches, float *empty_us,
+                           float *read_us);
+
 #ifdef __cplusplus
 }
 #endif

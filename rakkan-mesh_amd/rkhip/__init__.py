@@ -84,6 +84,7 @@ SIGNATURES = {
     "rk_graph_free": (ctypes.c_int, [P]),
     "rk_profile_start": (ctypes.c_int, [P]),
     "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
+    "rk_device_launch_floor": (ctypes.c_int, [P, I64, I32, I32, P, P]),
     "rk_stage_new": (ctypes.c_int, [P, P, P, I32, P, P, P]),
     "rk_stage_forward": (ctypes.c_int, [P, P, I32, I32]),
     "rk_stage_bytes": (I64, [P]),
@@ -461,6 +462,13 @@ class Device:
         buf = (ProfileEntry * 64)()
         self._check(lib().rk_profile_stop(self.h, ctypes.cast(buf, P), 64, ctypes.byref(n)))
         return {buf[i].kernel.decode(): (buf[i].calls, buf[i].ms) for i in range(min(n.value, 64))}
+
+    def launch_floor(self, nbytes, copies=8, launches=200):
+        """(empty-kernel us, plain-read us) per launch, back to back: the floor
+        under a launch that reads nbytes (rk_device_launch_floor)."""
+        e, r = ctypes.c_float(), ctypes.c_float()
+        self._check(lib().rk_device_launch_floor(self.h, nbytes, copies, launches, ctypes.byref(e), ctypes.byref(r)))
+        return e.value, r.value
 
     def arena(self, words, staging_words):
         return Arena(self, words, staging_words)

@@ -266,3 +266,17 @@ def test_graph_replays_match(dev):
     m8.free()
     m4.free()
     assert dev.used == 0
+
+
+def test_launch_floor(dev):
+    """rk_device_launch_floor: an empty launch costs time, a plain read of
+    18.9 MB costs more, and the read rate it implies stays under the HBM
+    peak (the copies rotate past the MALL); bad arguments are errors."""
+    nbytes = 18907136  # config 2's 4096x4096 product: codes, scales, input and output
+    empty_us, read_us = dev.launch_floor(nbytes, copies=32, launches=50)
+    assert 0.0 < empty_us < read_us
+    assert nbytes / (read_us * 1e-6) < 8.0e12 * 1.05
+    for args in [(0, 1, 1), (17, 1, 1), (nbytes, 0, 1), (nbytes, 1, 0)]:
+        with pytest.raises(rkhip.RKError) as e:
+            dev.launch_floor(*args)
+        assert e.value.code == rkhip.RK_ERR_ARGS
