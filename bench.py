@@ -749,6 +749,13 @@ def moe_bench(dev, rkhip, args):
         run(steps - 1)
         el = time.perf_counter() - t0
         ms_step = el / (steps - 1) * 1e3
+        # per-kernel times: eager launches stamped one by one, after one
+        # unstamped eager step (the first eager launches pay one-time host
+        # work between a kernel's start event and its dispatch)
+        start()
+        dev.profile_start()
+        run(1)
+        dev.profile_stop()
         start()
         dev.profile_start()
         run(4)

@@ -60,4 +60,10 @@ int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc);
 int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, const int32_t *xsum,
                   int tokens, float *out, bool residual, hipStream_t s);
 
+// The same from f32 inputs x [tokens][dim]: RMSNorm'd with norm_w (recip_n
+// = 1/dim, eps) or, norm_w null, taken as given, and quantized into qx/xs/
+// xsum (which the experts' products then read).
+int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *norm_w, float recip_n, float eps,
+                  int tokens, int8_t *qx, float *xs, int32_t *xsum, float *out, bool residual, hipStream_t s);
+
 }  // namespace rk

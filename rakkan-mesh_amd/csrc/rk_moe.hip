@@ -12,8 +12,10 @@
 //   h = float32(w·float32(silu(W1·xn)·(W3·xn)))  per selected expert
 //   y = Σ W2·h over the selected experts in ascending index, from +0
 //
-// Launches: the router's product (on the quantized input); the routing
-// (one wave per token); the grouping of the (token, slot) pairs by expert;
+// Launches: the router's product (on the quantized input; a batch of up to
+// 16 tokens a row per wave, the tokens' codes in LDS); the routing (one wave
+// per token); the grouping of the (token, slot) pairs by expert (counts and
+// places in parallel for up to 128 pairs);
 // each selected expert's W1/W3 rows for all the tokens that chose it, with
 // the gate, the weight and h's quantization; each selected expert's W2 rows
 // for those tokens; the ascending-order sum (optionally into a residual).
@@ -95,6 +97,62 @@ __device__ __forceinline__ void wave_rows_q8_multi(const uint8_t *const (&w)[NR]
             const float q4 = p2 + __shfl_down(p2, 4);
             res[j][r] = q4 + __shfl_down(q4, 8);
         }
+}
+
+// The router's product for a batch of up to kRouterMaxT tokens whose codes
+// fit kRouterLds: wave w of workgroup b takes row 4b + w (MatVecQ8's bits)
+// for every token, eight tokens a pass; lane l keeps, for token l/8 of the
+// pass, running sum l mod 8 (blocks l mod 8, +8, ... in order), so the sums
+// need no lane exchanges until the fixed tree ((0+1)+(2+3))+((4+5)+(6+7)).
+// The row's blocks are loaded once, up front; the tokens' codes are staged
+// in LDS. logits: [tokens][experts].
+constexpr int kRouterBpl = 8;  // blocks of a row per lane (rows up to 2048 wide)
+constexpr int kRouterMaxT = 16;
+__global__ __launch_bounds__(256) void moe_router_rows_kernel(const uint8_t *rw, const float *rws, int experts, int dim,
+                                                              const int8_t *qx, const float *xs, int tokens,
+                                                              float *logits) {
+    extern __shared__ __align__(16) char rlds[];
+    int8_t *sq = reinterpret_cast<int8_t *>(rlds);                             // [tokens][dim] codes
+    float *sxs = reinterpret_cast<float *>(rlds + (int64_t)tokens * dim);   // [tokens][dim/32] scales
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rl = lane & 7, tg = lane >> 3;
+    const int nb = dim >> 5;
+    const int rowi = blockIdx.x * 4 + wave, row = min(rowi, experts - 1);
+    const uint8_t *rp = rw + (int64_t)row * dim;
+    const float *rs = rws + (int64_t)row * nb;
+    int4 c0[kRouterBpl], c1[kRouterBpl];
+    float sw[kRouterBpl];
+#pragma unroll
+    for (int m = 0; m < kRouterBpl; m++) {
+        const int b = min(rl + 8 * m, nb - 1);  // blocks past the row are never summed
+        c0[m] = load_stream16(rp + 32 * b);
+        c1[m] = load_stream16(rp + 32 * b + 16);
+        sw[m] = rs[b];
+    }
+    for (int i = tid; i < (tokens * dim) >> 4; i += 256)
+        reinterpret_cast<int4 *>(sq)[i] = reinterpret_cast<const int4 *>(qx)[i];
+    for (int i = tid; i < tokens * nb; i += 256) sxs[i] = xs[i];
+    __syncthreads();
+    if (rowi >= experts) return;  // uniform over the wave
+    for (int t0 = 0; t0 < tokens; t0 += 8) {
+        const int t = min(t0 + tg, tokens - 1);
+        const int8_t *xq = sq + t * dim;
+        const float *xsc = sxs + t * nb;
+        float acc = 0.0f;
+#pragma unroll
+        for (int m = 0; m < kRouterBpl; m++) {
+            const int b = rl + 8 * m;
+            if (b < nb) {
+                const int4 *xp = reinterpret_cast<const int4 *>(xq + 32 * b);
+                const int sum = dot16(c1[m], xp[1], dot16(c0[m], xp[0], 0));
+                acc += (float)sum * (sw[m] * xsc[b]);
+            }
+        }
+        acc = acc + dppf_x1(acc);
+        acc = acc + dppf_x2(acc);
+        acc = acc + __int_as_float(dpp_mirror8(__float_as_int(acc)));
+        if (rl == 0 && t0 + tg < tokens) logits[(int64_t)(t0 + tg) * experts + row] = acc;
+    }
 }
 
 // 64-bit key of probability v at expert e for a max-reduction that picks
@@ -199,11 +257,19 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
 // selected, then at grp + 1 + g, + gcap, + 2·gcap their index (ascending),
 // first entry in the pair list and count, and the pair list from
 // grp + 1 + 3·gcap (each group's pairs in ascending order). One workgroup;
-// thread e counts expert e's pairs.
-__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, int npairs, int experts, int gcap,
+// thread e counts expert e's pairs, reading the selection from LDS (staged
+// there first when it fits kGroupLdsPairs).
+constexpr int kGroupLdsPairs = 8192;
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel_g, int npairs, int experts, int gcap,
                                                          int32_t *grp) {
     __shared__ int s_cnt[1024], s_any[1024];
+    extern __shared__ int s_selp[];
     const int e = threadIdx.x;
+    const bool staged = npairs <= kGroupLdsPairs;
+    if (staged)
+        for (int p = e; p < npairs; p += 1024) s_selp[p] = sel_g[p];
+    __syncthreads();
+    const int32_t *sel = staged ? s_selp : sel_g;
     int cnt = 0;
     if (e < experts)
         for (int p = 0; p < npairs; p++) cnt += sel[p] == e;
@@ -231,12 +297,81 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, int
     if (e == 1023) grp[0] = s_any[1023];
 }
 
+// The same grouping for up to kGroupFastPairs pairs and 1024 experts, with
+// no thread walking all the pairs: counts by LDS atomics, one wave's scans
+// over the experts (starts and group indices), and each pair's place among
+// its expert's pairs from the earlier pairs (eight threads a pair).
+constexpr int kGroupFastPairs = 128;
+__global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel, int npairs, int experts, int gcap,
+                                                              int32_t *grp) {
+    __shared__ int s_sel[kGroupFastPairs], s_cnt[1024], s_start[1024], s_gi[1024], s_total;
+    const int tid = threadIdx.x, lane = tid & 63;
+    if (tid < npairs) s_sel[tid] = sel[tid];
+    s_cnt[tid] = 0;
+    __syncthreads();
+    if (tid < npairs) atomicAdd(&s_cnt[s_sel[tid]], 1);
+    __syncthreads();
+    if (tid < 64) {
+        // lane l takes experts l·per .. l·per+per-1: local sums, then an
+        // exclusive scan of the lane totals across the wave
+        const int per = (experts + 63) / 64;
+        int c = 0, g = 0;
+        for (int i = 0; i < per; i++) {
+            const int e = lane * per + i;
+            if (e < experts) {
+                c += s_cnt[e];
+                g += s_cnt[e] > 0;
+            }
+        }
+        int ci = c, gi = g;  // inclusive scans
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int oc = __shfl_up(ci, d), og = __shfl_up(gi, d);
+            if (lane >= d) {
+                ci += oc;
+                gi += og;
+            }
+        }
+        int cs = ci - c, gs = gi - g;  // exclusive
+        for (int i = 0; i < per; i++) {
+            const int e = lane * per + i;
+            if (e < experts) {
+                s_start[e] = cs;
+                s_gi[e] = gs;
+                cs += s_cnt[e];
+                gs += s_cnt[e] > 0;
+            }
+        }
+        if (lane == 63) s_total = gi;
+    }
+    __syncthreads();
+    int32_t *gexp = grp + 1, *gstart = grp + 1 + gcap, *gcount = grp + 1 + 2 * gcap, *list = grp + 1 + 3 * gcap;
+    if (tid < experts && s_cnt[tid] > 0) {
+        const int g = s_gi[tid];
+        gexp[g] = tid;
+        gstart[g] = s_start[tid];
+        gcount[g] = s_cnt[tid];
+    }
+    // pair p's place: the earlier pairs of its expert (eight threads a pair)
+    const int p = tid >> 3, part = tid & 7;
+    if (p < npairs) {  // whole groups of eight
+        const int e = s_sel[p];
+        int n = 0;
+        for (int q = part; q < p; q += 8) n += s_sel[q] == e;
+        n += dpp_x1(n);
+        n += dpp_x2(n);
+        n += dpp_mirror8(n);
+        if (part == 0) list[s_start[e] + n] = p;
+    }
+    if (tid == 0) grp[0] = s_total;
+}
+
 // W1 and W3 rows of a selected expert for every pair that chose it:
 // h = w·(silu(W1·xn)·(W3·xn)), then h's Q8_0 block. Workgroup (group, block
 // of 32 hidden rows), eight waves of four hidden rows (W1 and W3 of each:
 // eight row dots), the group's pairs kMoePass at a time. Groups past the
 // count exit.
-__global__ __launch_bounds__(512) void moe_up_kernel(const uint8_t *const *w1, const float *const *s1,
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void moe_up_kernel(const uint8_t *const *w1, const float *const *s1,
                                                      const uint8_t *const *w3, const float *const *s3,
                                                      const int32_t *grp, int gcap, const float *wsel, int k,
                                                      const int8_t *qx, const float *xs, int dim, int hidden,
@@ -402,10 +537,13 @@ int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc) 
     return at;
 }
 
+static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, int tokens,
+                               float *out, bool residual, hipStream_t s);
+
 int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, const int32_t *xsum, int tokens,
                   float *out, bool residual, hipStream_t s) {
     rk_device *d = m->d;
-    const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
+    const int D = m->dim, K = m->topk, E = m->experts;
     if (tokens <= 0) return RK_OK;
     if (tokens > sc.cap) return fail(d, RK_ERR_ARGS, "moe: %d tokens beyond the scratch's %d", tokens, sc.cap);
     bool ok;
@@ -420,6 +558,12 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
         a.xsum = xsum;
         ProfScope p(d, s, "moe_router");
         ok = launch_fused(kFmtQ8, kProGlobal, kEpStore, a, d->cu, s);
+    } else if (tokens <= kRouterMaxT && D <= 32 * 8 * kRouterBpl) {
+        ProfScope p(d, s, "moe_router");
+        RK_LAUNCH(moe_router_rows_kernel, dim3((unsigned)((E + 3) / 4)), dim3(256),
+                  (size_t)tokens * D + (size_t)tokens * (D / 32) * 4, s, m->router->w, m->router->scales, E, D, qx,
+                  xs, tokens, sc.logits);
+        ok = true;
     } else {
         MmArgs a{};
         a.seg[0] = MatSeg{m->router->w, m->router->scales, sc.logits, m->router->rows};
@@ -437,12 +581,24 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
         ProfScope p(d, s, "moe_route");
         RK_LAUNCH(moe_route_kernel, dim3(tokens), dim3(64), (size_t)E * 4, s, sc.logits, E, K, sc.sel, sc.wsel);
     }
-    const int npairs = tokens * K;
-    const int groups = std::min(E, npairs);  // launched; those past the selected count exit
     {
         ProfScope p(d, s, "moe_group");
-        RK_LAUNCH(moe_group_kernel, dim3(1), dim3(1024), 0, s, sc.sel, npairs, E, sc.gcap, sc.grp);
+        const int npairs = tokens * K;
+        if (npairs <= kGroupFastPairs && E <= 1024)
+            RK_LAUNCH(moe_group_fast_kernel, dim3(1), dim3(1024), 0, s, sc.sel, npairs, E, sc.gcap, sc.grp);
+        else
+            RK_LAUNCH(moe_group_kernel, dim3(1), dim3(1024), npairs <= kGroupLdsPairs ? (size_t)npairs * 4 : 0, s,
+                      sc.sel, npairs, E, sc.gcap, sc.grp);
     }
+    return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s);
+}
+
+// The experts' products and sum after the routing (grouping in sc.grp).
+static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, int tokens,
+                               float *out, bool residual, hipStream_t s) {
+    rk_device *d = m->d;
+    const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
+    const int groups = std::min(E, tokens * K);  // launched; those past the selected count exit
     {
         ProfScope p(d, s, "moe_up");
         RK_LAUNCH(moe_up_kernel, dim3((unsigned)groups, (unsigned)(H / 32)), dim3(512), 0, s, m->w1, m->s1, m->w3,
@@ -461,6 +617,21 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(d, e, "moe launch");
     return RK_OK;
+}
+
+int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *norm_w, float recip_n, float eps,
+                  int tokens, int8_t *qx, float *xs, int32_t *xsum, float *out, bool residual, hipStream_t s) {
+    rk_device *d = m->d;
+    if (tokens <= 0) return RK_OK;
+    if (tokens > sc.cap) return fail(d, RK_ERR_ARGS, "moe: %d tokens beyond the scratch's %d", tokens, sc.cap);
+    if (norm_w) {
+        ProfScope p(d, s, "norm_quant");
+        launch_norm_quant(x, m->dim, norm_w, recip_n, eps, qx, xs, xsum, s, tokens);
+    } else {
+        ProfScope p(d, s, "quantize_acts");
+        launch_quantize_acts(x, (int64_t)tokens * m->dim, qx, xs, xsum, s);
+    }
+    return enqueue_moe_q(m, sc, qx, xs, xsum, tokens, out, residual, s);
 }
 
 // The standalone calls' scratch for up to `tokens` inputs (grown: a call
@@ -502,11 +673,7 @@ static int moe_own_scratch(rk_moe *m, int tokens) {
 // A standalone call: the input quantized into the handle's scratch, then
 // the feed-forward into d_y.
 static int enqueue_moe(rk_moe *m, const float *d_xn, int tokens, float *d_y, hipStream_t s) {
-    {
-        ProfScope p(m->d, s, "quantize_acts");
-        launch_quantize_acts(d_xn, (int64_t)tokens * m->dim, m->qx, m->xs, m->xsum, s);
-    }
-    return enqueue_moe_q(m, m->sc, m->qx, m->xs, m->xsum, tokens, d_y, false, s);
+    return enqueue_moe_x(m, m->sc, d_xn, nullptr, 0.0f, 0.0f, tokens, m->qx, m->xs, m->xsum, d_y, false, s);
 }
 
 }  // namespace rk

@@ -230,13 +230,10 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
     if (L.moe) {
         // a mixture of experts: its input RMSNorm_ffn(x) quantized into qb;
         // the experts' sum goes into the residual, x = Canonical(x + y)
-        {
-            ProfScope p(d, st, "norm_quant");
-            launch_norm_quant(s->x, c.dim, D.rms_ffn, c.recip_dim, c.norm_eps, s->qb.qx, s->qb.xs, s->qb.xsum, st);
-        }
         MoeScratch sc;
         moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
-        return enqueue_moe_q(L.moe, sc, s->qb.qx, s->qb.xs, s->qb.xsum, 1, s->x, true, st);
+        return enqueue_moe_x(L.moe, sc, s->x, D.rms_ffn, c.recip_dim, c.norm_eps, 1, s->qb.qx, s->qb.xs, s->qb.xsum,
+                             s->x, true, st);
     }
     // W1 row r and W3 row r interleaved (logical rows); h leaves quantized in qa.
     rk_matrix *w13[2] = {L.w1, L.w3};
@@ -499,15 +496,17 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, const
     a.x = s->bx;
     a.ldx = c.dim;
     if ((rc = batch_product(s, st, "wo", &L.wo, 1, kEpAdd, a))) return rc;
-    batch_norm(s, st, D.rms_ffn, n);
-    if (L.moe) {  // the experts' sums into the residual rows, x = Canonical(x + y)
+    if (L.moe) {  // RMSNorm_ffn(x) into bqb, and the experts' sums into the residual rows, x = Canonical(x + y)
         MoeScratch sc;
         moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
-        if ((rc = enqueue_moe_q(L.moe, sc, s->bqb.qx, s->bqb.xs, s->bqb.xsum, n, s->bx, true, st))) return rc;
+        if ((rc = enqueue_moe_x(L.moe, sc, s->bx, D.rms_ffn, c.recip_dim, c.norm_eps, n, s->bqb.qx, s->bqb.xs,
+                                s->bqb.xsum, s->bx, true, st)))
+            return rc;
         batch_norm(s, st, next_norm, n);
         hipError_t e = hipGetLastError();
         return e == hipSuccess ? RK_OK : hip_fail(d, e, "stage launch");
     }
+    batch_norm(s, st, D.rms_ffn, n);
     rk_matrix *w13[2] = {L.w1, L.w3};
     a = base;
     a.qx_out = s->bqa.qx;
