@@ -99,8 +99,53 @@ __device__ __forceinline__ void wave_rows_q8_multi(const uint8_t *const (&w)[NR]
         }
 }
 
-// The router's product for a batch of up to kRouterMaxT tokens whose codes
-// fit kRouterLds: wave w of workgroup b takes row 4b + w (MatVecQ8's bits)
+// ---- Row dots eight lanes a row: lane l of an aligned group of eight keeps
+// MatVecQ8's running sum l (blocks l, l+8, ... in order, from +0) of one
+// row, from the row's blocks it holds in registers; tree8 then forms
+// ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)) with no other lane exchange. ----
+
+// The row's blocks rl + 8m, m < BPL (clamped into the row: those past it
+// are never summed).
+template <int BPL>
+__device__ __forceinline__ void lane_row_load(int4 (&c0)[BPL], int4 (&c1)[BPL], float (&sw)[BPL], const uint8_t *row,
+                                              const float *rs, int nb, int rl) {
+#pragma unroll
+    for (int m = 0; m < BPL; m++) {
+        const int b = min(rl + 8 * m, nb - 1);
+        c0[m] = load_stream16(row + 32 * b);
+        c1[m] = load_stream16(row + 32 * b + 16);
+        sw[m] = rs[b];
+    }
+}
+
+// Running sum rl of the held row with one input (xq: codes, xsc: block
+// scales): exact block sums, times (row scale · input scale), in order.
+template <int BPL>
+__device__ __forceinline__ float lane_running_sum(const int4 (&c0)[BPL], const int4 (&c1)[BPL], const float (&sw)[BPL],
+                                                  const int8_t *xq, const float *xsc, int nb, int rl) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < BPL; m++) {
+        const int b = rl + 8 * m;
+        if (b < nb) {
+            const int4 *xp = reinterpret_cast<const int4 *>(xq + 32 * b);
+            const int sum = dot16(c1[m], xp[1], dot16(c0[m], xp[0], 0));
+            acc += (float)sum * (sw[m] * xsc[b]);
+        }
+    }
+    return acc;
+}
+
+// The fixed tree over the group's eight running sums, valid in all eight
+// lanes (float addition commutes, so each lane's pairing gives the same bits).
+__device__ __forceinline__ float tree8(float acc) {
+    acc = acc + dppf_x1(acc);
+    acc = acc + dppf_x2(acc);
+    return acc + __int_as_float(dpp_mirror8(__float_as_int(acc)));
+}
+
+// The router's product for a batch of up to kRouterMaxT tokens (their codes
+// and scales in LDS): wave w of workgroup b takes row 4b + w (MatVecQ8's bits)
 // for every token, eight tokens a pass; lane l keeps, for token l/8 of the
 // pass, running sum l mod 8 (blocks l mod 8, +8, ... in order), so the sums
 // need no lane exchanges until the fixed tree ((0+1)+(2+3))+((4+5)+(6+7)).
@@ -122,13 +167,7 @@ __global__ __launch_bounds__(256) void moe_router_rows_kernel(const uint8_t *rw,
     const float *rs = rws + (int64_t)row * nb;
     int4 c0[kRouterBpl], c1[kRouterBpl];
     float sw[kRouterBpl];
-#pragma unroll
-    for (int m = 0; m < kRouterBpl; m++) {
-        const int b = min(rl + 8 * m, nb - 1);  // blocks past the row are never summed
-        c0[m] = load_stream16(rp + 32 * b);
-        c1[m] = load_stream16(rp + 32 * b + 16);
-        sw[m] = rs[b];
-    }
+    lane_row_load<kRouterBpl>(c0, c1, sw, rp, rs, nb, rl);
     for (int i = tid; i < (tokens * dim) >> 4; i += 256)
         reinterpret_cast<int4 *>(sq)[i] = reinterpret_cast<const int4 *>(qx)[i];
     for (int i = tid; i < tokens * nb; i += 256) sxs[i] = xs[i];
@@ -136,21 +175,7 @@ __global__ __launch_bounds__(256) void moe_router_rows_kernel(const uint8_t *rw,
     if (rowi >= experts) return;  // uniform over the wave
     for (int t0 = 0; t0 < tokens; t0 += 8) {
         const int t = min(t0 + tg, tokens - 1);
-        const int8_t *xq = sq + t * dim;
-        const float *xsc = sxs + t * nb;
-        float acc = 0.0f;
-#pragma unroll
-        for (int m = 0; m < kRouterBpl; m++) {
-            const int b = rl + 8 * m;
-            if (b < nb) {
-                const int4 *xp = reinterpret_cast<const int4 *>(xq + 32 * b);
-                const int sum = dot16(c1[m], xp[1], dot16(c0[m], xp[0], 0));
-                acc += (float)sum * (sw[m] * xsc[b]);
-            }
-        }
-        acc = acc + dppf_x1(acc);
-        acc = acc + dppf_x2(acc);
-        acc = acc + __int_as_float(dpp_mirror8(__float_as_int(acc)));
+        const float acc = tree8(lane_running_sum<kRouterBpl>(c0, c1, sw, sq + t * dim, sxs + t * nb, nb, rl));
         if (rl == 0 && t0 + tg < tokens) logits[(int64_t)(t0 + tg) * experts + row] = acc;
     }
 }
@@ -487,6 +512,126 @@ __global__ __launch_bounds__(256) void moe_down_kernel(const uint8_t *const *w2,
     }
 }
 
+// The same W1/W3 and W2 products for inputs up to 2048 wide, eight lanes a
+// row dot: a wave's rows are loaded once, up front (BPL blocks a lane), and
+// the group's inputs are staged in LDS kExpTok at a time. moe_up8: wave w
+// takes hidden rows 4w..4w+3 of the workgroup's 32 (W1 of row q in lanes
+// 16q..16q+7, W3 in 16q+8..16q+15; the W3 dot moves beside the W1 dot by
+// one DPP row shift). moe_down8: wave w takes W2 rows 8w..8w+7 of the
+// workgroup's 32.
+constexpr int kExpTok = 16;
+
+__device__ __forceinline__ float row_shl8(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x108, 0xF, 0xF, false));
+}
+
+template <int BPL>
+__global__ __launch_bounds__(512) void moe_up8_kernel(const uint8_t *const *w1, const float *const *s1,
+                                                      const uint8_t *const *w3, const float *const *s3,
+                                                      const int32_t *grp, int gcap, const float *wsel, int k,
+                                                      const int8_t *qx, const float *xs, int dim, int hidden,
+                                                      int8_t *hq, float *hs, int32_t *hsum) {
+    extern __shared__ __align__(16) char ulds[];
+    const int g = blockIdx.x;
+    if (g >= grp[0]) return;  // uniform
+    const int e = grp[1 + g], start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
+    const int32_t *list = grp + 1 + 3 * gcap + start;
+    const int nb = dim >> 5;
+    int8_t *sq = reinterpret_cast<int8_t *>(ulds);                        // [kExpTok][dim] codes
+    float *sxs = reinterpret_cast<float *>(ulds + kExpTok * dim);          // [kExpTok][nb] scales
+    float *sh = sxs + kExpTok * nb;                                        // [kExpTok][32] h
+    int *spair = reinterpret_cast<int *>(sh + kExpTok * 32);               // [kExpTok] pairs
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rg = lane >> 3, rl = lane & 7, q = rg >> 1;
+    const int j = blockIdx.y * 32 + 4 * wave + q;  // hidden is a multiple of 32
+    const bool w3row = rg & 1;
+    int4 c0[BPL], c1[BPL];
+    float sw[BPL];
+    lane_row_load<BPL>(c0, c1, sw, (w3row ? w3[e] : w1[e]) + (int64_t)j * dim,
+                       (w3row ? s3[e] : s1[e]) + (int64_t)j * nb, nb, rl);
+    const int n16 = dim >> 4;
+    for (int p0 = 0; p0 < count; p0 += kExpTok) {
+        const int np = min(kExpTok, count - p0);
+        if (tid < np) spair[tid] = list[p0 + tid];
+        __syncthreads();
+        for (int i = tid; i < np * n16; i += 512) {
+            const int pi = i / n16, off = i - pi * n16;
+            reinterpret_cast<int4 *>(sq)[i] = reinterpret_cast<const int4 *>(qx + (int64_t)(spair[pi] / k) * dim)[off];
+        }
+        for (int i = tid; i < np * nb; i += 512) {
+            const int pi = i / nb, b = i - pi * nb;
+            sxs[i] = xs[(int64_t)(spair[pi] / k) * nb + b];
+        }
+        __syncthreads();
+        for (int pi = 0; pi < np; pi++) {
+            const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq + pi * dim, sxs + pi * nb, nb, rl));
+            const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
+            if ((lane & 15) == 0) sh[pi * 32 + 4 * wave + q] = wsel[spair[pi]] * silu_mul(v, v3);
+        }
+        __syncthreads();
+        // each pair's block of h: wave w takes pairs w, w+8, ...; lanes 0-7
+        // four values each (every lane of the wave calls the quantizer)
+        for (int pi = wave; pi < np; pi += 8) {
+            const float4 v4 = reinterpret_cast<const float4 *>(sh + pi * 32)[min(lane, 7)];
+            float d;
+            int cs;
+            const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
+            const int64_t base = (int64_t)spair[pi] * hidden + blockIdx.y * 32;
+            if (lane < 8) {
+                reinterpret_cast<uint32_t *>(hq + base)[lane] = pk;
+                if (lane == 0) {
+                    hs[base >> 5] = d;
+                    hsum[base >> 5] = cs;
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int BPL>
+__global__ __launch_bounds__(256) void moe_down8_kernel(const uint8_t *const *w2, const float *const *s2,
+                                                        const int32_t *grp, int gcap, const int8_t *hq, const float *hs,
+                                                        int dim, int hidden, float *o) {
+    extern __shared__ __align__(16) char dlds[];
+    const int g = blockIdx.x;
+    if (g >= grp[0]) return;  // uniform
+    const int e = grp[1 + g], start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
+    const int32_t *list = grp + 1 + 3 * gcap + start;
+    const int nb = hidden >> 5;
+    int8_t *sq = reinterpret_cast<int8_t *>(dlds);                        // [kExpTok][hidden] codes
+    float *sxs = reinterpret_cast<float *>(dlds + kExpTok * hidden);       // [kExpTok][nb] scales
+    int *spair = reinterpret_cast<int *>(sxs + kExpTok * nb);              // [kExpTok] pairs
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rg = lane >> 3, rl = lane & 7;
+    const int i = blockIdx.y * 32 + 8 * wave + rg;
+    int4 c0[BPL], c1[BPL];
+    float sw[BPL];
+    lane_row_load<BPL>(c0, c1, sw, w2[e] + (int64_t)min(i, dim - 1) * hidden,
+                       s2[e] + (int64_t)min(i, dim - 1) * nb, nb, rl);
+    const int n16 = hidden >> 4;
+    for (int p0 = 0; p0 < count; p0 += kExpTok) {
+        const int np = min(kExpTok, count - p0);
+        if (tid < np) spair[tid] = list[p0 + tid];
+        __syncthreads();
+        for (int u = tid; u < np * n16; u += 256) {
+            const int pi = u / n16, off = u - pi * n16;
+            reinterpret_cast<int4 *>(sq)[u] = reinterpret_cast<const int4 *>(hq + (int64_t)spair[pi] * hidden)[off];
+        }
+        for (int u = tid; u < np * nb; u += 256) {
+            const int pi = u / nb, b = u - pi * nb;
+            sxs[u] = hs[(int64_t)spair[pi] * nb + b];
+        }
+        __syncthreads();
+        for (int pi = 0; pi < np; pi++) {
+            const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq + pi * hidden, sxs + pi * nb, nb, rl));
+            if (rl == 0 && i < dim) o[(int64_t)spair[pi] * dim + i] = v;
+        }
+        __syncthreads();
+    }
+}
+
 // y_t = Σ o over the token's experts in ascending index, from +0; out_t = y_t,
 // or Canonical(out_t + y_t) (the layer's residual, model.go:608-610).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, int k, const float *o, int dim,
@@ -601,13 +746,39 @@ static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx
     const int groups = std::min(E, tokens * K);  // launched; those past the selected count exit
     {
         ProfScope p(d, s, "moe_up");
-        RK_LAUNCH(moe_up_kernel, dim3((unsigned)groups, (unsigned)(H / 32)), dim3(512), 0, s, m->w1, m->s1, m->w3,
-                  m->s3, sc.grp, sc.gcap, sc.wsel, K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
+        const int bpl = (D / 32 + 7) / 8;  // blocks of a W1/W3 row per lane
+        const size_t lds = (size_t)kExpTok * (D + (D / 32) * 4 + 32 * 4 + 4);
+        const dim3 grid((unsigned)groups, (unsigned)(H / 32));
+        if (bpl <= 2)
+            RK_LAUNCH(moe_up8_kernel<2>, grid, dim3(512), lds, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel,
+                      K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
+        else if (bpl <= 4)
+            RK_LAUNCH(moe_up8_kernel<4>, grid, dim3(512), lds, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel,
+                      K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
+        else if (bpl <= 8)
+            RK_LAUNCH(moe_up8_kernel<8>, grid, dim3(512), lds, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel,
+                      K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
+        else
+            RK_LAUNCH(moe_up_kernel, grid, dim3(512), 0, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel, K, qx,
+                      xs, D, H, sc.hq, sc.hs, sc.hsum);
     }
     {
         ProfScope p(d, s, "moe_down");
-        RK_LAUNCH(moe_down_kernel, dim3((unsigned)groups, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2, m->s2,
-                  sc.grp, sc.gcap, sc.hq, sc.hs, D, H, sc.o);
+        const int bpl = (H / 32 + 7) / 8;  // blocks of a W2 row per lane
+        const size_t lds = (size_t)kExpTok * (H + (H / 32) * 4 + 4);
+        const dim3 grid((unsigned)groups, (unsigned)((D + 31) / 32));
+        if (bpl <= 2)
+            RK_LAUNCH(moe_down8_kernel<2>, grid, dim3(256), lds, s, m->w2, m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
+                      sc.o);
+        else if (bpl <= 4)
+            RK_LAUNCH(moe_down8_kernel<4>, grid, dim3(256), lds, s, m->w2, m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
+                      sc.o);
+        else if (bpl <= 8)
+            RK_LAUNCH(moe_down8_kernel<8>, grid, dim3(256), lds, s, m->w2, m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
+                      sc.o);
+        else
+            RK_LAUNCH(moe_down_kernel, dim3((unsigned)groups, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2,
+                      m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H, sc.o);
     }
     {
         ProfScope p(d, s, "moe_combine");
