@@ -21,7 +21,8 @@ class GPUStage:
             up = {}
             for n in ("wq", "wk", "wv", "wo", "w1", "w2", "w3"):
                 m = getattr(ly, n)
-                up[n] = dev.upload(m.kind, m.rows, m.cols, m.q, m.scales)
+                w = {rkhip.F32: m.f32, rkhip.BF16: m.bf16}.get(m.kind, m.q)  # the Matrix's storage (model.go:133-148)
+                up[n] = dev.upload(m.kind, m.rows, m.cols, w, m.scales)
             self.mats.append(up)
             # gpustage.go vecLayout (model.go:297-313)
             allv, offs, at = [], {}, 0

@@ -1,8 +1,9 @@
 """A model's layers on the GPU give the CPU oracle's bits (the reference's
 TestGPUStagesMatchCPU, internal/llm/gpu_test.go:32-111): three architecture
 variants (Qwen2 QKV bias; Qwen3 QK-norm with head_dim 32, theta 1e6, eps
-1e-6; no GQA), each weight type, a 70-token prompt (two submissions) and six
-decode steps, every activation compared bitwise."""
+1e-6; no GQA), each weight type the reference runs there (float32 "",
+bf16, q8_0, q4_m, q4_0), a 70-token prompt (two submissions) and six decode
+steps, every activation compared bitwise."""
 import numpy as np
 import pytest
 
@@ -20,7 +21,7 @@ CONFIGS = [
 
 
 @pytest.mark.parametrize("ci", range(len(CONFIGS)))
-@pytest.mark.parametrize("dtype", ["q8_0", "q4_m", "q4_0"])
+@pytest.mark.parametrize("dtype", ["", "bf16", "q8_0", "q4_m", "q4_0"])
 def test_gpu_stages_match_cpu(dev, ci, dtype):
     c = Config(**{**CONFIGS[ci].__dict__, "dtype": dtype})
     m = Model(c, random_model(c, 9))
