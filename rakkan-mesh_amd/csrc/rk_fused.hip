@@ -613,6 +613,36 @@ bool launch_fused(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s)
 // (s_j+16 + s_j+24) by two DPP exchanges and lane 0 the final tree.
 constexpr int kScoreTile = 64;
 
+// Dot32(q_h, k_t) of head size hs (a multiple of 8; all loads issued at once
+// when hs is a compile-time constant) by the quad of lanes `sub` = lane & 3:
+// the result is in the quad's lane 0.
+__device__ __forceinline__ float quad_dot32(const float *qh, const float *kt, int sub, int hs) {
+    float s[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) s[k] = 0.0f;
+    for (int base = 8 * sub; base < hs; base += 32) {
+        const float4 k0 = *reinterpret_cast<const float4 *>(kt + base);
+        const float4 k1 = *reinterpret_cast<const float4 *>(kt + base + 4);
+        const float4 q0 = *reinterpret_cast<const float4 *>(qh + base);
+        const float4 q1 = *reinterpret_cast<const float4 *>(qh + base + 4);
+        s[0] += q0.x * k0.x;
+        s[1] += q0.y * k0.y;
+        s[2] += q0.z * k0.z;
+        s[3] += q0.w * k0.w;
+        s[4] += q1.x * k1.x;
+        s[5] += q1.y * k1.y;
+        s[6] += q1.z * k1.z;
+        s[7] += q1.w * k1.w;
+    }
+    float e[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float u = s[k] + dppf_x1(s[k]);  // lane 0: s_j + s_j+8; lane 2: s_j+16 + s_j+24
+        e[k] = u + dppf_x2(u);                 // lane 0: e_j
+    }
+    return ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+}
+
 template <int HS>  // head size when fixed at compile time (all loads issued at once), else 0
 __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const float *keys, float *att,
                                                          int32_t att_stride, const int32_t *ctl, AttBatch bt,
@@ -631,37 +661,25 @@ __global__ __launch_bounds__(256) void att_scores_kernel(const float *q, const f
     const bool valid = t < T;
     const float *kt = keys + (int64_t)(valid ? t : t0) * kv_dim + (int64_t)g * hs;
     const float *qh = q + (int64_t)h * hs;
-    float s[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) s[k] = 0.0f;
+    float dot;
     if ((hs & 7) == 0 && (kv_dim & 3) == 0) {
-        for (int base = 8 * sub; base < hs; base += 32) {  // unrolled when HS is fixed
-            const float4 k0 = *reinterpret_cast<const float4 *>(kt + base);
-            const float4 k1 = *reinterpret_cast<const float4 *>(kt + base + 4);
-            const float4 q0 = *reinterpret_cast<const float4 *>(qh + base);
-            const float4 q1 = *reinterpret_cast<const float4 *>(qh + base + 4);
-            s[0] += q0.x * k0.x;
-            s[1] += q0.y * k0.y;
-            s[2] += q0.z * k0.z;
-            s[3] += q0.w * k0.w;
-            s[4] += q1.x * k1.x;
-            s[5] += q1.y * k1.y;
-            s[6] += q1.z * k1.z;
-            s[7] += q1.w * k1.w;
-        }
+        dot = quad_dot32(qh, kt, sub, hs);
     } else {
+        float s[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) s[k] = 0.0f;
         for (int base = 8 * sub; base < hs; base += 32)
 #pragma unroll
             for (int k = 0; k < 8; k++)
                 if (base + k < hs) s[k] += qh[base + k] * kt[base + k];
-    }
-    float e[8];
+        float e[8];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
-        const float u = s[k] + dppf_x1(s[k]);  // lane 0: s_j + s_j+8; lane 2: s_j+16 + s_j+24
-        e[k] = u + dppf_x2(u);                 // lane 0: e_j
+        for (int k = 0; k < 8; k++) {
+            const float u = s[k] + dppf_x1(s[k]);
+            e[k] = u + dppf_x2(u);
+        }
+        dot = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
     }
-    const float dot = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
     if (sub == 0 && valid) att[(int64_t)h * att_stride + t] = dot * inv_sqrt;
 }
 

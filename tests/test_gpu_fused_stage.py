@@ -246,6 +246,18 @@ def test_generation_long_context(dev, case):
     check_generation(dev, m, prompt, 10, ctx)
 
 
+def test_generation_head128_to_context_end(dev):
+    """Head size 128 (the 8B, Qwen and Qwen3 heads) decoding at positions up
+    to the last of a 1024-position context: the largest context whose value
+    slices stay in registers (four product chunks) and eight score tiles,
+    every logit bitwise."""
+    c = Config(dim=256, hidden=384, layers=2, heads=4, kv_heads=2, vocab=64, seq_len=1024, head_dim=128,
+               dtype="q8_0")
+    m = Model(c, random_model(c, 7))
+    prompt = [int(t) for t in np.random.default_rng(4).integers(0, c.vocab, 1014)]
+    check_generation(dev, m, prompt, 10, 1024)
+
+
 def forward_one_by_one(st, xs, pos0):
     return np.stack([st.forward(xs[t], pos0 + t)[0] for t in range(len(xs))])
 
