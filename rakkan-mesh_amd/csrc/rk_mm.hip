@@ -195,32 +195,66 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) acc[ti][tj][k][i] = 0.0f;
 
-    // block k of the staged chunk into running sum k
-    auto kstep = [&](const MmStage &S, int k) __attribute__((always_inline)) {
+    // Block k of the staged chunk in three steps: its operand reads from LDS
+    // (kload), its MFMAs (kmma), its terms into running sum k (kterms). A
+    // chunk runs them two blocks apart: block k+2's reads and block k+1's
+    // MFMAs are issued before block k's terms, so neither the LDS nor the
+    // matrix results are waited for.
+    struct KOps {
         long fa[TI], fb[TJ];
-#pragma unroll
-        for (int ti = 0; ti < TI; ti++) fa[ti] = *reinterpret_cast<const long *>(&S.w[rb(ti) + ln][k * 32 + 8 * lq]);
-#pragma unroll
-        for (int tj = 0; tj < TJ; tj++) fb[tj] = *reinterpret_cast<const long *>(&S.x[tb(tj) + ln][k * 32 + 8 * lq]);
+        float4 wsv[TI];
+        float xsv[TJ];
+    };
+    struct KRes {
         v4i d[TI][TJ];
+        float4 wsv[TI];
+        float xsv[TJ];
+    };
+    auto kload = [&](const MmStage &S, int k, KOps &o) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++) o.fa[ti] = *reinterpret_cast<const long *>(&S.w[rb(ti) + ln][k * 32 + 8 * lq]);
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) o.fb[tj] = *reinterpret_cast<const long *>(&S.x[tb(tj) + ln][k * 32 + 8 * lq]);
+#pragma unroll
+        for (int ti = 0; ti < TI; ti++) o.wsv[ti] = *reinterpret_cast<const float4 *>(&S.ws[k][rb(ti) + 4 * lq]);
+#pragma unroll
+        for (int tj = 0; tj < TJ; tj++) o.xsv[tj] = S.xs[k][tb(tj) + ln];
+    };
+    auto kmma = [&](const KOps &o, KRes &r) __attribute__((always_inline)) {
 #pragma unroll
         for (int ti = 0; ti < TI; ti++)
 #pragma unroll
             for (int tj = 0; tj < TJ; tj++)
-                d[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(fa[ti], fb[tj], v4i{0, 0, 0, 0}, 0, 0, 0);
-        float4 wsv[TI];
-        float xsv[TJ];
+                r.d[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x32_i8(o.fa[ti], o.fb[tj], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-        for (int ti = 0; ti < TI; ti++) wsv[ti] = *reinterpret_cast<const float4 *>(&S.ws[k][rb(ti) + 4 * lq]);
+        for (int ti = 0; ti < TI; ti++) r.wsv[ti] = o.wsv[ti];
 #pragma unroll
-        for (int tj = 0; tj < TJ; tj++) xsv[tj] = S.xs[k][tb(tj) + ln];
+        for (int tj = 0; tj < TJ; tj++) r.xsv[tj] = o.xsv[tj];
+    };
+    auto kterms = [&](const KRes &r, int k) __attribute__((always_inline)) {
 #pragma unroll
         for (int ti = 0; ti < TI; ti++) {
-            const float w4[4] = {wsv[ti].x, wsv[ti].y, wsv[ti].z, wsv[ti].w};
+            const float w4[4] = {r.wsv[ti].x, r.wsv[ti].y, r.wsv[ti].z, r.wsv[ti].w};
 #pragma unroll
             for (int tj = 0; tj < TJ; tj++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[ti][tj][k][i] += (float)d[ti][tj][i] * (w4[i] * xsv[tj]);
+                for (int i = 0; i < 4; i++) acc[ti][tj][k][i] += (float)r.d[ti][tj][i] * (w4[i] * r.xsv[tj]);
+        }
+    };
+    // blocks 0..n-1 of a staged chunk, pipelined as above
+    auto chunk = [&](const MmStage &S, int n) __attribute__((always_inline)) {
+        KOps o[2];
+        KRes r[2];
+        kload(S, 0, o[0]);
+        if (n > 1) kload(S, 1, o[1]);
+        kmma(o[0], r[0]);
+#pragma unroll
+        for (int k = 0; k < kMmKB; k++) {
+            if (k + 2 < n) kload(S, k + 2, o[k & 1]);
+            if (k + 1 < n) kmma(o[(k + 1) & 1], r[(k + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k < n) kterms(r[k & 1], k);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -235,19 +269,11 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
         // the next chunk's loads (past the last chunk they re-read it and
         // fill the idle buffer, which nothing reads)
         stage_load((ci + 1) * kMmKB);
-        const MmStage &S = stg[ci & 1];
-#pragma unroll
-        for (int k = 0; k < kMmKB; k++) kstep(S, k);
+        chunk(stg[ci & 1], kMmKB);
         stage_store(stg[(ci + 1) & 1]);
         __syncthreads();
     }
-    if (nfull < nchunks) {
-        const MmStage &S = stg[nfull & 1];
-        const int c0 = nfull * kMmKB;
-#pragma unroll
-        for (int k = 0; k < kMmKB; k++)
-            if (c0 + k < nb) kstep(S, k);  // absent blocks are skipped, not added as zeros
-    }
+    if (nfull < nchunks) chunk(stg[nfull & 1], nb - nfull * kMmKB);  // absent blocks are skipped, not added as zeros
 
     // ---- results: the fixed tree of the eight running sums, then the
     // epilogue per (row, token) ----
