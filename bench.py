@@ -742,12 +742,16 @@ def moe_bench(dev, rkhip, args):
 
             def run(n):
                 st.seqs_run(n)
+        if args.eager:  # one launch at a time (for tools that cannot follow graph replays)
+            dev.profile_start()
         start()
         run(2)  # records the graph, touches every weight
         start()
         t0 = time.perf_counter()
         run(steps - 1)
         el = time.perf_counter() - t0
+        if args.eager:
+            dev.profile_stop()
         ms_step = el / (steps - 1) * 1e3
         # per-kernel times: eager launches stamped one by one, after one
         # unstamped eager step (the first eager launches pay one-time host

@@ -559,8 +559,8 @@ struct StreamInst {
 
 #define RK_SI(F, P, E, K, U, C) {F, P, E, K, U, C, stream_kernel<F, P, E, K, U, C>}
 
-// The widths of the configurations this build is measured on (Q8: 4096 and
-// 14336 columns, C = 4 and 14; Q4: 3584/4096 and 18944 columns, C = 2 and
+// The widths of the configurations this build is measured on (Q8: 2048, 4096 and
+// 14336 columns, C = 2, 4 and 14; Q4: 3584/4096 and 18944 columns, C = 2 and
 // 10); other widths take fused_kernel.
 const StreamInst kStreamInst[] = {
     RK_SI(kFmtQ8, kProQuant, kEpStore, 1, 4, 4),
@@ -586,6 +586,9 @@ const StreamInst kStreamInst[] = {
     RK_SI(kFmtQ4, kProGlobal, kEpAddCanon, 1, 5, 10),
     RK_SI(kFmtQ4, kProQuant, kEpStore, 2, 4, 2),
     RK_SI(kFmtQ4, kProGlobal, kEpStore, 2, 4, 2),
+    // 2048 columns (config 5: QKV with the attention RMSNorm, the router)
+    RK_SI(kFmtQ8, kProNorm, kEpStore, 2, 4, 2),
+    RK_SI(kFmtQ8, kProGlobal, kEpStore, 2, 4, 2),
 };
 #undef RK_SI
 
