@@ -1245,16 +1245,36 @@ void launch_embed_rows(const uint8_t *w, const float *scales, bool q4, const int
 // logit keeps index 0, as the reference's `>` scan does), writes it as the
 // token at pos[z]+1 when that position is past the prompt, and advances
 // pos[z].
-__global__ __launch_bounds__(256) void seqs_advance_kernel(const float *logits, int64_t vocab, int32_t *pos,
-                                                           const int32_t *prompt, int32_t *tokens, int64_t tok_stride,
-                                                           int32_t tokens_len) {
-    __shared__ float s_v[4];
-    __shared__ int s_i[4];
+__global__ __launch_bounds__(1024) void seqs_advance_kernel(const float *logits, int64_t vocab, int32_t *pos,
+                                                            const int32_t *prompt, int32_t *tokens,
+                                                            int64_t tok_stride, int32_t tokens_len) {
+    __shared__ float s_v[16];
+    __shared__ int s_i[16];
     const int z = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *row = logits + (int64_t)z * vocab;
     float bv = 0.0f;
     int bi = -1;
-    for (int64_t i = threadIdx.x; i < vocab; i += 256) {
+    // eight 16-byte loads in flight a thread (a position past the row
+    // re-reads the last group: merging an element twice changes nothing)
+    const int64_t n4 = (reinterpret_cast<uintptr_t>(row) & 15) == 0 ? vocab >> 2 : 0;
+    const float4 *r4 = reinterpret_cast<const float4 *>(row);
+    for (int64_t b = threadIdx.x; b < n4; b += 1024 * 8) {
+        float4 v[8];
+        int64_t g[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            g[u] = min(b + 1024 * u, n4 - 1);
+            v[u] = r4[g[u]];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if (e[c] == e[c]) argmax_merge(bv, bi, e[c], (int)(4 * g[u] + c));
+        }
+    }
+    for (int64_t i = 4 * n4 + threadIdx.x; i < vocab; i += 1024) {
         const float v = row[i];
         if (v == v) argmax_merge(bv, bi, v, (int)i);
     }
@@ -1272,7 +1292,7 @@ __global__ __launch_bounds__(256) void seqs_advance_kernel(const float *logits, 
     if (threadIdx.x == 0) {
         float v = 0.0f;
         int i = -1;
-        for (int w = 0; w < 4; w++) argmax_merge(v, i, s_v[w], s_i[w]);
+        for (int w = 0; w < 16; w++) argmax_merge(v, i, s_v[w], s_i[w]);
         if (row[0] != row[0] || i < 0) i = 0;  // a NaN first logit, or every logit NaN
         const int p = pos[z];
         if (p + 1 >= prompt[z] && p + 1 < tokens_len) tokens[(int64_t)z * tok_stride + p + 1] = i;
@@ -1282,7 +1302,7 @@ __global__ __launch_bounds__(256) void seqs_advance_kernel(const float *logits, 
 
 void launch_seqs_advance(const float *logits, int64_t vocab, int seqs, int32_t *pos, const int32_t *prompt,
                          int32_t *tokens, int64_t tok_stride, int32_t tokens_len, hipStream_t s) {
-    RK_LAUNCH(seqs_advance_kernel, dim3(seqs), dim3(256), 0, s, logits, vocab, pos, prompt, tokens, tok_stride,
+    RK_LAUNCH(seqs_advance_kernel, dim3(seqs), dim3(1024), 0, s, logits, vocab, pos, prompt, tokens, tok_stride,
               tokens_len);
 }
 

@@ -586,9 +586,11 @@ const StreamInst kStreamInst[] = {
     RK_SI(kFmtQ4, kProGlobal, kEpAddCanon, 1, 5, 10),
     RK_SI(kFmtQ4, kProQuant, kEpStore, 2, 4, 2),
     RK_SI(kFmtQ4, kProGlobal, kEpStore, 2, 4, 2),
-    // 2048 columns (config 5: QKV with the attention RMSNorm, the router)
+    // 2048 columns (config 5: QKV with the attention RMSNorm, the router,
+    // the classifier with the head's RMSNorm)
     RK_SI(kFmtQ8, kProNorm, kEpStore, 2, 4, 2),
     RK_SI(kFmtQ8, kProGlobal, kEpStore, 2, 4, 2),
+    RK_SI(kFmtQ8, kProNorm, kEpLogits, 2, 4, 2),
 };
 #undef RK_SI
 
