@@ -418,6 +418,37 @@ int rk_tensor_quantize(rk_device *dev, const float *a, int8_t *q, int64_t n, flo
  * i32 input (dtype RK_TENSOR_F32 / RK_TENSOR_I32; i8 is RK_ERR_ARGS). */
 int rk_tensor_scale(rk_device *dev, int32_t dtype, const void *a, float *out, int64_t n, float k);
 
+/* The tensor ABI across the worker process. The reference runs the tensor
+ * operators in an isolated worker whose seccomp allow-list has read and
+ * write on inherited descriptors but no ioctl or openat
+ * (internal/isolate/seccomp_linux_amd64.go:10-38): the worker cannot open a
+ * GPU. So the node process, which owns the device, serves the worker's
+ * products over a descriptor the worker inherits
+ * (internal/isolate/inherit_unix.go:10). The worker keeps tenMatmul's
+ * checks and gas (internal/sandbox/tensor.go:286-339) and sends the operands;
+ * the node answers with rk_tensor_matmul's result. Wire format (little-
+ * endian): a request is a 56-byte header {u32 'RKTQ', u32 op = 1 (matmul),
+ * i32 dtype, i32 transposed, i64 m, k, n, u64 a_bytes, b_bytes} then a's and
+ * b's bytes; a reply is {u32 'RKTA', i32 status, u64 c_bytes} then, for
+ * status 0, c's bytes. No reference counterpart as code: the reference's
+ * tensor operators run on the worker's CPU.
+ *
+ * Node side: serves requests from fd until the worker closes its end
+ * (returns RK_OK), each answered with rk_tensor_matmul's status and result
+ * (a device error is answered and serving goes on). A malformed request
+ * (magic, op, dtype, a dimension outside 1..2^24, sizes that do not match
+ * the dimensions) is answered with RK_ERR_ARGS and ends serving with
+ * RK_ERR_ARGS; one whose a + b + c bytes pass max_bytes (0: 1 GiB) with
+ * RK_ERR_OOM; a broken stream returns RK_ERR_HIP. Blocking; one call serves
+ * one worker, so several workers take one thread each. */
+int rk_tensor_serve(rk_device *dev, int32_t fd, int64_t max_bytes);
+/* Worker side: one product through the node on fd, with write and read on
+ * fd only (no device, no file opened). Returns the node's status for the
+ * request, RK_ERR_ARGS for arguments the request cannot carry, or
+ * RK_ERR_NO_DEVICE when the stream is closed or broken. */
+int rk_tensor_call(int32_t fd, int32_t dtype, int32_t transposed, int64_t m, int64_t k, int64_t n, const void *a,
+                   const void *b, void *c);
+
 /* internal/gpu/profile.go:82-109 StartProfile / StopProfile. While a
  * profile is active, every kernel the library launches is bracketed by HIP
  * events on the stream it runs on; stop waits for them and returns, per

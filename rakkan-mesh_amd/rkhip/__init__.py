@@ -85,6 +85,8 @@ SIGNATURES = {
     "rk_profile_start": (ctypes.c_int, [P]),
     "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
     "rk_device_launch_floor": (ctypes.c_int, [P, I64, I32, I32, P, P]),
+    "rk_tensor_serve": (ctypes.c_int, [P, I32, I64]),
+    "rk_tensor_call": (ctypes.c_int, [I32, I32, I32, I64, I64, I64, P, P, P]),
     "rk_stage_new": (ctypes.c_int, [P, P, P, I32, P, P, P]),
     "rk_stage_forward": (ctypes.c_int, [P, P, I32, I32]),
     "rk_stage_bytes": (I64, [P]),
@@ -168,6 +170,25 @@ def best(infos):
         if pick is None or rank > pick[0] or (rank == pick[0] and d.memory > pick[1].memory):
             pick = (rank, d)
     return pick[1] if pick else None
+
+
+def tensor_call(fd, a, b, transposed=False):
+    """The worker side of the tensor broker (rk_tensor_call): one matmul /
+    matmul_t through the node on descriptor fd, with reads and writes on fd
+    only (no device opened here). Raises RKError with the node's status."""
+    if a.dtype != b.dtype or a.dtype not in (np.float32, np.int8):
+        raise RKError(-1, "tensor call: f32 or i8 inputs of one type")
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    m, k = a.shape
+    n = b.shape[0] if transposed else b.shape[1]
+    if (b.shape[1] if transposed else b.shape[0]) != k:
+        raise RKError(-1, "tensor call: shapes differ")
+    dt = TENSOR_F32 if a.dtype == np.float32 else TENSOR_I8
+    c = np.empty((m, n), np.float32 if dt == TENSOR_F32 else np.int32)
+    rc = lib().rk_tensor_call(fd, dt, int(bool(transposed)), m, k, n, _ptr(a), _ptr(b), _ptr(c))
+    if rc != RK_OK:
+        raise RKError(rc, "tensor call through the broker")
+    return c
 
 
 def device_bytes_budget(info):
@@ -430,6 +451,11 @@ class Device:
         c = np.empty((m, n), np.float32 if dt == TENSOR_F32 else np.int32)
         self._check(lib().rk_tensor_matmul(self.h, dt, int(bool(transposed)), m, k, n, _ptr(a), _ptr(b), _ptr(c)))
         return c
+
+    def tensor_serve(self, fd, max_bytes=0):
+        """The node side of the tensor broker (rk_tensor_serve): answers the
+        worker's products arriving on descriptor fd until it closes its end."""
+        self._check(lib().rk_tensor_serve(self.h, fd, max_bytes))
 
     def tensor_quantize(self, a, k):
         a = np.ascontiguousarray(a, np.float32)
