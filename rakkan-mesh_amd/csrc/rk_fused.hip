@@ -714,19 +714,23 @@ void launch_att_scores(const float *q, const float *keys, float *att, int32_t at
 // tiles are double-buffered: the other waves write chunk c+1's while wave 0
 // sums chunk c. A slice holding a whole Q8 block is quantized for the next
 // product. The LDS can exceed 64 KiB (gfx950 gives a workgroup 160 KiB).
+// CH positions a chunk: 256, or 128 for contexts of up to 256 positions
+// (half the LDS: four workgroups a CU, for many short sequences at once).
 constexpr int kValSlice = 32;
 constexpr int kValThreads = 256;
 constexpr int kValChunk = 256;
-constexpr int kValPitch = kValChunk + 4;  // floats per element row (odd count of 16-byte units)
+constexpr int kValShortChunk = 128;
+constexpr int kValShortCtx = 256;
+// floats per element row of a product tile (an odd count of 16-byte units)
+constexpr int val_pitch(int ch) { return ch + 4; }
 // thread -> float4 column fq (elements 4fq..4fq+3) and position quad pq
 // (positions 4pq..4pq+3 of a round); rounds cover the chunk
 constexpr int kValQuads = kValThreads / (kValSlice / 4);             // position quads per round
-constexpr int kValRounds = kValChunk / (4 * kValQuads);              // rounds per chunk
 
 // VEC: head size and value-row stride are multiples of 4, so a thread's four
 // elements are one 16-byte load (a separate instance: a run-time choice would
 // be if-converted into four 4-byte loads for every shape).
-template <bool VEC>
+template <bool VEC, int CH>
 __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *att, int32_t att_stride,
                                                                  const float *vals, float *out, const int32_t *ctl,
                                                                  AttBatch bt, int kv_mul, int hs, int kv_dim,
@@ -735,6 +739,8 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
     __shared__ float s_red[kValThreads / 64];
     __shared__ float s_inv;
     float *sa = smem;            // [ctx_pad] scores -> weights
+    constexpr int kValPitch = val_pitch(CH), kValRounds = CH / (4 * kValQuads);
+    static_assert(kValRounds >= 1, "a chunk is whole rounds");
     float *sp = smem + ctx_pad;  // [2][kValSlice][kValPitch] product tiles of two chunks
     const int z = blockIdx.z;  // token of a batch (0 when the position comes from ctl)
     const int T = att_position(ctl, bt, z) + 1;
@@ -818,7 +824,7 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
     // so the other waves write chunk c+1's products while wave 0 sums chunk c.
     float acc = 0.0f;
     int buf = 0;
-    for (int c0 = 0; c0 < T; c0 += kValChunk, buf ^= 1) {
+    for (int c0 = 0; c0 < T; c0 += CH, buf ^= 1) {
         float *tile = sp + buf * (kValSlice * kValPitch);
 #pragma unroll
         for (int r = 0; r < kValRounds; r++) {
@@ -834,9 +840,9 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
             *reinterpret_cast<float4 *>(dst + 3 * kValPitch) =
                 make_float4(a4.x * vr[r][0].w, a4.y * vr[r][1].w, a4.z * vr[r][2].w, a4.w * vr[r][3].w);
         }
-        load_chunk(c0 + kValChunk);  // in flight while this chunk is summed
+        load_chunk(c0 + CH);  // in flight while this chunk is summed
         __syncthreads();
-        const int n = min(kValChunk, T - c0);
+        const int n = min(CH, T - c0);
         if (wave == 0 && lane < kValSlice) acc = lds_chain_sum(tile + lane * kValPitch, n, acc);
     }
     if (wave == 0 && lane < ne) out[(int64_t)h * hs + e0 + lane] = acc;
@@ -1059,23 +1065,23 @@ __global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float 
 static size_t att_values_reg_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + 2 * kValSlice * kVrChunk) * 4; }
 
 // Dynamic LDS of the values kernel for a context of ctx positions.
-static size_t att_values_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + 2 * kValSlice * kValPitch) * 4; }
+static size_t att_values_lds(int ctx, int ch) { return (size_t)(((ctx + 3) & ~3) + 2 * kValSlice * val_pitch(ch)) * 4; }
 
 // Dynamic LDS the values kernel may ask for: the device's 160 KiB less
 // room for its static LDS.
 constexpr size_t kValMaxDynLds = kMaxLdsBytes - 1024;
 
-int att_values_max_ctx() { return (int)(kValMaxDynLds / 4 - 2 * kValSlice * kValPitch) & ~3; }
+int att_values_max_ctx() { return (int)(kValMaxDynLds / 4 - 2 * kValSlice * val_pitch(kValChunk)) & ~3; }
 
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx,
                        float *xs, int32_t *xsum, hipStream_t s) {
     static std::once_flag once;
     std::call_once(once, [] {
-        (void)hipFuncSetAttribute((const void *)att_values_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)kValMaxDynLds);
-        (void)hipFuncSetAttribute((const void *)att_values_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)kValMaxDynLds);
+        (void)hipFuncSetAttribute((const void *)att_values_kernel<true, kValChunk>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kValMaxDynLds);
+        (void)hipFuncSetAttribute((const void *)att_values_kernel<false, kValChunk>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kValMaxDynLds);
         (void)hipFuncSetAttribute((const void *)att_values_reg_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)att_values_reg_lds(kVrMaxCtx));
     });
@@ -1084,6 +1090,22 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
         return;
     }
     if (hs % 32 != 0) qx = nullptr;
+    const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice, ctl ? 1 : bt.tokens);
+    const int ctx_pad = (ctx + 3) & ~3;
+    const bool vec = hs % 4 == 0 && kv_dim % 4 == 0;
+    if (ctx <= kValShortCtx) {
+        // short contexts: 128-position chunks (a third of the LDS, four
+        // workgroups a CU)
+        if (vec)
+            RK_LAUNCH((att_values_kernel<true, kValShortChunk>), grid, dim3(kValThreads),
+                      att_values_lds(ctx, kValShortChunk), s, att, att_stride, vals, out, ctl, bt, heads / kv_heads, hs,
+                      kv_dim, ctx_pad, qx, xs, xsum);
+        else
+            RK_LAUNCH((att_values_kernel<false, kValShortChunk>), grid, dim3(kValThreads),
+                      att_values_lds(ctx, kValShortChunk), s, att, att_stride, vals, out, ctl, bt, heads / kv_heads, hs,
+                      kv_dim, ctx_pad, qx, xs, xsum);
+        return;
+    }
     if (ctx <= kVrMaxCtx && hs % 32 == 0 && kv_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {
         const int nsl = hs / kValSlice;
         RK_LAUNCH(att_values_reg_kernel, dim3(heads * nsl, ctl ? 1 : bt.tokens), dim3(kVrThreads),
@@ -1091,14 +1113,12 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
                   (ctx + 3) & ~3, qx, xs, xsum);
         return;
     }
-    const dim3 grid(heads, (hs + kValSlice - 1) / kValSlice, ctl ? 1 : bt.tokens);
-    const int ctx_pad = (ctx + 3) & ~3;
-    if (hs % 4 == 0 && kv_dim % 4 == 0)
-        RK_LAUNCH(att_values_kernel<true>, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals, out,
-                  ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
+    if (vec)
+        RK_LAUNCH((att_values_kernel<true, kValChunk>), grid, dim3(kValThreads), att_values_lds(ctx, kValChunk), s, att,
+                  att_stride, vals, out, ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
     else
-        RK_LAUNCH(att_values_kernel<false>, grid, dim3(kValThreads), att_values_lds(ctx), s, att, att_stride, vals,
-                  out, ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
+        RK_LAUNCH((att_values_kernel<false, kValChunk>), grid, dim3(kValThreads), att_values_lds(ctx, kValChunk), s, att,
+                  att_stride, vals, out, ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
 }
 
 // QK-norm (internal/llm/model.go:551-558) and RoPE (:563-572) of one head
