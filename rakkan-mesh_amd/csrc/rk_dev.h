@@ -298,4 +298,62 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
     return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)i);
 }
 
+// ---- Row dots eight lanes a row: lane l of an aligned group of eight keeps
+// MatVecQ8's running sum l (blocks l, l+8, ... in order, from +0) of one
+// row, from the row's blocks it holds in registers; tree8 then forms
+// ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)) with no other lane exchange. ----
+
+// The row's blocks rl + 8m, m < BPL (clamped into the row: those past it
+// are never summed). STREAM: non-temporal loads, for rows read once.
+template <int BPL, bool STREAM = true>
+__device__ __forceinline__ void lane_row_load(int4 (&c0)[BPL], int4 (&c1)[BPL], float (&sw)[BPL], const uint8_t *row,
+                                              const float *rs, int nb, int rl) {
+#pragma unroll
+    for (int m = 0; m < BPL; m++) {
+        const int b = min(rl + 8 * m, nb - 1);
+        if (STREAM) {
+            c0[m] = load_stream16(row + 32 * b);
+            c1[m] = load_stream16(row + 32 * b + 16);
+        } else {
+            c0[m] = *reinterpret_cast<const int4 *>(row + 32 * b);
+            c1[m] = *reinterpret_cast<const int4 *>(row + 32 * b + 16);
+        }
+        sw[m] = rs[b];
+    }
+}
+
+// Running sum rl of the held row with one input (xq: codes, xsc: block
+// scales), continued from acc: exact block sums, times (row scale · input
+// scale), added in order.
+template <int BPL>
+__device__ __forceinline__ float lane_running_sum_from(float acc, const int4 (&c0)[BPL], const int4 (&c1)[BPL],
+                                                       const float (&sw)[BPL], const int8_t *xq, const float *xsc,
+                                                       int nb, int rl) {
+#pragma unroll
+    for (int m = 0; m < BPL; m++) {
+        const int b = rl + 8 * m;
+        if (b < nb) {
+            const int4 *xp = reinterpret_cast<const int4 *>(xq + 32 * b);
+            const int sum = dot16(c1[m], xp[1], dot16(c0[m], xp[0], 0));
+            acc += (float)sum * (sw[m] * xsc[b]);
+        }
+    }
+    return acc;
+}
+
+// The same from +0 (a row's blocks held whole).
+template <int BPL>
+__device__ __forceinline__ float lane_running_sum(const int4 (&c0)[BPL], const int4 (&c1)[BPL], const float (&sw)[BPL],
+                                                  const int8_t *xq, const float *xsc, int nb, int rl) {
+    return lane_running_sum_from<BPL>(0.0f, c0, c1, sw, xq, xsc, nb, rl);
+}
+
+// The fixed tree over the group's eight running sums, valid in all eight
+// lanes (float addition commutes, so each lane's pairing gives the same bits).
+__device__ __forceinline__ float tree8(float acc) {
+    acc = acc + dppf_x1(acc);
+    acc = acc + dppf_x2(acc);
+    return acc + __int_as_float(dpp_mirror8(__float_as_int(acc)));
+}
+
 }  // namespace rk

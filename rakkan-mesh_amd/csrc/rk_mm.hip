@@ -58,18 +58,23 @@ __device__ __forceinline__ void lds_put16(int8_t *p, v4i v) {
 // byte): the OR keeps every byte >= 8 so the subtraction borrows nowhere.
 __device__ __forceinline__ uint32_t nib_signed(uint32_t n) { return ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 
-// Source of logical output row g (< rows): segment and row in it.
-__device__ __forceinline__ const MatSeg &seg_of(const MmArgs &a, int g, int &r) {
+// Source of logical output row g (< rows): segment and row in it. The
+// segment is returned by value, its fields picked with selects: a reference
+// into the kernel-argument array under a lane-varying index made the
+// compiler copy the arguments to scratch and pick a wrong segment for some
+// lanes of a three-segment launch.
+__device__ __forceinline__ MatSeg seg_of(const MmArgs &a, int g, int &r) {
     r = g;
-    if (a.nseg > 1 && r >= a.seg[0].rows) {
-        r -= (int)a.seg[0].rows;
-        if (a.nseg > 2 && r >= a.seg[1].rows) {
-            r -= (int)a.seg[1].rows;
-            return a.seg[2];
-        }
-        return a.seg[1];
-    }
-    return a.seg[0];
+    const bool in1 = a.nseg > 1 && r >= a.seg[0].rows;
+    if (in1) r -= (int)a.seg[0].rows;
+    const bool in2 = in1 && a.nseg > 2 && r >= a.seg[1].rows;
+    if (in2) r -= (int)a.seg[1].rows;
+    MatSeg s;
+    s.w = in2 ? a.seg[2].w : in1 ? a.seg[1].w : a.seg[0].w;
+    s.ws = in2 ? a.seg[2].ws : in1 ? a.seg[1].ws : a.seg[0].ws;
+    s.out = in2 ? a.seg[2].out : in1 ? a.seg[1].out : a.seg[0].out;
+    s.rows = in2 ? a.seg[2].rows : in1 ? a.seg[1].rows : a.seg[0].rows;
+    return s;
 }
 
 }  // namespace
@@ -103,15 +108,15 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
     // results are never stored)
     auto row_src = [&](int m, const uint8_t *&w, const float *&ws) __attribute__((always_inline)) {
         int r;
-        const MatSeg *s;
+        MatSeg s;
         if (SILU) {
             r = min(row0 + (m & 31), a.rows - 1);
-            s = m < 32 ? &a.seg[0] : &a.seg[1];
+            s = m < 32 ? a.seg[0] : a.seg[1];
         } else {
-            s = &seg_of(a, min(row0 + m, a.rows - 1), r);
+            s = seg_of(a, min(row0 + m, a.rows - 1), r);
         }
-        w = s->w + (int64_t)r * rowbytes;
-        ws = s->ws + (int64_t)r * nb;
+        w = s.w + (int64_t)r * rowbytes;
+        ws = s.ws + (int64_t)r * nb;
     };
 
     // ---- staging: each thread's rows and tokens, fixed for the kernel ----
@@ -367,7 +372,7 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
                     const float v = res[ti][tj][i];
                     if (EPI == kEpStore) {
                         int r;
-                        const MatSeg &s = seg_of(a, g, r);
+                        const MatSeg s = seg_of(a, g, r);
                         s.out[(int64_t)t * s.rows + r] = a.bias ? v + a.bias[g] : v;
                     } else if (EPI == kEpAdd) {
                         float *p = a.x + (int64_t)t * a.ldx + g;
@@ -380,6 +385,124 @@ __global__ __launch_bounds__(kMmThreads) void mm_kernel(MmArgs a) {
             }
         }
     }
+}
+
+// ---- Small batches (up to kRowsMaxT tokens) of Q8 rows ----
+// A 64-token tile wastes most of its work on a few tokens and leaves a
+// product with few row tiles on few CUs. Here eight lanes hold a row's
+// blocks in registers, lane l of the eight the blocks l, l+8, ... (pieces of
+// 64 blocks at a time), and keep MatVecQ8's running sum l for each of the
+// workgroup's TPG tokens, whose codes and scales are staged in LDS (every
+// group of a wave reads the same input bytes at once: an LDS broadcast);
+// tree8 then gives each (row, token) the bits of its own product. A
+// workgroup owns 32 rows and one run of TPG tokens; the runs of a row tile
+// are adjacent on one XCD, so its rows come from HBM once.
+constexpr int kRowsThreads = 256;
+constexpr int kRowsPerWg = kRowsThreads / 8;
+constexpr int kRowsMaxT = 16;
+
+__host__ __device__ constexpr int rows_lds(int tpg, int cols) { return tpg * cols + tpg * (cols / 32) * 4; }
+
+template <int EPI, int TPG>
+__global__ __launch_bounds__(kRowsThreads) void mm_rows_kernel(MmArgs a, int ntg) {
+    extern __shared__ __align__(16) char lds[];
+    const int tid = threadIdx.x, grp = tid >> 3, rl = tid & 7;
+    const int cols = a.cols, nb = cols >> 5, T = a.tokens;
+    const int nrt = (a.rows + kRowsPerWg - 1) / kRowsPerWg;
+    const int total = nrt * ntg;
+    const int per = (total + 7) >> 3;
+    const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (tile >= total) return;
+    const int rt = tile / ntg, tg = tile - rt * ntg;
+    const int tok0 = tg * TPG, nt = min(TPG, T - tok0);
+
+    int8_t *xq = reinterpret_cast<int8_t *>(lds);                 // [nt][cols] codes
+    float *xsc = reinterpret_cast<float *>(lds + (size_t)TPG * cols);  // [nt][nb] scales
+    {
+        const int4 *src = reinterpret_cast<const int4 *>(a.qx + (int64_t)tok0 * cols);
+        const int np = nt * (cols >> 4);
+        for (int p = tid; p < np; p += kRowsThreads) reinterpret_cast<int4 *>(xq)[p] = src[p];
+        const float *ssrc = a.xs + (int64_t)tok0 * nb;
+        for (int p = tid; p < nt * nb; p += kRowsThreads) xsc[p] = ssrc[p];
+    }
+    __syncthreads();
+
+    const int g = rt * kRowsPerWg + grp;  // the group's output row
+    int r;
+    const MatSeg sg = seg_of(a, min(g, a.rows - 1), r);
+    const uint8_t *row = sg.w + (int64_t)r * cols;
+    const float *rs = sg.ws + (int64_t)r * nb;
+    float acc[TPG];
+#pragma unroll
+    for (int t = 0; t < TPG; t++) acc[t] = 0.0f;
+    for (int p0 = 0; p0 < nb; p0 += 64) {  // pieces of 64 blocks: each lane's eight
+        int4 c0[8], c1[8];
+        float sw[8];
+        lane_row_load<8, false>(c0, c1, sw, row + 32 * p0, rs + p0, nb - p0, rl);
+#pragma unroll
+        for (int t = 0; t < TPG; t++)
+            if (t < nt)
+                acc[t] = lane_running_sum_from<8>(acc[t], c0, c1, sw, xq + (size_t)t * cols + 32 * p0,
+                                                  xsc + t * nb + p0, nb - p0, rl);
+    }
+#pragma unroll
+    for (int t = 0; t < TPG; t++) acc[t] = tree8(acc[t]);
+    if (g >= a.rows) return;
+#pragma unroll
+    for (int t = 0; t < TPG; t++) {
+        if ((t & 7) != rl || t >= nt) continue;  // lane l stores tokens l, l+8
+        const float v = acc[t];
+        const int tk = tok0 + t;
+        if (EPI == kEpStore) {
+            sg.out[(int64_t)tk * sg.rows + r] = a.bias ? v + a.bias[g] : v;
+        } else if (EPI == kEpAdd) {
+            float *p = a.x + (int64_t)tk * a.ldx + g;
+            *p = *p + v;
+        } else if (EPI == kEpAddCanon) {
+            float *p = a.x + (int64_t)tk * a.ldx + g;
+            *p = canonical(*p + v);
+        }
+    }
+}
+
+template <int EPI, int TPG>
+static void launch_rows_one(const MmArgs &a, int ntg, unsigned grid, hipStream_t s) {
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute((const void *)mm_rows_kernel<EPI, TPG>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    });
+    RK_LAUNCH((mm_rows_kernel<EPI, TPG>), dim3(grid), dim3(kRowsThreads), (size_t)rows_lds(TPG, a.cols), s, a, ntg);
+}
+
+template <int EPI>
+static void launch_rows_epi(int tpg, const MmArgs &a, int ntg, unsigned grid, hipStream_t s) {
+    switch (tpg) {
+        case 2: launch_rows_one<EPI, 2>(a, ntg, grid, s); break;
+        case 4: launch_rows_one<EPI, 4>(a, ntg, grid, s); break;
+        case 8: launch_rows_one<EPI, 8>(a, ntg, grid, s); break;
+        default: launch_rows_one<EPI, 16>(a, ntg, grid, s); break;
+    }
+}
+
+// The small-batch kernel when it takes the product: Q8, a plain epilogue,
+// at most kRowsMaxT tokens, and the staged inputs within LDS. Tokens per
+// workgroup: the fewest runs that still give about 1024 workgroups.
+static bool launch_rows(int fmt, int epi, const MmArgs &a, hipStream_t s) {
+    if (fmt != kFmtQ8 || a.tokens > kRowsMaxT || (epi != kEpStore && epi != kEpAdd && epi != kEpAddCanon)) return false;
+    const int64_t nrt = (a.rows + kRowsPerWg - 1) / kRowsPerWg;
+    int tpg = kRowsMaxT;
+    while (tpg > 2 && (tpg >= 2 * a.tokens || nrt * ((a.tokens + tpg - 1) / tpg) < 1024)) tpg >>= 1;
+    if (rows_lds(tpg, a.cols) > 160 * 1024) return false;
+    const int ntg = (a.tokens + tpg - 1) / tpg;
+    const int64_t grid = ((nrt * ntg + 7) / 8) * 8;
+    if (grid > INT32_MAX) return false;
+    switch (epi) {
+        case kEpStore: launch_rows_epi<kEpStore>(tpg, a, ntg, (unsigned)grid, s); break;
+        case kEpAdd: launch_rows_epi<kEpAdd>(tpg, a, ntg, (unsigned)grid, s); break;
+        default: launch_rows_epi<kEpAddCanon>(tpg, a, ntg, (unsigned)grid, s); break;
+    }
+    return true;
 }
 
 template <int FMT, int EPI>
@@ -409,6 +532,7 @@ bool launch_mm(int fmt, int epi, const MmArgs &a, hipStream_t s) {
     if (a.cols < 32 || a.cols % 32 != 0) return false;
     if (epi == kEpSilu && (a.rows % 32 != 0 || a.nseg != 2)) return false;
     if (epi == kEpQKV && (a.hs % 2 != 0 || a.qdim % 2 != 0 || a.kvdim % 2 != 0 || a.row_base % 2 != 0)) return false;
+    if (launch_rows(fmt, epi, a, s)) return true;
     const int ntr = epi == kEpSilu ? a.rows / 32 : (a.rows + kMmRows - 1) / kMmRows;
     const int ntt = (a.tokens + kMmToks - 1) / kMmToks;
     const int64_t total = (int64_t)ntr * ntt;

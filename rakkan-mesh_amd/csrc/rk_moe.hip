@@ -99,51 +99,6 @@ __device__ __forceinline__ void wave_rows_q8_multi(const uint8_t *const (&w)[NR]
         }
 }
 
-// ---- Row dots eight lanes a row: lane l of an aligned group of eight keeps
-// MatVecQ8's running sum l (blocks l, l+8, ... in order, from +0) of one
-// row, from the row's blocks it holds in registers; tree8 then forms
-// ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)) with no other lane exchange. ----
-
-// The row's blocks rl + 8m, m < BPL (clamped into the row: those past it
-// are never summed).
-template <int BPL>
-__device__ __forceinline__ void lane_row_load(int4 (&c0)[BPL], int4 (&c1)[BPL], float (&sw)[BPL], const uint8_t *row,
-                                              const float *rs, int nb, int rl) {
-#pragma unroll
-    for (int m = 0; m < BPL; m++) {
-        const int b = min(rl + 8 * m, nb - 1);
-        c0[m] = load_stream16(row + 32 * b);
-        c1[m] = load_stream16(row + 32 * b + 16);
-        sw[m] = rs[b];
-    }
-}
-
-// Running sum rl of the held row with one input (xq: codes, xsc: block
-// scales): exact block sums, times (row scale · input scale), in order.
-template <int BPL>
-__device__ __forceinline__ float lane_running_sum(const int4 (&c0)[BPL], const int4 (&c1)[BPL], const float (&sw)[BPL],
-                                                  const int8_t *xq, const float *xsc, int nb, int rl) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int m = 0; m < BPL; m++) {
-        const int b = rl + 8 * m;
-        if (b < nb) {
-            const int4 *xp = reinterpret_cast<const int4 *>(xq + 32 * b);
-            const int sum = dot16(c1[m], xp[1], dot16(c0[m], xp[0], 0));
-            acc += (float)sum * (sw[m] * xsc[b]);
-        }
-    }
-    return acc;
-}
-
-// The fixed tree over the group's eight running sums, valid in all eight
-// lanes (float addition commutes, so each lane's pairing gives the same bits).
-__device__ __forceinline__ float tree8(float acc) {
-    acc = acc + dppf_x1(acc);
-    acc = acc + dppf_x2(acc);
-    return acc + __int_as_float(dpp_mirror8(__float_as_int(acc)));
-}
-
 // The router's product for a batch of up to kRouterMaxT tokens (their codes
 // and scales in LDS): wave w of workgroup b takes row 4b + w (MatVecQ8's bits)
 // for every token, eight tokens a pass; lane l keeps, for token l/8 of the

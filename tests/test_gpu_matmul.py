@@ -63,6 +63,35 @@ def test_matmul_segments_and_formats(dev):
         m.free()
 
 
+@pytest.mark.parametrize("tokens", [1, 2, 3, 7, 8, 9, 16])
+def test_small_batches_of_q8_rows(dev, tokens):
+    """Up to 16 tokens of Q8 rows take the small-batch kernel (eight lanes a
+    row, pieces of 64 blocks): rows not a multiple of the 32 a workgroup
+    owns, widths of one block, of a ragged last piece (65 and 129 blocks)
+    and of 4096 columns, and three matrices concatenated in one launch."""
+    rng = np.random.default_rng(700 + tokens)
+    for rows, cols in [(1, 32), (45, 2080), (130, 4096), (700, 4128), (3000, 256)]:
+        w = awkward(rng, rows * cols, 0.05)
+        x = awkward(rng, tokens * cols, 1.0).reshape(tokens, cols)
+        q8, s8 = oracle.quantize8(w)
+        m = dev.upload_q8(q8, s8, rows, cols)
+        same_rows(dev.matmul_t([m], x)[0], oracle.matmul_q8(q8, s8, x, tokens, rows, cols),
+                  f"{tokens} tokens {rows}x{cols}")
+        m.free()
+    cols = 2048
+    x = awkward(rng, tokens * cols, 1.0).reshape(tokens, cols)
+    ms, want = [], []
+    for rows in (96, 33, 33):
+        q, s = oracle.quantize8(awkward(rng, rows * cols, 0.05))
+        ms.append(dev.upload_q8(q, s, rows, cols))
+        want.append(oracle.matmul_q8(q, s, x, tokens, rows, cols))
+    for i, (g, wv) in enumerate(zip(dev.matmul_t(ms, x), want)):
+        same_rows(g, wv, f"{tokens} tokens, matrix {i}")
+    for m in ms:
+        m.free()
+    assert dev.used == 0
+
+
 @pytest.mark.parametrize("fmt", ["q8", "q4"])
 def test_matmul_prefill_shapes(dev, fmt):
     """Config-4 shapes (Qwen-7B: W1 18944x3584, W2 3584x18944) over a
