@@ -356,4 +356,60 @@ __device__ __forceinline__ float tree8(float acc) {
     return acc + __int_as_float(dpp_mirror8(__float_as_int(acc)));
 }
 
+// RMSNorm (internal/llm/model.go:632-638: ss = Dot32(x,x)·recip_n + eps,
+// out_i = w_i·(Rsqrt32(ss)·x_i)) of x, then the Q8_0 quantization
+// (internal/num/quant.go:34-53) of the result into qx/xs/xsum: the input of
+// the next product. Thread t holds groups g = t + k·NT (four values each)
+// of x and w in registers, loaded before the call; sx is LDS for n floats.
+// Every thread of the NT-thread workgroup calls it.
+template <int NT, int MAXG>
+__device__ void wg_norm_quant(const float4 *xv, const float4 *wv, int n, float recip_n, float eps, int8_t *qx,
+                              float *xs, int32_t *xsum, float *sx, float *bcast) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int ng = n >> 2;
+    // x transposed for Dot32: xt[j·pitch + m] = x_{j+32m} (n a multiple of 32)
+    const int steps = n >> 5, pitch = ((steps + 3) & ~3) + 4;
+#pragma unroll
+    for (int k = 0; k < MAXG; k++) {
+        const int g = tid + k * NT;
+        if (g < ng) {
+            const int i = 4 * g;
+            float *d = sx + (i & 31) * pitch + (i >> 5);
+            d[0] = xv[k].x;
+            d[pitch] = xv[k].y;
+            d[2 * pitch] = xv[k].z;
+            d[3 * pitch] = xv[k].w;
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const float s = lane < 32 ? lds_dot32_self_t(sx, pitch, steps, lane) : 0.0f;
+        const float dot = dot32_reduce(s);
+        if (lane == 0) *bcast = rsqrt32((dot * recip_n) + eps);
+    }
+    __syncthreads();
+    const float r = *bcast;
+#pragma unroll
+    for (int k = 0; k < MAXG; k++) {
+        if (k * NT < ng) {  // uniform
+            const int g = tid + k * NT;
+            float d;
+            int cs;
+            const uint32_t pk = quantize_group(wv[k].x * (r * xv[k].x), wv[k].y * (r * xv[k].y),
+                                               wv[k].z * (r * xv[k].z), wv[k].w * (r * xv[k].w), d, cs);
+            if (g < ng) {
+                reinterpret_cast<uint32_t *>(qx)[g] = pk;
+                if ((g & 7) == 0) {
+                    xs[g >> 3] = d;
+                    xsum[g >> 3] = cs;
+                }
+            }
+        }
+    }
+}
+
+// LDS of wg_norm_quant for n values: x transposed, 32 rows of the pitch.
+inline size_t norm_lds(int n) { return (size_t)32 * ((((n >> 5) + 3) & ~3) + 4) * 4; }
+
+
 }  // namespace rk

@@ -178,59 +178,81 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
 
 constexpr int kRoutePer = kMoeMaxExperts / 64;  // experts per lane at most
 
-// Routing of one token per workgroup (one wave): softmax, stable top-k,
-// normalized weights.
-__global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int experts, int k, int32_t *sel,
-                                                       float *wsel) {
-    extern __shared__ float sp[];  // [experts] probabilities
-    __shared__ float s_inv;
-    __shared__ int s_sel[kMoeMaxK];
-    const int t = blockIdx.x, lane = threadIdx.x;
-    const float *z = logits + (int64_t)t * experts;
-    float m = z[0];
-    for (int e = lane; e < experts; e += 64) {
-        sp[e] = z[e];
-        m = gomax(m, z[e]);
-    }
+// Routing of one token by one wave: softmax, stable top-k, normalized
+// weights, written to sel/wsel [k]. Every thread of the workgroup calls it
+// (its barrier is the workgroup's); `live` false: a wave without a token,
+// which only takes part in the barrier. z: the token's logits (global or
+// LDS); sp: [experts] floats of LDS, 16-byte aligned (may be z itself).
+// Lane r < k of a live wave returns the r-th selected expert. PER: experts
+// a lane holds (experts <= 64·PER).
+template <int PER>
+__device__ int route_wave(bool live, const float *z, int experts, int k, float *sp, int32_t *sel, float *wsel) {
+    const int lane = threadIdx.x & 63;
+    float m = live ? z[0] : 0.0f;
+    if (live)
+        for (int e = lane; e < experts; e += 64) {
+            const float v = z[e];
+            sp[e] = v;
+            m = gomax(m, v);
+        }
     m = wave_gomax(m);
-    for (int e = lane; e < experts; e += 64) sp[e] = exp32(sp[e] - m);
+    if (live)
+        for (int e = lane; e < experts; e += 64) sp[e] = exp32(sp[e] - m);
     __syncthreads();
-    if (lane == 0) s_inv = recip32(lds_chain_sum(sp, experts, 0.0f));
-    __syncthreads();
-    const float inv = s_inv;
-    unsigned long long key[kRoutePer];
+    // the one sequential sum: every lane runs the same chain (the reads
+    // broadcast), so the result is the same in all lanes
+    const float inv = live ? recip32(lds_chain_sum(sp, experts, 0.0f)) : 0.0f;
+    unsigned long long key[PER];
+    float pv[PER];
 #pragma unroll
-    for (int j = 0; j < kRoutePer; j++) {
+    for (int j = 0; j < PER; j++) {
         const int e = lane + 64 * j;
         key[j] = 0;
-        if (e < experts) {
-            const float p = sp[e] * inv;
-            sp[e] = p;
-            key[j] = route_key(p, e);
+        pv[j] = 0.0f;
+        if (live && e < experts) {
+            pv[j] = sp[e] * inv;
+            key[j] = route_key(pv[j], e);
         }
     }
-    // top-k: k rounds of the largest remaining key
+    // top-k: k rounds of the largest remaining key; lane r keeps round r's
+    int mine = 0;
     for (int r = 0; r < k; r++) {
         unsigned long long b = 0;
 #pragma unroll
-        for (int j = 0; j < kRoutePer; j++) b = key[j] > b ? key[j] : b;
+        for (int j = 0; j < PER; j++) b = key[j] > b ? key[j] : b;
         b = wave_max_u64(b);
 #pragma unroll
-        for (int j = 0; j < kRoutePer; j++)
+        for (int j = 0; j < PER; j++)
             if (key[j] == b) key[j] = 0;
-        if (lane == 0) s_sel[r] = (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
+        if (lane == r) mine = (int)(0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull));
     }
-    __syncthreads();
-    if (lane == 0) {
-        float sum = 0.0f;
-        for (int r = 0; r < k; r++) sum += sp[s_sel[r]];
-        s_inv = recip32(sum);
+    // each selected expert's probability, from the lane that holds it
+    float ps = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        if (64 * j < experts) {  // uniform
+            const float v = __shfl(pv[j], mine & 63);
+            if ((mine >> 6) == j) ps = v;
+        }
     }
-    __syncthreads();
-    if (lane < k) {
-        sel[(int64_t)t * k + lane] = s_sel[lane];
-        wsel[(int64_t)t * k + lane] = sp[s_sel[lane]] * s_inv;
+    // their sum in selection order, from +0 (the same in every lane)
+    float sum = 0.0f;
+    for (int r = 0; r < k; r++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ps), r));
+    const float inv2 = recip32(sum);
+    if (live && lane < k) {
+        sel[lane] = mine;
+        wsel[lane] = ps * inv2;
     }
+    return mine;
+}
+
+// Routing of one token per workgroup (one wave).
+template <int PER>
+__global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int experts, int k, int32_t *sel,
+                                                       float *wsel) {
+    extern __shared__ __align__(16) float sp[];  // [experts] probabilities
+    const int t = blockIdx.x;
+    (void)route_wave<PER>(true, logits + (int64_t)t * experts, experts, k, sp, sel + (int64_t)t * k, wsel + (int64_t)t * k);
 }
 
 // The (token, slot) pairs grouped by expert: grp[0] = the number of experts
@@ -280,16 +302,18 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel_g, i
 // The same grouping for up to kGroupFastPairs pairs and 1024 experts, with
 // no thread walking all the pairs: counts by LDS atomics, one wave's scans
 // over the experts (starts and group indices), and each pair's place among
-// its expert's pairs from the earlier pairs (eight threads a pair).
+// its expert's pairs from the earlier pairs (eight threads a pair). Every
+// thread of a 1024-thread workgroup calls it; s_sel: the pairs' experts in
+// LDS, written before a barrier.
 constexpr int kGroupFastPairs = 128;
-__global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel, int npairs, int experts, int gcap,
-                                                              int32_t *grp) {
-    __shared__ int s_sel[kGroupFastPairs], s_cnt[1024], s_start[1024], s_gi[1024], s_total;
+struct GroupLds {
+    int cnt[1024], start[1024], gi[1024], total;
+};
+__device__ void group_pairs_wg(const int *s_sel, int npairs, int experts, int gcap, int32_t *grp, GroupLds &gl) {
     const int tid = threadIdx.x, lane = tid & 63;
-    if (tid < npairs) s_sel[tid] = sel[tid];
-    s_cnt[tid] = 0;
+    gl.cnt[tid] = 0;
     __syncthreads();
-    if (tid < npairs) atomicAdd(&s_cnt[s_sel[tid]], 1);
+    if (tid < npairs) atomicAdd(&gl.cnt[s_sel[tid]], 1);
     __syncthreads();
     if (tid < 64) {
         // lane l takes experts l·per .. l·per+per-1: local sums, then an
@@ -299,8 +323,8 @@ __global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel
         for (int i = 0; i < per; i++) {
             const int e = lane * per + i;
             if (e < experts) {
-                c += s_cnt[e];
-                g += s_cnt[e] > 0;
+                c += gl.cnt[e];
+                g += gl.cnt[e] > 0;
             }
         }
         int ci = c, gi = g;  // inclusive scans
@@ -316,21 +340,21 @@ __global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel
         for (int i = 0; i < per; i++) {
             const int e = lane * per + i;
             if (e < experts) {
-                s_start[e] = cs;
-                s_gi[e] = gs;
-                cs += s_cnt[e];
-                gs += s_cnt[e] > 0;
+                gl.start[e] = cs;
+                gl.gi[e] = gs;
+                cs += gl.cnt[e];
+                gs += gl.cnt[e] > 0;
             }
         }
-        if (lane == 63) s_total = gi;
+        if (lane == 63) gl.total = gi;
     }
     __syncthreads();
     int32_t *gexp = grp + 1, *gstart = grp + 1 + gcap, *gcount = grp + 1 + 2 * gcap, *list = grp + 1 + 3 * gcap;
-    if (tid < experts && s_cnt[tid] > 0) {
-        const int g = s_gi[tid];
+    if (tid < experts && gl.cnt[tid] > 0) {
+        const int g = gl.gi[tid];
         gexp[g] = tid;
-        gstart[g] = s_start[tid];
-        gcount[g] = s_cnt[tid];
+        gstart[g] = gl.start[tid];
+        gcount[g] = gl.cnt[tid];
     }
     // pair p's place: the earlier pairs of its expert (eight threads a pair)
     const int p = tid >> 3, part = tid & 7;
@@ -341,9 +365,38 @@ __global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel
         n += dpp_x1(n);
         n += dpp_x2(n);
         n += dpp_mirror8(n);
-        if (part == 0) list[s_start[e] + n] = p;
+        if (part == 0) list[gl.start[e] + n] = p;
     }
-    if (tid == 0) grp[0] = s_total;
+    if (tid == 0) grp[0] = gl.total;
+}
+
+__global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel, int npairs, int experts, int gcap,
+                                                              int32_t *grp) {
+    __shared__ int s_sel[kGroupFastPairs];
+    __shared__ GroupLds gl;
+    if ((int)threadIdx.x < npairs) s_sel[threadIdx.x] = sel[threadIdx.x];
+    __syncthreads();
+    group_pairs_wg(s_sel, npairs, experts, gcap, grp, gl);
+}
+
+// Routing (wave t: token t) and grouping of up to kSelectTokens tokens in
+// one workgroup. sp: [tokens][ep] probabilities (ep: experts rounded up to 4).
+constexpr int kSelectTokens = 16;
+template <int PER>
+__global__ __launch_bounds__(1024) void moe_select_kernel(const float *logits, int tokens, int experts, int k,
+                                                          int32_t *sel, float *wsel, int gcap, int32_t *grp) {
+    extern __shared__ __align__(16) float sp_all[];
+    __shared__ int s_sel[kGroupFastPairs];
+    __shared__ GroupLds gl;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ep = (experts + 3) & ~3;
+    const bool live = wave < tokens;
+    const int t = live ? wave : 0;
+    const int mine = route_wave<PER>(live, logits + (int64_t)t * experts, experts, k, sp_all + t * ep,
+                                sel + (int64_t)t * k, wsel + (int64_t)t * k);
+    if (live && lane < k) s_sel[t * k + lane] = mine;
+    __syncthreads();
+    group_pairs_wg(s_sel, tokens * k, experts, gcap, grp, gl);
 }
 
 // W1 and W3 rows of a selected expert for every pair that chose it:
@@ -593,14 +646,13 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, in
                                                           float *out, int residual) {
     __shared__ int order[kMoeMaxK];  // the token's slots by ascending expert
     const int t = blockIdx.x;
-    if (threadIdx.x == 0) {
-        for (int s = 0; s < k; s++) order[s] = s;
-        for (int a = 1; a < k; a++)  // insertion sort of k <= 32 slots
-            for (int b = a; b > 0 && sel[(int64_t)t * k + order[b]] < sel[(int64_t)t * k + order[b - 1]]; b--) {
-                const int tmp = order[b];
-                order[b] = order[b - 1];
-                order[b - 1] = tmp;
-            }
+    if ((int)threadIdx.x < k) {
+        // a token's experts are distinct: slot s goes to place #{s': sel[s'] < sel[s]}
+        const int32_t *ts = sel + (int64_t)t * k;
+        const int e = ts[threadIdx.x];
+        int r = 0;
+        for (int q = 0; q < k; q++) r += ts[q] < e;
+        order[r] = threadIdx.x;
     }
     __syncthreads();
     const int i = blockIdx.y * 256 + threadIdx.x;
@@ -677,13 +729,33 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
         ok = launch_mm(kFmtQ8, kEpStore, a, s);
     }
     if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
+    const int npairs = tokens * K;
+    if (tokens <= kSelectTokens && npairs <= kGroupFastPairs && E <= 1024) {
+        static std::once_flag once;
+        std::call_once(once, [] {
+            (void)hipFuncSetAttribute((const void *)moe_select_kernel<kRoutePer>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kSelectTokens * 1024 * 4);
+        });
+        ProfScope p(d, s, "moe_select");
+        const size_t lds = (size_t)tokens * ((E + 3) & ~3) * 4;
+        if (E <= 128)
+            RK_LAUNCH(moe_select_kernel<2>, dim3(1), dim3(1024), lds, s, sc.logits, tokens, E, K, sc.sel, sc.wsel,
+                      sc.gcap, sc.grp);
+        else
+            RK_LAUNCH(moe_select_kernel<kRoutePer>, dim3(1), dim3(1024), lds, s, sc.logits, tokens, E, K, sc.sel,
+                      sc.wsel, sc.gcap, sc.grp);
+        return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s);
+    }
     {
         ProfScope p(d, s, "moe_route");
-        RK_LAUNCH(moe_route_kernel, dim3(tokens), dim3(64), (size_t)E * 4, s, sc.logits, E, K, sc.sel, sc.wsel);
+        const size_t lds = (size_t)((E + 3) & ~3) * 4;
+        if (E <= 128)
+            RK_LAUNCH(moe_route_kernel<2>, dim3(tokens), dim3(64), lds, s, sc.logits, E, K, sc.sel, sc.wsel);
+        else
+            RK_LAUNCH(moe_route_kernel<kRoutePer>, dim3(tokens), dim3(64), lds, s, sc.logits, E, K, sc.sel, sc.wsel);
     }
     {
         ProfScope p(d, s, "moe_group");
-        const int npairs = tokens * K;
         if (npairs <= kGroupFastPairs && E <= 1024)
             RK_LAUNCH(moe_group_fast_kernel, dim3(1), dim3(1024), 0, s, sc.sel, npairs, E, sc.gcap, sc.grp);
         else

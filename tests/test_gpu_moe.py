@@ -58,6 +58,18 @@ def test_moe_config5_shape(dev, tokens):
     assert dev.used == 0
 
 
+@pytest.mark.parametrize("experts,topk,tokens", [(200, 8, 1), (200, 8, 16), (200, 8, 40), (64, 32, 4),
+                                                  (64, 32, 5)])
+def test_moe_routing_launch_shapes(dev, experts, topk, tokens):
+    """More than 128 experts (a lane holds up to 16 of them), and the
+    routing of up to 16 tokens with at most 128 (token, slot) pairs in one
+    launch with the grouping, or one launch per token past that."""
+    rng = np.random.default_rng(experts * 7 + topk + tokens)
+    host, gpu = build(dev, rng, 128, 64, experts)
+    check(dev, host, gpu, topk, rng.normal(0, 1, (tokens, 128)).astype(np.float32))
+    assert dev.used == 0
+
+
 def test_moe_tied_router_logits(dev):
     """Experts whose router rows are equal tie: the lower index is taken
     first (a stable sort), on the GPU as in the oracle."""

@@ -141,6 +141,20 @@ def test_moe_stage_small_batch1_and_sequences(dev):
     assert dev.used == 0
 
 
+def test_moe_stage_many_experts(dev):
+    """200 experts, top 8 (a lane of the routing holds up to 16 experts):
+    one sequence, then three."""
+    m = moe_model(SMALL, experts=200, ehidden=32, topk=8, seed=4, lo=1e-3, hi=1e-2, router_scale=(1e-2, 5e-2))
+    g = GpuModel(dev, m)
+    try:
+        with oracle.matvec_threads(THREADS):
+            check_batch1(g, [3, 1, 4, 1, 5], 8, 64)
+            check_seqs(g, [[2, 7], [1, 8, 2, 8], [18]], 6, 64)
+    finally:
+        g.free()
+    assert dev.used == 0
+
+
 def test_moe_stage_sequences_reuse_and_one_sequence_stage(dev):
     """A stage of several sequences started twice (the second start
     overwrites every sequence's prompt and position), and a stage of one
