@@ -126,6 +126,15 @@ __device__ __forceinline__ int att_position(const int32_t *ctl, const AttBatch &
 void launch_att_scores(const float *q, const float *keys, float *att, int32_t att_stride, const int32_t *ctl,
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt,
                        hipStream_t s);
+// The same scores with QK-norm and RoPE of the position's raw q and k
+// (launch_qknorm_rope's steps) folded in, k and v stored into the caches:
+// for a decode step (ctl) or independent sequences (bt.pos); false (nothing
+// launched) for other batches or shapes.
+bool launch_att_scores_qkn(const float *q_raw, const float *k_raw, const float *v_raw, const float *q_norm,
+                           const float *k_norm, float recip_hs, float eps, const float *cos_t, const float *sin_t,
+                           float *keys, float *vals, float *att, int32_t att_stride, const int32_t *ctl,
+                           const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt,
+                           hipStream_t s);
 // Batches up to 1024 positions (head size a multiple of 32) run a group of
 // tokens per workgroup (rk_attn_batch.hip); the results are the same.
 bool att_group_fits(const AttBatch &bt, int hs, int kv_dim);

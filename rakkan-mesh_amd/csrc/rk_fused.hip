@@ -647,6 +647,89 @@ void launch_att_scores(const float *q, const float *keys, float *att, int32_t at
                   kv_dim, inv_sqrt);
 }
 
+// QK-norm and RoPE of one head by one wave: dst = RoPE_pos(w·(Rsqrt32(ss)·x))
+// with ss = Dot32(x, x)·recip_hs + eps; pair (2p, 2p+1) rotated by table
+// entry p. dst may be x (each lane reads its pairs before writing them, and
+// the dot is complete before any write).
+__device__ __forceinline__ void qk_norm_rope_wave(const float *x, const float *w, float recip_hs, float eps,
+                                                  const float *cos_t, const float *sin_t, int pos, int hs,
+                                                  float *dst) {
+    const int lane = threadIdx.x & 63;
+    const float dot = __shfl(dot32_half(x, x, hs, lane & 31, lane < 32), 0);
+    const float r = rsqrt32((dot * recip_hs) + eps);
+    const int half = hs >> 1;
+    for (int p = lane; p < half; p += 64) {
+        const float co = cos_t[(int64_t)pos * half + p], si = sin_t[(int64_t)pos * half + p];
+        const float v0 = w[2 * p] * (r * x[2 * p]), v1 = w[2 * p + 1] * (r * x[2 * p + 1]);
+        dst[2 * p] = (v0 * co) - (v1 * si);
+        dst[2 * p + 1] = (v0 * si) + (v1 * co);
+    }
+}
+
+// The scores of a decode step (or of independent sequences) with the
+// QK-norm and RoPE of the position's q and k folded in: wave 0 normalizes
+// the workgroup's q head into LDS, wave 1 (in the tile that holds the
+// position) the key of its kv head; the position's own score takes that key
+// from LDS, and one workgroup per kv head stores it and the raw v into the
+// caches (read by the values launch that follows). q_raw, k_raw, v_raw: the
+// token's QKV outputs, [tokens][heads·hs] and [tokens][kv_dim]. hs: a
+// multiple of 8, at most kQknMaxHs.
+constexpr int kQknMaxHs = 256;
+__global__ __launch_bounds__(256) void att_scores_qkn_kernel(const float *q_raw, const float *k_raw, const float *v_raw,
+                                                             const float *q_norm, const float *k_norm, float recip_hs,
+                                                             float eps, const float *cos_t, const float *sin_t,
+                                                             float *keys, float *vals, float *att, int32_t att_stride,
+                                                             const int32_t *ctl, AttBatch bt, int kv_mul, int hs,
+                                                             int kv_dim, float inv_sqrt) {
+    __shared__ __align__(16) float sq[kQknMaxHs], sk[kQknMaxHs];
+    const int z = blockIdx.z;
+    const int pos = att_position(ctl, bt, z), T = pos + 1;
+    const int t0 = blockIdx.y * kScoreTile;
+    if (t0 >= T) return;
+    const int heads = gridDim.x;
+    q_raw += (int64_t)z * heads * hs;
+    k_raw += (int64_t)z * kv_dim;
+    v_raw += (int64_t)z * kv_dim;
+    att += (int64_t)z * bt.att_stride;
+    keys += (int64_t)z * bt.cache_stride;
+    vals += (int64_t)z * bt.cache_stride;
+    const int h = blockIdx.x, g = h / kv_mul;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool here = pos < t0 + kScoreTile;  // the tile holds the position
+    if (wave == 0)
+        qk_norm_rope_wave(q_raw + (int64_t)h * hs, q_norm, recip_hs, eps, cos_t, sin_t, pos, hs, sq);
+    else if (wave == 1 && here)
+        qk_norm_rope_wave(k_raw + (int64_t)g * hs, k_norm, recip_hs, eps, cos_t, sin_t, pos, hs, sk);
+    __syncthreads();
+    if (here && h % kv_mul == 0 && wave == 2) {
+        float *kd = keys + (int64_t)pos * kv_dim + (int64_t)g * hs;
+        float *vd = vals + (int64_t)pos * kv_dim + (int64_t)g * hs;
+        const float *vs = v_raw + (int64_t)g * hs;
+        for (int i = lane; i < hs; i += 64) {
+            kd[i] = sk[i];
+            vd[i] = vs[i];
+        }
+    }
+    const int sub = threadIdx.x & 3;
+    const int t = t0 + (threadIdx.x >> 2);
+    const float *kt = t == pos ? sk : keys + (int64_t)(t < T ? t : t0) * kv_dim + (int64_t)g * hs;
+    const float dot = quad_dot32(sq, kt, sub, hs);
+    if (sub == 0 && t < T) att[(int64_t)h * att_stride + t] = dot * inv_sqrt;
+}
+
+bool launch_att_scores_qkn(const float *q_raw, const float *k_raw, const float *v_raw, const float *q_norm,
+                           const float *k_norm, float recip_hs, float eps, const float *cos_t, const float *sin_t,
+                           float *keys, float *vals, float *att, int32_t att_stride, const int32_t *ctl,
+                           const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, float inv_sqrt,
+                           hipStream_t s) {
+    if (!ctl && !bt.pos) return false;  // a prompt's batch: the grouped scores, after the norm launch
+    if (hs % 8 != 0 || hs > kQknMaxHs || kv_dim % 4 != 0 || kv_dim != kv_heads * hs) return false;
+    const dim3 grid(heads, (ctx + kScoreTile - 1) / kScoreTile, ctl ? 1 : bt.tokens);
+    RK_LAUNCH(att_scores_qkn_kernel, grid, dim3(256), 0, s, q_raw, k_raw, v_raw, q_norm, k_norm, recip_hs, eps, cos_t,
+              sin_t, keys, vals, att, att_stride, ctl, bt, heads / kv_heads, hs, kv_dim, inv_sqrt);
+    return true;
+}
+
 // Softmax and weighted values for a 32-element slice of one head per
 // workgroup (grid: heads, ceil(hs/32)). The order is the CPU's: Go max,
 // e_t = Exp32(s_t - max), one sequential sum, inv = Recip32(sum), a_t =
@@ -1075,7 +1158,6 @@ __global__ __launch_bounds__(64) void qknorm_rope_kernel(float *q, const float *
                                                          const int32_t *ctl, int32_t pos0, const int32_t *seq_pos,
                                                          int64_t cache_stride, float *kcache, float *vcache,
                                                          int heads, int hs, int kv_dim) {
-    extern __shared__ float sy[];  // [hs]
     // a batch: token blockIdx.y at pos0 + blockIdx.y (or, independent
     // sequences, at seq_pos[blockIdx.y] in its own caches), rows
     // [tokens][heads·hs] and [tokens][kv_dim]
@@ -1090,19 +1172,8 @@ __global__ __launch_bounds__(64) void qknorm_rope_kernel(float *q, const float *
     const bool isq = (int)blockIdx.x < heads;
     const int head = isq ? blockIdx.x : blockIdx.x - heads;
     const float *x = isq ? q + (int64_t)head * hs : k + (int64_t)head * hs;
-    const float *w = isq ? q_norm : k_norm;
-    const float dot = __shfl(dot32_half(x, x, hs, lane & 31, lane < 32), 0);
-    const float r = rsqrt32((dot * recip_hs) + eps);
-    for (int i = lane; i < hs; i += 64) sy[i] = w[i] * (r * x[i]);
-    __syncthreads();
-    const int half = hs >> 1;
     float *dst = isq ? q + (int64_t)head * hs : kcache + (int64_t)pos * kv_dim + (int64_t)head * hs;
-    for (int p = lane; p < half; p += 64) {
-        const float co = cos_t[(int64_t)pos * half + p], si = sin_t[(int64_t)pos * half + p];
-        const float v0 = sy[2 * p], v1 = sy[2 * p + 1];
-        dst[2 * p] = (v0 * co) - (v1 * si);
-        dst[2 * p + 1] = (v0 * si) + (v1 * co);
-    }
+    qk_norm_rope_wave(x, isq ? q_norm : k_norm, recip_hs, eps, cos_t, sin_t, pos, hs, dst);
     if (!isq) {
         float *vd = vcache + (int64_t)pos * kv_dim + (int64_t)head * hs;
         const float *vs = v + (int64_t)head * hs;
@@ -1114,7 +1185,7 @@ void launch_qknorm_rope(float *q, const float *k, const float *v, const float *q
                         float recip_hs, float eps, const float *cos_t, const float *sin_t, const int32_t *ctl,
                         int32_t pos0, int tokens, float *kcache, float *vcache, int heads, int kv_heads, int hs,
                         hipStream_t s, const int32_t *seq_pos, int64_t cache_stride) {
-    RK_LAUNCH(qknorm_rope_kernel, dim3(heads + kv_heads, ctl ? 1 : tokens), dim3(64), (size_t)hs * 4, s, q, k, v,
+    RK_LAUNCH(qknorm_rope_kernel, dim3(heads + kv_heads, ctl ? 1 : tokens), dim3(64), 0, s, q, k, v,
               q_norm, k_norm, recip_hs, eps, cos_t, sin_t, ctl, pos0, seq_pos, cache_stride, kcache, vcache, heads,
               hs, kv_heads * hs);
 }

@@ -150,14 +150,38 @@ static int stage_product(rk_stage *s, hipStream_t st, const char *name, const QS
 // reads a whole key row), the sequential sums few. (One launch computing
 // a head's scores in the workgroups of its value sums measured slower on
 // MI355X: each workgroup then reads all of the head's keys.)
-static void enqueue_attention(rk_stage *s, hipStream_t st, const float *q, const float *keys, const float *vals,
-                              float *att, float *out, const int32_t *ctl, const AttBatch &bt, const QScratch *qo) {
+// The raw k and v rows and the norm weights of a QK-norm layer: attention
+// then starts with the norm and RoPE of q and k and the caches' store.
+struct QkNorm {
+    const float *k, *v, *q_norm, *k_norm;
+};
+
+static void enqueue_attention(rk_stage *s, hipStream_t st, const float *q, float *keys, float *vals, float *att,
+                              float *out, const int32_t *ctl, const AttBatch &bt, const QScratch *qo,
+                              const QkNorm *qk = nullptr) {
     rk_device *d = s->d;
     const rk_stage_config &c = s->c;
     int8_t *qx = qo ? qo->qx : nullptr;
     float *xs = qo ? qo->xs : nullptr;
     int32_t *xsum = qo ? qo->xsum : nullptr;
-    {
+    bool scored = false;
+    if (qk) {
+        {
+            // a decode step or independent sequences: the norm folded into
+            // the scores launch
+            ProfScope p(d, st, "att_scores");
+            scored = launch_att_scores_qkn(q, qk->k, qk->v, qk->q_norm, qk->k_norm, c.recip_head, c.norm_eps,
+                                           s->cos_t, s->sin_t, keys, vals, att, c.ctx, ctl, bt, c.ctx, c.heads,
+                                           c.kv_heads, s->hs, s->kvdim, c.inv_sqrt, st);
+        }
+        if (!scored) {
+            ProfScope p(d, st, "qknorm_rope");
+            launch_qknorm_rope(const_cast<float *>(q), qk->k, qk->v, qk->q_norm, qk->k_norm, c.recip_head, c.norm_eps,
+                               s->cos_t, s->sin_t, ctl, bt.pos0, bt.tokens, keys, vals, c.heads, c.kv_heads, s->hs, st,
+                               bt.pos, bt.cache_stride);
+        }
+    }
+    if (!scored) {
         ProfScope p(d, st, "att_scores");
         launch_att_scores(q, keys, att, c.ctx, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, c.inv_sqrt, st);
     }
@@ -215,15 +239,13 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
                 return rc;
             i = j;
         }
-        ProfScope p(d, st, "qknorm_rope");
-        launch_qknorm_rope(s->q, s->k, s->v, D.q_norm, D.k_norm, c.recip_head, c.norm_eps, s->cos_t, s->sin_t,
-                           s->ctl, 0, 1, D.keys, D.vals, c.heads, c.kv_heads, s->hs, st);
     }
     // The attention output comes quantized when its Q8 blocks fall within
     // heads (head size a multiple of 32).
     const bool att_q = s->hs % 32 == 0;
-    enqueue_attention(s, st, s->q, D.keys, D.vals, s->att, s->att_out, s->ctl, AttBatch{},
-                      att_q ? &s->qa : nullptr);
+    const QkNorm qk{s->k, s->v, D.q_norm, D.k_norm};
+    enqueue_attention(s, st, s->q, D.keys, D.vals, s->att, s->att_out, s->ctl, AttBatch{}, att_q ? &s->qa : nullptr,
+                      c.qk_norm ? &qk : nullptr);
     float *xo[1] = {s->x};
     if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, nullptr, &L.wo, 1, xo, kEpAdd, base)))
         return rc;
@@ -467,12 +489,6 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, const
         for (int t = i; t < j; t++) row += (int)qkv[t]->rows;
         i = j;
     }
-    if (c.qk_norm) {
-        ProfScope p(d, st, "qknorm_rope");
-        launch_qknorm_rope(s->bq, s->bk, s->bv, D.q_norm, D.k_norm, c.recip_head, c.norm_eps, s->cos_t, s->sin_t,
-                           nullptr, bp.pos0, n, D.keys + bp.cache0, D.vals + bp.cache0, c.heads, c.kv_heads, s->hs, st,
-                           bp.seq_pos, bp.cache_stride);
-    }
     AttBatch bt;
     bt.pos0 = bp.pos0;
     bt.tokens = n;
@@ -484,8 +500,9 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, const
     // the attention output comes quantized when its Q8 blocks fall within
     // heads; else it is quantized by a launch of its own
     const bool att_q = s->hs % 32 == 0;
+    const QkNorm qk{s->bk, s->bv, D.q_norm, D.k_norm};
     enqueue_attention(s, st, s->bq, D.keys + bp.cache0, D.vals + bp.cache0, s->batt, s->batt_out, nullptr, bt,
-                      att_q ? &s->bqa : nullptr);
+                      att_q ? &s->bqa : nullptr, c.qk_norm ? &qk : nullptr);
     if (!att_q) {
         ProfScope p(d, st, "quantize_acts");
         launch_quantize_acts(s->batt_out, (int64_t)n * s->qdim, s->bqa.qx, s->bqa.xs, s->bqa.xsum, st);
