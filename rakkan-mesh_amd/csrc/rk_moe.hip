@@ -179,14 +179,15 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long k)
 constexpr int kRoutePer = kMoeMaxExperts / 64;  // experts per lane at most
 
 // Routing of one token by one wave: softmax, stable top-k, normalized
-// weights, written to sel/wsel [k]. Every thread of the workgroup calls it
-// (its barrier is the workgroup's); `live` false: a wave without a token,
-// which only takes part in the barrier. z: the token's logits (global or
-// LDS); sp: [experts] floats of LDS, 16-byte aligned (may be z itself).
-// Lane r < k of a live wave returns the r-th selected expert. PER: experts
-// a lane holds (experts <= 64·PER).
+// weights, written to sel/wsel [k] (when not null). Every thread of the
+// workgroup calls it (its barrier is the workgroup's); `live` false: a wave
+// without a token, which only takes part in the barrier. z: the token's
+// logits (global or LDS); sp: [experts] floats of LDS, 16-byte aligned (may
+// be z itself). Lane r < k of a live wave returns the r-th selected expert
+// and its weight (wt). PER: experts a lane holds (experts <= 64·PER).
 template <int PER>
-__device__ int route_wave(bool live, const float *z, int experts, int k, float *sp, int32_t *sel, float *wsel) {
+__device__ int route_wave(bool live, const float *z, int experts, int k, float *sp, int32_t *sel, float *wsel,
+                          float &wt) {
     const int lane = threadIdx.x & 63;
     float m = live ? z[0] : 0.0f;
     if (live)
@@ -239,9 +240,10 @@ __device__ int route_wave(bool live, const float *z, int experts, int k, float *
     float sum = 0.0f;
     for (int r = 0; r < k; r++) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ps), r));
     const float inv2 = recip32(sum);
-    if (live && lane < k) {
+    wt = ps * inv2;
+    if (live && lane < k && sel) {
         sel[lane] = mine;
-        wsel[lane] = ps * inv2;
+        wsel[lane] = wt;
     }
     return mine;
 }
@@ -252,7 +254,9 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
                                                        float *wsel) {
     extern __shared__ __align__(16) float sp[];  // [experts] probabilities
     const int t = blockIdx.x;
-    (void)route_wave<PER>(true, logits + (int64_t)t * experts, experts, k, sp, sel + (int64_t)t * k, wsel + (int64_t)t * k);
+    float wt;
+    (void)route_wave<PER>(true, logits + (int64_t)t * experts, experts, k, sp, sel + (int64_t)t * k,
+                          wsel + (int64_t)t * k, wt);
 }
 
 // The (token, slot) pairs grouped by expert: grp[0] = the number of experts
@@ -392,8 +396,9 @@ __global__ __launch_bounds__(1024) void moe_select_kernel(const float *logits, i
     const int ep = (experts + 3) & ~3;
     const bool live = wave < tokens;
     const int t = live ? wave : 0;
+    float wt;
     const int mine = route_wave<PER>(live, logits + (int64_t)t * experts, experts, k, sp_all + t * ep,
-                                sel + (int64_t)t * k, wsel + (int64_t)t * k);
+                                     sel + (int64_t)t * k, wsel + (int64_t)t * k, wt);
     if (live && lane < k) s_sel[t * k + lane] = mine;
     __syncthreads();
     group_pairs_wg(s_sel, tokens * k, experts, gcap, grp, gl);
@@ -598,6 +603,92 @@ __global__ __launch_bounds__(512) void moe_up8_kernel(const uint8_t *const *w1, 
     }
 }
 
+// Byte offset of moe_up1_kernel's float region (after the codes, scales and
+// code sums of the normed input).
+__host__ __device__ inline int up1_lds_r(int dim) { return (dim + 8 * (dim >> 5) + 15) & ~15; }
+
+// One token's W1/W3 rows with the routing and the RMSNorm folded in: each
+// workgroup routes the token itself (wave 0; every workgroup gets the same
+// selection), takes the g-th selected expert by ascending index (g =
+// blockIdx.x, the grouping's order), loads that expert's rows, and forms
+// RMSNorm_ffn(x)'s Q8_0 form in LDS while the rows are in flight; workgroup
+// (0, 0) also writes the selection, the weights and the grouping (one pair
+// a group) for the W2 products and the sum. h as moe_up8_kernel's.
+template <int BPL, int PER>
+__global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const float *norm_w, float recip_n, float eps,
+                                                      const float *logits, int experts, int k,
+                                                      const uint8_t *const *w1, const float *const *s1,
+                                                      const uint8_t *const *w3, const float *const *s3, int dim,
+                                                      int hidden, int32_t *sel, float *wsel, int gcap, int32_t *grp,
+                                                      int8_t *hq, float *hs, int32_t *hsum) {
+    extern __shared__ __align__(16) char ulds[];
+    __shared__ float bcast, s_w;
+    __shared__ int s_e, s_slot;
+    __shared__ __align__(16) float sh[32];
+    const int nb = dim >> 5;
+    int8_t *sq = reinterpret_cast<int8_t *>(ulds);                              // [dim] codes
+    float *sxs = reinterpret_cast<float *>(ulds + dim);                         // [nb] scales
+    int32_t *sxsum = reinterpret_cast<int32_t *>(ulds + dim + 4 * nb);          // [nb] code sums
+    float *sp = reinterpret_cast<float *>(ulds + up1_lds_r(dim));               // [experts] probabilities
+    float *sn = sp + ((experts + 3) & ~3);                                      // the norm's transposed x
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    float4 xv[1], wv[1];
+    {
+        const int g4 = min(tid, (dim >> 2) - 1);
+        xv[0] = reinterpret_cast<const float4 *>(x)[g4];
+        wv[0] = reinterpret_cast<const float4 *>(norm_w)[g4];
+    }
+    const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
+    float wt;
+    const int mine = route_wave<PER>(wave == 0, logits, experts, k, sp, lead ? sel : nullptr, wsel, wt);
+    if (wave == 0 && lane < k) {
+        int r = 0;  // place among the selection by ascending index (the experts are distinct)
+        for (int q = 0; q < k; q++) r += __shfl(mine, q) < mine;
+        if (r == (int)blockIdx.x) {
+            s_e = mine;
+            s_w = wt;
+            s_slot = lane;
+        }
+        if (lead) {
+            grp[1 + r] = mine;
+            grp[1 + gcap + r] = r;
+            grp[1 + 2 * gcap + r] = 1;
+            grp[1 + 3 * gcap + r] = lane;  // pair (token 0, slot lane)
+            if (lane == 0) grp[0] = k;
+        }
+    }
+    __syncthreads();
+    const int e = s_e;
+    const int rg = lane >> 3, rl = lane & 7, q = rg >> 1;
+    const int j = blockIdx.y * 32 + 4 * wave + q;
+    const bool w3row = rg & 1;
+    int4 c0[BPL], c1[BPL];
+    float sw[BPL];
+    lane_row_load<BPL>(c0, c1, sw, (w3row ? w3[e] : w1[e]) + (int64_t)j * dim,
+                       (w3row ? s3[e] : s1[e]) + (int64_t)j * nb, nb, rl);
+    wg_norm_quant<512, 1>(xv, wv, dim, recip_n, eps, sq, sxs, sxsum, sn, &bcast);
+    __syncthreads();
+    const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq, sxs, nb, rl));
+    const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
+    if ((lane & 15) == 0) sh[4 * wave + q] = s_w * silu_mul(v, v3);
+    __syncthreads();
+    if (wave == 0) {
+        const float4 v4 = reinterpret_cast<const float4 *>(sh)[min(lane, 7)];
+        float d;
+        int cs;
+        const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
+        const int64_t base = (int64_t)s_slot * hidden + blockIdx.y * 32;
+        if (lane < 8) {
+            reinterpret_cast<uint32_t *>(hq + base)[lane] = pk;
+            if (lane == 0) {
+                hs[base >> 5] = d;
+                hsum[base >> 5] = cs;
+            }
+        }
+    }
+}
+
 template <int BPL>
 __global__ __launch_bounds__(256) void moe_down8_kernel(const uint8_t *const *w2, const float *const *s2,
                                                         const int32_t *grp, int gcap, const int8_t *hq, const float *hs,
@@ -691,6 +782,7 @@ int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc) 
 
 static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, int tokens,
                                float *out, bool residual, hipStream_t s);
+static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *out, bool residual, hipStream_t s);
 
 int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, const int32_t *xsum, int tokens,
                   float *out, bool residual, hipStream_t s) {
@@ -789,6 +881,14 @@ static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx
             RK_LAUNCH(moe_up_kernel, grid, dim3(512), 0, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel, K, qx,
                       xs, D, H, sc.hq, sc.hs, sc.hsum);
     }
+    return enqueue_moe_down(m, sc, tokens, out, residual, s);
+}
+
+// The W2 products of the grouped pairs (h in sc) and the sum.
+static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *out, bool residual, hipStream_t s) {
+    rk_device *d = m->d;
+    const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
+    const int groups = std::min(E, tokens * K);  // launched; those past the selected count exit
     {
         ProfScope p(d, s, "moe_down");
         const int bpl = (H / 32 + 7) / 8;  // blocks of a W2 row per lane
@@ -822,6 +922,47 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
     rk_device *d = m->d;
     if (tokens <= 0) return RK_OK;
     if (tokens > sc.cap) return fail(d, RK_ERR_ARGS, "moe: %d tokens beyond the scratch's %d", tokens, sc.cap);
+    const int D = m->dim, E = m->experts, K = m->topk, H = m->hidden;
+    if (norm_w && tokens == 1 && D <= 2048 && E <= 1024 && K <= kMoeMaxK) {
+        // one token: the router's product with the RMSNorm in its prologue,
+        // then the W1/W3 rows with the routing and the norm folded in (the
+        // normed input is never stored: qx, xs and xsum are left as they are)
+        FusedArgs a{};
+        a.seg[0] = MatSeg{m->router->w, m->router->scales, sc.logits, m->router->rows};
+        a.nseg = 1;
+        a.cols = D;
+        a.rows = E;
+        a.x = x;
+        a.norm_w = norm_w;
+        a.recip_n = recip_n;
+        a.norm_eps = eps;
+        bool ok;
+        {
+            ProfScope p(d, s, "moe_router");
+            ok = launch_fused(kFmtQ8, kProNorm, kEpStore, a, d->cu, s);
+        }
+        if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
+        const int bpl = (D / 32 + 7) / 8;
+        const size_t lds = (size_t)up1_lds_r(D) + (size_t)((E + 3) & ~3) * 4 + norm_lds(D);
+        {
+            ProfScope p(d, s, "moe_up");
+#define RK_UP1(B, P)                                                                                               \
+    RK_LAUNCH((moe_up1_kernel<B, P>), dim3((unsigned)K, (unsigned)(H / 32)), dim3(512), lds, s, x, norm_w, recip_n, \
+              eps, sc.logits, E, K, m->w1, m->s1, m->w3, m->s3, D, H, sc.sel, sc.wsel, sc.gcap, sc.grp, sc.hq,     \
+              sc.hs, sc.hsum)
+            if (E <= 128) {
+                if (bpl <= 2) RK_UP1(2, 2);
+                else if (bpl <= 4) RK_UP1(4, 2);
+                else RK_UP1(8, 2);
+            } else {
+                if (bpl <= 2) RK_UP1(2, kRoutePer);
+                else if (bpl <= 4) RK_UP1(4, kRoutePer);
+                else RK_UP1(8, kRoutePer);
+            }
+#undef RK_UP1
+        }
+        return enqueue_moe_down(m, sc, tokens, out, residual, s);
+    }
     if (norm_w) {
         ProfScope p(d, s, "norm_quant");
         launch_norm_quant(x, m->dim, norm_w, recip_n, eps, qx, xs, xsum, s, tokens);
