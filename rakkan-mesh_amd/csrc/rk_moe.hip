@@ -731,6 +731,39 @@ __global__ __launch_bounds__(256) void moe_down8_kernel(const uint8_t *const *w2
     }
 }
 
+// One token's W2 rows and the sum in one launch: workgroup b takes output
+// rows R·b .. R·b+R-1 (R = 64 / k) of every selected expert (group of eight
+// lanes gi: expert group gi / R, row gi mod R; h read from global), then
+// lane r adds row r's k products in ascending expert order from +0 (the
+// grouping's order) into y, out = y or Canonical(out + y). The same bits as
+// moe_down8_kernel followed by moe_combine_kernel.
+template <int BPL>
+__global__ __launch_bounds__(512) void moe_down1_kernel(const uint8_t *const *w2, const float *const *s2,
+                                                        const int32_t *grp, int gcap, int k, const int8_t *hq,
+                                                        const float *hs, int dim, int hidden, float *out,
+                                                        int residual) {
+    __shared__ float sv[64];
+    const int R = 64 / k;
+    const int tid = threadIdx.x, gi = tid >> 3, rl = tid & 7;
+    const int g = min(gi / R, k - 1), r = gi - (gi / R) * R;
+    const int i = blockIdx.x * R + r;
+    const int nb = hidden >> 5;
+    const int e = grp[1 + g], p = grp[1 + 3 * gcap + grp[1 + gcap + g]];
+    int4 c0[BPL], c1[BPL];
+    float sw[BPL];
+    lane_row_load<BPL>(c0, c1, sw, w2[e] + (int64_t)min(i, dim - 1) * hidden, s2[e] + (int64_t)min(i, dim - 1) * nb,
+                       nb, rl);
+    const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, hq + (int64_t)p * hidden, hs + (int64_t)p * nb, nb, rl));
+    if (rl == 0 && gi < k * R) sv[gi] = v;
+    __syncthreads();
+    if (tid < R && blockIdx.x * R + tid < dim) {
+        float y = 0.0f;
+        for (int q = 0; q < k; q++) y += sv[q * R + tid];
+        float *dst = out + blockIdx.x * R + tid;
+        *dst = residual ? canonical(*dst + y) : y;
+    }
+}
+
 // y_t = Σ o over the token's experts in ascending index, from +0; out_t = y_t,
 // or Canonical(out_t + y_t) (the layer's residual, model.go:608-610).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, int k, const float *o, int dim,
@@ -961,7 +994,23 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
             }
 #undef RK_UP1
         }
-        return enqueue_moe_down(m, sc, tokens, out, residual, s);
+        if (H / 32 > 8 * 8) return enqueue_moe_down(m, sc, tokens, out, residual, s);
+        {
+            ProfScope p(d, s, "moe_down");
+            const int R = 64 / K, hbpl = (H / 32 + 7) / 8;
+            const dim3 grid((unsigned)((D + R - 1) / R));
+            if (hbpl <= 2)
+                RK_LAUNCH(moe_down1_kernel<2>, grid, dim3(512), 0, s, m->w2, m->s2, sc.grp, sc.gcap, K, sc.hq, sc.hs,
+                          D, H, out, residual ? 1 : 0);
+            else if (hbpl <= 4)
+                RK_LAUNCH(moe_down1_kernel<4>, grid, dim3(512), 0, s, m->w2, m->s2, sc.grp, sc.gcap, K, sc.hq, sc.hs,
+                          D, H, out, residual ? 1 : 0);
+            else
+                RK_LAUNCH(moe_down1_kernel<8>, grid, dim3(512), 0, s, m->w2, m->s2, sc.grp, sc.gcap, K, sc.hq, sc.hs,
+                          D, H, out, residual ? 1 : 0);
+        }
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? RK_OK : hip_fail(d, e, "moe launch");
     }
     if (norm_w) {
         ProfScope p(d, s, "norm_quant");
