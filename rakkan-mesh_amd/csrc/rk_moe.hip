@@ -14,11 +14,14 @@
 //
 // Launches: the router's product (on the quantized input; a batch of up to
 // 16 tokens a row per wave, the tokens' codes in LDS); the routing (one wave
-// per token); the grouping of the (token, slot) pairs by expert (counts and
-// places in parallel for up to 128 pairs);
-// each selected expert's W1/W3 rows for all the tokens that chose it, with
-// the gate, the weight and h's quantization; each selected expert's W2 rows
-// for those tokens; the ascending-order sum (optionally into a residual).
+// per token) and the grouping of the (token, slot) pairs by expert (counts
+// and places in parallel for up to 128 pairs), one launch for up to 16
+// tokens; each selected expert's W1/W3 rows for all the tokens that chose
+// it, with the gate, the weight and h's quantization; each selected
+// expert's W2 rows for those tokens; the ascending-order sum (optionally
+// into a residual). One token with its RMSNorm (a decode step): the router
+// with the norm in its prologue, the W1/W3 kernel routing the token itself,
+// and W2 with the sum: three launches.
 // An expert's rows are read from memory once per call however many tokens
 // chose it: a wave loads a chunk of its rows and dots it with each of the
 // group's inputs. Every expert product is a row dot of MatVecQ8 (integer
