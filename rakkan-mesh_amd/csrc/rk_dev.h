@@ -17,6 +17,22 @@ __device__ __forceinline__ int4 load_stream16(const void *p) {
     return make_int4(v.x, v.y, v.z, v.w);
 }
 
+// Loads through a pointer known to be global memory. A pointer read from
+// memory (a table of per-expert rows) is generic to the compiler, which then
+// issues flat loads; those count against the LDS wait counter too, so every
+// wait for an LDS access would also wait for them.
+typedef const __attribute__((address_space(1))) rk_v4i *rk_gv4i;
+typedef const __attribute__((address_space(1))) float *rk_gf;
+__device__ __forceinline__ int4 load_stream16_g(const void *p) {
+    const rk_v4i v = __builtin_nontemporal_load((rk_gv4i)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ int4 load16_g(const void *p) {
+    const rk_v4i v = *(rk_gv4i)p;
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float loadf_g(const float *p) { return *(rk_gf)p; }
+
 // Exact integer sum of a lane pair (quad_perm [1,0,3,2]).
 __device__ __forceinline__ int pair_sum(int s) { return s + __builtin_amdgcn_mov_dpp(s, 0xB1, 0xF, 0xF, false); }
 
@@ -304,7 +320,8 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int i) {
 // ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)) with no other lane exchange. ----
 
 // The row's blocks rl + 8m, m < BPL (clamped into the row: those past it
-// are never summed). STREAM: non-temporal loads, for rows read once.
+// are never summed), row and rs in global memory. STREAM: non-temporal
+// loads, for rows read once.
 template <int BPL, bool STREAM = true>
 __device__ __forceinline__ void lane_row_load(int4 (&c0)[BPL], int4 (&c1)[BPL], float (&sw)[BPL], const uint8_t *row,
                                               const float *rs, int nb, int rl) {
@@ -312,13 +329,13 @@ __device__ __forceinline__ void lane_row_load(int4 (&c0)[BPL], int4 (&c1)[BPL], 
     for (int m = 0; m < BPL; m++) {
         const int b = min(rl + 8 * m, nb - 1);
         if (STREAM) {
-            c0[m] = load_stream16(row + 32 * b);
-            c1[m] = load_stream16(row + 32 * b + 16);
+            c0[m] = load_stream16_g(row + 32 * b);
+            c1[m] = load_stream16_g(row + 32 * b + 16);
         } else {
-            c0[m] = *reinterpret_cast<const int4 *>(row + 32 * b);
-            c1[m] = *reinterpret_cast<const int4 *>(row + 32 * b + 16);
+            c0[m] = load16_g(row + 32 * b);
+            c1[m] = load16_g(row + 32 * b + 16);
         }
-        sw[m] = rs[b];
+        sw[m] = loadf_g(rs + b);
     }
 }
 

@@ -17,6 +17,8 @@ struct MoeScratch {
     int32_t *sel = nullptr;        // [cap][topk] selected experts, selection order
     float *wsel = nullptr;         // [cap][topk] their weights
     int32_t *grp = nullptr;        // groups: count, expert[gcap], start[gcap], pairs[gcap], pair list[cap·topk]
+    float *gwt = nullptr;          // [cap·topk] the pair list's weights (wsel of each listed pair)
+    const void **gptr = nullptr;   // [gcap][6] each group's expert rows: W1, W1 scales, W3, W3 scales, W2, W2 scales
     int8_t *hq = nullptr;          // [cap·topk][hidden] each (token, slot)'s h, quantized
     float *hs = nullptr;
     int32_t *hsum = nullptr;

@@ -67,8 +67,8 @@ __device__ __forceinline__ void wave_rows_q8_multi(const uint8_t *const (&w)[NR]
         float sw[NR];
 #pragma unroll
         for (int r = 0; r < NR; r++) {
-            wv[r] = load_stream16(w[r] + o);
-            sw[r] = ws[r][o >> 5];
+            wv[r] = load_stream16_g(w[r] + o);  // (table pointers: global loads, not flat)
+            sw[r] = loadf_g(ws[r] + (o >> 5));
         }
         const int b0 = c * 32 + (lane >> 1);
 #pragma unroll
@@ -262,6 +262,22 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
                           wsel + (int64_t)t * k, wt);
 }
 
+// The experts' row tables, and group g's rows written beside the grouping
+// (so the expert kernels find their rows with one load, not two).
+struct MoeTabs {
+    const uint8_t *const *w1, *const *w3, *const *w2;
+    const float *const *s1, *const *s3, *const *s2;
+};
+__device__ __forceinline__ void group_rows(const MoeTabs &tb, int g, int e, const void **gptr) {
+    const void **d = gptr + 6 * g;
+    d[0] = tb.w1[e];
+    d[1] = tb.s1[e];
+    d[2] = tb.w3[e];
+    d[3] = tb.s3[e];
+    d[4] = tb.w2[e];
+    d[5] = tb.s2[e];
+}
+
 // The (token, slot) pairs grouped by expert: grp[0] = the number of experts
 // selected, then at grp + 1 + g, + gcap, + 2·gcap their index (ascending),
 // first entry in the pair list and count, and the pair list from
@@ -269,8 +285,9 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
 // thread e counts expert e's pairs, reading the selection from LDS (staged
 // there first when it fits kGroupLdsPairs).
 constexpr int kGroupLdsPairs = 8192;
-__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel_g, int npairs, int experts, int gcap,
-                                                         int32_t *grp) {
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel_g, const float *wsel, int npairs,
+                                                         int experts, int gcap, int32_t *grp, float *gwt, MoeTabs tb,
+                                                         const void **gptr) {
     __shared__ int s_cnt[1024], s_any[1024];
     extern __shared__ int s_selp[];
     const int e = threadIdx.x;
@@ -296,12 +313,16 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel_g, i
     int32_t *gexp = grp + 1, *gstart = grp + 1 + gcap, *gcount = grp + 1 + 2 * gcap, *list = grp + 1 + 3 * gcap;
     if (cnt > 0) {
         const int g = s_any[e] - 1, start = s_cnt[e] - cnt;
+        group_rows(tb, g, e, gptr);
         gexp[g] = e;
         gstart[g] = start;
         gcount[g] = cnt;
         int k = 0;
         for (int p = 0; p < npairs; p++)
-            if (sel[p] == e) list[start + k++] = p;
+            if (sel[p] == e) {
+                gwt[start + k] = wsel[p];
+                list[start + k++] = p;
+            }
     }
     if (e == 1023) grp[0] = s_any[1023];
 }
@@ -316,7 +337,8 @@ constexpr int kGroupFastPairs = 128;
 struct GroupLds {
     int cnt[1024], start[1024], gi[1024], total;
 };
-__device__ void group_pairs_wg(const int *s_sel, int npairs, int experts, int gcap, int32_t *grp, GroupLds &gl) {
+__device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, int experts, int gcap, int32_t *grp,
+                               float *gwt, const MoeTabs &tb, const void **gptr, GroupLds &gl) {
     const int tid = threadIdx.x, lane = tid & 63;
     gl.cnt[tid] = 0;
     __syncthreads();
@@ -362,6 +384,7 @@ __device__ void group_pairs_wg(const int *s_sel, int npairs, int experts, int gc
         gexp[g] = tid;
         gstart[g] = gl.start[tid];
         gcount[g] = gl.cnt[tid];
+        group_rows(tb, g, tid, gptr);
     }
     // pair p's place: the earlier pairs of its expert (eight threads a pair)
     const int p = tid >> 3, part = tid & 7;
@@ -372,18 +395,26 @@ __device__ void group_pairs_wg(const int *s_sel, int npairs, int experts, int gc
         n += dpp_x1(n);
         n += dpp_x2(n);
         n += dpp_mirror8(n);
-        if (part == 0) list[gl.start[e] + n] = p;
+        if (part == 0) {
+            list[gl.start[e] + n] = p;
+            gwt[gl.start[e] + n] = s_wt[p];
+        }
     }
     if (tid == 0) grp[0] = gl.total;
 }
 
-__global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel, int npairs, int experts, int gcap,
-                                                              int32_t *grp) {
+__global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel, const float *wsel, int npairs,
+                                                              int experts, int gcap, int32_t *grp, float *gwt,
+                                                              MoeTabs tb, const void **gptr) {
     __shared__ int s_sel[kGroupFastPairs];
+    __shared__ float s_wt[kGroupFastPairs];
     __shared__ GroupLds gl;
-    if ((int)threadIdx.x < npairs) s_sel[threadIdx.x] = sel[threadIdx.x];
+    if ((int)threadIdx.x < npairs) {
+        s_sel[threadIdx.x] = sel[threadIdx.x];
+        s_wt[threadIdx.x] = wsel[threadIdx.x];
+    }
     __syncthreads();
-    group_pairs_wg(s_sel, npairs, experts, gcap, grp, gl);
+    group_pairs_wg(s_sel, s_wt, npairs, experts, gcap, grp, gwt, tb, gptr, gl);
 }
 
 // Routing (wave t: token t) and grouping of up to kSelectTokens tokens in
@@ -391,9 +422,11 @@ __global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel
 constexpr int kSelectTokens = 16;
 template <int PER>
 __global__ __launch_bounds__(1024) void moe_select_kernel(const float *logits, int tokens, int experts, int k,
-                                                          int32_t *sel, float *wsel, int gcap, int32_t *grp) {
+                                                          int32_t *sel, float *wsel, int gcap, int32_t *grp,
+                                                          float *gwt, MoeTabs tb, const void **gptr) {
     extern __shared__ __align__(16) float sp_all[];
     __shared__ int s_sel[kGroupFastPairs];
+    __shared__ float s_wt[kGroupFastPairs];
     __shared__ GroupLds gl;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ep = (experts + 3) & ~3;
@@ -402,9 +435,12 @@ __global__ __launch_bounds__(1024) void moe_select_kernel(const float *logits, i
     float wt;
     const int mine = route_wave<PER>(live, logits + (int64_t)t * experts, experts, k, sp_all + t * ep,
                                      sel + (int64_t)t * k, wsel + (int64_t)t * k, wt);
-    if (live && lane < k) s_sel[t * k + lane] = mine;
+    if (live && lane < k) {
+        s_sel[t * k + lane] = mine;
+        s_wt[t * k + lane] = wt;
+    }
     __syncthreads();
-    group_pairs_wg(s_sel, tokens * k, experts, gcap, grp, gl);
+    group_pairs_wg(s_sel, s_wt, tokens * k, experts, gcap, grp, gwt, tb, gptr, gl);
 }
 
 // W1 and W3 rows of a selected expert for every pair that chose it:
@@ -541,49 +577,99 @@ __device__ __forceinline__ float row_shl8(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x108, 0xF, 0xF, false));
 }
 
-template <int BPL>
-__global__ __launch_bounds__(512) void moe_up8_kernel(const uint8_t *const *w1, const float *const *s1,
-                                                      const uint8_t *const *w3, const float *const *s3,
-                                                      const int32_t *grp, int gcap, const float *wsel, int k,
-                                                      const int8_t *qx, const float *xs, int dim, int hidden,
-                                                      int8_t *hq, float *hs, int32_t *hsum) {
+// LDS of moe_up8_kernel for inputs `dim` wide: kExpTok inputs' codes and
+// scales (each region padded by a stripe of direct-to-LDS loads), h, the
+// pass's pairs and their weights.
+__host__ __device__ constexpr int up8_q_bytes(int dim) { return kExpTok * dim + 1024; }
+__host__ __device__ constexpr int up8_s_bytes(int dim) { return kExpTok * (dim >> 5) * 4 + 256; }
+__host__ __device__ constexpr int up8_lds(int dim) {
+    return up8_q_bytes(dim) + up8_s_bytes(dim) + kExpTok * 32 * 4 + kExpTok * 8;
+}
+
+// ALL: the call's tokens (at most kExpTok) are staged in LDS at the start,
+// every one of them, so the staging does not wait for the pair list; else
+// each pass stages its own pairs' inputs. The group's rows, count and list
+// are found with one load each (the grouping wrote the rows' addresses).
+template <int BPL, bool ALL>
+__global__ __launch_bounds__(512) void moe_up8_kernel(const void *const *gptr, const int32_t *grp, int gcap,
+                                                      const float *gwt, int k, const int8_t *qx, const float *xs,
+                                                      int tokens, int dim, int hidden, int8_t *hq, float *hs,
+                                                      int32_t *hsum) {
     extern __shared__ __align__(16) char ulds[];
-    const int g = blockIdx.x;
-    if (g >= grp[0]) return;  // uniform
-    const int e = grp[1 + g], start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
-    const int32_t *list = grp + 1 + 3 * gcap + start;
+    const int g = blockIdx.y;  // groups slowest: the live groups are dispatched first
     const int nb = dim >> 5;
-    int8_t *sq = reinterpret_cast<int8_t *>(ulds);                        // [kExpTok][dim] codes
-    float *sxs = reinterpret_cast<float *>(ulds + kExpTok * dim);          // [kExpTok][nb] scales
-    float *sh = sxs + kExpTok * nb;                                        // [kExpTok][32] h
-    int *spair = reinterpret_cast<int *>(sh + kExpTok * 32);               // [kExpTok] pairs
+    int8_t *sq = reinterpret_cast<int8_t *>(ulds);                                  // [kExpTok][dim] codes
+    float *sxs = reinterpret_cast<float *>(ulds + up8_q_bytes(dim));                 // [kExpTok][nb] scales
+    float *sh = reinterpret_cast<float *>(ulds + up8_q_bytes(dim) + up8_s_bytes(dim));  // [kExpTok][32] h
+    int *spair = reinterpret_cast<int *>(sh + kExpTok * 32);                         // [kExpTok] pairs
+    float *swt = reinterpret_cast<float *>(spair + kExpTok);                         // [kExpTok] their weights
+    // independent loads first: the group count, this group's rows, start, count
+    const int ngroups = grp[0];
+    const uint8_t *w1 = static_cast<const uint8_t *>(gptr[6 * g]);
+    const float *s1 = static_cast<const float *>(gptr[6 * g + 1]);
+    const uint8_t *w3 = static_cast<const uint8_t *>(gptr[6 * g + 2]);
+    const float *s3 = static_cast<const float *>(gptr[6 * g + 3]);
+    const int start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
+    if (g >= ngroups) return;  // uniform
+    const int32_t *list = grp + 1 + 3 * gcap + start;
+    const float *lwt = gwt + start;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rg = lane >> 3, rl = lane & 7, q = rg >> 1;
-    const int j = blockIdx.y * 32 + 4 * wave + q;  // hidden is a multiple of 32
+    const int j = blockIdx.x * 32 + 4 * wave + q;  // hidden is a multiple of 32
     const bool w3row = rg & 1;
+    // the first pass's pairs and weights, then (ALL) every token's input,
+    // then the rows: loads return in issue order
+    int lp = 0;
+    float lw = 0.0f;
+    if (tid < min(kExpTok, count)) {
+        lp = list[tid];
+        lw = lwt[tid];
+    }
+    if (ALL) {
+        // stripes of 64 pieces a wave; a last stripe's surplus lanes repeat
+        // the last piece into the padding after the region
+        const int nq = (tokens * dim) >> 4, ns = tokens * nb;
+        for (int p0 = wave * 64; p0 < nq; p0 += 512)
+            __builtin_amdgcn_global_load_lds(qx + 16 * min(p0 + lane, nq - 1), lds_ptr(sq + 16 * p0), 16, 0, 0);
+        for (int p0 = wave * 64; p0 < ns; p0 += 512)
+            __builtin_amdgcn_global_load_lds(xs + min(p0 + lane, ns - 1), lds_ptr(sxs + p0), 4, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, (w3row ? w3[e] : w1[e]) + (int64_t)j * dim,
-                       (w3row ? s3[e] : s1[e]) + (int64_t)j * nb, nb, rl);
+    lane_row_load<BPL>(c0, c1, sw, (w3row ? w3 : w1) + (int64_t)j * dim, (w3row ? s3 : s1) + (int64_t)j * nb, nb, rl);
+    __builtin_amdgcn_sched_barrier(0);
     const int n16 = dim >> 4;
     for (int p0 = 0; p0 < count; p0 += kExpTok) {
         const int np = min(kExpTok, count - p0);
-        if (tid < np) spair[tid] = list[p0 + tid];
-        __syncthreads();
-        for (int i = tid; i < np * n16; i += 512) {
-            const int pi = i / n16, off = i - pi * n16;
-            reinterpret_cast<int4 *>(sq)[i] = reinterpret_cast<const int4 *>(qx + (int64_t)(spair[pi] / k) * dim)[off];
+        if (p0 > 0 && tid < np) {
+            lp = list[p0 + tid];
+            lw = lwt[p0 + tid];
         }
-        for (int i = tid; i < np * nb; i += 512) {
-            const int pi = i / nb, b = i - pi * nb;
-            sxs[i] = xs[(int64_t)(spair[pi] / k) * nb + b];
+        if (tid < np) {
+            spair[tid] = lp;
+            swt[tid] = lw;
         }
+        if (ALL) __builtin_amdgcn_s_waitcnt(0);  // the direct-to-LDS loads (and the rows) have landed
         __syncthreads();
+        if (!ALL) {
+            for (int i = tid; i < np * n16; i += 512) {
+                const int pi = i / n16, off = i - pi * n16;
+                reinterpret_cast<int4 *>(sq)[i] =
+                    reinterpret_cast<const int4 *>(qx + (int64_t)(spair[pi] / k) * dim)[off];
+            }
+            for (int i = tid; i < np * nb; i += 512) {
+                const int pi = i / nb, b = i - pi * nb;
+                sxs[i] = xs[(int64_t)(spair[pi] / k) * nb + b];
+            }
+            __syncthreads();
+        }
         for (int pi = 0; pi < np; pi++) {
-            const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq + pi * dim, sxs + pi * nb, nb, rl));
+            const int u = ALL ? spair[pi] / k : pi;  // the input's place in LDS
+            const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq + u * dim, sxs + u * nb, nb, rl));
             const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
-            if ((lane & 15) == 0) sh[pi * 32 + 4 * wave + q] = wsel[spair[pi]] * silu_mul(v, v3);
+            if ((lane & 15) == 0) sh[pi * 32 + 4 * wave + q] = swt[pi] * silu_mul(v, v3);
         }
         __syncthreads();
         // each pair's block of h: wave w takes pairs w, w+8, ...; lanes 0-7
@@ -593,7 +679,7 @@ __global__ __launch_bounds__(512) void moe_up8_kernel(const uint8_t *const *w1, 
             float d;
             int cs;
             const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
-            const int64_t base = (int64_t)spair[pi] * hidden + blockIdx.y * 32;
+            const int64_t base = (int64_t)spair[pi] * hidden + blockIdx.x * 32;
             if (lane < 8) {
                 reinterpret_cast<uint32_t *>(hq + base)[lane] = pk;
                 if (lane == 0) {
@@ -693,13 +779,17 @@ __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const floa
 }
 
 template <int BPL>
-__global__ __launch_bounds__(256) void moe_down8_kernel(const uint8_t *const *w2, const float *const *s2,
-                                                        const int32_t *grp, int gcap, const int8_t *hq, const float *hs,
-                                                        int dim, int hidden, float *o) {
+__global__ __launch_bounds__(256) void moe_down8_kernel(const void *const *gptr, const int32_t *grp, int gcap,
+                                                        const int8_t *hq, const float *hs, int dim, int hidden,
+                                                        float *o) {
     extern __shared__ __align__(16) char dlds[];
-    const int g = blockIdx.x;
-    if (g >= grp[0]) return;  // uniform
-    const int e = grp[1 + g], start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
+    const int g = blockIdx.y;  // groups slowest: the live groups are dispatched first
+    // independent loads first: the group count, this group's rows, start, count
+    const int ngroups = grp[0];
+    const uint8_t *w2 = static_cast<const uint8_t *>(gptr[6 * g + 4]);
+    const float *s2 = static_cast<const float *>(gptr[6 * g + 5]);
+    const int start = grp[1 + gcap + g], count = grp[1 + 2 * gcap + g];
+    if (g >= ngroups) return;  // uniform
     const int32_t *list = grp + 1 + 3 * gcap + start;
     const int nb = hidden >> 5;
     int8_t *sq = reinterpret_cast<int8_t *>(dlds);                        // [kExpTok][hidden] codes
@@ -707,15 +797,22 @@ __global__ __launch_bounds__(256) void moe_down8_kernel(const uint8_t *const *w2
     int *spair = reinterpret_cast<int *>(sxs + kExpTok * nb);              // [kExpTok] pairs
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rg = lane >> 3, rl = lane & 7;
-    const int i = blockIdx.y * 32 + 8 * wave + rg;
+    const int i = blockIdx.x * 32 + 8 * wave + rg;
+    // the first pass's pairs, requested before the rows (loads return in
+    // issue order)
+    int lp = 0;
+    if (tid < min(kExpTok, count)) lp = list[tid];
+    __builtin_amdgcn_sched_barrier(0);
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, w2[e] + (int64_t)min(i, dim - 1) * hidden,
-                       s2[e] + (int64_t)min(i, dim - 1) * nb, nb, rl);
+    lane_row_load<BPL>(c0, c1, sw, w2 + (int64_t)min(i, dim - 1) * hidden, s2 + (int64_t)min(i, dim - 1) * nb, nb,
+                       rl);
+    __builtin_amdgcn_sched_barrier(0);
     const int n16 = hidden >> 4;
     for (int p0 = 0; p0 < count; p0 += kExpTok) {
         const int np = min(kExpTok, count - p0);
-        if (tid < np) spair[tid] = list[p0 + tid];
+        if (p0 > 0 && tid < np) lp = list[p0 + tid];
+        if (tid < np) spair[tid] = lp;
         __syncthreads();
         for (int u = tid; u < np * n16; u += 256) {
             const int pi = u / n16, off = u - pi * n16;
@@ -808,6 +905,8 @@ int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc) 
     s.sel = reinterpret_cast<int32_t *>(take(4 * T * K));
     s.wsel = reinterpret_cast<float *>(take(4 * T * K));
     s.grp = reinterpret_cast<int32_t *>(take(4 * (1 + 3 * G + T * K)));
+    s.gwt = reinterpret_cast<float *>(take(4 * T * K));
+    s.gptr = reinterpret_cast<const void **>(take(8 * 6 * G));
     s.hq = reinterpret_cast<int8_t *>(take(T * K * H));
     s.hs = reinterpret_cast<float *>(take(4 * T * K * (H / 32)));
     s.hsum = reinterpret_cast<int32_t *>(take(4 * T * K * (H / 32)));
@@ -858,6 +957,7 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
     }
     if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
     const int npairs = tokens * K;
+    const MoeTabs tabs{m->w1, m->w3, m->w2, m->s1, m->s3, m->s2};
     if (tokens <= kSelectTokens && npairs <= kGroupFastPairs && E <= 1024) {
         static std::once_flag once;
         std::call_once(once, [] {
@@ -868,10 +968,10 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
         const size_t lds = (size_t)tokens * ((E + 3) & ~3) * 4;
         if (E <= 128)
             RK_LAUNCH(moe_select_kernel<2>, dim3(1), dim3(1024), lds, s, sc.logits, tokens, E, K, sc.sel, sc.wsel,
-                      sc.gcap, sc.grp);
+                      sc.gcap, sc.grp, sc.gwt, tabs, sc.gptr);
         else
             RK_LAUNCH(moe_select_kernel<kRoutePer>, dim3(1), dim3(1024), lds, s, sc.logits, tokens, E, K, sc.sel,
-                      sc.wsel, sc.gcap, sc.grp);
+                      sc.wsel, sc.gcap, sc.grp, sc.gwt, tabs, sc.gptr);
         return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s);
     }
     {
@@ -885,10 +985,11 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
     {
         ProfScope p(d, s, "moe_group");
         if (npairs <= kGroupFastPairs && E <= 1024)
-            RK_LAUNCH(moe_group_fast_kernel, dim3(1), dim3(1024), 0, s, sc.sel, npairs, E, sc.gcap, sc.grp);
+            RK_LAUNCH(moe_group_fast_kernel, dim3(1), dim3(1024), 0, s, sc.sel, sc.wsel, npairs, E, sc.gcap, sc.grp,
+                      sc.gwt, tabs, sc.gptr);
         else
             RK_LAUNCH(moe_group_kernel, dim3(1), dim3(1024), npairs <= kGroupLdsPairs ? (size_t)npairs * 4 : 0, s,
-                      sc.sel, npairs, E, sc.gcap, sc.grp);
+                      sc.sel, sc.wsel, npairs, E, sc.gcap, sc.grp, sc.gwt, tabs, sc.gptr);
     }
     return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s);
 }
@@ -902,20 +1003,26 @@ static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx
     {
         ProfScope p(d, s, "moe_up");
         const int bpl = (D / 32 + 7) / 8;  // blocks of a W1/W3 row per lane
-        const size_t lds = (size_t)kExpTok * (D + (D / 32) * 4 + 32 * 4 + 4);
-        const dim3 grid((unsigned)groups, (unsigned)(H / 32));
-        if (bpl <= 2)
-            RK_LAUNCH(moe_up8_kernel<2>, grid, dim3(512), lds, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel,
-                      K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
-        else if (bpl <= 4)
-            RK_LAUNCH(moe_up8_kernel<4>, grid, dim3(512), lds, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel,
-                      K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
-        else if (bpl <= 8)
-            RK_LAUNCH(moe_up8_kernel<8>, grid, dim3(512), lds, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel,
-                      K, qx, xs, D, H, sc.hq, sc.hs, sc.hsum);
-        else
+        const dim3 grid8((unsigned)(H / 32), (unsigned)groups), grid((unsigned)groups, (unsigned)(H / 32));
+        const bool all = tokens <= kExpTok;
+        const size_t lds = (size_t)up8_lds(D);
+#define RK_UP8(B, A)                                                                                                 \
+    RK_LAUNCH((moe_up8_kernel<B, A>), grid8, dim3(512), lds, s, sc.gptr, sc.grp, sc.gcap, sc.gwt, K, qx, xs, tokens, D, \
+              H, sc.hq, sc.hs, sc.hsum)
+        if (bpl <= 2) {
+            if (all) RK_UP8(2, true);
+            else RK_UP8(2, false);
+        } else if (bpl <= 4) {
+            if (all) RK_UP8(4, true);
+            else RK_UP8(4, false);
+        } else if (bpl <= 8) {
+            if (all) RK_UP8(8, true);
+            else RK_UP8(8, false);
+        } else {
             RK_LAUNCH(moe_up_kernel, grid, dim3(512), 0, s, m->w1, m->s1, m->w3, m->s3, sc.grp, sc.gcap, sc.wsel, K, qx,
                       xs, D, H, sc.hq, sc.hs, sc.hsum);
+        }
+#undef RK_UP8
     }
     return enqueue_moe_down(m, sc, tokens, out, residual, s);
 }
@@ -929,15 +1036,15 @@ static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *
         ProfScope p(d, s, "moe_down");
         const int bpl = (H / 32 + 7) / 8;  // blocks of a W2 row per lane
         const size_t lds = (size_t)kExpTok * (H + (H / 32) * 4 + 4);
-        const dim3 grid((unsigned)groups, (unsigned)((D + 31) / 32));
+        const dim3 grid((unsigned)((D + 31) / 32), (unsigned)groups);
         if (bpl <= 2)
-            RK_LAUNCH(moe_down8_kernel<2>, grid, dim3(256), lds, s, m->w2, m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
+            RK_LAUNCH(moe_down8_kernel<2>, grid, dim3(256), lds, s, sc.gptr, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
                       sc.o);
         else if (bpl <= 4)
-            RK_LAUNCH(moe_down8_kernel<4>, grid, dim3(256), lds, s, m->w2, m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
+            RK_LAUNCH(moe_down8_kernel<4>, grid, dim3(256), lds, s, sc.gptr, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
                       sc.o);
         else if (bpl <= 8)
-            RK_LAUNCH(moe_down8_kernel<8>, grid, dim3(256), lds, s, m->w2, m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
+            RK_LAUNCH(moe_down8_kernel<8>, grid, dim3(256), lds, s, sc.gptr, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
                       sc.o);
         else
             RK_LAUNCH(moe_down_kernel, dim3((unsigned)groups, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2,
