@@ -278,75 +278,20 @@ __device__ __forceinline__ void group_rows(const MoeTabs &tb, int g, int e, cons
     d[5] = tb.s2[e];
 }
 
-// The (token, slot) pairs grouped by expert: grp[0] = the number of experts
-// selected, then at grp + 1 + g, + gcap, + 2·gcap their index (ascending),
-// first entry in the pair list and count, and the pair list from
-// grp + 1 + 3·gcap (each group's pairs in ascending order). One workgroup;
-// thread e counts expert e's pairs, reading the selection from LDS (staged
-// there first when it fits kGroupLdsPairs).
-constexpr int kGroupLdsPairs = 8192;
-__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel_g, const float *wsel, int npairs,
-                                                         int experts, int gcap, int32_t *grp, float *gwt, MoeTabs tb,
-                                                         const void **gptr) {
-    __shared__ int s_cnt[1024], s_any[1024];
-    extern __shared__ int s_selp[];
-    const int e = threadIdx.x;
-    const bool staged = npairs <= kGroupLdsPairs;
-    if (staged)
-        for (int p = e; p < npairs; p += 1024) s_selp[p] = sel_g[p];
-    __syncthreads();
-    const int32_t *sel = staged ? s_selp : sel_g;
-    int cnt = 0;
-    if (e < experts)
-        for (int p = 0; p < npairs; p++) cnt += sel[p] == e;
-    s_cnt[e] = cnt;
-    s_any[e] = cnt > 0;
-    __syncthreads();
-    // inclusive scans (Hillis-Steele) of the counts and of the group marks
-    for (int d = 1; d < 1024; d <<= 1) {
-        const int c = e >= d ? s_cnt[e - d] : 0, a = e >= d ? s_any[e - d] : 0;
-        __syncthreads();
-        s_cnt[e] += c;
-        s_any[e] += a;
-        __syncthreads();
-    }
-    int32_t *gexp = grp + 1, *gstart = grp + 1 + gcap, *gcount = grp + 1 + 2 * gcap, *list = grp + 1 + 3 * gcap;
-    if (cnt > 0) {
-        const int g = s_any[e] - 1, start = s_cnt[e] - cnt;
-        group_rows(tb, g, e, gptr);
-        gexp[g] = e;
-        gstart[g] = start;
-        gcount[g] = cnt;
-        int k = 0;
-        for (int p = 0; p < npairs; p++)
-            if (sel[p] == e) {
-                gwt[start + k] = wsel[p];
-                list[start + k++] = p;
-            }
-    }
-    if (e == 1023) grp[0] = s_any[1023];
-}
-
-// The same grouping for up to kGroupFastPairs pairs and 1024 experts, with
-// no thread walking all the pairs: counts by LDS atomics, one wave's scans
-// over the experts (starts and group indices), and each pair's place among
-// its expert's pairs from the earlier pairs (eight threads a pair). Every
-// thread of a 1024-thread workgroup calls it; s_sel: the pairs' experts in
-// LDS, written before a barrier.
 constexpr int kGroupFastPairs = 128;
 struct GroupLds {
     int cnt[1024], start[1024], gi[1024], total;
 };
-__device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, int experts, int gcap, int32_t *grp,
-                               float *gwt, const MoeTabs &tb, const void **gptr, GroupLds &gl) {
+
+// The scans over the experts' counts (one wave; lane l takes experts
+// l·per .. l·per+per-1: local sums, then an exclusive scan of the lane
+// totals across the wave): each expert's first place and group index, and
+// the number of groups. Then each selected expert's group entry and rows.
+// Every thread of a 1024-thread workgroup calls it, after the counts.
+__device__ void group_scan_info(GroupLds &gl, int experts, int gcap, int32_t *grp, const MoeTabs &tb,
+                                const void **gptr) {
     const int tid = threadIdx.x, lane = tid & 63;
-    gl.cnt[tid] = 0;
-    __syncthreads();
-    if (tid < npairs) atomicAdd(&gl.cnt[s_sel[tid]], 1);
-    __syncthreads();
     if (tid < 64) {
-        // lane l takes experts l·per .. l·per+per-1: local sums, then an
-        // exclusive scan of the lane totals across the wave
         const int per = (experts + 63) / 64;
         int c = 0, g = 0;
         for (int i = 0; i < per; i++) {
@@ -378,7 +323,7 @@ __device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, 
         if (lane == 63) gl.total = gi;
     }
     __syncthreads();
-    int32_t *gexp = grp + 1, *gstart = grp + 1 + gcap, *gcount = grp + 1 + 2 * gcap, *list = grp + 1 + 3 * gcap;
+    int32_t *gexp = grp + 1, *gstart = grp + 1 + gcap, *gcount = grp + 1 + 2 * gcap;
     if (tid < experts && gl.cnt[tid] > 0) {
         const int g = gl.gi[tid];
         gexp[g] = tid;
@@ -386,7 +331,56 @@ __device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, 
         gcount[g] = gl.cnt[tid];
         group_rows(tb, g, tid, gptr);
     }
+    if (tid == 0) grp[0] = gl.total;
+}
+
+// The (token, slot) pairs grouped by expert: grp[0] = the number of experts
+// selected, then at grp + 1 + g, + gcap, + 2·gcap their index (ascending),
+// first entry in the pair list and count, and the pair list from
+// grp + 1 + 3·gcap, with the listed pairs' weights in gwt and each group's
+// rows in gptr. One workgroup, any number of pairs: counts by LDS atomics,
+// the scans, then each pair's place by a ticket of its expert's count. The
+// order of a group's pairs is then not fixed; no result depends on it (each
+// pair's products are its own, and the sum over a token's experts follows
+// the experts' order).
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, const float *wsel, int npairs,
+                                                         int experts, int gcap, int32_t *grp, float *gwt, MoeTabs tb,
+                                                         const void **gptr) {
+    __shared__ GroupLds gl;
+    __shared__ int fill[1024];
+    const int tid = threadIdx.x;
+    gl.cnt[tid] = 0;
+    fill[tid] = 0;
+    __syncthreads();
+    for (int p = tid; p < npairs; p += 1024) atomicAdd(&gl.cnt[sel[p]], 1);
+    __syncthreads();
+    group_scan_info(gl, experts, gcap, grp, tb, gptr);
+    int32_t *list = grp + 1 + 3 * gcap;
+    for (int p = tid; p < npairs; p += 1024) {
+        const int e = sel[p];
+        const float w = wsel[p];
+        const int at = gl.start[e] + atomicAdd(&fill[e], 1);
+        list[at] = p;
+        gwt[at] = w;
+    }
+}
+
+// The same grouping for up to kGroupFastPairs pairs and 1024 experts, with
+// no thread walking all the pairs: counts by LDS atomics, one wave's scans
+// over the experts (starts and group indices), and each pair's place among
+// its expert's pairs from the earlier pairs (eight threads a pair). Every
+// thread of a 1024-thread workgroup calls it; s_sel: the pairs' experts in
+// LDS, written before a barrier.
+__device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, int experts, int gcap, int32_t *grp,
+                               float *gwt, const MoeTabs &tb, const void **gptr, GroupLds &gl) {
+    const int tid = threadIdx.x;
+    gl.cnt[tid] = 0;
+    __syncthreads();
+    if (tid < npairs) atomicAdd(&gl.cnt[s_sel[tid]], 1);
+    __syncthreads();
+    group_scan_info(gl, experts, gcap, grp, tb, gptr);
     // pair p's place: the earlier pairs of its expert (eight threads a pair)
+    int32_t *list = grp + 1 + 3 * gcap;
     const int p = tid >> 3, part = tid & 7;
     if (p < npairs) {  // whole groups of eight
         const int e = s_sel[p];
@@ -400,7 +394,6 @@ __device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, 
             gwt[gl.start[e] + n] = s_wt[p];
         }
     }
-    if (tid == 0) grp[0] = gl.total;
 }
 
 __global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel, const float *wsel, int npairs,
@@ -988,7 +981,7 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
             RK_LAUNCH(moe_group_fast_kernel, dim3(1), dim3(1024), 0, s, sc.sel, sc.wsel, npairs, E, sc.gcap, sc.grp,
                       sc.gwt, tabs, sc.gptr);
         else
-            RK_LAUNCH(moe_group_kernel, dim3(1), dim3(1024), npairs <= kGroupLdsPairs ? (size_t)npairs * 4 : 0, s,
+            RK_LAUNCH(moe_group_kernel, dim3(1), dim3(1024), 0, s,
                       sc.sel, sc.wsel, npairs, E, sc.gcap, sc.grp, sc.gwt, tabs, sc.gptr);
     }
     return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s);
