@@ -1123,15 +1123,16 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
     const bool vec = hs % 4 == 0 && kv_dim % 4 == 0;
     if (ctx <= kValShortCtx) {
         // short contexts: 128-position chunks (a third of the LDS, four
-        // workgroups a CU)
+        // workgroups a CU); up to one chunk, one tile (eight a CU)
+        const size_t lds = ctx <= kValShortChunk
+                               ? (size_t)(ctx_pad + kValSlice * val_pitch(kValShortChunk)) * 4
+                               : att_values_lds(ctx, kValShortChunk);
         if (vec)
-            RK_LAUNCH((att_values_kernel<true, kValShortChunk>), grid, dim3(kValThreads),
-                      att_values_lds(ctx, kValShortChunk), s, att, att_stride, vals, out, ctl, bt, heads / kv_heads, hs,
-                      kv_dim, ctx_pad, qx, xs, xsum);
+            RK_LAUNCH((att_values_kernel<true, kValShortChunk>), grid, dim3(kValThreads), lds, s, att, att_stride, vals,
+                      out, ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
         else
-            RK_LAUNCH((att_values_kernel<false, kValShortChunk>), grid, dim3(kValThreads),
-                      att_values_lds(ctx, kValShortChunk), s, att, att_stride, vals, out, ctl, bt, heads / kv_heads, hs,
-                      kv_dim, ctx_pad, qx, xs, xsum);
+            RK_LAUNCH((att_values_kernel<false, kValShortChunk>), grid, dim3(kValThreads), lds, s, att, att_stride,
+                      vals, out, ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
         return;
     }
     if (ctx <= kVrMaxCtx && hs % 32 == 0 && kv_dim % 4 == 0 && (reinterpret_cast<uintptr_t>(vals) & 15) == 0) {

@@ -487,12 +487,13 @@ static void launch_rows_epi(int tpg, const MmArgs &a, int ntg, unsigned grid, hi
 
 // The small-batch kernel when it takes the product: Q8, a plain epilogue,
 // at most kRowsMaxT tokens, and the staged inputs within LDS. Tokens per
-// workgroup: the fewest runs that still give about 1024 workgroups.
+// workgroup: halved (down to 2) while the workgroups still fit one round of
+// about 1024 (four a CU).
 static bool launch_rows(int fmt, int epi, const MmArgs &a, hipStream_t s) {
     if (fmt != kFmtQ8 || a.tokens > kRowsMaxT || (epi != kEpStore && epi != kEpAdd && epi != kEpAddCanon)) return false;
     const int64_t nrt = (a.rows + kRowsPerWg - 1) / kRowsPerWg;
     int tpg = kRowsMaxT;
-    while (tpg > 2 && (tpg >= 2 * a.tokens || nrt * ((a.tokens + tpg - 1) / tpg) < 1024)) tpg >>= 1;
+    while (tpg > 2 && (tpg >= 2 * a.tokens || nrt * ((a.tokens + tpg / 2 - 1) / (tpg / 2)) <= 1024)) tpg >>= 1;
     if (rows_lds(tpg, a.cols) > 160 * 1024) return false;
     const int ntg = (a.tokens + tpg - 1) / tpg;
     const int64_t grid = ((nrt * ntg + 7) / 8) * 8;
