@@ -63,12 +63,14 @@ def test_matmul_segments_and_formats(dev):
         m.free()
 
 
-@pytest.mark.parametrize("tokens", [1, 2, 3, 7, 8, 9, 16])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 7, 8, 9, 16, 17, 33, 64])
 def test_small_batches_of_q8_rows(dev, tokens):
     """Up to 16 tokens of Q8 rows take the small-batch kernel (eight lanes a
-    row, pieces of 64 blocks): rows not a multiple of the 32 a workgroup
-    owns, widths of one block, of a ragged last piece (65 and 129 blocks)
-    and of 4096 columns, and three matrices concatenated in one launch."""
+    row, pieces of 64 blocks), and up to 64 when the 64 x 64 MFMA tiles
+    would cover few CUs (every shape here): rows not a multiple of the 32 a
+    workgroup owns, widths of one block, of a ragged last piece (65 and 129
+    blocks) and of 4096 columns, and three matrices concatenated in one
+    launch."""
     rng = np.random.default_rng(700 + tokens)
     for rows, cols in [(1, 32), (45, 2080), (130, 4096), (700, 4128), (3000, 256)]:
         w = awkward(rng, rows * cols, 0.05)
