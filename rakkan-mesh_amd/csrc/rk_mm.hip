@@ -486,16 +486,17 @@ static void launch_rows_epi(int tpg, const MmArgs &a, int ntg, unsigned grid, hi
 }
 
 // The small-batch kernel when it takes the product: Q8, a plain epilogue,
-// at most kRowsMaxT tokens (or up to kRowsWideT when the 64 x 64 tiles
-// would cover under half the CUs), and the staged inputs within LDS. Tokens
-// per workgroup: halved (down to 2) while the workgroups still fit one
-// round of about 1024 (four a CU).
+// at most kRowsMaxT tokens, or up to kRowsWideT when the product is small
+// enough (rows·tokens up to kRowsWideWork: measured on MI355X, the 64 x 64
+// tiles then cover few CUs and take longer, as for a short prompt's Wo;
+// past it the tiles win, as for its QKV), and the staged inputs within LDS.
+// Tokens per workgroup: halved (down to 2) while the workgroups still fit
+// one round of about 1024 (four a CU).
 constexpr int kRowsWideT = 64;
+constexpr int64_t kRowsWideWork = 196608;
 static bool launch_rows(int fmt, int epi, const MmArgs &a, hipStream_t s) {
     if (fmt != kFmtQ8 || (epi != kEpStore && epi != kEpAdd && epi != kEpAddCanon)) return false;
-    if (a.tokens > kRowsMaxT &&
-        (a.tokens > kRowsWideT || (int64_t)((a.rows + kMmRows - 1) / kMmRows) * ((a.tokens + kMmToks - 1) / kMmToks) >= 128))
-        return false;
+    if (a.tokens > kRowsMaxT && (a.tokens > kRowsWideT || (int64_t)a.rows * a.tokens > kRowsWideWork)) return false;
     const int64_t nrt = (a.rows + kRowsPerWg - 1) / kRowsPerWg;
     int tpg = kRowsMaxT;
     while (tpg > 2 && (tpg >= 2 * a.tokens || nrt * ((a.tokens + tpg / 2 - 1) / (tpg / 2)) <= 1024)) tpg >>= 1;
