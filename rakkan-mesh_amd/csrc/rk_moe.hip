@@ -268,14 +268,28 @@ struct MoeTabs {
     const uint8_t *const *w1, *const *w3, *const *w2;
     const float *const *s1, *const *s3, *const *s2;
 };
-__device__ __forceinline__ void group_rows(const MoeTabs &tb, int g, int e, const void **gptr) {
+// Thread e's expert's six row addresses, read at a kernel's start (they
+// do not depend on the routing) so they are in registers by the time the
+// grouping writes them.
+struct ExpRows {
+    const void *p[6];
+};
+__device__ __forceinline__ ExpRows expert_rows(const MoeTabs &tb, int e, int experts) {
+    ExpRows r{};
+    if (e < experts) {
+        r.p[0] = tb.w1[e];
+        r.p[1] = tb.s1[e];
+        r.p[2] = tb.w3[e];
+        r.p[3] = tb.s3[e];
+        r.p[4] = tb.w2[e];
+        r.p[5] = tb.s2[e];
+    }
+    return r;
+}
+__device__ __forceinline__ void group_rows(const ExpRows &r, int g, const void **gptr) {
     const void **d = gptr + 6 * g;
-    d[0] = tb.w1[e];
-    d[1] = tb.s1[e];
-    d[2] = tb.w3[e];
-    d[3] = tb.s3[e];
-    d[4] = tb.w2[e];
-    d[5] = tb.s2[e];
+#pragma unroll
+    for (int i = 0; i < 6; i++) d[i] = r.p[i];
 }
 
 constexpr int kGroupFastPairs = 128;
@@ -288,7 +302,7 @@ struct GroupLds {
 // totals across the wave): each expert's first place and group index, and
 // the number of groups. Then each selected expert's group entry and rows.
 // Every thread of a 1024-thread workgroup calls it, after the counts.
-__device__ void group_scan_info(GroupLds &gl, int experts, int gcap, int32_t *grp, const MoeTabs &tb,
+__device__ void group_scan_info(GroupLds &gl, int experts, int gcap, int32_t *grp, const ExpRows &rows,
                                 const void **gptr) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid < 64) {
@@ -329,7 +343,7 @@ __device__ void group_scan_info(GroupLds &gl, int experts, int gcap, int32_t *gr
         gexp[g] = tid;
         gstart[g] = gl.start[tid];
         gcount[g] = gl.cnt[tid];
-        group_rows(tb, g, tid, gptr);
+        group_rows(rows, g, gptr);
     }
     if (tid == 0) grp[0] = gl.total;
 }
@@ -349,12 +363,13 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, con
     __shared__ GroupLds gl;
     __shared__ int fill[1024];
     const int tid = threadIdx.x;
+    const ExpRows rows = expert_rows(tb, tid, experts);
     gl.cnt[tid] = 0;
     fill[tid] = 0;
     __syncthreads();
     for (int p = tid; p < npairs; p += 1024) atomicAdd(&gl.cnt[sel[p]], 1);
     __syncthreads();
-    group_scan_info(gl, experts, gcap, grp, tb, gptr);
+    group_scan_info(gl, experts, gcap, grp, rows, gptr);
     int32_t *list = grp + 1 + 3 * gcap;
     for (int p = tid; p < npairs; p += 1024) {
         const int e = sel[p];
@@ -372,13 +387,13 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, con
 // thread of a 1024-thread workgroup calls it; s_sel: the pairs' experts in
 // LDS, written before a barrier.
 __device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, int experts, int gcap, int32_t *grp,
-                               float *gwt, const MoeTabs &tb, const void **gptr, GroupLds &gl) {
+                               float *gwt, const ExpRows &rows, const void **gptr, GroupLds &gl) {
     const int tid = threadIdx.x;
     gl.cnt[tid] = 0;
     __syncthreads();
     if (tid < npairs) atomicAdd(&gl.cnt[s_sel[tid]], 1);
     __syncthreads();
-    group_scan_info(gl, experts, gcap, grp, tb, gptr);
+    group_scan_info(gl, experts, gcap, grp, rows, gptr);
     // pair p's place: the earlier pairs of its expert (eight threads a pair)
     int32_t *list = grp + 1 + 3 * gcap;
     const int p = tid >> 3, part = tid & 7;
@@ -402,12 +417,13 @@ __global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel
     __shared__ int s_sel[kGroupFastPairs];
     __shared__ float s_wt[kGroupFastPairs];
     __shared__ GroupLds gl;
+    const ExpRows rows = expert_rows(tb, threadIdx.x, experts);
     if ((int)threadIdx.x < npairs) {
         s_sel[threadIdx.x] = sel[threadIdx.x];
         s_wt[threadIdx.x] = wsel[threadIdx.x];
     }
     __syncthreads();
-    group_pairs_wg(s_sel, s_wt, npairs, experts, gcap, grp, gwt, tb, gptr, gl);
+    group_pairs_wg(s_sel, s_wt, npairs, experts, gcap, grp, gwt, rows, gptr, gl);
 }
 
 // Routing (wave t: token t) and grouping of up to kSelectTokens tokens in
@@ -422,6 +438,7 @@ __global__ __launch_bounds__(1024) void moe_select_kernel(const float *logits, i
     __shared__ float s_wt[kGroupFastPairs];
     __shared__ GroupLds gl;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const ExpRows rows = expert_rows(tb, threadIdx.x, experts);
     const int ep = (experts + 3) & ~3;
     const bool live = wave < tokens;
     const int t = live ? wave : 0;
@@ -433,7 +450,7 @@ __global__ __launch_bounds__(1024) void moe_select_kernel(const float *logits, i
         s_wt[t * k + lane] = wt;
     }
     __syncthreads();
-    group_pairs_wg(s_sel, s_wt, tokens * k, experts, gcap, grp, gwt, tb, gptr, gl);
+    group_pairs_wg(s_sel, s_wt, tokens * k, experts, gcap, grp, gwt, rows, gptr, gl);
 }
 
 // W1 and W3 rows of a selected expert for every pair that chose it:
