@@ -59,13 +59,26 @@ int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc);
 // codes, xs/xsum [tokens][dim/32]): out = y, or (residual) out =
 // Canonical(out + y), rows [tokens][dim]. Enqueue only; it allocates
 // nothing, so it may be recorded into a graph.
+struct MoeNext;
 int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, const int32_t *xsum,
-                  int tokens, float *out, bool residual, hipStream_t s);
+                  int tokens, float *out, bool residual, hipStream_t s, const MoeNext *next = nullptr);
+
+// The next product's input, formed after the sum into the residual:
+// RMSNorm of each new row with norm_w, quantized into qx/xs/xsum.
+struct MoeNext {
+    const float *norm_w;
+    float recip_n, eps;
+    int8_t *qx;
+    float *xs;
+    int32_t *xsum;
+};
 
 // The same from f32 inputs x [tokens][dim]: RMSNorm'd with norm_w (recip_n
 // = 1/dim, eps) or, norm_w null, taken as given, and quantized into qx/xs/
-// xsum (which the experts' products then read).
+// xsum (which the experts' products then read). With `next` (residual only,
+// several tokens), the sum's launch also forms the next product's input.
 int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *norm_w, float recip_n, float eps,
-                  int tokens, int8_t *qx, float *xs, int32_t *xsum, float *out, bool residual, hipStream_t s);
+                  int tokens, int8_t *qx, float *xs, int32_t *xsum, float *out, bool residual, hipStream_t s,
+                  const MoeNext *next = nullptr);
 
 }  // namespace rk

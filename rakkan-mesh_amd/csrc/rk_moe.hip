@@ -897,6 +897,53 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, in
     *dst = residual ? canonical(*dst + acc) : acc;
 }
 
+// The ascending-order sum into the residual (moe_combine_kernel's steps),
+// then RMSNorm of each new row with the next layer's weights and its Q8_0
+// form (norm_quant_kernel's steps): one workgroup a token, four values a
+// thread.
+constexpr int kCnThreads = 1024;
+constexpr int kCnGroups = (kMaxNormCols / 4 + kCnThreads - 1) / kCnThreads;
+__global__ __launch_bounds__(kCnThreads) void moe_combine_norm_kernel(const int32_t *sel, int k, const float *o,
+                                                                      int dim, float *out, const float *norm_w,
+                                                                      float recip_n, float eps, int8_t *qx, float *xs,
+                                                                      int32_t *xsum) {
+    extern __shared__ __align__(16) float sxn[];
+    __shared__ float bcast;
+    __shared__ int order[kMoeMaxK];  // the token's slots by ascending expert
+    const int t = blockIdx.x, tid = threadIdx.x;
+    if (tid < k) {
+        const int32_t *ts = sel + (int64_t)t * k;
+        const int e = ts[tid];
+        int r = 0;
+        for (int q = 0; q < k; q++) r += ts[q] < e;
+        order[r] = tid;
+    }
+    __syncthreads();
+    const int ng = dim >> 2;
+    float4 xv[kCnGroups], wv[kCnGroups];
+#pragma unroll
+    for (int kk = 0; kk < kCnGroups; kk++) {
+        const int gu = tid + kk * kCnThreads, g = min(gu, ng - 1);
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int q = 0; q < k; q++) {
+            const float4 ov = reinterpret_cast<const float4 *>(o + ((int64_t)t * k + order[q]) * dim)[g];
+            acc.x += ov.x;
+            acc.y += ov.y;
+            acc.z += ov.z;
+            acc.w += ov.w;
+        }
+        float4 *dst = reinterpret_cast<float4 *>(out + (int64_t)t * dim) + g;
+        const float4 x0 = *dst;
+        const float4 x1 = make_float4(canonical(x0.x + acc.x), canonical(x0.y + acc.y), canonical(x0.z + acc.z),
+                                      canonical(x0.w + acc.w));
+        if (gu < ng) *dst = x1;
+        xv[kk] = x1;
+        wv[kk] = reinterpret_cast<const float4 *>(norm_w)[g];
+    }
+    wg_norm_quant<kCnThreads, kCnGroups>(xv, wv, dim, recip_n, eps, qx + (int64_t)t * dim,
+                                          xs + (int64_t)t * (dim >> 5), xsum + (int64_t)t * (dim >> 5), sxn, &bcast);
+}
+
 }  // namespace
 
 int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc) {
@@ -926,11 +973,12 @@ int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc) 
 }
 
 static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, int tokens,
-                               float *out, bool residual, hipStream_t s);
-static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *out, bool residual, hipStream_t s);
+                               float *out, bool residual, hipStream_t s, const MoeNext *next = nullptr);
+static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *out, bool residual, hipStream_t s,
+                            const MoeNext *next = nullptr);
 
 int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, const int32_t *xsum, int tokens,
-                  float *out, bool residual, hipStream_t s) {
+                  float *out, bool residual, hipStream_t s, const MoeNext *next) {
     rk_device *d = m->d;
     const int D = m->dim, K = m->topk, E = m->experts;
     if (tokens <= 0) return RK_OK;
@@ -982,7 +1030,7 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
         else
             RK_LAUNCH(moe_select_kernel<kRoutePer>, dim3(1), dim3(1024), lds, s, sc.logits, tokens, E, K, sc.sel,
                       sc.wsel, sc.gcap, sc.grp, sc.gwt, tabs, sc.gptr);
-        return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s);
+        return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s, next);
     }
     {
         ProfScope p(d, s, "moe_route");
@@ -1001,12 +1049,12 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
             RK_LAUNCH(moe_group_kernel, dim3(1), dim3(1024), 0, s,
                       sc.sel, sc.wsel, npairs, E, sc.gcap, sc.grp, sc.gwt, tabs, sc.gptr);
     }
-    return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s);
+    return enqueue_moe_experts(m, sc, qx, xs, tokens, out, residual, s, next);
 }
 
 // The experts' products and sum after the routing (grouping in sc.grp).
 static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float *xs, int tokens,
-                               float *out, bool residual, hipStream_t s) {
+                               float *out, bool residual, hipStream_t s, const MoeNext *next) {
     rk_device *d = m->d;
     const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
     const int groups = std::min(E, tokens * K);  // launched; those past the selected count exit
@@ -1034,11 +1082,13 @@ static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx
         }
 #undef RK_UP8
     }
-    return enqueue_moe_down(m, sc, tokens, out, residual, s);
+    return enqueue_moe_down(m, sc, tokens, out, residual, s, next);
 }
 
-// The W2 products of the grouped pairs (h in sc) and the sum.
-static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *out, bool residual, hipStream_t s) {
+// The W2 products of the grouped pairs (h in sc) and the sum (with `next`:
+// and the next product's input).
+static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *out, bool residual, hipStream_t s,
+                            const MoeNext *next) {
     rk_device *d = m->d;
     const int D = m->dim, H = m->hidden, K = m->topk, E = m->experts;
     const int groups = std::min(E, tokens * K);  // launched; those past the selected count exit
@@ -1060,10 +1110,19 @@ static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *
             RK_LAUNCH(moe_down_kernel, dim3((unsigned)groups, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2,
                       m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H, sc.o);
     }
-    {
+    if (next && residual && D % 32 == 0 && D <= kMaxNormCols) {
+        ProfScope p(d, s, "moe_combine");
+        RK_LAUNCH(moe_combine_norm_kernel, dim3((unsigned)tokens), dim3(kCnThreads), norm_lds(D), s, sc.sel, K, sc.o,
+                  D, out, next->norm_w, next->recip_n, next->eps, next->qx, next->xs, next->xsum);
+    } else {
         ProfScope p(d, s, "moe_combine");
         RK_LAUNCH(moe_combine_kernel, dim3((unsigned)tokens, (unsigned)((D + 255) / 256)), dim3(256), 0, s, sc.sel, K,
                   sc.o, D, out, residual ? 1 : 0);
+        if (next) {
+            ProfScope p2(d, s, "norm_quant");
+            launch_norm_quant(out, D, next->norm_w, next->recip_n, next->eps, next->qx, next->xs, next->xsum, s,
+                              tokens);
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(d, e, "moe launch");
@@ -1071,7 +1130,8 @@ static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *
 }
 
 int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *norm_w, float recip_n, float eps,
-                  int tokens, int8_t *qx, float *xs, int32_t *xsum, float *out, bool residual, hipStream_t s) {
+                  int tokens, int8_t *qx, float *xs, int32_t *xsum, float *out, bool residual, hipStream_t s,
+                  const MoeNext *next) {
     rk_device *d = m->d;
     if (tokens <= 0) return RK_OK;
     if (tokens > sc.cap) return fail(d, RK_ERR_ARGS, "moe: %d tokens beyond the scratch's %d", tokens, sc.cap);
@@ -1114,7 +1174,7 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
             }
 #undef RK_UP1
         }
-        if (H / 32 > 8 * 8) return enqueue_moe_down(m, sc, tokens, out, residual, s);
+        if (H / 32 > 8 * 8) return enqueue_moe_down(m, sc, tokens, out, residual, s, next);
         {
             ProfScope p(d, s, "moe_down");
             const int R = 64 / K, hbpl = (H / 32 + 7) / 8;
@@ -1129,6 +1189,10 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
                 RK_LAUNCH(moe_down1_kernel<8>, grid, dim3(512), 0, s, m->w2, m->s2, sc.grp, sc.gcap, K, sc.hq, sc.hs,
                           D, H, out, residual ? 1 : 0);
         }
+        if (next) {
+            ProfScope p(d, s, "norm_quant");
+            launch_norm_quant(out, D, next->norm_w, next->recip_n, next->eps, next->qx, next->xs, next->xsum, s, 1);
+        }
         hipError_t e = hipGetLastError();
         return e == hipSuccess ? RK_OK : hip_fail(d, e, "moe launch");
     }
@@ -1139,7 +1203,7 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
         ProfScope p(d, s, "quantize_acts");
         launch_quantize_acts(x, (int64_t)tokens * m->dim, qx, xs, xsum, s);
     }
-    return enqueue_moe_q(m, sc, qx, xs, xsum, tokens, out, residual, s);
+    return enqueue_moe_q(m, sc, qx, xs, xsum, tokens, out, residual, s, next);
 }
 
 // The standalone calls' scratch for up to `tokens` inputs (grown: a call

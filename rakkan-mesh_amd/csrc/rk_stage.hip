@@ -516,10 +516,11 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, const
     if (L.moe) {  // RMSNorm_ffn(x) into bqb, and the experts' sums into the residual rows, x = Canonical(x + y)
         MoeScratch sc;
         moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
+        // the sum's launch also forms the next layer's normed input in bqb
+        const MoeNext nx{next_norm, c.recip_dim, c.norm_eps, s->bqb.qx, s->bqb.xs, s->bqb.xsum};
         if ((rc = enqueue_moe_x(L.moe, sc, s->bx, D.rms_ffn, c.recip_dim, c.norm_eps, n, s->bqb.qx, s->bqb.xs,
-                                s->bqb.xsum, s->bx, true, st)))
+                                s->bqb.xsum, s->bx, true, st, next_norm ? &nx : nullptr)))
             return rc;
-        batch_norm(s, st, next_norm, n);
         hipError_t e = hipGetLastError();
         return e == hipSuccess ? RK_OK : hip_fail(d, e, "stage launch");
     }
