@@ -675,6 +675,10 @@ __device__ __forceinline__ void qk_norm_rope_wave(const float *x, const float *w
 // token's QKV outputs, [tokens][heads·hs] and [tokens][kv_dim]. hs: a
 // multiple of 8, at most kQknMaxHs.
 constexpr int kQknMaxHs = 256;
+// HS: the head size when it is 128 (the keys of the workgroup's positions
+// then load into registers before the norm, so the dots wait on LDS only),
+// else 0 (the keys read at the dots).
+template <int HS>
 __global__ __launch_bounds__(256) void att_scores_qkn_kernel(const float *q_raw, const float *k_raw, const float *v_raw,
                                                              const float *q_norm, const float *k_norm, float recip_hs,
                                                              float eps, const float *cos_t, const float *sin_t,
@@ -696,6 +700,19 @@ __global__ __launch_bounds__(256) void att_scores_qkn_kernel(const float *q_raw,
     const int h = blockIdx.x, g = h / kv_mul;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const bool here = pos < t0 + kScoreTile;  // the tile holds the position
+    const int sub = threadIdx.x & 3;
+    const int t = t0 + (threadIdx.x >> 2);
+    // HS = 128: this lane's part of its position's key (the position's own
+    // row is taken from LDS below; its cache row is read here and dropped)
+    float4 kr[HS ? HS / 32 : 1][2];
+    if (HS) {
+        const float *kg = keys + (int64_t)(t < T ? t : t0) * kv_dim + (int64_t)g * hs + 8 * sub;
+#pragma unroll
+        for (int it = 0; it < (HS ? HS / 32 : 1); it++) {
+            kr[it][0] = *reinterpret_cast<const float4 *>(kg + 32 * it);
+            kr[it][1] = *reinterpret_cast<const float4 *>(kg + 32 * it + 4);
+        }
+    }
     if (wave == 0)
         qk_norm_rope_wave(q_raw + (int64_t)h * hs, q_norm, recip_hs, eps, cos_t, sin_t, pos, hs, sq);
     else if (wave == 1 && here)
@@ -710,10 +727,43 @@ __global__ __launch_bounds__(256) void att_scores_qkn_kernel(const float *q_raw,
             vd[i] = vs[i];
         }
     }
-    const int sub = threadIdx.x & 3;
-    const int t = t0 + (threadIdx.x >> 2);
-    const float *kt = t == pos ? sk : keys + (int64_t)(t < T ? t : t0) * kv_dim + (int64_t)g * hs;
-    const float dot = quad_dot32(sq, kt, sub, hs);
+    float dot;
+    if (HS) {
+        if (t == pos) {
+#pragma unroll
+            for (int it = 0; it < (HS ? HS / 32 : 1); it++) {
+                kr[it][0] = *reinterpret_cast<const float4 *>(sk + 8 * sub + 32 * it);
+                kr[it][1] = *reinterpret_cast<const float4 *>(sk + 8 * sub + 32 * it + 4);
+            }
+        }
+        // quad_dot32's steps on the held key
+        float sacc[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) sacc[k] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < (HS ? HS / 32 : 1); it++) {
+            const float4 q0 = *reinterpret_cast<const float4 *>(sq + 8 * sub + 32 * it);
+            const float4 q1 = *reinterpret_cast<const float4 *>(sq + 8 * sub + 32 * it + 4);
+            sacc[0] += q0.x * kr[it][0].x;
+            sacc[1] += q0.y * kr[it][0].y;
+            sacc[2] += q0.z * kr[it][0].z;
+            sacc[3] += q0.w * kr[it][0].w;
+            sacc[4] += q1.x * kr[it][1].x;
+            sacc[5] += q1.y * kr[it][1].y;
+            sacc[6] += q1.z * kr[it][1].z;
+            sacc[7] += q1.w * kr[it][1].w;
+        }
+        float e[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float u = sacc[k] + dppf_x1(sacc[k]);
+            e[k] = u + dppf_x2(u);
+        }
+        dot = ((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]));
+    } else {
+        const float *kt = t == pos ? sk : keys + (int64_t)(t < T ? t : t0) * kv_dim + (int64_t)g * hs;
+        dot = quad_dot32(sq, kt, sub, hs);
+    }
     if (sub == 0 && t < T) att[(int64_t)h * att_stride + t] = dot * inv_sqrt;
 }
 
@@ -725,8 +775,12 @@ bool launch_att_scores_qkn(const float *q_raw, const float *k_raw, const float *
     if (!ctl && !bt.pos) return false;  // a prompt's batch: the grouped scores, after the norm launch
     if (hs % 8 != 0 || hs > kQknMaxHs || kv_dim % 4 != 0 || kv_dim != kv_heads * hs) return false;
     const dim3 grid(heads, (ctx + kScoreTile - 1) / kScoreTile, ctl ? 1 : bt.tokens);
-    RK_LAUNCH(att_scores_qkn_kernel, grid, dim3(256), 0, s, q_raw, k_raw, v_raw, q_norm, k_norm, recip_hs, eps, cos_t,
-              sin_t, keys, vals, att, att_stride, ctl, bt, heads / kv_heads, hs, kv_dim, inv_sqrt);
+    if (hs == 128)
+        RK_LAUNCH(att_scores_qkn_kernel<128>, grid, dim3(256), 0, s, q_raw, k_raw, v_raw, q_norm, k_norm, recip_hs, eps,
+                  cos_t, sin_t, keys, vals, att, att_stride, ctl, bt, heads / kv_heads, hs, kv_dim, inv_sqrt);
+    else
+        RK_LAUNCH(att_scores_qkn_kernel<0>, grid, dim3(256), 0, s, q_raw, k_raw, v_raw, q_norm, k_norm, recip_hs, eps,
+                  cos_t, sin_t, keys, vals, att, att_stride, ctl, bt, heads / kv_heads, hs, kv_dim, inv_sqrt);
     return true;
 }
 
