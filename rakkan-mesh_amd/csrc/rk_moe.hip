@@ -717,9 +717,10 @@ template <int BPL, int PER>
 __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const float *norm_w, float recip_n, float eps,
                                                       const float *logits, int experts, int k,
                                                       const uint8_t *const *w1, const float *const *s1,
-                                                      const uint8_t *const *w3, const float *const *s3, int dim,
+                                                      const uint8_t *const *w3, const float *const *s3,
+                                                      const uint8_t *const *w2, const float *const *s2, int dim,
                                                       int hidden, int32_t *sel, float *wsel, int gcap, int32_t *grp,
-                                                      int8_t *hq, float *hs, int32_t *hsum) {
+                                                      const void **gptr, int8_t *hq, float *hs, int32_t *hsum) {
     extern __shared__ __align__(16) char ulds[];
     __shared__ float bcast, s_w;
     __shared__ int s_e, s_slot;
@@ -754,6 +755,8 @@ __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const floa
             grp[1 + gcap + r] = r;
             grp[1 + 2 * gcap + r] = 1;
             grp[1 + 3 * gcap + r] = lane;  // pair (token 0, slot lane)
+            gptr[6 * r + 4] = w2[mine];    // the W2 rows the sum's launch reads
+            gptr[6 * r + 5] = s2[mine];
             if (lane == 0) grp[0] = k;
         }
     }
@@ -848,21 +851,23 @@ __global__ __launch_bounds__(256) void moe_down8_kernel(const void *const *gptr,
 // grouping's order) into y, out = y or Canonical(out + y). The same bits as
 // moe_down8_kernel followed by moe_combine_kernel.
 template <int BPL>
-__global__ __launch_bounds__(512) void moe_down1_kernel(const uint8_t *const *w2, const float *const *s2,
-                                                        const int32_t *grp, int gcap, int k, const int8_t *hq,
-                                                        const float *hs, int dim, int hidden, float *out,
-                                                        int residual) {
+__global__ __launch_bounds__(512) void moe_down1_kernel(const void *const *gptr, const int32_t *grp, int gcap, int k,
+                                                        const int8_t *hq, const float *hs, int dim, int hidden,
+                                                        float *out, int residual) {
     __shared__ float sv[64];
     const int R = 64 / k;
     const int tid = threadIdx.x, gi = tid >> 3, rl = tid & 7;
     const int g = min(gi / R, k - 1), r = gi - (gi / R) * R;
     const int i = blockIdx.x * R + r;
     const int nb = hidden >> 5;
-    const int e = grp[1 + g], p = grp[1 + 3 * gcap + grp[1 + gcap + g]];
+    // the one-token grouping (moe_up1_kernel's): group g's pair is list[g],
+    // its W2 rows at gptr[6g + 4], [6g + 5]
+    const uint8_t *w2 = static_cast<const uint8_t *>(gptr[6 * g + 4]);
+    const float *s2 = static_cast<const float *>(gptr[6 * g + 5]);
+    const int p = grp[1 + 3 * gcap + g];
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, w2[e] + (int64_t)min(i, dim - 1) * hidden, s2[e] + (int64_t)min(i, dim - 1) * nb,
-                       nb, rl);
+    lane_row_load<BPL>(c0, c1, sw, w2 + (int64_t)min(i, dim - 1) * hidden, s2 + (int64_t)min(i, dim - 1) * nb, nb, rl);
     const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, hq + (int64_t)p * hidden, hs + (int64_t)p * nb, nb, rl));
     if (rl == 0 && gi < k * R) sv[gi] = v;
     __syncthreads();
@@ -1161,8 +1166,8 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
             ProfScope p(d, s, "moe_up");
 #define RK_UP1(B, P)                                                                                               \
     RK_LAUNCH((moe_up1_kernel<B, P>), dim3((unsigned)K, (unsigned)(H / 32)), dim3(512), lds, s, x, norm_w, recip_n, \
-              eps, sc.logits, E, K, m->w1, m->s1, m->w3, m->s3, D, H, sc.sel, sc.wsel, sc.gcap, sc.grp, sc.hq,     \
-              sc.hs, sc.hsum)
+              eps, sc.logits, E, K, m->w1, m->s1, m->w3, m->s3, m->w2, m->s2, D, H, sc.sel, sc.wsel, sc.gcap,       \
+              sc.grp, sc.gptr, sc.hq, sc.hs, sc.hsum)
             if (E <= 128) {
                 if (bpl <= 2) RK_UP1(2, 2);
                 else if (bpl <= 4) RK_UP1(4, 2);
@@ -1180,14 +1185,14 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
             const int R = 64 / K, hbpl = (H / 32 + 7) / 8;
             const dim3 grid((unsigned)((D + R - 1) / R));
             if (hbpl <= 2)
-                RK_LAUNCH(moe_down1_kernel<2>, grid, dim3(512), 0, s, m->w2, m->s2, sc.grp, sc.gcap, K, sc.hq, sc.hs,
-                          D, H, out, residual ? 1 : 0);
+                RK_LAUNCH(moe_down1_kernel<2>, grid, dim3(512), 0, s, sc.gptr, sc.grp, sc.gcap, K, sc.hq, sc.hs, D,
+                          H, out, residual ? 1 : 0);
             else if (hbpl <= 4)
-                RK_LAUNCH(moe_down1_kernel<4>, grid, dim3(512), 0, s, m->w2, m->s2, sc.grp, sc.gcap, K, sc.hq, sc.hs,
-                          D, H, out, residual ? 1 : 0);
+                RK_LAUNCH(moe_down1_kernel<4>, grid, dim3(512), 0, s, sc.gptr, sc.grp, sc.gcap, K, sc.hq, sc.hs, D,
+                          H, out, residual ? 1 : 0);
             else
-                RK_LAUNCH(moe_down1_kernel<8>, grid, dim3(512), 0, s, m->w2, m->s2, sc.grp, sc.gcap, K, sc.hq, sc.hs,
-                          D, H, out, residual ? 1 : 0);
+                RK_LAUNCH(moe_down1_kernel<8>, grid, dim3(512), 0, s, sc.gptr, sc.grp, sc.gcap, K, sc.hq, sc.hs, D,
+                          H, out, residual ? 1 : 0);
         }
         if (next) {
             ProfScope p(d, s, "norm_quant");
