@@ -25,38 +25,52 @@ namespace {
 constexpr int kGrpTok = 16;    // tokens per workgroup
 constexpr int kGrpMaxT = 1024;  // positions a group's weights keep in LDS
 constexpr int kScTile = 64;    // positions per scores workgroup
-constexpr int kGvChunk = 128;  // value positions per LDS tile
+constexpr int kGvChunk = 32;   // value positions per LDS tile
 constexpr int kGvPitch = kGvChunk + 4;  // floats per element row (odd count of 16-byte units)
+constexpr int kGvSlices = 4;   // 32-element slices of a head per values workgroup
+constexpr int kGvElems = 32 * kGvSlices;
 constexpr int kGvThreads = 512;         // eight waves, two tokens each
 constexpr int kHs = 128;                // head size of the scores kernel
 
-// acc + Σ a[t]·v[t] for t < n in order (float32), a and v in LDS (16-byte
-// aligned): products then sums, four positions per pair of reads, the next
-// four positions' reads issued before the current ones are summed.
-__device__ __forceinline__ float lds_dot_chain(const float *a, const float *v, int n, float acc) {
+// acc[s] + Σ a[t]·v_s[t] for t < n in order, for the four rows v_s = v +
+// 32·s·kGvPitch (float32; each product rounded, then added), a and v in LDS
+// (16-byte aligned). Four independent chains keep the adds issuing every
+// cycle they can; the next four positions' reads are issued before the
+// current ones are summed.
+__device__ __forceinline__ void lds_dot_chain4(const float *a, const float *v, int n, float (&acc)[kGvSlices]) {
     const float4 *a4 = reinterpret_cast<const float4 *>(a);
-    const float4 *v4 = reinterpret_cast<const float4 *>(v);
     const int nq = n >> 2;
+    auto vq = [&](int s, int k) { return reinterpret_cast<const float4 *>(v + 32 * s * kGvPitch)[k]; };
+    auto add4 = [&](const float4 &ca, const float4 (&cv)[kGvSlices]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < kGvSlices; s++) acc[s] += ca.x * cv[s].x;
+#pragma unroll
+        for (int s = 0; s < kGvSlices; s++) acc[s] += ca.y * cv[s].y;
+#pragma unroll
+        for (int s = 0; s < kGvSlices; s++) acc[s] += ca.z * cv[s].z;
+#pragma unroll
+        for (int s = 0; s < kGvSlices; s++) acc[s] += ca.w * cv[s].w;
+    };
     if (nq > 0) {
-        float4 ca = a4[0], cv = v4[0];
+        float4 ca = a4[0], cv[kGvSlices];
+#pragma unroll
+        for (int s = 0; s < kGvSlices; s++) cv[s] = vq(s, 0);
         for (int k = 1; k < nq; k++) {
-            const float4 na = a4[k], nv = v4[k];
+            float4 na = a4[k], nv[kGvSlices];
+#pragma unroll
+            for (int s = 0; s < kGvSlices; s++) nv[s] = vq(s, k);
             __builtin_amdgcn_sched_barrier(0);
-            acc += ca.x * cv.x;
-            acc += ca.y * cv.y;
-            acc += ca.z * cv.z;
-            acc += ca.w * cv.w;
+            add4(ca, cv);
             __builtin_amdgcn_sched_barrier(0);
             ca = na;
-            cv = nv;
+#pragma unroll
+            for (int s = 0; s < kGvSlices; s++) cv[s] = nv[s];
         }
-        acc += ca.x * cv.x;
-        acc += ca.y * cv.y;
-        acc += ca.z * cv.z;
-        acc += ca.w * cv.w;
+        add4(ca, cv);
     }
-    for (int t = nq << 2; t < n; t++) acc += a[t] * v[t];
-    return acc;
+    for (int t = nq << 2; t < n; t++)
+#pragma unroll
+        for (int s = 0; s < kGvSlices; s++) acc[s] += a[t] * v[32 * s * kGvPitch + t];
 }
 
 }  // namespace
@@ -121,21 +135,23 @@ __global__ __launch_bounds__(256) void att_scores_group_kernel(const float *q, c
     }
 }
 
-// Softmax and weighted values of a 32-element slice of one head for the
-// group's tokens. Half-wave zl (lanes 32·(zl&1).. of wave zl/2) owns token
-// z0 + zl: its softmax over its positions, then element lane%32's sum.
+// Softmax and weighted values of up to four 32-element slices of one head
+// (elements e0 .. e0+127) for the group's tokens. Half-wave zl (lanes
+// 32·(zl&1).. of wave zl/2) owns token z0 + zl: its softmax over its
+// positions, once, then the sums of elements e0 + 32·s + lane%32.
 __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const float *att, int32_t att_stride,
                                                                       const float *vals, float *out, AttBatch bt,
                                                                       int kv_mul, int hs, int kv_dim, int apitch,
                                                                       int8_t *qx, float *xs, int32_t *xsum) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float s_inv[kGrpTok];
-    __shared__ __align__(16) float s_out[kGrpTok][32];
+    __shared__ __align__(16) float s_out[kGrpTok][kGvElems];
     float *sa = smem;                         // [kGrpTok][apitch] weights a_t
-    float *vt = smem + kGrpTok * apitch;      // [2][32][kGvPitch] value tiles, transposed
+    float *vt = smem + kGrpTok * apitch;      // [2][kGvElems][kGvPitch] value tiles, transposed
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x, g = h / kv_mul;
-    const int e0 = blockIdx.y * 32;
+    const int e0 = blockIdx.y * kGvElems;
+    const int ns = min(kGvSlices, (hs - e0) >> 5);  // slices of the head here
     const int z0 = blockIdx.z * kGrpTok;
     const int nz = min(kGrpTok, bt.tokens - z0);
     const int zl = 2 * wave + (lane >> 5), l32 = lane & 31;
@@ -144,10 +160,11 @@ __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const floa
     const int tmax = bt.pos0 + z0 + nz;
     float *az = sa + zl * apitch;
 
-    // ---- the value tiles' loads: thread (elements 4·fq.., positions
-    // 2·pq, 2·pq+1 of the chunk); positions past tmax clamped, never summed
-    const int fq = tid & 7, pq = tid >> 3;
-    const float *vbase = vals + (int64_t)g * hs + e0 + 4 * fq;
+    // ---- the value tiles' loads: thread (elements e0 + 4·fq.., positions
+    // 2·pq, 2·pq+1 of the chunk); positions past tmax and elements past the
+    // head clamped, never summed or stored
+    const int fq = tid & 31, pq = tid >> 5;
+    const float *vbase = vals + (int64_t)g * hs + min(e0 + 4 * fq, hs - 4);
     float4 v0, v1;
     auto load_tile = [&](int c0) {
         v0 = *reinterpret_cast<const float4 *>(vbase + (int64_t)min(c0 + 2 * pq, tmax - 1) * kv_dim);
@@ -181,38 +198,42 @@ __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const floa
     // ---- values: tiles of kGvChunk positions, double-buffered ----
     store_tile(vt);
     __syncthreads();
-    float acc = 0.0f;
+    float acc[kGvSlices] = {};
     int buf = 0;
     for (int c0 = 0; c0 < tmax; c0 += kGvChunk, buf ^= 1) {
         load_tile(c0 + kGvChunk);  // the next tile, in flight during the sums
-        const float *tile = vt + buf * (32 * kGvPitch);
+        const float *tile = vt + buf * (kGvElems * kGvPitch);
         const int n = max(0, min(kGvChunk, Tz - c0));
-        acc = lds_dot_chain(az + c0, tile + l32 * kGvPitch, n, acc);
+        lds_dot_chain4(az + c0, tile + l32 * kGvPitch, n, acc);
         // the other buffer was last read two tiles ago, before the barrier
         // that ended that iteration
-        store_tile(vt + (buf ^ 1) * (32 * kGvPitch));
+        store_tile(vt + (buf ^ 1) * (kGvElems * kGvPitch));
         __syncthreads();
     }
 
-    const int ne = min(32, hs - e0);
     const bool live = zl < nz;
-    if (live && l32 < ne) out[(int64_t)(z0 + zl) * bt.out_stride + (int64_t)h * hs + e0 + l32] = acc;
-    if (qx && ne == 32) {
-        // the slice is one Q8_0 block of each token's next input: lanes 0-7
-        // of the half take four values each
-        s_out[zl][l32] = acc;
+    const int64_t base = (int64_t)(z0 + zl) * bt.out_stride + (int64_t)h * hs + e0;
+#pragma unroll
+    for (int s = 0; s < kGvSlices; s++)
+        if (live && s < ns) out[base + 32 * s + l32] = acc[s];
+    if (qx) {
+        // each slice is one Q8_0 block of each token's next input (hs is a
+        // multiple of 32): lanes 8·s.. 8·s+7 of the half take slice s, four
+        // values each (every lane calls the quantizer)
+#pragma unroll
+        for (int s = 0; s < kGvSlices; s++) s_out[zl][32 * s + l32] = acc[s];
         __syncthreads();
-        const int q = min(l32, 7);
-        const float4 v4 = reinterpret_cast<const float4 *>(&s_out[zl][0])[q];
+        const int sb = l32 >> 3, q = l32 & 7;
+        const float4 v4 = reinterpret_cast<const float4 *>(&s_out[zl][32 * sb])[q];
         float d;
         int cs;
         const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
-        const int64_t base = (int64_t)(z0 + zl) * bt.out_stride + (int64_t)h * hs + e0;
-        if (live && l32 < 8) {
-            reinterpret_cast<uint32_t *>(qx + base)[l32] = pk;
-            if (l32 == 0) {
-                xs[base >> 5] = d;
-                xsum[base >> 5] = cs;
+        const int64_t bb = base + 32 * sb;
+        if (live && sb < ns) {
+            reinterpret_cast<uint32_t *>(qx + bb)[q] = pk;
+            if (q == 0) {
+                xs[bb >> 5] = d;
+                xsum[bb >> 5] = cs;
             }
         }
     }
@@ -237,12 +258,12 @@ void launch_att_values_group(const float *att, int32_t att_stride, const float *
     static std::once_flag once;
     std::call_once(once, [] {
         (void)hipFuncSetAttribute((const void *)att_values_group_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)(kMaxLdsBytes - 4096));
+                                  (int)(kMaxLdsBytes - 12288));
     });
     const int tmax = bt.pos0 + bt.tokens;
     const int apitch = ((tmax + 3) & ~3) + 4;
-    const size_t lds = ((size_t)kGrpTok * apitch + 2 * 32 * kGvPitch) * 4;
-    const dim3 grid(heads, hs / 32, (bt.tokens + kGrpTok - 1) / kGrpTok);
+    const size_t lds = ((size_t)kGrpTok * apitch + 2 * kGvElems * kGvPitch) * 4;
+    const dim3 grid(heads, (hs + kGvElems - 1) / kGvElems, (bt.tokens + kGrpTok - 1) / kGrpTok);
     RK_LAUNCH(att_values_group_kernel, grid, dim3(kGvThreads), lds, s, att, att_stride, vals, out, bt,
               heads / kv_heads, hs, kv_dim, apitch, qx, xs, xsum);
 }
