@@ -152,7 +152,9 @@ __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const floa
     const int h = blockIdx.x, g = h / kv_mul;
     const int e0 = blockIdx.y * kGvElems;
     const int ns = min(kGvSlices, (hs - e0) >> 5);  // slices of the head here
-    const int z0 = blockIdx.z * kGrpTok;
+    // the last token groups (the most positions) are dispatched first, so
+    // the short ones fill the machine's last round
+    const int z0 = (int)(gridDim.z - 1 - blockIdx.z) * kGrpTok;
     const int nz = min(kGrpTok, bt.tokens - z0);
     const int zl = 2 * wave + (lane >> 5), l32 = lane & 31;
     const int zc = min(zl, nz - 1);      // halves past the batch repeat its last token, unstored
