@@ -12,15 +12,17 @@ namespace rk {
 // the kernel's own start and end (hipExtLaunchKernelGGL).
 struct LaunchEvents {
     hipEvent_t start, stop;
+    bool launched;  // a launch in the scope recorded them
 };
 extern thread_local LaunchEvents *g_launch_events;
 
 #define RK_LAUNCH(kernel, grid, block, shmem, stream, ...)                                                  \
     do {                                                                                                    \
-        if (::rk::g_launch_events)                                                                          \
+        if (::rk::g_launch_events) {                                                                        \
             hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, ::rk::g_launch_events->start,        \
                                   ::rk::g_launch_events->stop, 0, __VA_ARGS__);                             \
-        else                                                                                                \
+            ::rk::g_launch_events->launched = true;                                                         \
+        } else                                                                                              \
             hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                            \
     } while (0)
 

@@ -153,7 +153,8 @@ int enqueue_matmuls(rk_device *d, int32_t n, rk_matrix *const *ms, float *const 
 // (rk_noalloc.hip); called by rk_device_open.
 int noalloc_setup(rk_device *d);
 
-// Times the one kernel launched in its scope when the device is profiling.
+// Times the one kernel launched in its scope when the device is profiling
+// (a scope that ends without a launch records nothing).
 class ProfScope {
   public:
     ProfScope(rk_device *d, hipStream_t s, const char *kernel);
@@ -162,6 +163,8 @@ class ProfScope {
     ProfScope &operator=(const ProfScope &) = delete;
 
   private:
+    rk_device *d_ = nullptr;
+    const char *kernel_ = nullptr;
     LaunchEvents ev_{};
 };
 }  // namespace rk

@@ -79,13 +79,27 @@ static hipEvent_t take_event(rk_device *d) {
 ProfScope::ProfScope(rk_device *d, hipStream_t, const char *kernel) {
     if (!d->profiling || d->capturing) return;
     hipEvent_t a = take_event(d), b = take_event(d);
-    if (!a || !b) return;
-    d->prof.push_back({kernel, a, b});
-    ev_ = LaunchEvents{a, b};
+    if (!a || !b) {
+        if (a) d->event_pool.push_back(a);
+        if (b) d->event_pool.push_back(b);
+        return;
+    }
+    d_ = d;
+    kernel_ = kernel;
+    ev_ = LaunchEvents{a, b, false};
     g_launch_events = &ev_;
 }
 
-ProfScope::~ProfScope() { g_launch_events = nullptr; }
+ProfScope::~ProfScope() {
+    g_launch_events = nullptr;
+    if (!d_) return;
+    if (ev_.launched) {
+        d_->prof.push_back({kernel_, ev_.start, ev_.stop});
+    } else {  // never recorded: back to the pool
+        d_->event_pool.push_back(ev_.start);
+        d_->event_pool.push_back(ev_.stop);
+    }
+}
 
 // Device bytes held (Device.Used), under the accounting lock.
 void add_used(rk_device *d, int64_t bytes) {

@@ -141,6 +141,29 @@ def test_moe_stage_small_batch1_and_sequences(dev):
     assert dev.used == 0
 
 
+def test_profiling_a_qk_norm_prompt(dev):
+    """Per-launch timing over a prompt of a QK-norm stage: the batched path
+    opens a timing scope for the fused norm-and-scores launch, which it then
+    declines (no launch), and times the separate norm and scores launches
+    instead. The declined scope records nothing, so the readout holds only
+    launches that ran, one of each per layer."""
+    m = moe_model(SMALL, experts=12, ehidden=64, topk=3, seed=1, lo=1e-3, hi=1e-2, router_scale=(1e-2, 5e-2))
+    g = GpuModel(dev, m)
+    try:
+        st = g.stage(96)
+        st.generate_start([1, 5, 9, 2, 7, 30, 11])
+        dev.profile_start()
+        st.generate_run(6)  # the prompt's first six positions: one batch
+        prof = dev.profile_stop()
+        st.free()
+    finally:
+        g.free()
+    layers = SMALL.layers
+    assert prof["qknorm_rope"][0] == layers and prof["att_scores"][0] == layers, prof
+    assert all(calls > 0 and ms >= 0.0 for calls, ms in prof.values()), prof
+    assert dev.used == 0
+
+
 def test_moe_stage_many_experts(dev):
     """200 experts, top 8 (a lane of the routing holds up to 16 experts):
     one sequence, then three."""
