@@ -25,19 +25,25 @@ namespace {
 constexpr int kGrpTok = 16;    // tokens per workgroup
 constexpr int kGrpMaxT = 1024;  // positions a group's weights keep in LDS
 constexpr int kScTile = 64;    // positions per scores workgroup
-constexpr int kGvChunk = 32;   // value positions per LDS tile
-constexpr int kGvPitch = kGvChunk + 4;  // floats per element row (odd count of 16-byte units)
-constexpr int kGvSlices = 4;   // 32-element slices of a head per values workgroup
-constexpr int kGvElems = 32 * kGvSlices;
+// The values workgroup's shape: SL 32-element slices of a head (SL = 4, or
+// 1 for grids too small to fill the machine otherwise); its value tiles hold
+// 128/SL positions (two a thread) of 32·SL elements.
+#define RK_GV_SHAPE(SL)                                                                        \
+    constexpr int kGvSlices = SL;                    /* slices per workgroup */                \
+    constexpr int kGvElems = 32 * kGvSlices;         /* elements per workgroup */              \
+    constexpr int kGvChunk = 128 / kGvSlices;        /* value positions per LDS tile */        \
+    constexpr int kGvPitch = kGvChunk + 4;           /* floats per element row (odd count of 16-byte units) */
 constexpr int kGvThreads = 512;         // eight waves, two tokens each
 constexpr int kHs = 128;                // head size of the scores kernel
 
-// acc[s] + Σ a[t]·v_s[t] for t < n in order, for the four rows v_s = v +
+// acc[s] + Σ a[t]·v_s[t] for t < n in order, for the SL rows v_s = v +
 // 32·s·kGvPitch (float32; each product rounded, then added), a and v in LDS
-// (16-byte aligned). Four independent chains keep the adds issuing every
-// cycle they can; the next four positions' reads are issued before the
-// current ones are summed.
-__device__ __forceinline__ void lds_dot_chain4(const float *a, const float *v, int n, float (&acc)[kGvSlices]) {
+// (16-byte aligned). Independent chains (SL of them) keep the adds issuing;
+// the next four positions' reads are issued before the current ones are
+// summed.
+template <int SL>
+__device__ __forceinline__ void lds_dot_chain(const float *a, const float *v, int n, float (&acc)[SL]) {
+    constexpr int kGvSlices = SL, kGvPitch = 128 / SL + 4;  // as RK_GV_SHAPE(SL)
     const float4 *a4 = reinterpret_cast<const float4 *>(a);
     const int nq = n >> 2;
     auto vq = [&](int s, int k) { return reinterpret_cast<const float4 *>(v + 32 * s * kGvPitch)[k]; };
@@ -135,14 +141,16 @@ __global__ __launch_bounds__(256) void att_scores_group_kernel(const float *q, c
     }
 }
 
-// Softmax and weighted values of up to four 32-element slices of one head
-// (elements e0 .. e0+127) for the group's tokens. Half-wave zl (lanes
+// Softmax and weighted values of up to SL 32-element slices of one head
+// (elements e0 .. e0+32·SL-1) for the group's tokens. Half-wave zl (lanes
 // 32·(zl&1).. of wave zl/2) owns token z0 + zl: its softmax over its
 // positions, once, then the sums of elements e0 + 32·s + lane%32.
+template <int SL>
 __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const float *att, int32_t att_stride,
                                                                       const float *vals, float *out, AttBatch bt,
                                                                       int kv_mul, int hs, int kv_dim, int apitch,
                                                                       int8_t *qx, float *xs, int32_t *xsum) {
+    RK_GV_SHAPE(SL)
     extern __shared__ __align__(16) float smem[];
     __shared__ float s_inv[kGrpTok];
     __shared__ __align__(16) float s_out[kGrpTok][kGvElems];
@@ -165,7 +173,7 @@ __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const floa
     // ---- the value tiles' loads: thread (elements e0 + 4·fq.., positions
     // 2·pq, 2·pq+1 of the chunk); positions past tmax and elements past the
     // head clamped, never summed or stored
-    const int fq = tid & 31, pq = tid >> 5;
+    const int fq = tid % (kGvElems / 4), pq = tid / (kGvElems / 4);
     const float *vbase = vals + (int64_t)g * hs + min(e0 + 4 * fq, hs - 4);
     float4 v0, v1;
     auto load_tile = [&](int c0) {
@@ -206,7 +214,7 @@ __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const floa
         load_tile(c0 + kGvChunk);  // the next tile, in flight during the sums
         const float *tile = vt + buf * (kGvElems * kGvPitch);
         const int n = max(0, min(kGvChunk, Tz - c0));
-        lds_dot_chain4(az + c0, tile + l32 * kGvPitch, n, acc);
+        lds_dot_chain<SL>(az + c0, tile + l32 * kGvPitch, n, acc);
         // the other buffer was last read two tiles ago, before the barrier
         // that ended that iteration
         store_tile(vt + (buf ^ 1) * (kGvElems * kGvPitch));
@@ -225,13 +233,13 @@ __global__ __launch_bounds__(kGvThreads) void att_values_group_kernel(const floa
 #pragma unroll
         for (int s = 0; s < kGvSlices; s++) s_out[zl][32 * s + l32] = acc[s];
         __syncthreads();
-        const int sb = l32 >> 3, q = l32 & 7;
+        const int sb = min(l32 >> 3, kGvSlices - 1), q = l32 & 7;
         const float4 v4 = reinterpret_cast<const float4 *>(&s_out[zl][32 * sb])[q];
         float d;
         int cs;
         const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
         const int64_t bb = base + 32 * sb;
-        if (live && sb < ns) {
+        if (live && (l32 >> 3) < ns) {
             reinterpret_cast<uint32_t *>(qx + bb)[q] = pk;
             if (q == 0) {
                 xs[bb >> 5] = d;
@@ -254,20 +262,35 @@ void launch_att_scores_group(const float *q, const float *keys, float *att, int3
               inv_sqrt);
 }
 
-void launch_att_values_group(const float *att, int32_t att_stride, const float *vals, float *out, const AttBatch &bt,
+template <int SL>
+static void launch_values_sl(const float *att, int32_t att_stride, const float *vals, float *out, const AttBatch &bt,
                              int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
                              hipStream_t s) {
+    RK_GV_SHAPE(SL)
     static std::once_flag once;
     std::call_once(once, [] {
-        (void)hipFuncSetAttribute((const void *)att_values_group_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)(kMaxLdsBytes - 12288));
+        (void)hipFuncSetAttribute((const void *)att_values_group_kernel<SL>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)(kMaxLdsBytes - 12288));
     });
     const int tmax = bt.pos0 + bt.tokens;
     const int apitch = ((tmax + 3) & ~3) + 4;
     const size_t lds = ((size_t)kGrpTok * apitch + 2 * kGvElems * kGvPitch) * 4;
     const dim3 grid(heads, (hs + kGvElems - 1) / kGvElems, (bt.tokens + kGrpTok - 1) / kGrpTok);
-    RK_LAUNCH(att_values_group_kernel, grid, dim3(kGvThreads), lds, s, att, att_stride, vals, out, bt,
+    RK_LAUNCH(att_values_group_kernel<SL>, grid, dim3(kGvThreads), lds, s, att, att_stride, vals, out, bt,
               heads / kv_heads, hs, kv_dim, apitch, qx, xs, xsum);
+}
+
+void launch_att_values_group(const float *att, int32_t att_stride, const float *vals, float *out, const AttBatch &bt,
+                             int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
+                             hipStream_t s) {
+    // four slices a workgroup (the softmax once per head and token group)
+    // unless that leaves fewer workgroups than CUs (a short batch): then one
+    // slice a workgroup, four times the workgroups
+    const int64_t wgs4 = (int64_t)heads * ((hs + 127) / 128) * ((bt.tokens + kGrpTok - 1) / kGrpTok);
+    if (wgs4 >= 256)
+        launch_values_sl<4>(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s);
+    else
+        launch_values_sl<1>(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s);
 }
 
 }  // namespace rk
