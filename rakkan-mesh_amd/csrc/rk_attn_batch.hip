@@ -12,7 +12,8 @@
 // What a group changes is only who loads what: a key tile serves the
 // group's sixteen queries, a value tile the group's sixteen weight rows, and
 // a workgroup runs sixteen tokens' sequential sums side by side (one per
-// half-wave for the softmax, one per lane and element for the values).
+// half-wave for the softmax, one per lane and element for the values, a
+// lane holding the elements e, e+32, e+64, e+96 of its token).
 #include <mutex>
 
 #include "rk_dev.h"
