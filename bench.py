@@ -821,8 +821,8 @@ def main():
     ap.add_argument("--prefill-decode", type=int, default=64)
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py runs on one GPU: this build has no multi-GPU path (how the products would shard is "
-              "described in DESIGN.md, not built). Use --gpus 1.", file=sys.stderr)
+        print("bench.py runs on one GPU: this build has no multi-GPU path (the products' sharding is a "
+              "design, not built). Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import rkhip
