@@ -60,6 +60,7 @@ def _declare(L):
         "rko_transcendental_words": (None, [P, I64]),
         "rko_matvec": (None, [P, P, P]), "rko_rope_table": (None, [P, I32, P, P]),
         "rko_rmsnorm": (None, [P, P, P, I64, F32]), "rko_softmax": (None, [P, I64]), "rko_silu": (F32, [F32]),
+        "rko_inv_sqrt_head": (F32, [ctypes.c_int]),
         "rko_attention_head": (None, [P, P, P, I64, ctypes.c_int, ctypes.c_int, F32, P, P]),
         "rko_set_matvec_threads": (None, [ctypes.c_int]),
         "rko_forward": (None, [P, P, I32, P, P, P, P, I32, P, I32, P]),

@@ -730,12 +730,17 @@ static void rotate(float *v, int i, float co, float si) {
     v[i + 1] = (v0 * si) + (v1 * co);
 }
 
+/* internal/llm/model.go:529, gpustage.go:125: the scores' scale,
+ * float32(1/math.Sqrt(float64(hs))): a float64 square root and division,
+ * rounded once more to float32. */
+float rko_inv_sqrt_head(int hs) { return (float)(1.0 / sqrt((double)hs)); }
+
 /* internal/llm/model.go:522-613 Stage.Forward */
 void rko_forward(const rko_config *c, const rko_layer *layers, int32_t nlayers, const float *cos_t, const float *sin_t,
                  float **keys, float **vals, int32_t ctx, float *x, int32_t pos, float *scratch) {
     int hs = head_size(c), qDim = c->heads * hs, kvDim = c->kv_heads * hs, dim = c->dim, hidden = c->hidden;
     int kvMul = c->heads / c->kv_heads, half = hs / 2;
-    float invSqrt = (float)(1.0 / sqrt((double)hs));
+    float invSqrt = rko_inv_sqrt_head(hs);
     float eps = eps_of(c);
     float *xb = scratch, *xb2 = xb + dim, *q = xb2 + dim, *k = q + qDim, *v = k + kvDim, *attOut = v + kvDim;
     float *hb = attOut + qDim, *hb2 = hb + hidden, *att = hb2 + hidden;

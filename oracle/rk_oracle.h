@@ -11,6 +11,15 @@
  * definition in rk_oracle.c. Compiled with -O2 -ffp-contract=off
  * -fno-fast-math on x86-64 (SSE scalar float: every float32 operation rounds
  * once, as Go's explicit conversions demand).
+ *
+ * Each function is pinned, not just restated. The pins are the
+ * reference's known answers and digests, its DeepSeek vectors, closed forms
+ * and brute force, and exact-rational restatements that catch each
+ * plausible slip (tests/test_oracle_*.py). Two areas are "parity unpinned"
+ * against the reference:
+ * - the MoE routing (rko_topk, rko_moe_ffn): the reference has no such
+ *   model, so this build's own contract stands in for it;
+ * - NaN payloads and Go's int8(NaN), which the parity inputs exclude.
  */
 #ifndef RK_ORACLE_H
 #define RK_ORACLE_H
@@ -130,6 +139,7 @@ void rko_softmax(float *x, int64_t n);
 void rko_attention_head(const float *qh, const float *keys, const float *vals, int64_t kv_stride, int hs,
                         int positions, float inv_sqrt, float *att, float *out);
 float rko_silu(float v);
+float rko_inv_sqrt_head(int hs);
 void rko_num_eval(int fn, const float *in, float *out, int64_t n);
 /* One token through layers [0, nlayers) at position pos, x in place.
  * keys/vals: per layer [ctx][kvDim]. scratch: at least

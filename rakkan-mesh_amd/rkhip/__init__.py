@@ -128,6 +128,14 @@ class StageLayer(ctypes.Structure):
                                  "q_norm", "k_norm", "moe")]
 
 
+def inv_sqrt_head(hs):
+    """The attention scores' scale as the Go host computes it
+    (internal/llm/model.go:529, gpustage.go:125):
+    float32(1/math.Sqrt(float64(hs))), a float64 square root and division
+    (each correctly rounded) rounded once more to float32."""
+    return np.float32(1.0 / np.sqrt(np.float64(hs)))
+
+
 def lib():
     """The loaded librkhip.so; raises if it is not built."""
     global _lib
@@ -584,7 +592,7 @@ class Stage:
                  norm_eps=1e-5, qkv_bias=False, qk_norm=False, seqs=1):
         hs = head_dim if head_dim > 0 else dim // heads
         rd, rh = dev.num_eval(FN_RECIP32, np.array([dim, hs], np.float32))
-        inv_sqrt = np.float32(1.0 / np.sqrt(np.float64(hs)))  # float32(1/math.Sqrt(float64(hs)))
+        inv_sqrt = inv_sqrt_head(hs)
         self.dev, self.dim, self.ctx, self.hs, self.seqs = dev, dim, ctx, hs, seqs
         self.cfg = StageConfig(dim, hidden, heads, kv_heads, head_dim, ctx, int(qkv_bias), int(qk_norm),
                                float(np.float32(norm_eps)), float(rd), float(rh), float(inv_sqrt), seqs)

@@ -1,7 +1,6 @@
 """The reference's GPU stage (internal/llm/gpustage.go) driven through the
 Batch C-ABI, operation for operation: what internal/llm keeps doing on top
 of the cgo shim. Used by the stage parity tests."""
-import math
 
 import numpy as np
 
@@ -93,7 +92,7 @@ class GPUStage:
         eps = c.eps()
         recip_dim = oracle.recip32(np.float32(c.dim))  # num.Recip32, computed by the Go host
         recip_head = oracle.recip32(np.float32(hs))
-        inv_sqrt = np.float32(1 / math.sqrt(hs))
+        inv_sqrt = rkhip.inv_sqrt_head(hs)
         half = hs // 2
         o = self.offs
         for li in range(len(self.layers)):
