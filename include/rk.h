@@ -264,6 +264,10 @@ int rk_graph_begin(rk_device *dev);
 int rk_graph_end(rk_device *dev, rk_graph **out);
 /* Enqueues `times` replays on the device stream and waits for them. */
 int rk_graph_launch(rk_graph *g, int32_t times);
+/* rk_graph_launch with the replays bracketed by two events on the device
+ * stream: *ms is the device time from the first replay's start to the last
+ * one's end (the host's enqueue cost is not in it). */
+int rk_graph_launch_timed(rk_graph *g, int32_t times, float *ms);
 int rk_graph_free(rk_graph *g);
 
 /* ---- Stages: a run of llama-family layers resident on one device ----

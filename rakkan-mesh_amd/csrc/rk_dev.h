@@ -240,15 +240,11 @@ __device__ __forceinline__ uint32_t quantize_group(float v0, float v1, float v2,
     a = __builtin_elementwise_maximum(a, __int_as_float(dpp_mirror8(__float_as_int(a))));
     a = canonical(a);  // Go max gives the canonical NaN
     d = a * u2f(k1_127);
+    // a zero or NaN scale gives codes 0 (quant.go:44-46): v·0 is ±0 or NaN,
+    // both code 0, so the codes need no branch
     const bool zero = (d == 0.0f) || (d != d);
-    const float id = recip32(d);
-    int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
-    if (!zero) {
-        c0 = q8_code(v0, id);
-        c1 = q8_code(v1, id);
-        c2 = q8_code(v2, id);
-        c3 = q8_code(v3, id);
-    }
+    const float id = zero ? 0.0f : recip32(d);
+    const int c0 = q8_code(v0, id), c1 = q8_code(v1, id), c2 = q8_code(v2, id), c3 = q8_code(v3, id);
     int s = c0 + c1 + c2 + c3;
     s += dpp_x1(s);
     s += dpp_x2(s);
@@ -267,18 +263,13 @@ __device__ __forceinline__ void quantize_block32(const float4 (&v)[8], uint32_t 
     for (int k = 0; k < 8; k++) a = abs_max3(abs_max3(a, v[k].x, v[k].y), v[k].z, v[k].w);
     a = canonical(a);
     d = a * u2f(k1_127);
+    // a zero or NaN scale gives codes 0 (v·0 is ±0 or NaN: code 0, no branch)
     const bool zero = (d == 0.0f) || (d != d);
-    const float id = recip32(d);
+    const float id = zero ? 0.0f : recip32(d);
     int s = 0;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        int c0 = 0, c1 = 0, c2 = 0, c3 = 0;
-        if (!zero) {
-            c0 = q8_code(v[k].x, id);
-            c1 = q8_code(v[k].y, id);
-            c2 = q8_code(v[k].z, id);
-            c3 = q8_code(v[k].w, id);
-        }
+        const int c0 = q8_code(v[k].x, id), c1 = q8_code(v[k].y, id), c2 = q8_code(v[k].z, id), c3 = q8_code(v[k].w, id);
         s += (c0 + c1) + (c2 + c3);
         pk[k] = (uint32_t)(c0 & 255) | ((uint32_t)(c1 & 255) << 8) | ((uint32_t)(c2 & 255) << 16) |
                 ((uint32_t)(c3 & 255) << 24);

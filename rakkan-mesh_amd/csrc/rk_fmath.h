@@ -57,15 +57,20 @@ __device__ __forceinline__ float split(float x, int &e) {
     return u2f((b & 0x7fffffu) | (127u << 23));
 }
 
-// internal/num/recip.go:38-67 Recip32.
+// internal/num/recip.go:38-67 Recip32, without branches: the main path runs
+// for every input and the special cases (NaN, ±0, ±Inf; a subnormal input's
+// scaling into the normal range; Scale2 for a result outside it) are picked
+// by selects, so the code is one straight run (a one-time prologue pays for
+// every branch target it has to fetch). Pow2's argument is out of range only
+// on the paths the selects discard.
 __device__ __forceinline__ float recip32(float x) {
-    if (x != x) return u2f(kCanonNaN);
-    uint32_t sign = f2u(x) & 0x80000000u;
-    float ax = u2f(f2u(x) & 0x7fffffffu);
-    if (ax == 0.0f) return u2f(sign | 0x7f800000u);
-    if (ax == __builtin_inff()) return u2f(sign);
-    int e;
-    float m = split(ax, e);
+    const uint32_t bx = f2u(x);
+    const uint32_t sign = bx & 0x80000000u;
+    const uint32_t ab = bx & 0x7fffffffu;
+    const bool sub = (ab >> 23) == 0;
+    const uint32_t b = sub ? f2u(u2f(ab) * pow2(64)) : ab;
+    const int e = (sub ? -64 : 0) + (int)(b >> 23) - 127;
+    const float m = u2f((b & 0x7fffffu) | (127u << 23));
     float r = u2f(k24_17) - (u2f(k8_17) * m);
 #pragma unroll
     for (int i = 0; i < 3; i++) {
@@ -73,11 +78,12 @@ __device__ __forceinline__ float recip32(float x) {
         float t = r * (1.0f - mr);
         r = r + t;
     }
-    if (e > 126 || e < -127)
-        r = scale2(r, -e);
-    else
-        r = r * pow2(-e);
-    return u2f(f2u(r) | sign);
+    const int k = -e, k1 = k / 2;
+    const float rs = (r * pow2(k1)) * pow2(k - k1);  // Scale2(r, -e)
+    const float rd = r * pow2(k);
+    r = (e > 126 || e < -127) ? rs : rd;
+    const uint32_t out = ab > 0x7f800000u ? kCanonNaN : ab == 0 ? (sign | 0x7f800000u) : ab == 0x7f800000u ? sign : (f2u(r) | sign);
+    return u2f(out);
 }
 
 // internal/num/recip.go:70-93 Rsqrt32.

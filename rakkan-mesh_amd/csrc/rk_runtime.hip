@@ -731,6 +731,25 @@ int rk_graph_launch(rk_graph *g, int32_t times) {
     return RK_OK;
 }
 
+int rk_graph_launch_timed(rk_graph *g, int32_t times, float *ms) {
+    if (!g || times < 0 || !ms) return RK_ERR_ARGS;
+    rk_device *d = g->d;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIP_TRY(d, hipEventCreate(&e0), "event create");
+    hipError_t e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipEventRecord(e0, d->stream);
+    for (int32_t i = 0; i < times && e == hipSuccess; i++) e = hipGraphLaunch(g->exec, d->stream);
+    if (e == hipSuccess) e = hipEventRecord(e1, d->stream);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (e != hipSuccess) return hip_fail(d, e, "timed graph launch");
+    return RK_OK;
+}
+
 int rk_graph_free(rk_graph *g) {
     if (!g) return RK_ERR_ARGS;
     (void)hipGraphExecDestroy(g->exec);

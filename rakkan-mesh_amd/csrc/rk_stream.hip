@@ -339,7 +339,17 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
         // weight loads issued after them are outstanding
         __builtin_amdgcn_s_waitcnt(vmcnt_wait(2 * U));
     }
-    if (PRO != kProGlobal || !XR) __syncthreads();
+    if (PRO == kProGlobal && !XR) {
+        // The workgroup barrier without __syncthreads' fence: at the fence
+        // the compiler counts the direct-to-LDS loads above as pending (it
+        // does not see the wait) and would wait for every weight load in
+        // flight. This wave's LDS writes are done (the wait above); the
+        // memory clobber keeps the LDS reads below after the barrier.
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+    } else if (PRO != kProGlobal) {
+        __syncthreads();
+    }
     if (PRO != kProGlobal && XR) {
 #pragma unroll
         for (int c = 0; c < C; c++) {

@@ -81,6 +81,7 @@ SIGNATURES = {
     "rk_graph_begin": (ctypes.c_int, [P]),
     "rk_graph_end": (ctypes.c_int, [P, P]),
     "rk_graph_launch": (ctypes.c_int, [P, I32]),
+    "rk_graph_launch_timed": (ctypes.c_int, [P, I32, P]),
     "rk_graph_free": (ctypes.c_int, [P]),
     "rk_profile_start": (ctypes.c_int, [P]),
     "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
@@ -537,6 +538,13 @@ class Graph:
 
     def launch(self, times=1):
         self.dev._check(lib().rk_graph_launch(self.h, times))
+
+    def launch_timed(self, times=1):
+        """Replays `times` times and returns the device milliseconds from
+        the first replay's start to the last one's end (stream events)."""
+        ms = ctypes.c_float()
+        self.dev._check(lib().rk_graph_launch_timed(self.h, times, ctypes.byref(ms)))
+        return ms.value
 
     def free(self):
         if self.h:
