@@ -160,7 +160,10 @@ size_t stream_norm_lds(int n) { return (size_t)32 * ((((n >> 5) + 3) & ~3) + 4) 
 // the 32 writing lanes of a Q8 chunk fall in distinct banks.
 constexpr int stream_k8p(int fmt, int c) { return (((fmt == kFmtQ8 ? c * 32 : c * 64) / 8 + 3) & ~3) + 4; }
 
-template <int FMT, int PRO, int EPI, int K, int U, int C>
+// PF: the last U steps of a batch prefetch the next batch's first chunks.
+// Without (a workgroup of one batch) those steps issue no loads, and the
+// waits are fixed counts all the same.
+template <int FMT, int PRO, int EPI, int K, int U, int C, bool PF>
 __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
     extern __shared__ __align__(16) char lds[];
     __shared__ float s_wv[16];
@@ -223,10 +226,32 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
             xv[k] = reinterpret_cast<const float4 *>(a.x)[g];
             wv[k] = reinterpret_cast<const float4 *>(a.norm_w)[g];
         }
-    } else if (PRO == kProQuant) {
-        const float4 *xp = reinterpret_cast<const float4 *>(a.x) + 8 * min((int)threadIdx.x, nb - 1);
+    } else if (PRO == kProQuant && XR) {
+        // only the waves that quantize a block load x
+        if ((int)threadIdx.x - lane < nb) {  // uniform
+            const float4 *xp = reinterpret_cast<const float4 *>(a.x) + 8 * min((int)threadIdx.x, nb - 1);
 #pragma unroll
-        for (int k = 0; k < 8; k++) xb[k] = xp[k];
+            for (int k = 0; k < 8; k++) xb[k] = xp[k];
+        }
+    } else if (PRO == kProQuant) {
+        // A wide input (rows of more than 4 chunks): x staged in LDS as it
+        // lies in memory (the term buffer's room, unused until the batches)
+        // by direct-to-LDS loads of 1 KiB, wave w taking blocks
+        // 64w .. 64w+63; then a barrier, so every wave's loads of x are
+        // issued before any weight load of the workgroup (the vector memory
+        // queue is in issue order: x behind the weights' first rounds came
+        // in microseconds late).
+        if (wave * 64 < nb) {  // uniform
+            const int nq4 = cols >> 2;
+            float *xf = reinterpret_cast<float *>(lds + a.lds_norm);
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int p0 = (wave * 64 + 8 * k) * 8;  // the load's first 16-byte piece
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const float4 *>(a.x) + min(p0 + lane, nq4 - 1),
+                                                 lds_ptr(xf + 4 * p0), 16, 0, 0);
+            }
+        }
+        asm volatile("s_barrier" ::: "memory");  // issue order only: no wait for the loads
     } else if (XR) {
 #pragma unroll
         for (int c = 0; c < C; c++) {
@@ -288,7 +313,10 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
     // end re-read its last piece; their blocks are never summed). Past the
     // last batch the same loads go to empty buffers (no records): they
     // return zeros without touching memory, so every batch issues the same
-    // loads and the waits stay fixed counts.
+    // loads and the waits stay fixed counts. They still pass through the
+    // vector memory queue, which backs up at a launch's start (measured: a
+    // 4096x4096 product 5.70 -> 5.17 us without them), so a workgroup of
+    // one batch is built without the prefetch (PF false).
     constexpr int NR = (U + C - 1) / C;  // rows the prefetch of a batch's first U chunks reaches
     Row rsrc[K];
     auto set_row = [&](Row &r, int l, bool live) {
@@ -321,6 +349,30 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
     if (PRO == kProNorm) {
         norm_quant_rt<MG>(xv, wv, cols, nt, a.recip_n, a.norm_eps, sqx, sxs, sxsum,
                           reinterpret_cast<float *>(lds + a.lds_norm), &s_rn);
+    } else if (PRO == kProQuant && !XR) {
+        // one block a lane from the staged x, once this wave's loads of it
+        // are in (issued before its 2U weight loads; the wait is outside the
+        // branch so that no path meets the barrier with them pending). The
+        // block's eight 16-byte pieces are read from piece l mod 8 on, so a
+        // read's lanes fall in distinct banks; the maximum and the code sum
+        // do not depend on that order, and each piece's codes go to its place.
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait(2 * U));
+        const int b = wave * 64 + lane;
+        if (b < nb) {
+            const float4 *xb4 = reinterpret_cast<const float4 *>(lds + a.lds_norm) + b * 8;
+            float4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = xb4[(j + lane) & 7];
+            uint32_t pk[8];
+            float d;
+            int cs;
+            quantize_block32(v, pk, d, cs);
+            uint32_t *q = reinterpret_cast<uint32_t *>(sqx) + b * 8;
+#pragma unroll
+            for (int j = 0; j < 8; j++) q[(j + lane) & 7] = pk[j];
+            sxs[b] = d;
+            sxsum[b] = cs;
+        }
     } else if (PRO == kProQuant) {
         // one block per thread (Recip32 once a block)
         if ((int)threadIdx.x < nb) {
@@ -376,8 +428,10 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
         load_ops(j);
         const bool next = j + 1 < nbatch;  // uniform: the last U chunks prefetch the next batch's first
         Row rn[NR];
+        if (PF) {
 #pragma unroll
-        for (int h = 0; h < NR; h++) set_row(rn[h], R0 + (j + 1) * RB + wave * K + h, next);
+            for (int h = 0; h < NR; h++) set_row(rn[h], R0 + (j + 1) * RB + wave * K + h, next);
+        }
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const int h = s / C, c = s % C, slot = s % U;
@@ -425,7 +479,7 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
             }
             if (s + U < NS)
                 load_step(rsrc, s + U, slot);
-            else
+            else if (PF)
                 load_step(rn, s + U - NS, slot);
         }
         // the rows: lane group g adds running sum L of row g in block order
@@ -487,12 +541,14 @@ __global__ __launch_bounds__(1024) void stream_kernel(FusedArgs a, int nbatch) {
                     nan0 = true;
             }
         }
+        if (PF) {
 #pragma unroll
-        for (int h = 0; h < K; h++) {
-            if (h < NR)
-                rsrc[h] = rn[h];
-            else
-                set_row(rsrc[h], R0 + (j + 1) * RB + wave * K + h, next);
+            for (int h = 0; h < K; h++) {
+                if (h < NR)
+                    rsrc[h] = rn[h];
+                else
+                    set_row(rsrc[h], R0 + (j + 1) * RB + wave * K + h, next);
+            }
         }
     }
 
@@ -564,10 +620,10 @@ typedef void (*StreamFn)(FusedArgs, int);
 
 struct StreamInst {
     int fmt, pro, epi, k, u, c;
-    StreamFn fn;
+    StreamFn fn, fn1;  // prefetching the next batch; one batch a workgroup
 };
 
-#define RK_SI(F, P, E, K, U, C) {F, P, E, K, U, C, stream_kernel<F, P, E, K, U, C>}
+#define RK_SI(F, P, E, K, U, C) {F, P, E, K, U, C, stream_kernel<F, P, E, K, U, C, true>, stream_kernel<F, P, E, K, U, C, false>}
 
 // The widths of the configurations this build is measured on (Q8: 2048, 4096 and
 // 14336 columns, C = 2, 4 and 14; Q4: 3584/4096 and 18944 columns, C = 2 and
@@ -711,17 +767,19 @@ bool launch_stream(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s
     }
     a.lds_res = a.lds_norm = at;
     const int tb = W * K * 8 * k8p * 4;
-    at += std::max(tb, pro == kProNorm ? (int)stream_norm_lds(cols) : 0);
+    // (a wide quantize prologue stages x there: 8 KiB for each wave's 64 blocks)
+    at += std::max(tb, pro == kProNorm ? (int)stream_norm_lds(cols) : pro == kProQuant && !xr ? (nb + 63) / 64 * 8192 : 0);
     a.lds_ep = at;
     if (hq) at += al16(a.rows_per_wg / 2 * 4);
     a.lds_bytes = at;
     if (at > kStreamLdsMax) return false;
+    const StreamFn fn = nbatch > 1 ? inst->fn : inst->fn1;
     if (at > 64 * 1024) {
         static std::mutex mu;
         std::lock_guard<std::mutex> l(mu);
-        (void)hipFuncSetAttribute((const void *)inst->fn, hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLdsMax);
+        (void)hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLdsMax);
     }
-    RK_LAUNCH(inst->fn, dim3(grid), dim3(64 * W), (size_t)at, s, a, nbatch);
+    RK_LAUNCH(fn, dim3(grid), dim3(64 * W), (size_t)at, s, a, nbatch);
     return true;
 }
 
