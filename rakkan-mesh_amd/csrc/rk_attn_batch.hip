@@ -283,12 +283,13 @@ static void launch_values_sl(const float *att, int32_t att_stride, const float *
 
 void launch_att_values_group(const float *att, int32_t att_stride, const float *vals, float *out, const AttBatch &bt,
                              int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
-                             hipStream_t s) {
+                             hipStream_t s, int cu) {
     // four slices a workgroup (the softmax once per head and token group)
-    // unless that leaves fewer workgroups than CUs (a short batch): then one
-    // slice a workgroup, four times the workgroups
+    // unless that leaves fewer workgroups than the device has CUs (a short
+    // batch; cu 0: the MI355X's 256): then one slice a workgroup, four
+    // times the workgroups
     const int64_t wgs4 = (int64_t)heads * ((hs + 127) / 128) * ((bt.tokens + kGrpTok - 1) / kGrpTok);
-    if (wgs4 >= 256)
+    if (wgs4 >= (cu > 0 ? cu : 256))
         launch_values_sl<4>(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s);
     else
         launch_values_sl<1>(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s);

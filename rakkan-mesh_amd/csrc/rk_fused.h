@@ -142,12 +142,12 @@ void launch_att_scores_group(const float *q, const float *keys, float *att, int3
                              int heads, int kv_heads, int kv_dim, float inv_sqrt, hipStream_t s);
 void launch_att_values_group(const float *att, int32_t att_stride, const float *vals, float *out, const AttBatch &bt,
                              int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
-                             hipStream_t s);
+                             hipStream_t s, int cu = 0);
 // With qx non-null (head size a multiple of 32), the output is also
 // quantized (Q8_0 blocks of the next product's input).
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx,
-                       float *xs, int32_t *xsum, hipStream_t s);
+                       float *xs, int32_t *xsum, hipStream_t s, int cu = 0);
 // QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches, at
 // the position in ctl (or, ctl null, for `tokens` rows at pos0, pos0+1, ...;
 // or, seq_pos set, row z at seq_pos[z] in caches cache_stride floats apart).

@@ -1157,7 +1157,7 @@ int att_values_max_ctx() { return (int)(kValMaxDynLds / 4 - 2 * kValSlice * val_
 
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx,
-                       float *xs, int32_t *xsum, hipStream_t s) {
+                       float *xs, int32_t *xsum, hipStream_t s, int cu) {
     static std::once_flag once;
     std::call_once(once, [] {
         (void)hipFuncSetAttribute((const void *)att_values_kernel<true, kValChunk>,
@@ -1168,7 +1168,7 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
                                   (int)att_values_reg_lds(kVrMaxCtx));
     });
     if (!ctl && att_group_fits(bt, hs, kv_dim)) {
-        launch_att_values_group(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s);
+        launch_att_values_group(att, att_stride, vals, out, bt, heads, kv_heads, hs, kv_dim, qx, xs, xsum, s, cu);
         return;
     }
     if (hs % 32 != 0) qx = nullptr;

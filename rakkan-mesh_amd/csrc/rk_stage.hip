@@ -186,7 +186,8 @@ static void enqueue_attention(rk_stage *s, hipStream_t st, const float *q, float
         launch_att_scores(q, keys, att, c.ctx, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, c.inv_sqrt, st);
     }
     ProfScope p(d, st, "att_values");
-    launch_att_values(att, c.ctx, vals, out, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, qx, xs, xsum, st);
+    launch_att_values(att, c.ctx, vals, out, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, qx, xs, xsum, st,
+                      d->cu);
 }
 
 // The launches of one layer (Stage.Forward's body, model.go:530-611). The

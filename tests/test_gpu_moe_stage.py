@@ -141,6 +141,23 @@ def test_moe_stage_small_batch1_and_sequences(dev):
     assert dev.used == 0
 
 
+def test_moe_stage_expert_hidden_over_2048(dev):
+    """An expert hidden width of 2080 (over 64 blocks a lane group of eight
+    holds): one token's W2 rows then go through the general down kernel,
+    reading the grouping that the W1/W3 launch's lead workgroup wrote, in
+    place of the one-token down kernel. One sequence, then two (the grouped
+    path of several tokens), every logit against the oracle."""
+    m = moe_model(SMALL, experts=6, ehidden=2080, topk=2, seed=6, lo=1e-3, hi=1e-2, router_scale=(1e-2, 5e-2))
+    g = GpuModel(dev, m)
+    try:
+        with oracle.matvec_threads(THREADS):
+            check_batch1(g, [4, 9, 1], 6, 32)
+            check_seqs(g, [[2, 8], [5]], 4, 32)
+    finally:
+        g.free()
+    assert dev.used == 0
+
+
 def test_profiling_a_qk_norm_prompt(dev):
     """Per-launch timing over a prompt of a QK-norm stage: the batched path
     opens a timing scope for the fused norm-and-scores launch, which it then
