@@ -446,12 +446,8 @@ int rk_tensor_scale(rk_device *dev, int32_t dtype, const void *a, float *out, in
  * RK_ERR_OOM; a broken stream returns RK_ERR_HIP. Blocking; one call serves
  * one worker, so several workers take one thread each. */
 int rk_tensor_serve(rk_device *dev, int32_t fd, int64_t max_bytes);
-/* Worker side: one product through the node on fd, with write and read on
- * fd only (no device, no file opened). Returns the node's status for the
- * request, RK_ERR_ARGS for arguments the request cannot carry, or
- * RK_ERR_NO_DEVICE when the stream is closed or broken. */
-int rk_tensor_call(int32_t fd, int32_t dtype, int32_t transposed, int64_t m, int64_t k, int64_t n, const void *a,
-                   const void *b, void *c);
+/* The worker side, rk_tensor_call, is in librkworker.so (rk_worker.h): a
+ * host-only library, so the worker loads none of the GPU runtime. */
 
 /* internal/gpu/profile.go:82-109 StartProfile / StopProfile. While a
  * profile is active, every kernel the library launches is bracketed by HIP

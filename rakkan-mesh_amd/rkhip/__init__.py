@@ -9,6 +9,10 @@ import os
 
 import numpy as np
 
+# The error type is the broker worker module's (librkworker.so, host only),
+# so a status from either library is one class to catch.
+from rkworker import RKError
+
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "librkhip.so")
 HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "rk.h")
@@ -22,12 +26,6 @@ I64 = ctypes.c_int64
 F = ctypes.c_float
 
 _lib = None
-
-
-class RKError(RuntimeError):
-    def __init__(self, code, msg):
-        super().__init__(f"rk error {code}: {msg}")
-        self.code = code
 
 
 class DeviceInfo(ctypes.Structure):
@@ -87,7 +85,6 @@ SIGNATURES = {
     "rk_profile_stop": (ctypes.c_int, [P, P, I32, P]),
     "rk_device_launch_floor": (ctypes.c_int, [P, I64, I32, I32, P, P]),
     "rk_tensor_serve": (ctypes.c_int, [P, I32, I64]),
-    "rk_tensor_call": (ctypes.c_int, [I32, I32, I32, I64, I64, I64, P, P, P]),
     "rk_stage_new": (ctypes.c_int, [P, P, P, I32, P, P, P]),
     "rk_stage_forward": (ctypes.c_int, [P, P, I32, I32]),
     "rk_stage_bytes": (I64, [P]),
@@ -182,22 +179,11 @@ def best(infos):
 
 
 def tensor_call(fd, a, b, transposed=False):
-    """The worker side of the tensor broker (rk_tensor_call): one matmul /
-    matmul_t through the node on descriptor fd, with reads and writes on fd
-    only (no device opened here). Raises RKError with the node's status."""
-    if a.dtype != b.dtype or a.dtype not in (np.float32, np.int8):
-        raise RKError(-1, "tensor call: f32 or i8 inputs of one type")
-    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
-    m, k = a.shape
-    n = b.shape[0] if transposed else b.shape[1]
-    if (b.shape[1] if transposed else b.shape[0]) != k:
-        raise RKError(-1, "tensor call: shapes differ")
-    dt = TENSOR_F32 if a.dtype == np.float32 else TENSOR_I8
-    c = np.empty((m, n), np.float32 if dt == TENSOR_F32 else np.int32)
-    rc = lib().rk_tensor_call(fd, dt, int(bool(transposed)), m, k, n, _ptr(a), _ptr(b), _ptr(c))
-    if rc != RK_OK:
-        raise RKError(rc, "tensor call through the broker")
-    return c
+    """The worker side of the tensor broker, as rkworker.tensor_call (which
+    a worker process imports alone: librkworker.so, no GPU runtime)."""
+    import rkworker
+
+    return rkworker.tensor_call(fd, a, b, transposed)
 
 
 def device_bytes_budget(info):

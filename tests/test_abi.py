@@ -10,8 +10,8 @@ import pytest
 import rkhip
 
 
-def header_functions():
-    src = open(rkhip.HEADER).read()
+def header_functions(path=None):
+    src = open(path or rkhip.HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     return sorted(set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(rk_\w+)\s*\(", src, flags=re.M)))
 
@@ -30,6 +30,21 @@ def test_library_exports_every_declared_symbol():
 
 def test_bindings_cover_the_header():
     assert sorted(rkhip.SIGNATURES) == header_functions()
+
+
+def test_worker_library_exports_what_rk_worker_h_declares():
+    """librkworker.so (the tensor broker's worker side, host code only)
+    against include/rk_worker.h, and its bindings (rkworker.py)."""
+    import rkworker
+
+    names = header_functions(rkworker.HEADER)
+    assert names == ["rk_tensor_call"]
+    out = subprocess.run(["nm", "-D", "--defined-only", rkworker.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT (rk_\w+)$", out.stdout, flags=re.M))
+    assert set(names) <= exported
+    assert sorted(rkworker.SIGNATURES) == names
+    for n in names:
+        getattr(rkworker.lib(), n)
 
 
 def test_no_device_is_an_error_not_a_crash():

@@ -5,7 +5,9 @@ products over an inherited socket (internal/isolate/inherit_unix.go:10),
 and this process answers them on the GPU. The results equal the oracle's
 and the direct product's bits; malformed and oversized requests are
 answered with their error and end serving."""
+import errno
 import os
+import platform
 import socket
 import subprocess
 import sys
@@ -28,10 +30,15 @@ def bits(x):
 
 
 def test_worker_products_through_the_node(dev, tmp_path):
+    """The worker process loads librkworker.so alone and runs under a filter
+    that refuses open and ioctl (opening /dev/kfd gives EPERM there); the
+    node serves its products on the device, every result the oracle's bits."""
     node, worker = socket.socketpair()
     out = tmp_path / "res.npz"
-    p = subprocess.Popen([sys.executable, broker_worker.__file__, str(worker.fileno()), str(out)],
-                         pass_fds=(worker.fileno(),))
+    args = [sys.executable, broker_worker.__file__, str(worker.fileno()), str(out)]
+    if platform.machine() == "x86_64":
+        args.append("--seccomp")
+    p = subprocess.Popen(args, pass_fds=(worker.fileno(),))
     worker.close()
     err = []
 
@@ -53,6 +60,8 @@ def test_worker_products_through_the_node(dev, tmp_path):
     assert not t.is_alive() and not err, err
     assert rc == 0
     res = np.load(out)
+    if platform.machine() == "x86_64":
+        assert int(res["kfd_open_errno"]) == errno.EPERM
     for name, a, b, tr in broker_worker.cases():
         want = oracle.tensor_matmul_f32(a, b, tr) if a.dtype == np.float32 else oracle.tensor_matmul_i8(a, b, tr)
         assert np.array_equal(bits(res[name]), bits(want)), name
