@@ -557,6 +557,19 @@ def decode_bench(dev, rkhip, args):
     dev.profile_start()
     st.generate_run(8)
     prof = dev.profile_stop()
+    # The same loop drawing from softmax(logits / 0.8) with a seeded
+    # xorshift64* state on the device (sample.go:26-43): the step ends with
+    # the sampler's launches instead of the argmax's.
+    st.sampler(0.8, 1234)
+    st.generate_start(prompt)
+    st.generate_run(prompt_len)
+    t3 = time.perf_counter()
+    st.generate_run(steps - 9)
+    t4 = time.perf_counter()
+    dev.profile_start()
+    st.generate_run(8)
+    prof_s = dev.profile_stop()
+    toks_s = st.tokens(prompt_len, 8)
     weight_bytes = sum(m.bytes for m in mats) - embed.bytes
     kv_bytes = layers * 2 * kvdim * 4 * (prompt_len + steps / 2)  # average positions read per decode step
     per_token = weight_bytes + kv_bytes + 4 * vocab
@@ -574,6 +587,11 @@ def decode_bench(dev, rkhip, args):
                    "first_tokens": [int(t) for t in toks[:8]],
                    "kernels_us_per_token": {k: round(v[1] / 8 * 1e3, 2) for k, v in prof.items()},
                    "kernel_launches_per_token": {k: v[0] // 8 for k, v in prof.items()}},
+        "decode_sampled": {"temperature": 0.8, "seed": 1234,
+                           "tok_s": round((steps - 9) / (t4 - t3), 2),
+                           "ms_per_token": round((t4 - t3) / (steps - 9) * 1e3, 4),
+                           "sample_us_per_token": round(prof_s.get("sample", (0, 0.0))[1] / 8 * 1e3, 2),
+                           "first_tokens": [int(t) for t in toks_s]},
     }
     st.free()
     for m in mats:

@@ -365,6 +365,23 @@ int rk_stage_seqs_start(rk_stage *s, const int32_t *prompts, const int32_t *lens
 int rk_stage_seqs_run(rk_stage *s, int32_t steps, float *logits);
 /* Tokens of sequence `seq` at positions from..from+n-1. */
 int rk_stage_seqs_tokens(rk_stage *s, int32_t seq, int32_t from, int32_t n, int32_t *out);
+/* The next-token choice of sequence `seq` (0 on a stage of one sequence):
+ * temperature <= 0 the greedy argmax (the default); otherwise a draw from
+ * softmax(logits / temperature) with the xorshift64* generator seeded by
+ * `seed` (0: the reference's fixed seed), bit for bit as the reference's
+ * Sampler (internal/llm/sample.go:11-43; NewSampler per request at
+ * internal/llm/generate.go:446, Sample per generated token at :538). The
+ * state lives on the device, advances once per sampled token inside the
+ * recorded step, and persists until set again: call it before each
+ * generation for the reference's one sampler per request. */
+int rk_stage_sampler(rk_stage *s, int32_t seq, float temperature, uint64_t seed);
+/* Sampler.Sample (internal/llm/sample.go:26-43) of `rows` rows of host
+ * logits [rows][vocab] on the device: row z with temperature[z] and the
+ * generator state state[z] (as NewSampler leaves it: a zero seed already
+ * replaced), which advances when the row is sampled (temperature > 0 or
+ * NaN); tokens[z] the pick. Blocking. */
+int rk_sample_logits(rk_device *d, const float *logits, int64_t vocab, int32_t rows, const float *temperature,
+                     uint64_t *state, int32_t *tokens);
 
 /* ---- The device's float functions (internal/num), for host callers and
  * tests: out[i] = f(in[i]) computed by the same device code the kernels use.

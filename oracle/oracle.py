@@ -61,6 +61,8 @@ def _declare(L):
         "rko_matvec": (None, [P, P, P]), "rko_rope_table": (None, [P, I32, P, P]),
         "rko_rmsnorm": (None, [P, P, P, I64, F32]), "rko_softmax": (None, [P, I64]), "rko_silu": (F32, [F32]),
         "rko_inv_sqrt_head": (F32, [ctypes.c_int]),
+        "rko_sampler_seed": (ctypes.c_uint64, [ctypes.c_uint64]), "rko_sampler_next": (F32, [P]),
+        "rko_sample_probs": (None, [P, I64, F32, P]), "rko_sample": (I32, [P, I64, F32, P]),
         "rko_attention_head": (None, [P, P, P, I64, ctypes.c_int, ctypes.c_int, F32, P, P]),
         "rko_set_matvec_threads": (None, [ctypes.c_int]),
         "rko_forward": (None, [P, P, I32, P, P, P, P, I32, P, I32, P]),
@@ -109,6 +111,31 @@ def num_eval(fn, x):
     out = np.empty_like(x)
     lib().rko_num_eval(fn, ptr(x), ptr(out), x.size)
     return out
+
+
+class Sampler:
+    """internal/llm/sample.go Sampler: NewSampler(temperature, seed), then
+    sample(logits) per generated token (the state advances one draw a
+    sampled token)."""
+
+    def __init__(self, temperature, seed):
+        self.temperature = np.float32(temperature)
+        self.state = ctypes.c_uint64(lib().rko_sampler_seed(ctypes.c_uint64(seed)))
+
+    def next(self):
+        return np.float32(lib().rko_sampler_next(ctypes.byref(self.state)))
+
+    def sample(self, logits):
+        v = np.ascontiguousarray(logits, np.float32)
+        return int(lib().rko_sample(ptr(v), v.size, self.temperature, ctypes.byref(self.state)))
+
+
+def sample_probs(logits, temperature):
+    """p of Sample before the draw: softmax(logits / T) (sample.go:30-35)."""
+    v = np.ascontiguousarray(logits, np.float32)
+    p = np.empty_like(v)
+    lib().rko_sample_probs(ptr(v), v.size, np.float32(temperature), ptr(p))
+    return p
 
 
 def argmax(v):

@@ -820,6 +820,49 @@ int32_t rko_argmax(const float *v, int64_t n) {
     return (int32_t)best;
 }
 
+/* internal/llm/sample.go:11-16 NewSampler: a zero seed is replaced. */
+uint64_t rko_sampler_seed(uint64_t seed) { return seed == 0 ? 0x9e3779b97f4a7c15ULL : seed; }
+
+/* internal/llm/sample.go:18-24 next: xorshift64*, the top 24 bits of the
+ * scrambled state over 2^24 (exact: k < 2^24 converts exactly and the
+ * division is by a power of two). */
+float rko_sampler_next(uint64_t *state) {
+    uint64_t s = *state;
+    s ^= s >> 12;
+    s ^= s << 25;
+    s ^= s >> 27;
+    *state = s;
+    return (float)((s * 0x2545f4914f6cdd1dULL) >> 40) / (float)(1 << 24);
+}
+
+/* internal/llm/sample.go:30-35: p_i = logit_i / T (a float32 division),
+ * softmax (model.go:640-654). */
+void rko_sample_probs(const float *logits, int64_t n, float temperature, float *p) {
+    for (int64_t i = 0; i < n; i++) p[i] = logits[i] / temperature;
+    rko_softmax(p, n);
+}
+
+/* internal/llm/sample.go:26-43 Sample: temperature <= 0 the greedy argmax;
+ * else one draw r and the first i with r < cum, cum += p_i in order from
+ * +0 (float32), else the last index. */
+int32_t rko_sample(const float *logits, int64_t n, float temperature, uint64_t *state) {
+    if (temperature <= 0) return rko_argmax(logits, n);
+    float *p = malloc((size_t)n * 4);
+    rko_sample_probs(logits, n, temperature, p);
+    const float r = rko_sampler_next(state);
+    float cum = 0.0f;
+    int64_t pick = n - 1;
+    for (int64_t i = 0; i < n; i++) {
+        cum += p[i];
+        if (r < cum) {
+            pick = i;
+            break;
+        }
+    }
+    free(p);
+    return (int32_t)pick;
+}
+
 /* ------------------------------------------------------------------ */
 /* MoE feed-forward. The reference has no llama-family MoE; this build's
  * contract follows the dsv41 precedent (internal/llm/dsv41/ops.go:64-73

@@ -149,6 +149,10 @@ void rko_forward(const rko_config *c, const rko_layer *layers, int32_t nlayers, 
 void rko_embed(const rko_config *c, const rko_mat *table, int32_t token, float *x);
 void rko_logits(const rko_config *c, const float *rms_final, const rko_mat *wcls, const float *x, float *logits);
 int32_t rko_argmax(const float *v, int64_t n);
+uint64_t rko_sampler_seed(uint64_t seed);
+float rko_sampler_next(uint64_t *state);
+void rko_sample_probs(const float *logits, int64_t n, float temperature, float *p);
+int32_t rko_sample(const float *logits, int64_t n, float temperature, uint64_t *state);
 
 /* ---- MoE layer feed-forward (this build's contract; see rk_oracle.c) ---- */
 void rko_topk(const float *v, int32_t n, int32_t k, int32_t *idx);

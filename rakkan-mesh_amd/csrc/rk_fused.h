@@ -172,13 +172,35 @@ void launch_embed_rows(const uint8_t *w, const float *scales, bool q4, const int
 // prompt), and pos[z] advances.
 void launch_seqs_advance(const float *logits, int64_t vocab, int seqs, int32_t *pos, const int32_t *prompt,
                          int32_t *tokens, int64_t tok_stride, int32_t tokens_len, hipStream_t s);
-// RMSNorm(x) with norm_w quantized into qx/xs/xsum (one workgroup; n <=
-// kMaxNormCols).
+// The seeded sampler's step (internal/llm/sample.go:26-43) for `seqs`
+// logits rows [seqs][vocab]: sequence z picks its token at pos[z]+1 when
+// that position is past its prompt (the argmax when temps[z] <= 0, else a
+// draw from softmax(logits/T) with the xorshift64* state states[z], which
+// advances once a draw), and pos[z] advances. terms: [seqs][stride] floats
+// (sample_terms_stride), part: [seqs][sample_parts()] floats, both scratch.
+struct SampleArgs {
+    const float *logits;
+    int64_t vocab;
+    int seqs;
+    int32_t *pos;
+    const int32_t *prompt;
+    int32_t *tokens;
+    int64_t tok_stride;
+    int32_t tokens_len;
+    const float *temps;
+    uint64_t *states;
+    float *terms, *part;
+    unsigned long long *amax;  // one sequence: the classifier's argmax keys, cleared (else null)
+};
+int64_t sample_terms_stride(int64_t vocab);
+int sample_parts();
+void launch_sample(const SampleArgs &a, hipStream_t s);
 // The greedy argmax's end (internal/llm/sample.go:45-53): folds the
 // classifier's argmax keys into the next token at position+1 (when the
 // position's logits were computed), clears them, and advances the position.
 void launch_advance(int32_t *ctl, unsigned long long *amax, int32_t *tokens, int32_t tokens_len, hipStream_t s);
-// `tokens` rows of [tokens][n] at once (one workgroup each).
+// RMSNorm(x) with norm_w quantized into qx/xs/xsum: `tokens` rows of
+// [tokens][n] at once (one workgroup each; n <= kMaxNormCols).
 void launch_norm_quant(const float *x, int n, const float *norm_w, float recip_n, float eps, int8_t *qx, float *xs,
                        int32_t *xsum, hipStream_t s, int tokens = 1);
 

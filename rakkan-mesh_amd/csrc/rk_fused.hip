@@ -1330,73 +1330,6 @@ void launch_embed_rows(const uint8_t *w, const float *scales, bool q4, const int
               seq_pos);
 }
 
-// Independent sequences' greedy step (internal/llm/sample.go:45-53 per
-// sequence): workgroup z takes the argmax of logits row z (the first index
-// holding the largest value; NaNs are never candidates, and a NaN first
-// logit keeps index 0, as the reference's `>` scan does), writes it as the
-// token at pos[z]+1 when that position is past the prompt, and advances
-// pos[z].
-__global__ __launch_bounds__(1024) void seqs_advance_kernel(const float *logits, int64_t vocab, int32_t *pos,
-                                                            const int32_t *prompt, int32_t *tokens,
-                                                            int64_t tok_stride, int32_t tokens_len) {
-    __shared__ float s_v[16];
-    __shared__ int s_i[16];
-    const int z = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const float *row = logits + (int64_t)z * vocab;
-    float bv = 0.0f;
-    int bi = -1;
-    // eight 16-byte loads in flight a thread (a position past the row
-    // re-reads the last group: merging an element twice changes nothing)
-    const int64_t n4 = (reinterpret_cast<uintptr_t>(row) & 15) == 0 ? vocab >> 2 : 0;
-    const float4 *r4 = reinterpret_cast<const float4 *>(row);
-    for (int64_t b = threadIdx.x; b < n4; b += 1024 * 8) {
-        float4 v[8];
-        int64_t g[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            g[u] = min(b + 1024 * u, n4 - 1);
-            v[u] = r4[g[u]];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                if (e[c] == e[c]) argmax_merge(bv, bi, e[c], (int)(4 * g[u] + c));
-        }
-    }
-    for (int64_t i = 4 * n4 + threadIdx.x; i < vocab; i += 1024) {
-        const float v = row[i];
-        if (v == v) argmax_merge(bv, bi, v, (int)i);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_down(bv, off);
-        const int oi = __shfl_down(bi, off);
-        argmax_merge(bv, bi, ov, oi);
-    }
-    if (lane == 0) {
-        s_v[wave] = bv;
-        s_i[wave] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float v = 0.0f;
-        int i = -1;
-        for (int w = 0; w < 16; w++) argmax_merge(v, i, s_v[w], s_i[w]);
-        if (row[0] != row[0] || i < 0) i = 0;  // a NaN first logit, or every logit NaN
-        const int p = pos[z];
-        if (p + 1 >= prompt[z] && p + 1 < tokens_len) tokens[(int64_t)z * tok_stride + p + 1] = i;
-        pos[z] = p + 1;
-    }
-}
-
-void launch_seqs_advance(const float *logits, int64_t vocab, int seqs, int32_t *pos, const int32_t *prompt,
-                         int32_t *tokens, int64_t tok_stride, int32_t tokens_len, hipStream_t s) {
-    RK_LAUNCH(seqs_advance_kernel, dim3(seqs), dim3(1024), 0, s, logits, vocab, pos, prompt, tokens, tok_stride,
-              tokens_len);
-}
-
 __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(const float *x, int n, const float *norm_w,
                                                                   float recip_n, float eps, int8_t *qx, float *xs,
                                                                   int32_t *xsum) {

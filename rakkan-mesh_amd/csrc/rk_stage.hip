@@ -38,6 +38,15 @@ struct rk_stage {
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *att_out = nullptr;
     float *h = nullptr, *cos_t = nullptr, *sin_t = nullptr, *logits = nullptr, *rms_final = nullptr;
     int64_t logits_n = 0;  // floats of logits (and of its pinned staging)
+    int64_t logits_dev = 0;  // floats of the logits allocation (logits, then the sampler's terms)
+    // The next-token choice (rk_stage_sampler): temperatures and xorshift64*
+    // states per sequence on the device, the sampler's scratch (terms after
+    // the logits), and whether any sequence samples (the recorded step then
+    // ends with the sampler instead of the greedy argmax).
+    float *smp_temp = nullptr, *smp_part = nullptr, *smp_terms = nullptr;
+    uint64_t *smp_state = nullptr;
+    std::vector<float> smp_t;
+    bool sampling = false;
     int32_t *ctl = nullptr, *tokens = nullptr;
     unsigned long long *amax = nullptr;  // the classifier's argmax keys
     int8_t *qx = nullptr;  // the fallback quantize's output
@@ -286,6 +295,26 @@ static int enqueue_layers(rk_stage *s, hipStream_t st, bool qb_ready) {
 // Layers on the activation the host wrote to x.
 static int enqueue_forward(rk_stage *s, hipStream_t st) { return enqueue_layers(s, st, false); }
 
+// The sampler's launch for `seqs` logits rows (SampleArgs).
+static SampleArgs sample_args(rk_stage *s, int seqs, int32_t *pos, const int32_t *prompt, int32_t *tokens,
+                              int64_t tok_stride, unsigned long long *amax) {
+    SampleArgs a{};
+    a.logits = s->logits;
+    a.vocab = s->wcls->rows;
+    a.seqs = seqs;
+    a.pos = pos;
+    a.prompt = prompt;
+    a.tokens = tokens;
+    a.tok_stride = tok_stride;
+    a.tokens_len = s->c.ctx + 1;
+    a.temps = s->smp_temp;
+    a.states = s->smp_state;
+    a.terms = s->smp_terms;
+    a.part = s->smp_part;
+    a.amax = amax;
+    return a;
+}
+
 // One generation step: embed the position's token, the layers, the head.
 static int enqueue_token(rk_stage *s, hipStream_t st) {
     rk_device *d = s->d;
@@ -302,8 +331,13 @@ static int enqueue_token(rk_stage *s, hipStream_t st) {
     a.gate = 1;
     float *lo[1] = {s->logits};
     if ((rc = stage_product(s, st, "logits", nullptr, s->x, s->rms_final, &s->wcls, 1, lo, kEpLogits, a))) return rc;
-    ProfScope p(d, st, "advance");
-    launch_advance(s->ctl, s->amax, s->tokens, s->c.ctx + 1, st);
+    if (s->sampling) {
+        ProfScope p(d, st, "sample");
+        launch_sample(sample_args(s, 1, s->ctl + kCtlPos, s->ctl + kCtlPrompt, s->tokens, 0, s->amax), st);
+    } else {
+        ProfScope p(d, st, "advance");
+        launch_advance(s->ctl, s->amax, s->tokens, s->c.ctx + 1, st);
+    }
     return RK_OK;
 }
 
@@ -589,7 +623,10 @@ static int enqueue_seqs_step(rk_stage *s, hipStream_t st) {
     a.qx = s->bqb.qx;
     a.xs = s->bqb.xs;
     if ((rc = batch_product(s, st, "logits", &s->wcls, 1, kEpStore, a))) return rc;
-    {
+    if (s->sampling) {
+        ProfScope p(d, st, "sample");
+        launch_sample(sample_args(s, S, s->seq_pos, s->seq_prompt, s->seq_tokens, ctx + 1, nullptr), st);
+    } else {
         ProfScope p(d, st, "advance");
         launch_seqs_advance(s->logits, s->wcls->rows, S, s->seq_pos, s->seq_prompt, s->seq_tokens, ctx + 1,
                             (int32_t)(ctx + 1), st);
@@ -616,6 +653,22 @@ __global__ void set_ctl_kernel(int32_t *ctl, unsigned long long *amax, int32_t p
 static int one_sequence(rk_stage *s, const char *what) {
     if (s->seqs == 1) return RK_OK;
     return fail(s->d, RK_ERR_ARGS, "%s: the stage decodes %d sequences (rk_stage_seqs_*)", what, s->seqs);
+}
+
+// Drops the recorded generation steps (they are recorded again on next use).
+static void drop_steps(rk_stage *s) {
+    if (s->x_token) {
+        (void)hipGraphExecDestroy(s->x_token);
+        (void)hipGraphDestroy(s->g_token);
+        s->x_token = nullptr;
+        s->g_token = nullptr;
+    }
+    if (s->x_seqs) {
+        (void)hipGraphExecDestroy(s->x_seqs);
+        (void)hipGraphDestroy(s->g_seqs);
+        s->x_seqs = nullptr;
+        s->g_seqs = nullptr;
+    }
 }
 
 static bool valid_mat(const rk_matrix *m, rk_device *d, int64_t rows, int64_t cols) {
@@ -676,6 +729,7 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
     s->half = hs / 2;
     s->seqs = seqs;
     s->layers.assign(layers, layers + n_layers);
+    s->smp_t.assign(seqs, 0.0f);
     // Layout: sizes in bytes, each 256-byte aligned.
     const int64_t ctx = c->ctx;
     const int64_t widest = std::max<int64_t>(std::max<int64_t>(c->dim, qdim), c->hidden);
@@ -707,6 +761,9 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
     take((void **)&s->seq_pos, 4 * seqs);
     take((void **)&s->seq_prompt, 4 * seqs);
     take((void **)&s->seq_tokens, 4 * seqs * (ctx + 1));
+    take((void **)&s->smp_temp, 4 * seqs);
+    take((void **)&s->smp_state, 8 * seqs);
+    take((void **)&s->smp_part, 4 * seqs * sample_parts());
     // the MoE layers' shared scratch, for the largest batch the stage runs
     if (any_moe) {
         s->moe_cap = batch_cap(*c, seqs);
@@ -849,6 +906,7 @@ int rk_stage_free(rk_stage *s) {
     if (s->g_seqs) (void)hipGraphDestroy(s->g_seqs);
     (void)hipFree(s->mem);
     (void)hipFree(s->bmem);
+    (void)hipFree(s->logits);
     if (s->h_x) (void)hipHostFree(s->h_x);
     if (s->h_ctl) (void)hipHostFree(s->h_ctl);
     if (s->h_seq) (void)hipHostFree(s->h_seq);
@@ -868,32 +926,25 @@ int rk_stage_set_head(rk_stage *s, rk_matrix *embed, rk_matrix *wcls, const floa
         return fail(d, RK_ERR_ARGS, "rk_stage_set_head: embedding or classifier of the wrong shape or format");
     Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
-    if (s->x_token) {
-        (void)hipGraphExecDestroy(s->x_token);
-        (void)hipGraphDestroy(s->g_token);
-        s->x_token = nullptr;
-        s->g_token = nullptr;
-    }
-    if (s->x_seqs) {
-        (void)hipGraphExecDestroy(s->x_seqs);
-        (void)hipGraphDestroy(s->g_seqs);
-        s->x_seqs = nullptr;
-        s->g_seqs = nullptr;
-    }
-    // logits of every sequence, [seqs][vocab]
+    drop_steps(s);
+    // logits of every sequence, [seqs][vocab], then the sampler's terms
+    // [seqs][stride] (16-byte aligned)
     const int64_t nl = wcls->rows * s->seqs;
-    if (s->logits && nl > s->logits_n) {
+    const int64_t nl_pad = (nl + 63) & ~(int64_t)63;
+    const int64_t ndev = nl_pad + s->seqs * sample_terms_stride(wcls->rows);
+    if (s->logits && (nl > s->logits_n || ndev > s->logits_dev)) {
         HIP_TRY(d, hipStreamSynchronize(d->stream), "logits");
         (void)hipFree(s->logits);
         (void)hipHostFree(s->h_logits);
         s->logits = nullptr;
         s->h_logits = nullptr;
-        s->bytes -= 4 * s->logits_n;
-        add_used(d, -4 * s->logits_n);
+        s->bytes -= 4 * s->logits_dev;
+        add_used(d, -4 * s->logits_dev);
         s->logits_n = 0;
+        s->logits_dev = 0;
     }
     if (!s->logits) {
-        int rc = dev_alloc(d, (void **)&s->logits, (size_t)4 * nl, "logits");
+        int rc = dev_alloc(d, (void **)&s->logits, (size_t)4 * ndev, "logits");
         if (rc) return rc;
         hipError_t e = hipHostMalloc((void **)&s->h_logits, (size_t)4 * nl, hipHostMallocDefault);
         if (e != hipSuccess) {
@@ -902,9 +953,11 @@ int rk_stage_set_head(rk_stage *s, rk_matrix *embed, rk_matrix *wcls, const floa
             return hip_fail(d, e, "logits staging");
         }
         s->logits_n = nl;
-        s->bytes += 4 * nl;
-        add_used(d, 4 * nl);
+        s->logits_dev = ndev;
+        s->bytes += 4 * ndev;
+        add_used(d, 4 * ndev);
     }
+    s->smp_terms = s->logits + nl_pad;
     HIP_TRY(d, hipMemcpyAsync(s->rms_final, rms_final, (size_t)4 * s->c.dim, hipMemcpyHostToDevice, d->stream),
             "head upload");
     HIP_TRY(d, hipStreamSynchronize(d->stream), "head upload");
@@ -1098,6 +1151,31 @@ int rk_stage_seqs_run(rk_stage *s, int32_t steps, float *logits) {
     }
     HIP_TRY(d, hipStreamSynchronize(d->stream), "seqs run");
     for (int32_t &p : s->seq_at) p += steps;
+    return RK_OK;
+}
+
+int rk_stage_sampler(rk_stage *s, int32_t seq, float temperature, uint64_t seed) {
+    if (!s) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    if (seq < 0 || seq >= s->seqs)
+        return fail(d, RK_ERR_ARGS, "rk_stage_sampler: sequence %d of %d", seq, s->seqs);
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    hipStream_t st = d->stream;
+    HIP_TRY(d, hipStreamSynchronize(st), "sampler");
+    // internal/llm/sample.go:11-16: a zero seed is replaced
+    const uint64_t state = seed == 0 ? 0x9e3779b97f4a7c15ull : seed;
+    HIP_TRY(d, hipMemcpyAsync(s->smp_temp + seq, &temperature, 4, hipMemcpyHostToDevice, st), "sampler");
+    HIP_TRY(d, hipMemcpyAsync(s->smp_state + seq, &state, 8, hipMemcpyHostToDevice, st), "sampler");
+    HIP_TRY(d, hipStreamSynchronize(st), "sampler");
+    s->smp_t[seq] = temperature;
+    // NaN samples, as in the reference (only temperature <= 0 is greedy)
+    bool sampling = false;
+    for (float t : s->smp_t) sampling = sampling || !(t <= 0.0f);
+    if (sampling != s->sampling) {
+        drop_steps(s);
+        s->sampling = sampling;
+    }
     return RK_OK;
 }
 

@@ -97,6 +97,8 @@ SIGNATURES = {
     "rk_stage_seqs_start": (ctypes.c_int, [P, P, P]),
     "rk_stage_seqs_run": (ctypes.c_int, [P, I32, P]),
     "rk_stage_seqs_tokens": (ctypes.c_int, [P, I32, I32, I32, P]),
+    "rk_stage_sampler": (ctypes.c_int, [P, I32, ctypes.c_float, ctypes.c_uint64]),
+    "rk_sample_logits": (ctypes.c_int, [P, P, I64, I32, P, P, P]),
     "rk_num_eval": (ctypes.c_int, [P, I32, P, P, I64]),
     "rk_moe_new": (ctypes.c_int, [P, P, I32, P, P, P, I32, P]),
     "rk_moe_ffn": (ctypes.c_int, [P, P, I32, P, P, P]),
@@ -507,6 +509,20 @@ class Device:
         self._check(lib().rk_num_eval(self.h, fn, _ptr(x), _ptr(out), x.size))
         return out
 
+    def sample_logits(self, logits, temperature, state):
+        """rk_sample_logits: Sampler.Sample of each row of logits [rows][vocab]
+        with temperature[z] and generator state[z] (uint64, updated in place);
+        the picked tokens."""
+        lg = np.ascontiguousarray(logits, np.float32)
+        lg = lg.reshape(1, -1) if lg.ndim == 1 else lg
+        rows, vocab = lg.shape
+        t = np.ascontiguousarray(np.broadcast_to(np.asarray(temperature, np.float32), (rows,)), np.float32)
+        if state.dtype != np.uint64 or state.shape != (rows,) or not state.flags.c_contiguous:
+            raise ValueError("state: a contiguous uint64 array of one state a row")
+        out = np.empty(rows, np.int32)
+        self._check(lib().rk_sample_logits(self.h, _ptr(lg), vocab, rows, _ptr(t), _ptr(state), _ptr(out)))
+        return out
+
     def graph_begin(self):
         self._check(lib().rk_graph_begin(self.h))
 
@@ -664,6 +680,11 @@ class Stage:
         out = np.empty(n, np.int32)
         self.dev._check(lib().rk_stage_seqs_tokens(self.h, seq, start, n, _ptr(out)))
         return out
+
+    def sampler(self, temperature, seed, seq=0):
+        """rk_stage_sampler: NewSampler(temperature, seed) for sequence seq
+        (internal/llm/sample.go:11-16); temperature <= 0 is the greedy argmax."""
+        self.dev._check(lib().rk_stage_sampler(self.h, seq, float(np.float32(temperature)), int(seed) & (2**64 - 1)))
 
     @property
     def bytes(self):
