@@ -19,10 +19,10 @@
 // a power-of-two scaling), except when t/u is a tie (x.5: the even neighbour
 // depends on m) or m' reaches 2^24 (the next binade's coarser grid). Between
 // such events the sum is integer addition, which is associative: a
-// workgroup scan over 16384 terms advances s at once. At an event the term
-// is added as a float, the grid is re-read from the new s, and the chunk
-// resumes after it. The first kSmpPre terms, where s is still small and
-// events are dense, are added one by one.
+// workgroup scan over a chunk of terms (up to 8192) advances s at once. At an
+// event the term is added as a float, the grid is re-read from the new s,
+// and the chunk resumes after it. The first kSmpPre terms, where s is still
+// small and events are dense, are added one by one.
 #include "rk_dev.h"
 #include "rk_fused.h"
 #include "rk_runtime.h"
@@ -31,12 +31,10 @@ namespace rk {
 
 namespace {
 
-constexpr int kSmpThreads = 1024;
+constexpr int kSmpThreads = 256;
 constexpr int kSmpWaves = kSmpThreads / 64;
-constexpr int kSmpPer = 16;                          // terms a thread per chunk
-constexpr int kSmpChunk = kSmpThreads * kSmpPer;     // terms a scan step
 constexpr int kSmpPre = 256;                         // terms added one by one first
-constexpr int kSmpParts = 64;                        // workgroups a row (max and terms)
+constexpr int kSmpParts = 256;                       // workgroups a row (max and terms)
 constexpr int kSmpPartThreads = 256;
 constexpr uint32_t kGridTop = 1u << 24;              // m reaches the next binade
 constexpr uint32_t kGridCap = 1u << 25;              // saturation of the scans (past kGridTop)
@@ -62,10 +60,23 @@ __device__ __forceinline__ float grid_value(uint32_t m, int eu) {
     return m < 0x800000u ? u2f(m) : u2f(((uint32_t)(eu + 150) << 23) + (m - 0x800000u));
 }
 
+// Inclusive prefix sum over the wave's 64 lanes (sums below 2^32): within
+// each row of 16 by row shifts, then across rows by the row broadcasts.
+__device__ __forceinline__ uint32_t wave_scan_add(uint32_t v) {
+    uint32_t t = v;
+    t += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);  // row_shr:1
+    t += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);  // row_shr:2
+    t += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x113, 0xf, 0xf, true);  // row_shr:3
+    t += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)t, 0x114, 0xf, 0xe, false); // row_shr:4, lanes 4-15
+    t += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)t, 0x118, 0xf, 0xc, false); // row_shr:8, lanes 8-15
+    t += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)t, 0x142, 0xa, 0xf, false); // row_bcast:15, rows 1, 3
+    t += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)t, 0x143, 0xc, 0xf, false); // row_bcast:31, rows 2, 3
+    return t;
+}
+
 struct SmpLds {
     uint32_t wt[kSmpWaves];  // the waves' sums
-    int me[kSmpWaves];       // the waves' first event
-    int mh[kSmpWaves];       // the waves' first hit (r < running sum)
+    int emin[2], hmin[2];    // a step's first event and first hit (r < running sum), by step parity
     float cand[kSmpThreads]; // each thread's running sum after its first event
     alignas(16) float pre[kSmpPre];
     float bv[kSmpWaves];
@@ -99,65 +110,118 @@ __device__ void lds_chain_cum(float *p, int n) {
     }
 }
 
-// The running sum over terms e[i] (times scale when kSearch) for i in
-// [kSmpPre, n), from s: the scan steps of the file comment. kSearch: stops
-// at the first i where r < the sum after term i, in `hit` (else -1). Every
-// thread of the workgroup calls it; every value that steers it is uniform.
-template <bool kSearch>
-__device__ float grid_chain(const float *e, int n, int e4, float scale, float s, float r, int &hit, SmpLds &sm) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    hit = -1;
-    for (int c0 = kSmpPre; c0 < n; c0 += kSmpChunk) {
-        float t[kSmpPer];
-        const int b4 = (c0 >> 2) + tid * (kSmpPer / 4);
+// One thread's terms on grid g for the positions [lo, hi) of its PER:
+// running increments pre[] (from 0), and the events (a tie, or a term at or
+// past the next binade, or NaN) as bits. Positions outside add nothing.
+template <int PER, bool kChecked>
+__device__ __forceinline__ uint32_t grid_terms(const float (&t)[PER], const Grid &g, int lo, int hi,
+                                               uint32_t (&pre)[PER], uint32_t &evm) {
+    uint32_t acc = 0;
+    evm = 0;
 #pragma unroll
-        for (int k = 0; k < kSmpPer / 4; k++) {
-            const float4 v = reinterpret_cast<const float4 *>(e)[min(b4 + k, e4 - 1)];
-            t[4 * k] = v.x;
-            t[4 * k + 1] = v.y;
-            t[4 * k + 2] = v.z;
-            t[4 * k + 3] = v.w;
+    for (int j = 0; j < PER; j++) {
+        const float q = __builtin_amdgcn_ldexpf(t[j], -g.eu);
+        const bool big = !(q < 16777216.0f);
+        const float qs = big ? 0.0f : q;
+        const float qr = __builtin_rintf(qs);
+        const bool tie = __builtin_fabsf(qs - qr) == 0.5f;
+        uint32_t inc = big ? kGridCap : (uint32_t)qr;
+        bool ev = big || tie;
+        if (kChecked) {
+            const bool valid = j >= lo && j < hi;
+            inc = valid ? inc : 0u;
+            ev = ev && valid;
+        }
+        acc += inc;  // at most PER·2^25: no wrap
+        pre[j] = acc;
+        evm |= ev ? (1u << j) : 0u;
+    }
+    return acc;
+}
+
+// A chunk's terms for the thread: positions c0 + tid·PER + [0, PER), as
+// float4 (c0 and the row 16-byte aligned; the row holds n rounded up to 4).
+template <int PER>
+__device__ __forceinline__ void load_chunk(const float *e, int c0, int n, float4 (&v)[PER / 4]) {
+    static_assert(PER % 4 == 0, "float4 loads");
+    const int last4 = ((n + 3) >> 2) - 1;
+    const int b4 = (c0 + (int)threadIdx.x * PER) >> 2;
+#pragma unroll
+    for (int k = 0; k < PER / 4; k++) v[k] = reinterpret_cast<const float4 *>(e)[min(b4 + k, last4)];
+}
+
+// The running sum over terms e[i] (times scale when kSearch) for i in
+// [c_begin, min(c_end, n)), from s, in chunks of kSmpThreads·PER terms: the
+// scan steps of the file comment. kSearch: stops at the first i where r <
+// the sum after term i, in `hit` (else -1). Every thread of the workgroup
+// calls it; every value that steers it is uniform. ph: the step parity,
+// which alternates over every step of the kernel (a step's minima are reset
+// before its first barrier, the previous step's read after its second).
+template <bool kSearch, int PER>
+__device__ float grid_chain(const float *e, int c_begin, int c_end, int n, float scale, float s, float r, int &hit,
+                            int &ph, const float4 (&first)[PER / 4], SmpLds &sm) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int kChunk = kSmpThreads * PER;
+    const int end = min(c_end, n);
+    hit = -1;
+    // the first chunk's terms come loaded; each chunk's steps run while the
+    // next chunk's loads are in flight
+    float4 cur[PER / 4];
+#pragma unroll
+    for (int k = 0; k < PER / 4; k++) cur[k] = first[k];
+    for (int c0 = c_begin; c0 < end; c0 += kChunk) {
+        const int base = tid * PER;  // the thread's first position in the chunk
+        const bool more = c0 + kChunk < end;
+        float4 nxt[PER / 4];
+        if (more) load_chunk<PER>(e, c0 + kChunk, n, nxt);
+        float t[PER];
+#pragma unroll
+        for (int k = 0; k < PER / 4; k++) {
+            t[4 * k] = cur[k].x;
+            t[4 * k + 1] = cur[k].y;
+            t[4 * k + 2] = cur[k].z;
+            t[4 * k + 3] = cur[k].w;
         }
         if (kSearch) {
 #pragma unroll
-            for (int j = 0; j < kSmpPer; j++) t[j] = t[j] * scale;
+            for (int j = 0; j < PER; j++) t[j] = t[j] * scale;
         }
-        const int base = tid * kSmpPer;        // the thread's first position in the chunk
-        const int valid_end = min(kSmpChunk, n - c0);
+        const int valid_end = min(kChunk, end - c0);
         int from = 0;
         while (true) {
             // a NaN sum stays NaN, and r < NaN never holds
             if (s != s) return s;
             const Grid g = grid_of(s);
-            const float rq = kSearch ? __builtin_amdgcn_ldexpf(r, -g.eu) : 0.0f;
-            // the thread's terms on the grid: increments, and events (ties,
-            // terms past the binade, NaN)
-            uint32_t pre[kSmpPer];
-            uint32_t evm = 0, acc = 0;
+            // the thread's increments and events
+            const int lo = from - base, hi = valid_end - base;
+            uint32_t pre[PER], evm, acc;
+            // one path a wave: every lane's positions valid, none, or a mix
+            // (the checked path, right for any thread)
+            const bool full = lo <= 0 && hi >= PER, none = lo >= PER || hi <= 0;
+            const unsigned long long bfull = __ballot(full), bnone = __ballot(none);
+            const unsigned long long all = __ballot(true);
+            if (bfull == all) {
+                acc = grid_terms<PER, false>(t, g, lo, hi, pre, evm);
+            } else if (bnone != all) {
+                acc = grid_terms<PER, true>(t, g, lo, hi, pre, evm);
+            } else {
 #pragma unroll
-            for (int j = 0; j < kSmpPer; j++) {
-                const int pos = base + j;
-                const bool valid = pos >= from && pos < valid_end;
-                const float q = __builtin_amdgcn_ldexpf(t[j], -g.eu);
-                const bool big = !(q < 16777216.0f);
-                const float qs = big ? 0.0f : q;
-                const float qr = __builtin_rintf(qs);
-                const bool tie = qs - __builtin_floorf(qs) == 0.5f;
-                const uint32_t inc = big ? kGridCap : (uint32_t)qr;
-                acc = valid ? sat_add(acc, inc) : acc;
-                pre[j] = acc;
-                evm |= (valid && (big || tie)) ? (1u << j) : 0u;
+                for (int j = 0; j < PER; j++) pre[j] = 0;
+                acc = 0;
+                evm = 0;
             }
-            // exclusive prefix of the threads' sums in the workgroup
-            uint32_t v = acc;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t u = __shfl_up(v, o);
-                v = lane >= o ? sat_add(v, u) : v;
+            // exclusive prefix of the threads' sums in the workgroup. A
+            // thread's sum is taken at most 2^24 (a sum that large crosses
+            // at or before the thread's end, so the positions after it need
+            // no exact offset), and a wave's then stays below 2^31.
+            const uint32_t tv = min(acc, kGridTop);
+            const uint32_t incl = wave_scan_add(tv);
+            const uint32_t ex = incl - tv;
+            if (lane == 63) sm.wt[wave] = incl;
+            if (tid == 0) {
+                sm.emin[ph] = kNone;
+                sm.hmin[ph] = kNone;
             }
-            uint32_t ex = __shfl_up(v, 1);
-            ex = lane ? ex : 0u;
-            if (lane == 63) sm.wt[wave] = v;
             __syncthreads();
             uint32_t woff = 0, total = 0;
 #pragma unroll
@@ -167,41 +231,65 @@ __device__ float grid_chain(const float *e, int n, int e4, float scale, float s,
                 total = sat_add(total, x);
             }
             const uint32_t off = sat_add(woff, ex);
-            // the thread's first event and first hit; the sum after its
-            // first event (exact when it is the workgroup's first)
+            // pre[] grows with j: the first position at or past a threshold
+            // is the count of those below it. The sum after position j is
+            // (m + off + pre[j])·2^eu; it leaves the grid at m + off +
+            // pre[j] >= 2^24, and passes r at m + off + pre[j] > r·2^-eu.
+            const uint32_t room = kGridTop - g.m;
+            const uint32_t thr = off >= room ? 0u : room - off;
+            uint32_t hthr = 0xFFFFFFFFu;
+            if (kSearch) {
+                // r >= s, so floor(r·2^-eu) >= m
+                const float rq = __builtin_amdgcn_ldexpf(r, -g.eu);
+                if (rq < 33554432.0f) {
+                    const uint32_t need = (uint32_t)__builtin_floorf(rq) + 1u - g.m;
+                    hthr = off >= need ? 0u : need - off;
+                }
+            }
+            // (pre[PER-1] = acc: a thread whose end stays below a threshold
+            // needs no count)
+            int nc = thr == 0 ? 0 : PER, nh = hthr == 0 ? 0 : PER;
+            if (thr != 0 && acc >= thr) {
+                nc = 0;
+#pragma unroll
+                for (int j = 0; j < PER; j++) nc += pre[j] < thr ? 1 : 0;
+            }
+            if (kSearch && hthr != 0 && acc >= hthr) {
+                nh = 0;
+#pragma unroll
+                for (int j = 0; j < PER; j++) nh += pre[j] < hthr ? 1 : 0;
+            }
+            const int jev = min(nc, evm ? (int)__builtin_ctz(evm) : PER);
+            // the thread's first event, and the sum after it (exact when it
+            // is the workgroup's first)
             int je = kNone, jh = kNone;
             float cand = 0.0f;
-            uint32_t prev = off;
+            if (jev < PER) {
+                float tj = t[0];
+                uint32_t pb = 0;
+                if (jev > 0) {
 #pragma unroll
-            for (int j = 0; j < kSmpPer; j++) {
-                const int pos = base + j;
-                const bool valid = pos >= from && pos < valid_end;
-                const uint32_t pj = sat_add(off, pre[j]);
-                const bool ev = valid && (((evm >> j) & 1u) || g.m + pj >= kGridTop);
-                if (ev && je == kNone) {
-                    je = pos;
-                    cand = grid_value(g.m + prev, g.eu) + t[j];
+                    for (int j = 1; j < PER; j++) {
+                        tj = jev == j ? t[j] : tj;
+                        pb = jev == j ? pre[j - 1] : pb;
+                    }
                 }
-                if (kSearch && valid && !ev && je == kNone && jh == kNone && (float)(g.m + pj) > rq) jh = pos;
-                prev = pj;
+                je = base + jev;
+                cand = grid_value(g.m + off + pb, g.eu) + tj;
             }
-            // positions grow with the lane: a wave's first is its lowest lane's
+            if (kSearch && nh < jev) jh = base + nh;
+            // Every position after a crossing or a hit qualifies too: only
+            // the wave's first (its lowest such lane: positions grow with
+            // the lane) takes part in the minimum.
             const unsigned long long be = __ballot(je != kNone);
             const unsigned long long bh = __ballot(jh != kNone);
-            if (lane == 0) {
-                sm.me[wave] = be ? __builtin_amdgcn_readlane(je, __builtin_ctzll(be)) : kNone;
-                sm.mh[wave] = bh ? __builtin_amdgcn_readlane(jh, __builtin_ctzll(bh)) : kNone;
-            }
+            if (be && lane == (int)__builtin_ctzll(be)) atomicMin(&sm.emin[ph], je);
+            if (bh && lane == (int)__builtin_ctzll(bh)) atomicMin(&sm.hmin[ph], jh);
             sm.cand[tid] = cand;
             __syncthreads();
-            int es = kNone, hs = kNone;
-#pragma unroll
-            for (int w = 0; w < kSmpWaves; w++) {
-                es = min(es, sm.me[w]);
-                hs = min(hs, sm.mh[w]);
-            }
-            es = __builtin_amdgcn_readfirstlane(es);
-            hs = __builtin_amdgcn_readfirstlane(hs);
+            const int es = __builtin_amdgcn_readfirstlane(sm.emin[ph]);
+            const int hs = __builtin_amdgcn_readfirstlane(sm.hmin[ph]);
+            ph ^= 1;
             if (kSearch && hs < es) {
                 hit = c0 + hs;
                 return s;
@@ -210,13 +298,17 @@ __device__ float grid_chain(const float *e, int n, int e4, float scale, float s,
                 s = grid_value(g.m + total, g.eu);
                 break;
             }
-            s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sm.cand[es / kSmpPer])));
+            s = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(sm.cand[es / PER])));
             if (kSearch && r < s) {
                 hit = c0 + es;
                 return s;
             }
             from = es + 1;
             if (from >= valid_end) break;
+        }
+        if (more) {
+#pragma unroll
+            for (int k = 0; k < PER / 4; k++) cur[k] = nxt[k];
         }
     }
     return s;
@@ -226,9 +318,12 @@ __device__ float grid_chain(const float *e, int n, int e4, float scale, float s,
 // kSmpPre one by one, then grid_chain. kSearch: the first i where r < the
 // sum after term i, in `hit` (else -1).
 template <bool kSearch>
-__device__ float chain(const float *e, int n, int e4, float scale, float r, int &hit, SmpLds &sm) {
+__device__ float chain(const float *e, int n, float scale, float r, int &hit, int &ph, SmpLds &sm) {
     const int tid = threadIdx.x;
     const int np = min(n, kSmpPre);
+    // the scan's first chunk, loading while the first terms are added
+    float4 c4[1];
+    if (n > kSmpPre) load_chunk<4>(e, kSmpPre, n, c4);
     // pads are +0: the sums past n repeat the last
     if (tid < kSmpPre) sm.pre[tid] = tid < np ? (kSearch ? e[tid] * scale : e[tid]) : 0.0f;
     if (tid == 0) sm.first = kNone;
@@ -238,7 +333,9 @@ __device__ float chain(const float *e, int n, int e4, float scale, float r, int 
     const float s = sm.pre[np - 1];
     hit = -1;
     if (kSearch) {
-        if (tid < np && r < sm.pre[tid]) atomicMin(&sm.first, tid);
+        // the sums grow with the position: the wave's lowest lane is its first
+        const unsigned long long b = __ballot(tid < np && r < sm.pre[min(tid, kSmpPre - 1)]);
+        if (b && (tid & 63) == (int)__builtin_ctzll(b)) atomicMin(&sm.first, tid);
         __syncthreads();
         const int f = sm.first;
         if (f != kNone) {
@@ -247,13 +344,25 @@ __device__ float chain(const float *e, int n, int e4, float scale, float r, int 
         }
     }
     __syncthreads();  // the prefix is read before grid_chain's LDS is reused
-    return grid_chain<kSearch>(e, n, e4, scale, s, r, hit, sm);
+    // chunks of 1024, 4096, then 8192 terms: binade crossings are densest
+    // early, and a step after an event rescans the rest of its chunk
+    static_assert(kSmpThreads == 256, "the chunk schedule");
+    float x = grid_chain<kSearch, 4>(e, kSmpPre, kSmpPre + 1024, n, scale, s, r, hit, ph, c4, sm);
+    if (hit >= 0 || n <= kSmpPre + 1024) return x;
+    float4 c16[4];
+    load_chunk<16>(e, kSmpPre + 1024, n, c16);
+    x = grid_chain<kSearch, 16>(e, kSmpPre + 1024, kSmpPre + 5120, n, scale, x, r, hit, ph, c16, sm);
+    if (hit >= 0 || n <= kSmpPre + 5120) return x;
+    float4 c32[8];
+    load_chunk<32>(e, kSmpPre + 5120, n, c32);
+    return grid_chain<kSearch, 32>(e, kSmpPre + 5120, n, n, scale, x, r, hit, ph, c32, sm);
 }
 
 // The greedy argmax of a row (sample.go:45-53): the first index holding the
 // largest value; NaNs are never candidates, and a NaN first logit (or every
 // logit NaN) gives index 0, as the reference's `>` scan does. Valid in
 // thread 0; every thread calls it.
+template <int NT>
 __device__ int wg_argmax(const float *row, int64_t vocab, float *s_v, int *s_i) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float bv = 0.0f;
@@ -262,12 +371,12 @@ __device__ int wg_argmax(const float *row, int64_t vocab, float *s_v, int *s_i) 
     // re-reads the last group: merging an element twice changes nothing)
     const int64_t n4 = (reinterpret_cast<uintptr_t>(row) & 15) == 0 ? vocab >> 2 : 0;
     const float4 *r4 = reinterpret_cast<const float4 *>(row);
-    for (int64_t b = threadIdx.x; b < n4; b += 1024 * 8) {
+    for (int64_t b = threadIdx.x; b < n4; b += NT * 8) {
         float4 v[8];
         int64_t g[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            g[u] = min(b + 1024 * u, n4 - 1);
+            g[u] = min(b + NT * u, n4 - 1);
             v[u] = r4[g[u]];
         }
 #pragma unroll
@@ -278,7 +387,7 @@ __device__ int wg_argmax(const float *row, int64_t vocab, float *s_v, int *s_i) 
                 if (e[c] == e[c]) argmax_merge(bv, bi, e[c], (int)(4 * g[u] + c));
         }
     }
-    for (int64_t i = 4 * n4 + threadIdx.x; i < vocab; i += 1024) {
+    for (int64_t i = 4 * n4 + threadIdx.x; i < vocab; i += NT) {
         const float v = row[i];
         if (v == v) argmax_merge(bv, bi, v, (int)i);
     }
@@ -296,7 +405,7 @@ __device__ int wg_argmax(const float *row, int64_t vocab, float *s_v, int *s_i) 
     float v = 0.0f;
     int i = -1;
     if (threadIdx.x == 0) {
-        for (int w = 0; w < 16; w++) argmax_merge(v, i, s_v[w], s_i[w]);
+        for (int w = 0; w < NT / 64; w++) argmax_merge(v, i, s_v[w], s_i[w]);
         if (row[0] != row[0] || i < 0) i = 0;
     }
     return i;
@@ -320,9 +429,16 @@ __global__ __launch_bounds__(kSmpPartThreads) void sample_max_kernel(const float
     const float T = temps[z];
     if (!picks(pos, prompt, z, tokens_len) || T <= 0) return;
     const float *row = logits + (int64_t)z * vocab;
+    constexpr int64_t kStride = (int64_t)kSmpParts * kSmpPartThreads;
     float m = row[0] / T;
-    for (int64_t i = (int64_t)blockIdx.x * kSmpPartThreads + threadIdx.x; i < vocab; i += kSmpParts * kSmpPartThreads)
-        m = gomax(m, row[i] / T);
+    // four loads in flight a thread (a position past the row re-reads row[0])
+    for (int64_t i0 = (int64_t)blockIdx.x * kSmpPartThreads + threadIdx.x; i0 < vocab; i0 += 4 * kStride) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = row[i0 + k * kStride < vocab ? i0 + k * kStride : 0];
+#pragma unroll
+        for (int k = 0; k < 4; k++) m = gomax(m, v[k] / T);
+    }
     m = wave_gomax(m);
     if ((threadIdx.x & 63) == 0) s_m[threadIdx.x >> 6] = m;
     __syncthreads();
@@ -343,12 +459,23 @@ __global__ __launch_bounds__(kSmpPartThreads) void sample_terms_kernel(const flo
     const int z = blockIdx.y;
     const float T = temps[z];
     if (!picks(pos, prompt, z, tokens_len) || T <= 0) return;
-    static_assert(kSmpParts == 64, "one partial a lane");
-    const float mx = wave_gomax(part[z * kSmpParts + (threadIdx.x & 63)]);
+    static_assert(kSmpParts % 64 == 0, "partials a lane");
+    const float *pz = part + (int64_t)z * kSmpParts + (threadIdx.x & 63);
+    float mx = pz[0];
+#pragma unroll
+    for (int k = 1; k < kSmpParts / 64; k++) mx = gomax(mx, pz[64 * k]);
+    mx = wave_gomax(mx);
     const float *row = logits + (int64_t)z * vocab;
     float *e = terms + (int64_t)z * estride;
-    for (int64_t i = (int64_t)blockIdx.x * kSmpPartThreads + threadIdx.x; i < vocab; i += kSmpParts * kSmpPartThreads)
-        e[i] = exp32(row[i] / T - mx);
+    constexpr int64_t kStride = (int64_t)kSmpParts * kSmpPartThreads;
+    for (int64_t i0 = (int64_t)blockIdx.x * kSmpPartThreads + threadIdx.x; i0 < vocab; i0 += 4 * kStride) {
+        float v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = row[i0 + k * kStride < vocab ? i0 + k * kStride : 0];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (i0 + k * kStride < vocab) e[i0 + k * kStride] = exp32(v[k] / T - mx);
+    }
 }
 
 // One workgroup a sequence: the token at pos[z]+1 (the argmax when T <= 0,
@@ -369,13 +496,12 @@ __global__ __launch_bounds__(kSmpThreads) void sample_pick_kernel(const float *l
     const float T = temps[z];
     int token = 0;
     if (pick && T <= 0) {
-        token = wg_argmax(logits + (int64_t)z * vocab, vocab, sm.bv, sm.bi);
+        token = wg_argmax<kSmpThreads>(logits + (int64_t)z * vocab, vocab, sm.bv, sm.bi);
     } else if (pick) {
         const int n = (int)vocab;
         const float *e = terms + (int64_t)z * estride;
-        const int e4 = (int)(estride >> 2);
-        int hit;
-        const float S = chain<false>(e, n, e4, 1.0f, 0.0f, hit, sm);
+        int hit, ph = 0;
+        const float S = chain<false>(e, n, 1.0f, 0.0f, hit, ph, sm);
         const float inv = recip32(S);
         // the draw (sample.go:18-24), after the softmax as the reference
         // takes it; the state advances once a sampled token
@@ -389,7 +515,7 @@ __global__ __launch_bounds__(kSmpThreads) void sample_pick_kernel(const float *l
         }
         __syncthreads();
         const float r = sm.r;
-        chain<true>(e, n, e4, inv, r, hit, sm);
+        chain<true>(e, n, inv, r, hit, ph, sm);
         token = hit >= 0 ? hit : n - 1;
     }
     __syncthreads();  // every thread has read pos[z] before it moves
@@ -408,7 +534,7 @@ __global__ __launch_bounds__(1024) void seqs_advance_kernel(const float *logits,
     __shared__ float s_v[16];
     __shared__ int s_i[16];
     const int z = blockIdx.x;
-    const int i = wg_argmax(logits + (int64_t)z * vocab, vocab, s_v, s_i);
+    const int i = wg_argmax<1024>(logits + (int64_t)z * vocab, vocab, s_v, s_i);
     if (threadIdx.x == 0) {
         const int p = pos[z];
         if (p + 1 >= prompt[z] && p + 1 < tokens_len) tokens[(int64_t)z * tok_stride + p + 1] = i;
