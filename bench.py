@@ -769,9 +769,11 @@ def moe_bench(dev, rkhip, args):
         start()
         run(2)  # records the graph, touches every weight
         start()
+        st.moe_stats()  # the device's grouping counters restart here
         t0 = time.perf_counter()
         run(steps - 1)
         el = time.perf_counter() - t0
+        selected, groupings = st.moe_stats()
         if args.eager:
             dev.profile_stop()
         ms_step = el / (steps - 1) * 1e3
@@ -786,16 +788,22 @@ def moe_bench(dev, rkhip, args):
         dev.profile_start()
         run(4)
         prof = dev.profile_stop()
-        # distinct experts a step streams per layer: every one of the 8 at
-        # batch 1; at batch 16 the expected count under independent uniform
-        # routing, E·(1 - (1 - k/E)^16)
-        distinct = topk if batch == 1 else experts * (1 - (1 - topk / experts) ** batch)
+        # distinct experts a step streams per layer: the 8 selected at batch
+        # 1; at batch 16 the device's own count, each layer's grouping of the
+        # step's (token, slot) pairs summed over the timed steps
+        if batch == 1:
+            distinct = topk
+        else:
+            if groupings != nl * (steps - 1):
+                raise RuntimeError(f"moe bench: {groupings} groupings for {nl} layers x {steps - 1} steps")
+            distinct = selected / groupings
         step_bytes = nl * (attn_bytes + router_bytes + distinct * expert_bytes + batch * kv_read) + cls_bytes
         out[f"batch{batch}"] = {
             "tok_s": round(batch / (ms_step / 1e3), 1),
             "ms_per_step": round(ms_step, 4),
             "tokens_per_step": batch,
-            "distinct_experts_per_layer": round(distinct, 1),
+            "distinct_experts_per_layer": round(distinct, 2),
+            "distinct_experts_source": "top-k" if batch == 1 else "device grouping count",
             "bytes_per_step": int(step_bytes),
             "effective_GB/s": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
             "frac_of_hbm_peak": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -375,6 +375,13 @@ int rk_stage_seqs_tokens(rk_stage *s, int32_t seq, int32_t from, int32_t n, int3
  * recorded step, and persists until set again: call it before each
  * generation for the reference's one sampler per request. */
 int rk_stage_sampler(rk_stage *s, int32_t seq, float temperature, uint64_t seed);
+/* The experts selected by the stage's MoE layers when several tokens run
+ * together (independent sequences, prompt batches): the sum of each
+ * grouping's distinct experts, and the number of groupings (one a MoE layer
+ * a batch), since the stage was made or last asked; the counters restart.
+ * No counterpart in the reference (which has no MoE model of this family):
+ * it measures how much expert weight a batched step reads. */
+int rk_stage_moe_stats(rk_stage *s, int64_t *selected, int64_t *groupings);
 /* Sampler.Sample (internal/llm/sample.go:26-43) of `rows` rows of host
  * logits [rows][vocab] on the device: row z with temperature[z] and the
  * generator state state[z] (as NewSampler leaves it: a zero seed already

@@ -23,6 +23,9 @@ struct MoeScratch {
     float *hs = nullptr;
     int32_t *hsum = nullptr;
     float *o = nullptr;            // [cap·topk][dim] each (token, slot)'s W2·h
+    // optional: each grouping of several tokens adds its selected experts'
+    // count to stat[0] and 1 to stat[1]
+    unsigned long long *stat = nullptr;
 };
 
 }  // namespace rk

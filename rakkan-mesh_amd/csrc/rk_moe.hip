@@ -267,6 +267,9 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float *logits, int 
 struct MoeTabs {
     const uint8_t *const *w1, *const *w3, *const *w2;
     const float *const *s1, *const *s3, *const *s2;
+    // optional counters: the experts selected (summed over groupings), and
+    // the groupings (MoeScratch::stat)
+    unsigned long long *stat;
 };
 // Thread e's expert's six row addresses, read at a kernel's start (they
 // do not depend on the routing) so they are in registers by the time the
@@ -303,7 +306,7 @@ struct GroupLds {
 // the number of groups. Then each selected expert's group entry and rows.
 // Every thread of a 1024-thread workgroup calls it, after the counts.
 __device__ void group_scan_info(GroupLds &gl, int experts, int gcap, int32_t *grp, const ExpRows &rows,
-                                const void **gptr) {
+                                const void **gptr, unsigned long long *stat) {
     const int tid = threadIdx.x, lane = tid & 63;
     if (tid < 64) {
         const int per = (experts + 63) / 64;
@@ -345,7 +348,13 @@ __device__ void group_scan_info(GroupLds &gl, int experts, int gcap, int32_t *gr
         gcount[g] = gl.cnt[tid];
         group_rows(rows, g, gptr);
     }
-    if (tid == 0) grp[0] = gl.total;
+    if (tid == 0) {
+        grp[0] = gl.total;
+        if (stat) {
+            atomicAdd(&stat[0], (unsigned long long)gl.total);
+            atomicAdd(&stat[1], 1ull);
+        }
+    }
 }
 
 // The (token, slot) pairs grouped by expert: grp[0] = the number of experts
@@ -369,7 +378,7 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, con
     __syncthreads();
     for (int p = tid; p < npairs; p += 1024) atomicAdd(&gl.cnt[sel[p]], 1);
     __syncthreads();
-    group_scan_info(gl, experts, gcap, grp, rows, gptr);
+    group_scan_info(gl, experts, gcap, grp, rows, gptr, tb.stat);
     int32_t *list = grp + 1 + 3 * gcap;
     for (int p = tid; p < npairs; p += 1024) {
         const int e = sel[p];
@@ -387,13 +396,14 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *sel, con
 // thread of a 1024-thread workgroup calls it; s_sel: the pairs' experts in
 // LDS, written before a barrier.
 __device__ void group_pairs_wg(const int *s_sel, const float *s_wt, int npairs, int experts, int gcap, int32_t *grp,
-                               float *gwt, const ExpRows &rows, const void **gptr, GroupLds &gl) {
+                               float *gwt, const ExpRows &rows, const void **gptr, GroupLds &gl,
+                               unsigned long long *stat) {
     const int tid = threadIdx.x;
     gl.cnt[tid] = 0;
     __syncthreads();
     if (tid < npairs) atomicAdd(&gl.cnt[s_sel[tid]], 1);
     __syncthreads();
-    group_scan_info(gl, experts, gcap, grp, rows, gptr);
+    group_scan_info(gl, experts, gcap, grp, rows, gptr, stat);
     // pair p's place: the earlier pairs of its expert (eight threads a pair)
     int32_t *list = grp + 1 + 3 * gcap;
     const int p = tid >> 3, part = tid & 7;
@@ -423,7 +433,7 @@ __global__ __launch_bounds__(1024) void moe_group_fast_kernel(const int32_t *sel
         s_wt[threadIdx.x] = wsel[threadIdx.x];
     }
     __syncthreads();
-    group_pairs_wg(s_sel, s_wt, npairs, experts, gcap, grp, gwt, rows, gptr, gl);
+    group_pairs_wg(s_sel, s_wt, npairs, experts, gcap, grp, gwt, rows, gptr, gl, tb.stat);
 }
 
 // Routing (wave t: token t) and grouping of up to kSelectTokens tokens in
@@ -450,7 +460,7 @@ __global__ __launch_bounds__(1024) void moe_select_kernel(const float *logits, i
         s_wt[t * k + lane] = wt;
     }
     __syncthreads();
-    group_pairs_wg(s_sel, s_wt, tokens * k, experts, gcap, grp, gwt, rows, gptr, gl);
+    group_pairs_wg(s_sel, s_wt, tokens * k, experts, gcap, grp, gwt, rows, gptr, gl, tb.stat);
 }
 
 // W1 and W3 rows of a selected expert for every pair that chose it:
@@ -702,18 +712,96 @@ __global__ __launch_bounds__(512) void moe_up8_kernel(const void *const *gptr, c
     }
 }
 
-// Byte offset of moe_up1_kernel's float region (after the codes, scales and
-// code sums of the normed input).
-__host__ __device__ inline int up1_lds_r(int dim) { return (dim + 8 * (dim >> 5) + 15) & ~15; }
+// moe_up1_kernel's LDS: the normed input's codes, scales and code sums,
+// then per expert (E rounded up to 4) a float, a 64-bit key and a rank, the
+// norm's transposed x, and the experts' W1/W3 row and scale pointers.
+struct Up1Lds {
+    int sxs, sxsum, sp, skey, srank, sn, stab, bytes;
+};
+__host__ __device__ inline Up1Lds up1_lds(int dim, int experts) {
+    Up1Lds l;
+    const int nb = dim >> 5, ep = (experts + 3) & ~3;
+    l.sxs = dim;
+    l.sxsum = l.sxs + 4 * nb;
+    l.sp = (l.sxsum + 4 * nb + 15) & ~15;
+    l.skey = l.sp + 4 * ep;
+    l.srank = l.skey + 8 * ep;
+    l.sn = (l.srank + 4 * ep + 15) & ~15;
+    l.stab = l.sn + 32 * ((((dim >> 5) + 3) & ~3) + 4) * 4;
+    l.bytes = l.stab + 8 * 4 * experts;
+    return l;
+}
+constexpr int kUp1MaxExperts = 512;
 
-// One token's W1/W3 rows with the routing and the RMSNorm folded in: each
-// workgroup routes the token itself (wave 0; every workgroup gets the same
-// selection), takes the g-th selected expert by ascending index (g =
-// blockIdx.x, the grouping's order), loads that expert's rows, and forms
-// RMSNorm_ffn(x)'s Q8_0 form in LDS while the rows are in flight; workgroup
-// (0, 0) also writes the selection, the weights and the grouping (one pair
-// a group) for the W2 products and the sum. h as moe_up8_kernel's.
-template <int BPL, int PER>
+// route_wave's softmax of one token by one wave (every lane calls it): lg
+// holds the logits of experts lane + 64j; the probabilities go to sp and
+// each expert's key (route_key) to skey. Every lane runs the one sequential
+// sum (the wave's LDS writes precede its reads), so all get the same inv.
+template <int LPER>
+__device__ __forceinline__ void up1_softmax(const float (&lg)[LPER], int experts, float *sp, unsigned long long *skey) {
+    const int lane = threadIdx.x & 63;
+    float m = lg[0];
+#pragma unroll
+    for (int j = 0; j < LPER; j++)
+        if (lane + 64 * j < experts) m = gomax(m, lg[j]);
+    m = wave_gomax(m);
+#pragma unroll
+    for (int j = 0; j < LPER; j++)
+        if (lane + 64 * j < experts) sp[lane + 64 * j] = exp32(lg[j] - m);
+    const float inv = recip32(lds_chain_sum(sp, experts, 0.0f));
+#pragma unroll
+    for (int j = 0; j < LPER; j++) {
+        const int e = lane + 64 * j;
+        if (e < experts) {
+            const float pv = sp[e] * inv;
+            sp[e] = pv;
+            skey[e] = route_key(pv, e);
+        }
+    }
+}
+
+// The stable top-k as ranks over a 512-thread workgroup: each expert's
+// count of larger keys (keys are distinct, so the k largest have ranks
+// 0..k-1, in the order route_wave's rounds pick them), TPE threads an
+// expert, each counting over a slice of the keys (pairs read 16 bytes at a
+// time, four reads in flight), summed into srank (cleared before) by LDS
+// atomics. Every thread calls it; skey and srank in LDS.
+__device__ __forceinline__ void expert_ranks(const unsigned long long *skey, int *srank, int experts) {
+    const int tid = threadIdx.x;
+    int ep = 1;
+    while (ep < experts) ep <<= 1;
+    const int tpe = max(1, 512 / ep);
+    const int slice = ((experts + tpe - 1) / tpe + 1) & ~1;  // even: 16-byte pairs
+    const int e = tid / tpe, part = tid - e * tpe;
+    if (e >= experts) return;
+    const unsigned long long ke = skey[e];
+    int c = 0, q = part * slice;
+    const int hi = min(experts, q + slice);
+    for (; q + 8 <= hi; q += 8) {
+        const ulonglong2 *p2 = reinterpret_cast<const ulonglong2 *>(skey + q);
+        const ulonglong2 a = p2[0], b = p2[1], u = p2[2], v = p2[3];
+        c += (a.x > ke) + (a.y > ke) + (b.x > ke) + (b.y > ke) + (u.x > ke) + (u.y > ke) + (v.x > ke) + (v.y > ke);
+    }
+    for (; q < hi; q++) c += skey[q] > ke ? 1 : 0;
+    if (c) atomicAdd(&srank[e], c);
+}
+
+// One token's W1/W3 rows with the ffn RMSNorm and the routing folded in.
+// Every workgroup forms RMSNorm_ffn(x)'s Q8_0 input in LDS and routes the
+// token itself (every workgroup gets the same selection); workgroup (g, b)
+// then takes the g-th selected expert by ascending index and its hidden
+// rows 32b .. 32b+31 (W1 and W3 of each: eight row dots a wave, eight lanes
+// a row); h as moe_up8_kernel's. Workgroup (0, 0) also writes the
+// selection, the weights and the grouping (one pair a group) for the W2
+// products and the sum. The routing's steps are route_wave's, spread over
+// the workgroup: wave 1 the softmax while wave 0 runs the norm's Dot32
+// chain, then the stable top-k as ranks (each expert's count of larger
+// keys; keys are distinct) by all waves, the weights by wave 0. The
+// experts' row pointers are staged in LDS while the token is routed.
+// (Computing the router's logits in every workgroup instead, from its rows
+// in L2, was measured slower: issuing 1.125·E·dim bytes of row loads per
+// workgroup took longer than the router's own launch.)
+template <int BPL>
 __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const float *norm_w, float recip_n, float eps,
                                                       const float *logits, int experts, int k,
                                                       const uint8_t *const *w1, const float *const *s1,
@@ -724,33 +812,99 @@ __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const floa
     extern __shared__ __align__(16) char ulds[];
     __shared__ float bcast, s_w;
     __shared__ int s_e, s_slot;
+    __shared__ int ssel[kMoeMaxK];
     __shared__ __align__(16) float sh[32];
+    const Up1Lds L = up1_lds(dim, experts);
     const int nb = dim >> 5;
-    int8_t *sq = reinterpret_cast<int8_t *>(ulds);                              // [dim] codes
-    float *sxs = reinterpret_cast<float *>(ulds + dim);                         // [nb] scales
-    int32_t *sxsum = reinterpret_cast<int32_t *>(ulds + dim + 4 * nb);          // [nb] code sums
-    float *sp = reinterpret_cast<float *>(ulds + up1_lds_r(dim));               // [experts] probabilities
-    float *sn = sp + ((experts + 3) & ~3);                                      // the norm's transposed x
+    int8_t *sq = reinterpret_cast<int8_t *>(ulds);                                  // [dim] codes
+    float *sxs = reinterpret_cast<float *>(ulds + L.sxs);                          // [nb] scales
+    int32_t *sxsum = reinterpret_cast<int32_t *>(ulds + L.sxsum);                  // [nb] code sums
+    float *sp = reinterpret_cast<float *>(ulds + L.sp);                            // [experts] probabilities
+    unsigned long long *skey = reinterpret_cast<unsigned long long *>(ulds + L.skey);
+    int *srank = reinterpret_cast<int *>(ulds + L.srank);
+    float *sn = reinterpret_cast<float *>(ulds + L.sn);                            // the norm's transposed x
+    const void **stab = reinterpret_cast<const void **>(ulds + L.stab);            // [4][experts] row pointers
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    float4 xv[1], wv[1];
-    {
-        const int g4 = min(tid, (dim >> 2) - 1);
-        xv[0] = reinterpret_cast<const float4 *>(x)[g4];
-        wv[0] = reinterpret_cast<const float4 *>(norm_w)[g4];
+    const int rg = lane >> 3, rl = lane & 7;
+    // loads: x and the norm weights (a group of four a thread), the logits
+    // (wave 1), the row pointer tables
+    const int ng = dim >> 2;
+    const int g4 = min(tid, ng - 1);
+    const float4 xv = reinterpret_cast<const float4 *>(x)[g4];
+    const float4 wv = reinterpret_cast<const float4 *>(norm_w)[g4];
+    constexpr int kLPer = kUp1MaxExperts / 64;
+    float lg[kLPer];
+    if (wave == 1) {
+#pragma unroll
+        for (int j = 0; j < kLPer; j++) lg[j] = logits[min(lane + 64 * j, experts - 1)];
     }
+    for (int t = tid; t < 4 * experts; t += 512) {
+        const int tab = t / experts, e = t - tab * experts;
+        stab[t] = tab == 0 ? (const void *)w1[e] : tab == 1 ? (const void *)s1[e] : tab == 2 ? (const void *)w3[e]
+                                                                                           : (const void *)s3[e];
+    }
+    // x transposed for Dot32 (xt[j·pitch + m] = x_{j+32m}); ranks cleared
+    const int steps = dim >> 5, pitch = ((steps + 3) & ~3) + 4;
+    if (tid < ng) {
+        const int i = 4 * tid;
+        float *d = sn + (i & 31) * pitch + (i >> 5);
+        d[0] = xv.x;
+        d[pitch] = xv.y;
+        d[2 * pitch] = xv.z;
+        d[3 * pitch] = xv.w;
+    }
+    for (int e = tid; e < experts; e += 512) srank[e] = 0;
+    __syncthreads();
+    if (wave == 0) {
+        // RMSNorm (model.go:632-638): ss = Dot32(x, x)·recip_n + eps
+        const float sq32 = lane < 32 ? lds_dot32_self_t(sn, pitch, steps, lane) : 0.0f;
+        const float dot = dot32_reduce(sq32);
+        if (lane == 0) bcast = rsqrt32((dot * recip_n) + eps);
+    } else if (wave == 1) {
+        up1_softmax<kLPer>(lg, experts, sp, skey);
+    }
+    __syncthreads();
+    {
+        // the normed input's Q8_0 (quant.go:34-53): out_i = w_i·(r·x_i)
+        const float r = bcast;
+        float d;
+        int cs;
+        const uint32_t pk = quantize_group(wv.x * (r * xv.x), wv.y * (r * xv.y), wv.z * (r * xv.z),
+                                           wv.w * (r * xv.w), d, cs);
+        if (tid < ng) {
+            reinterpret_cast<uint32_t *>(sq)[tid] = pk;
+            if ((tid & 7) == 0) {
+                sxs[tid >> 3] = d;
+                sxsum[tid >> 3] = cs;
+            }
+        }
+    }
+    __syncthreads();
+    expert_ranks(skey, srank, experts);
+    __syncthreads();
+    for (int e = tid; e < experts; e += 512)
+        if (srank[e] < k) ssel[srank[e]] = e;
+    __syncthreads();
     const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
-    float wt;
-    const int mine = route_wave<PER>(wave == 0, logits, experts, k, sp, lead ? sel : nullptr, wsel, wt);
     if (wave == 0 && lane < k) {
+        const int mine = ssel[lane];
+        const float ps = sp[mine];
+        // the weights (route_wave's): the selected probabilities' sum in
+        // selection order from +0, times its Recip32
+        float sum = 0.0f;
+        for (int r = 0; r < k; r++) sum += __shfl(ps, r);
+        const float wt = ps * recip32(sum);
         int r = 0;  // place among the selection by ascending index (the experts are distinct)
-        for (int q = 0; q < k; q++) r += __shfl(mine, q) < mine;
+        for (int q = 0; q < k; q++) r += ssel[q] < mine;
         if (r == (int)blockIdx.x) {
             s_e = mine;
             s_w = wt;
             s_slot = lane;
         }
         if (lead) {
+            sel[lane] = mine;
+            wsel[lane] = wt;
             grp[1 + r] = mine;
             grp[1 + gcap + r] = r;
             grp[1 + 2 * gcap + r] = 1;
@@ -762,15 +916,14 @@ __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const floa
     }
     __syncthreads();
     const int e = s_e;
-    const int rg = lane >> 3, rl = lane & 7, q = rg >> 1;
+    const int q = rg >> 1;
     const int j = blockIdx.y * 32 + 4 * wave + q;
     const bool w3row = rg & 1;
+    const uint8_t *wrow = static_cast<const uint8_t *>(stab[(w3row ? 2 : 0) * experts + e]);
+    const float *srow = static_cast<const float *>(stab[(w3row ? 3 : 1) * experts + e]);
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, (w3row ? w3[e] : w1[e]) + (int64_t)j * dim,
-                       (w3row ? s3[e] : s1[e]) + (int64_t)j * nb, nb, rl);
-    wg_norm_quant<512, 1>(xv, wv, dim, recip_n, eps, sq, sxs, sxsum, sn, &bcast);
-    __syncthreads();
+    lane_row_load<BPL>(c0, c1, sw, wrow + (int64_t)j * dim, srow + (int64_t)j * nb, nb, rl);
     const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq, sxs, nb, rl));
     const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
     if ((lane & 15) == 0) sh[4 * wave + q] = s_w * silu_mul(v, v3);
@@ -1020,7 +1173,7 @@ int enqueue_moe_q(rk_moe *m, const MoeScratch &sc, const int8_t *qx, const float
     }
     if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
     const int npairs = tokens * K;
-    const MoeTabs tabs{m->w1, m->w3, m->w2, m->s1, m->s3, m->s2};
+    const MoeTabs tabs{m->w1, m->w3, m->w2, m->s1, m->s3, m->s2, sc.stat};
     if (tokens <= kSelectTokens && npairs <= kGroupFastPairs && E <= 1024) {
         static std::once_flag once;
         std::call_once(once, [] {
@@ -1141,7 +1294,7 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
     if (tokens <= 0) return RK_OK;
     if (tokens > sc.cap) return fail(d, RK_ERR_ARGS, "moe: %d tokens beyond the scratch's %d", tokens, sc.cap);
     const int D = m->dim, E = m->experts, K = m->topk, H = m->hidden;
-    if (norm_w && tokens == 1 && D <= 2048 && E <= 1024 && K <= kMoeMaxK) {
+    if (norm_w && tokens == 1 && D <= 2048 && E <= kUp1MaxExperts && K <= kMoeMaxK) {
         // one token: the router's product with the RMSNorm in its prologue,
         // then the W1/W3 rows with the routing and the norm folded in (the
         // normed input is never stored: qx, xs and xsum are left as they are)
@@ -1161,22 +1314,16 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
         }
         if (!ok) return fail(d, RK_ERR_UNSUPPORTED, "rk_moe: the router's product has no kernel");
         const int bpl = (D / 32 + 7) / 8;
-        const size_t lds = (size_t)up1_lds_r(D) + (size_t)((E + 3) & ~3) * 4 + norm_lds(D);
+        const size_t lds = (size_t)up1_lds(D, E).bytes;
         {
             ProfScope p(d, s, "moe_up");
-#define RK_UP1(B, P)                                                                                               \
-    RK_LAUNCH((moe_up1_kernel<B, P>), dim3((unsigned)K, (unsigned)(H / 32)), dim3(512), lds, s, x, norm_w, recip_n, \
+#define RK_UP1(B)                                                                                                  \
+    RK_LAUNCH((moe_up1_kernel<B>), dim3((unsigned)K, (unsigned)(H / 32)), dim3(512), lds, s, x, norm_w, recip_n,     \
               eps, sc.logits, E, K, m->w1, m->s1, m->w3, m->s3, m->w2, m->s2, D, H, sc.sel, sc.wsel, sc.gcap,       \
               sc.grp, sc.gptr, sc.hq, sc.hs, sc.hsum)
-            if (E <= 128) {
-                if (bpl <= 2) RK_UP1(2, 2);
-                else if (bpl <= 4) RK_UP1(4, 2);
-                else RK_UP1(8, 2);
-            } else {
-                if (bpl <= 2) RK_UP1(2, kRoutePer);
-                else if (bpl <= 4) RK_UP1(4, kRoutePer);
-                else RK_UP1(8, kRoutePer);
-            }
+            if (bpl <= 2) RK_UP1(2);
+            else if (bpl <= 4) RK_UP1(4);
+            else RK_UP1(8);
 #undef RK_UP1
         }
         if (H / 32 > 8 * 8) return enqueue_moe_down(m, sc, tokens, out, residual, s, next);

@@ -93,6 +93,8 @@ struct rk_stage {
     // another), laid out per layer for moe_cap tokens.
     char *moe_mem = nullptr;
     int moe_cap = 0;
+    // the groupings' counters (MoeScratch::stat): experts selected, groupings
+    unsigned long long *moe_stat = nullptr;
 };
 
 namespace rk {
@@ -264,6 +266,7 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
         // the experts' sum goes into the residual, x = Canonical(x + y)
         MoeScratch sc;
         moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
+        sc.stat = s->moe_stat;
         return enqueue_moe_x(L.moe, sc, s->x, D.rms_ffn, c.recip_dim, c.norm_eps, 1, s->qb.qx, s->qb.xs, s->qb.xsum,
                              s->x, true, st);
     }
@@ -551,6 +554,7 @@ static int enqueue_layer_batch(rk_stage *s, int li, hipStream_t st, int n, const
     if (L.moe) {  // RMSNorm_ffn(x) into bqb, and the experts' sums into the residual rows, x = Canonical(x + y)
         MoeScratch sc;
         moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
+        sc.stat = s->moe_stat;
         // the sum's launch also forms the next layer's normed input in bqb
         const MoeNext nx{next_norm, c.recip_dim, c.norm_eps, s->bqb.qx, s->bqb.xs, s->bqb.xsum};
         if ((rc = enqueue_moe_x(L.moe, sc, s->bx, D.rms_ffn, c.recip_dim, c.norm_eps, n, s->bqb.qx, s->bqb.xs,
@@ -771,6 +775,7 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
         for (int i = 0; i < n_layers; i++)
             if (layers[i].moe) mb = std::max(mb, moe_scratch_layout(layers[i].moe, s->moe_cap, nullptr, nullptr));
         take((void **)&s->moe_mem, mb);
+        take((void **)&s->moe_stat, 16);
     }
     s->ld.resize(n_layers);
     const int64_t bias_n = c->qkv_bias ? qdim + 2 * kvdim : 0;
@@ -1151,6 +1156,23 @@ int rk_stage_seqs_run(rk_stage *s, int32_t steps, float *logits) {
     }
     HIP_TRY(d, hipStreamSynchronize(d->stream), "seqs run");
     for (int32_t &p : s->seq_at) p += steps;
+    return RK_OK;
+}
+
+int rk_stage_moe_stats(rk_stage *s, int64_t *selected, int64_t *groupings) {
+    if (!s || !selected || !groupings) return RK_ERR_ARGS;
+    rk_device *d = s->d;
+    *selected = 0;
+    *groupings = 0;
+    if (!s->moe_stat) return RK_OK;
+    Hold hold(d->gate);
+    HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
+    unsigned long long v[2] = {0, 0};
+    HIP_TRY(d, hipStreamSynchronize(d->stream), "moe stats");
+    HIP_TRY(d, hipMemcpy(v, s->moe_stat, 16, hipMemcpyDeviceToHost), "moe stats");
+    HIP_TRY(d, hipMemset(s->moe_stat, 0, 16), "moe stats");
+    *selected = (int64_t)v[0];
+    *groupings = (int64_t)v[1];
     return RK_OK;
 }
 

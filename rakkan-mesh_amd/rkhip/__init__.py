@@ -99,6 +99,7 @@ SIGNATURES = {
     "rk_stage_seqs_tokens": (ctypes.c_int, [P, I32, I32, I32, P]),
     "rk_stage_sampler": (ctypes.c_int, [P, I32, ctypes.c_float, ctypes.c_uint64]),
     "rk_sample_logits": (ctypes.c_int, [P, P, I64, I32, P, P, P]),
+    "rk_stage_moe_stats": (ctypes.c_int, [P, P, P]),
     "rk_num_eval": (ctypes.c_int, [P, I32, P, P, I64]),
     "rk_moe_new": (ctypes.c_int, [P, P, I32, P, P, P, I32, P]),
     "rk_moe_ffn": (ctypes.c_int, [P, P, I32, P, P, P]),
@@ -685,6 +686,13 @@ class Stage:
         """rk_stage_sampler: NewSampler(temperature, seed) for sequence seq
         (internal/llm/sample.go:11-16); temperature <= 0 is the greedy argmax."""
         self.dev._check(lib().rk_stage_sampler(self.h, seq, float(np.float32(temperature)), int(seed) & (2**64 - 1)))
+
+    def moe_stats(self):
+        """rk_stage_moe_stats: (experts selected summed over the batched MoE
+        groupings, groupings) since the last call; the counters restart."""
+        a, b = ctypes.c_int64(), ctypes.c_int64()
+        self.dev._check(lib().rk_stage_moe_stats(self.h, ctypes.byref(a), ctypes.byref(b)))
+        return a.value, b.value
 
     @property
     def bytes(self):

@@ -234,3 +234,30 @@ def test_config5_shape_batch1_and_16_sequences(dev):
     finally:
         g.free()
     assert dev.used == 0
+
+
+def test_moe_stats_count_each_groupings_experts(dev):
+    """rk_stage_moe_stats: one grouping a MoE layer a batched step. Two
+    sequences with the same prompt choose the same experts at every layer
+    and step, so each grouping holds exactly top-k experts; different
+    prompts hold between top-k and min(experts, 2·top-k)."""
+    m = moe_model(SMALL, experts=12, ehidden=64, topk=3, seed=1, lo=1e-3, hi=1e-2, router_scale=(1e-2, 5e-2))
+    g = GpuModel(dev, m)
+    steps = 6
+    try:
+        for prompts, same in (([[3, 8, 1], [3, 8, 1]], True), ([[3, 8, 1], [40, 2, 9, 17]], False)):
+            st = g.stage(96, seqs=2)
+            st.seqs_start(prompts)
+            st.moe_stats()  # the prompts' batches counted so far
+            st.seqs_run(steps)
+            selected, groupings = st.moe_stats()
+            assert groupings == SMALL.layers * steps
+            if same:
+                assert selected == 3 * groupings
+            else:
+                assert 3 * groupings <= selected <= 6 * groupings and selected > 3 * groupings
+            assert st.moe_stats() == (0, 0)
+            st.free()
+    finally:
+        g.free()
+    assert dev.used == 0
