@@ -97,6 +97,21 @@ int rk_matrix_upload(rk_device *dev, int32_t kind, int64_t rows, int64_t cols, c
 int rk_matrix_upload_mx(rk_device *dev, int32_t kind, int64_t rows, int64_t cols, const uint8_t *w,
                         const uint8_t *e8m0, rk_matrix **out);
 
+/* internal/gpu/device.go:575-581, 609-618, 704-723 Upload of
+ * Format{FP4Chunks, E8M0Chunks, AlignRows} (stacked experts, uploaded piece
+ * by piece and never gathered on the host whole; internal/llm/dsv41/gpu.go:
+ * 177-184): the codes as n_w pieces w[i] of w_len[i] bytes and the E8M0
+ * scales as n_s pieces, each list read as one run of bytes, laid out as
+ * rk_matrix_upload_mx's. align_rows > 0: rows must be a whole number of
+ * runs of that many rows (and, for E4M3, a multiple of 32), else
+ * "gpu: rows not a whole number of aligned runs". The matrix is one device
+ * allocation, so the runs are whole by construction. The same checks and
+ * messages as rk_matrix_upload_mx, in the reference's order. */
+int rk_matrix_upload_mx_chunks(rk_device *dev, int32_t kind, int64_t rows, int64_t cols, int32_t n_w,
+                               const uint8_t *const *w, const int64_t *w_len, int32_t n_s,
+                               const uint8_t *const *e8m0, const int64_t *s_len, int32_t align_rows,
+                               rk_matrix **out);
+
 /* internal/gpu/device.go:548 Matrix.unrounded: raw != 0 leaves an E4M3 /
  * E2M1 matrix's products in float32 (num.MatVecFP8Unrounded), for checks
  * where bfloat16 would hide the last bits. */

@@ -506,27 +506,58 @@ int rk_matrix_upload(rk_device *d, int32_t kind, int64_t rows, int64_t cols, con
 
 // internal/gpu/device.go:587-700 Upload of Format{FP8 | FP4, E8M0}: codes
 // [rows][row bytes] and their scale bytes as given.
-int rk_matrix_upload_mx(rk_device *d, int32_t kind, int64_t rows, int64_t cols, const uint8_t *w,
-                        const uint8_t *e8m0, rk_matrix **out) {
-    if (!d || !out || !w || !e8m0) return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: null argument");
+int rk_matrix_upload_mx_chunks(rk_device *d, int32_t kind, int64_t rows, int64_t cols, int32_t n_w,
+                               const uint8_t *const *w, const int64_t *w_len, int32_t n_s,
+                               const uint8_t *const *e8m0, const int64_t *s_len, int32_t align_rows,
+                               rk_matrix **out) {
+    if (!d || !out || n_w <= 0 || n_s <= 0 || !w || !w_len || !e8m0 || !s_len)
+        return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: null argument");
     *out = nullptr;
     if (kind != RK_FP8 && kind != RK_FP4) return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: format %d", kind);
-    if (rows <= 0 || cols <= 0 || cols > kMaxCols || rows > (int64_t)1 << 24)
+    // the pieces, each read as one run of bytes (device.go:704-723 gatherer)
+    int64_t wtot = 0, stot = 0;
+    for (int32_t i = 0; i < n_w; i++) {
+        if (w_len[i] < 0 || (w_len[i] > 0 && !w[i])) return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: null chunk");
+        wtot += w_len[i];
+    }
+    for (int32_t i = 0; i < n_s; i++) {
+        if (s_len[i] < 0 || (s_len[i] > 0 && !e8m0[i]))
+            return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: null chunk");
+        stot += s_len[i];
+    }
+    const int64_t row_bytes = kind == RK_FP8 ? cols : cols / 2;
+    if (rows <= 0 || cols <= 0 || cols > kMaxCols || rows > (int64_t)1 << 24 || wtot != rows * row_bytes)
         return fail(d, RK_ERR_ARGS, "gpu: matrix %lld×%lld out of range", (long long)rows, (long long)cols);
-    if (cols % 32 != 0) return fail(d, RK_ERR_ARGS, "gpu: block-scaled matrix of the wrong shape");
     const int64_t nb = cols / 32;
-    const int64_t wbytes = kind == RK_FP8 ? rows * cols : rows * cols / 2;
-    // E2M1 scales are repacked into the products' tile layout
-    const int64_t sbytes = kind == RK_FP8 ? (rows + 31) / 32 * nb : mx_fp4_scale_bytes(rows, cols);
+    const int64_t blocks = kind == RK_FP8 ? (rows + 31) / 32 * nb : rows * nb;
+    if (cols % 32 != 0 || stot != blocks) return fail(d, RK_ERR_ARGS, "gpu: block-scaled matrix of the wrong shape");
+    if (kind == RK_FP8) {  // num.ValidE4M3: the NaN codes are refused
+        for (int32_t c = 0; c < n_w; c++)
+            for (int64_t i = 0; i < w_len[c]; i++)
+                if ((w[c][i] & 0x7f) == 0x7f) return fail(d, RK_ERR_ARGS, "gpu: NaN in E4M3 weights");
+    }
+    // device.go:611-618: runs of align_rows rows (an expert's) kept whole.
+    // One allocation holds every row here, so the runs are whole already;
+    // the shape rule is the reference's.
+    if (align_rows > 0 && (rows % align_rows != 0 || (kind == RK_FP8 && align_rows % 32 != 0)))
+        return fail(d, RK_ERR_ARGS, "gpu: rows not a whole number of aligned runs");
+    // the scale bytes (small) gathered on the host; E2M1's repacked into the
+    // products' tile layout
+    std::vector<uint8_t> sc((size_t)blocks);
+    {
+        int64_t at = 0;
+        for (int32_t c = 0; c < n_s; c++) {
+            if (s_len[c]) memcpy(sc.data() + at, e8m0[c], (size_t)s_len[c]);
+            at += s_len[c];
+        }
+    }
+    const int64_t sbytes = kind == RK_FP8 ? blocks : mx_fp4_scale_bytes(rows, cols);
     std::vector<uint8_t> packed;
+    const uint8_t *sdev = sc.data();
     if (kind == RK_FP4) {
         packed.resize((size_t)sbytes);
-        mx_fp4_pack_scales(e8m0, rows, cols, packed.data());
-        e8m0 = packed.data();
-    }
-    if (kind == RK_FP8) {  // num.ValidE4M3: the NaN codes are refused
-        for (int64_t i = 0; i < wbytes; i++)
-            if ((w[i] & 0x7f) == 0x7f) return fail(d, RK_ERR_ARGS, "gpu: NaN in E4M3 weights");
+        mx_fp4_pack_scales(sc.data(), rows, cols, packed.data());
+        sdev = packed.data();
     }
     Hold hold(d->gate);
     HIP_TRY(d, hipSetDevice(d->index), "hipSetDevice");
@@ -536,25 +567,44 @@ int rk_matrix_upload_mx(rk_device *d, int32_t kind, int64_t rows, int64_t cols, 
     m->rows = rows;
     m->cols = cols;
     int rc;
-    if ((rc = dev_alloc(d, (void **)&m->w, (size_t)wbytes, "matrix")) ||
+    if ((rc = dev_alloc(d, (void **)&m->w, (size_t)wtot, "matrix")) ||
         (rc = dev_alloc(d, (void **)&m->e8m0, (size_t)sbytes, "matrix scales"))) {
         (void)hipFree(m->w);
         delete m;
         return rc;
     }
-    hipError_t e = hipMemcpyAsync(m->w, w, (size_t)wbytes, hipMemcpyHostToDevice, d->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(m->e8m0, e8m0, (size_t)sbytes, hipMemcpyHostToDevice, d->stream);
+    // the codes piece by piece into place: never gathered on the host
+    hipError_t e = hipSuccess;
+    int64_t at = 0;
+    for (int32_t c = 0; c < n_w && e == hipSuccess; c++) {
+        if (w_len[c]) e = hipMemcpyAsync(m->w + at, w[c], (size_t)w_len[c], hipMemcpyHostToDevice, d->stream);
+        at += w_len[c];
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(m->e8m0, sdev, (size_t)sbytes, hipMemcpyHostToDevice, d->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(d->stream);
     if (e != hipSuccess) {
+        (void)hipGetLastError();
         (void)hipFree(m->w);
         (void)hipFree(m->e8m0);
         delete m;
         return hip_fail(d, e, "matrix upload");
     }
-    m->bytes = wbytes + sbytes;
+    m->bytes = wtot + sbytes;
     add_used(d, m->bytes);
     *out = m;
     return RK_OK;
+}
+
+int rk_matrix_upload_mx(rk_device *d, int32_t kind, int64_t rows, int64_t cols, const uint8_t *w,
+                        const uint8_t *e8m0, rk_matrix **out) {
+    if (!d || !out || !w || !e8m0) return fail(d, RK_ERR_ARGS, "rk_matrix_upload_mx: null argument");
+    if (rows <= 0 || cols <= 0 || cols > kMaxCols || rows > (int64_t)1 << 24) {
+        *out = nullptr;
+        return fail(d, RK_ERR_ARGS, "gpu: matrix %lld×%lld out of range", (long long)rows, (long long)cols);
+    }
+    const int64_t wlen = kind == RK_FP8 ? rows * cols : rows * (cols / 2);
+    const int64_t slen = kind == RK_FP8 ? (rows + 31) / 32 * (cols / 32) : rows * (cols / 32);
+    return rk_matrix_upload_mx_chunks(d, kind, rows, cols, 1, &w, &wlen, 1, &e8m0, &slen, 0, out);
 }
 
 int rk_matrix_set_raw(rk_matrix *m, int32_t raw) {

@@ -45,6 +45,7 @@ SIGNATURES = {
     "rk_matrix_free": (ctypes.c_int, [P]),
     "rk_matrix_upload_mx": (ctypes.c_int, [P, I32, I64, I64, P, P, P]),
     "rk_matrix_set_raw": (ctypes.c_int, [P, I32]),
+    "rk_matrix_upload_mx_chunks": (ctypes.c_int, [P, I32, I64, I64, I32, P, P, I32, P, P, I32, P]),
     "rk_batch_quantize_fp8": (ctypes.c_int, [P, I64, I64]),
     "rk_batch_expert_matvecs": (ctypes.c_int, [P, P, I64, I64, I32, I64, I64, I32, I64, I64]),
     "rk_batch_matvecs_batch": (ctypes.c_int, [P, P, I64, I64, I64, I64, I32]),
@@ -389,6 +390,20 @@ class Device:
         e8m0 = np.ascontiguousarray(e8m0, dtype=np.uint8)
         h = P()
         self._check(lib().rk_matrix_upload_mx(self.h, kind, rows, cols, _ptr(w), _ptr(e8m0), ctypes.byref(h)))
+        return Matrix(self, h, kind, rows, cols)
+
+    def upload_mx_chunks(self, kind, rows, cols, w_chunks, s_chunks, align_rows=0):
+        """Format{FP4Chunks, E8M0Chunks, AlignRows}: the codes and the scale
+        bytes each given as a list of pieces read as one."""
+        ws = [np.ascontiguousarray(c, dtype=np.uint8) for c in w_chunks]
+        ss = [np.ascontiguousarray(c, dtype=np.uint8) for c in s_chunks]
+        wp = (P * len(ws))(*[c.ctypes.data for c in ws])
+        wl = (I64 * len(ws))(*[c.size for c in ws])
+        sp = (P * len(ss))(*[c.ctypes.data for c in ss])
+        sl = (I64 * len(ss))(*[c.size for c in ss])
+        h = P()
+        self._check(lib().rk_matrix_upload_mx_chunks(self.h, kind, rows, cols, len(ws), wp, wl, len(ss), sp, sl,
+                                                     align_rows, ctypes.byref(h)))
         return Matrix(self, h, kind, rows, cols)
 
     def upload_q8(self, q, s, rows, cols):

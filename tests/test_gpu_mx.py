@@ -515,3 +515,57 @@ def same_values(got, want, what):
     nan = np.isnan(w)
     assert np.array_equal(np.isnan(g), nan), f"{what}: NaN positions differ"
     same_bits(g[~nan], w[~nan], what)
+
+
+def test_chunked_stacked_experts(dev):
+    """device.go:575-581, 609-618, 704-723: stacked experts given as pieces
+    (Format{FP4Chunks, E8M0Chunks, AlignRows}, as dsv41/gpu.go:177-184 makes
+    them, one piece an expert) equal the matrix uploaded whole, bit for bit,
+    and the oracle; pieces cut anywhere (not at rows) read as one; E4M3
+    scales in pieces too."""
+    rng = np.random.default_rng(44)
+    experts, erows, cols = 6, 96, 512
+    rows = experts * erows
+    x = mx_input(rng, cols)
+    ws = [rng.integers(0, 256, erows * cols // 2).astype(np.uint8) for _ in range(experts)]
+    ss = [random_scales(rng, erows * cols // 32) for _ in range(experts)]
+    w, s = np.concatenate(ws), np.concatenate(ss)
+    whole = dev.upload_mx(rkhip.FP4, rows, cols, w, s)
+    per_expert = dev.upload_mx_chunks(rkhip.FP4, rows, cols, ws, ss, align_rows=erows)
+    cut = [0, 1, 1000, 1001, 77777, w.size]
+    odd = dev.upload_mx_chunks(rkhip.FP4, rows, cols, [w[a:b] for a, b in zip(cut, cut[1:])],
+                               [s[:5], s[5:5], s[5:]])
+    try:
+        want = oracle.matvec_fp4(w, s, x, rows, cols, bf16=True)
+        for m in (whole, per_expert, odd):
+            same_bits(dev.matvec(m, x), want, "chunked FP4")
+        fw, fs = random_fp8(rng, 64, 256)
+        m8 = dev.upload_mx_chunks(rkhip.FP8, 64, 256, [fw[:3000], fw[3000:]], [fs[:7], fs[7:]], align_rows=32)
+        try:
+            same_bits(dev.matvec(m8, x[:256]), oracle.matvec_fp8(fw, fs, x[:256], 64, 256, bf16=True), "chunked FP8")
+        finally:
+            m8.free()
+    finally:
+        for m in (whole, per_expert, odd):
+            m.free()
+    assert dev.used == 0
+
+
+def test_chunked_upload_errors(dev):
+    """The reference's checks on pieces (device.go:604-618): the pieces'
+    total against the shape, the scales' count, NaN codes in any piece, and
+    AlignRows (whole runs; E4M3 runs of a multiple of 32 rows)."""
+    z = lambda n: np.zeros(n, np.uint8)  # noqa: E731
+    with pytest.raises(rkhip.RKError, match="out of range"):
+        dev.upload_mx_chunks(rkhip.FP4, 4, 64, [z(64), z(63)], [z(8)])
+    with pytest.raises(rkhip.RKError, match="wrong shape"):
+        dev.upload_mx_chunks(rkhip.FP4, 4, 64, [z(64), z(64)], [z(7)])
+    with pytest.raises(rkhip.RKError, match="NaN in E4M3 weights"):
+        dev.upload_mx_chunks(rkhip.FP8, 2, 32, [z(40), np.full(24, 0xFF, np.uint8)], [np.array([127], np.uint8)])
+    with pytest.raises(rkhip.RKError, match="aligned runs"):
+        dev.upload_mx_chunks(rkhip.FP4, 6, 64, [z(192)], [z(12)], align_rows=4)
+    with pytest.raises(rkhip.RKError, match="aligned runs"):
+        dev.upload_mx_chunks(rkhip.FP8, 64, 32, [z(2048)], [z(2)], align_rows=16)
+    m = dev.upload_mx_chunks(rkhip.FP4, 6, 64, [z(192)], [z(12)], align_rows=3)
+    m.free()
+    assert dev.used == 0
