@@ -86,6 +86,10 @@ __device__ __forceinline__ float lds_sum_fixed(const float *p, float acc) {
 // and the cache policy of a streamed weight load (non-temporal).
 constexpr int kRsrcWord3 = 0x00020000;
 constexpr int kAuxStream = 2;
+// The cache policy of an agent-scope load (sc1: the level where every XCD
+// sees the same data), as the compiler gives a relaxed agent-scope atomic
+// load.
+constexpr int kAuxCoherent = 16;
 
 // The LDS address space form of a pointer into the kernel's LDS (the
 // destination operand of a direct-to-LDS load).

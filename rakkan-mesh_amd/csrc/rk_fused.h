@@ -40,6 +40,21 @@ constexpr int kMaxLdsCols = 16384;
 // that one recorded token replays unchanged at every position.
 enum : int { kCtlPos = 0, kCtlPrompt = 1, kCtlWords = 4 };
 
+// 64-bit words of a hand-off between the workgroups of one launch
+// (launch_att_values_wo): producers done, waiting workgroups started, a
+// waiter gave up, then one flag word per XCD, 128 bytes apart. Zero when
+// allocated; never reset.
+enum : int {
+    kSyncDone = 0,
+    kSyncArrive = 1,
+    kSyncError = 2,
+    kSyncFlag = 16,
+    kSyncFlagStride = 16,
+    kSyncWords = kSyncFlag + 8 * kSyncFlagStride
+};
+// Longest wait of a waiting workgroup: 20 ms of the 100 MHz real-time clock.
+constexpr unsigned long long kSyncTimeout = 2000000ull;
+
 // The classifier's greedy argmax is folded into kArgmaxSlots 64-bit keys
 // (atomicMax, spread over slots so the workgroups do not queue on one
 // address); the key of logit v at row i orders by value, then by lower row.
@@ -148,6 +163,18 @@ void launch_att_values_group(const float *att, int32_t att_stride, const float *
 void launch_att_values(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                        const AttBatch &bt, int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx,
                        float *xs, int32_t *xsum, hipStream_t s, int cu = 0);
+// The values of a decode step (position in ctl) and the Wo product that
+// reads their Q8_0 form, x[r] += Wo_r·attn, in one launch: the values
+// workgroups as launch_att_values (contexts past 256 and up to 1024), then
+// workgroups of 32 Wo rows whose codes are requested at the launch's start
+// and wait for the last values workgroup through `sync` (kSyncWords words).
+// The results are those of the two launches, bit for bit. False (nothing
+// launched) when the shapes are not the ones it takes: a Q8_0 Wo of
+// 3073..4096 columns (heads·hs), rows a multiple of 32.
+bool launch_att_values_wo(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
+                          int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
+                          const uint8_t *wo_w, const float *wo_ws, int64_t wo_rows, int64_t wo_cols, float *x,
+                          unsigned long long *sync, hipStream_t s);
 // QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches, at
 // the position in ctl (or, ctl null, for `tokens` rows at pos0, pos0+1, ...;
 // or, seq_pos set, row z at seq_pos[z] in caches cache_stride floats apart).

@@ -1017,18 +1017,83 @@ __device__ __forceinline__ float swz_chain_sum(const float *row, int n, int key,
     return acc;
 }
 
-__global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float *att, int32_t att_stride,
-                                                                    const float *vals, float *out, const int32_t *ctl,
-                                                                    AttBatch bt, int kv_mul, int hs, int kv_dim,
-                                                                    int nsl, int ctx_pad, int8_t *qx, float *xs,
-                                                                    int32_t *xsum) {
+// A hand-off inside one launch, from the workgroups that produce an input
+// to those that wait for all of it (att_values_wo_kernel), through the
+// words of `sync` (kSync*; zero when the owner is made, never reset).
+// Launches of one stream run one after another, so a count that every
+// producer (na of them) or every waiting workgroup (nw) of a launch adds
+// one to tells the launch's number:
+//  * a producer stores its part with agent-scope stores (to the level where
+//    every XCD's loads of that scope look), waits until they are complete,
+//    then adds one to kSyncDone; the producer whose add completes a
+//    launch's count writes the launch's number into the flag words, one
+//    128-byte line per XCD, so that the waiting workgroups of each XCD poll
+//    their own line (measured: a hand-off in about 0.5 us where polls of
+//    one shared word took about 6);
+//  * a waiting workgroup adds one to kSyncArrive: the count before its add,
+//    over nw, plus one is this launch's number. It polls its flag
+//    (agent-scope loads) until the flag holds that number, then reads the
+//    part with agent-scope loads.
+// No fence is needed: the wait for the stores' completion orders them
+// before the count. The poll is bounded by the device's real-time clock
+// (kSyncTimeout); a workgroup that gives up sets kSyncError, which the
+// stage reads after the step.
+__device__ __forceinline__ void sync_signal_done(unsigned long long *sync, int na) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
+    if ((threadIdx.x & 63) == 0) {
+        const unsigned long long old =
+            __hip_atomic_fetch_add(sync + kSyncDone, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((old + 1) % (unsigned long long)na == 0) {
+            const unsigned long long n = (old + 1) / (unsigned long long)na;
+#pragma unroll
+            for (int xcd = 0; xcd < 8; xcd++)
+                __hip_atomic_store(sync + kSyncFlag + kSyncFlagStride * xcd, n, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// The waiting side, by the whole workgroup: thread 0 registers and polls,
+// then every wave passes a barrier (without a fence, so loads in flight are
+// not waited for).
+__device__ __forceinline__ void sync_wait_ready(unsigned long long *sync, int nw) {
+    if (threadIdx.x == 0) {
+        const unsigned long long want =
+            __hip_atomic_fetch_add(sync + kSyncArrive, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) /
+                (unsigned long long)nw +
+            1;
+        const unsigned long long *f = sync + kSyncFlag + kSyncFlagStride * (blockIdx.x & 7);
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        bool ok = false;
+        for (int i = 0; i < (1 << 24); i++) {
+            const unsigned long long v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((long long)(v - want) >= 0) {
+                ok = true;
+                break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (!ok) __hip_atomic_store(sync + kSyncError, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_barrier" ::: "memory");
+}
+
+// The body of att_values_reg_kernel for workgroup bx of token z. SIG: the
+// values launch that also runs the Wo product (att_values_wo_kernel): the
+// slice's Q8_0 block is stored through to the device's coherence point and
+// the workgroup then counts itself done in `sync` (sync_signal_done).
+template <bool SIG>
+__device__ __forceinline__ void att_values_reg_body(const float *att, int32_t att_stride, const float *vals,
+                                                    float *out, const int32_t *ctl, const AttBatch &bt, int kv_mul,
+                                                    int hs, int kv_dim, int nsl, int ctx_pad, int8_t *qx, float *xs,
+                                                    int32_t *xsum, int bx, int z, unsigned long long *sync, int na) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float s_red[4];
     __shared__ float s_inv;
     __shared__ __align__(16) float s_res[kValSlice];
     float *sa = smem;               // [ctx_pad] scores -> e_t
     float *tiles = smem + ctx_pad;  // [2][32][kVrChunk] products, swizzled rows
-    const int z = blockIdx.y;       // token of a batch (0 when the position comes from ctl)
     const int T = att_position(ctl, bt, z) + 1;
     const int nch = (T + kVrChunk - 1) / kVrChunk;
     att += (int64_t)z * bt.att_stride;
@@ -1039,7 +1104,7 @@ __global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float 
         xs += (int64_t)z * (bt.out_stride >> 5);
         xsum += (int64_t)z * (bt.out_stride >> 5);
     }
-    const int h = blockIdx.x / nsl, e0 = (blockIdx.x % nsl) * kValSlice;
+    const int h = bx / nsl, e0 = (bx % nsl) * kValSlice;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // waves 4-7: float4 column fq (elements 4fq..4fq+3) and position quads
     // pq, pq + 32 of each chunk
@@ -1134,7 +1199,19 @@ __global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float 
         int cs;
         const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
         const int64_t base = (int64_t)h * hs + e0;
-        if (lane < 8) {
+        if (SIG) {
+            // agent-scope stores (written through to where every XCD's
+            // loads of that scope look), complete before the count
+            if (lane < 8) {
+                __hip_atomic_store(reinterpret_cast<uint32_t *>(qx + base) + lane, pk, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) {
+                    __hip_atomic_store(xs + (base >> 5), d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    xsum[base >> 5] = cs;
+                }
+            }
+            sync_signal_done(sync, na);
+        } else if (lane < 8) {
             reinterpret_cast<uint32_t *>(qx + base)[lane] = pk;
             if (lane == 0) {
                 xs[base >> 5] = d;
@@ -1142,6 +1219,15 @@ __global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float 
             }
         }
     }
+}
+
+__global__ __launch_bounds__(kVrThreads) void att_values_reg_kernel(const float *att, int32_t att_stride,
+                                                                    const float *vals, float *out, const int32_t *ctl,
+                                                                    AttBatch bt, int kv_mul, int hs, int kv_dim,
+                                                                    int nsl, int ctx_pad, int8_t *qx, float *xs,
+                                                                    int32_t *xsum) {
+    att_values_reg_body<false>(att, att_stride, vals, out, ctl, bt, kv_mul, hs, kv_dim, nsl, ctx_pad, qx, xs, xsum,
+                               blockIdx.x, blockIdx.y, nullptr, 0);
 }
 
 static size_t att_values_reg_lds(int ctx) { return (size_t)(((ctx + 3) & ~3) + 2 * kValSlice * kVrChunk) * 4; }
@@ -1202,6 +1288,179 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
     else
         RK_LAUNCH((att_values_kernel<false, kValChunk>), grid, dim3(kValThreads), att_values_lds(ctx, kValChunk), s, att,
                   att_stride, vals, out, ctl, bt, heads / kv_heads, hs, kv_dim, ctx_pad, qx, xs, xsum);
+}
+
+// ---------------------------------------------------------------------------
+// The values and the Wo product in one launch.
+
+struct AttWoArgs {
+    const float *att, *vals;
+    float *out;
+    const int32_t *ctl;
+    int32_t att_stride;
+    int kv_mul, hs, kv_dim, nsl, ctx_pad;
+    int8_t *qx;
+    float *xs;
+    int32_t *xsum;
+    const uint8_t *w;  // Wo codes [rows][cols], scales [rows][cols/32]
+    const float *ws;
+    float *x;  // the residual: x[r] += the product's row r
+    int rows, cols;
+    unsigned long long *sync;
+    int na, nw;  // values workgroups (producers), Wo workgroups
+};
+
+// The values kernel holds about 200 VGPRs a lane (its value stripes), so a
+// CU takes one workgroup of this launch: 32 Wo rows a workgroup leave
+// 4096 / 32 = 128 of them beside the 128 values workgroups of a 32-head
+// model, one launch round on 256 CUs.
+constexpr int kWoRowsPerWave = 4;
+constexpr int kWoRows = (kVrThreads / 64) * kWoRowsPerWave;  // rows of a Wo workgroup
+
+// Floats of one row's term buffer: [running sum L][block / 8], the row's
+// C·32 blocks over 8 sums rounded up to 4 and padded by 4 (the writing
+// lanes of a chunk in distinct banks).
+constexpr int wo_k8p(int c) { return ((c * 32 / 8 + 3) & ~3) + 4; }
+
+// Workgroup wi of the Wo product (C chunks of 1 KiB a row, K rows a wave):
+// each wave requests all of its rows' codes and scales at once, then the
+// workgroup waits for the values' Q8_0 output, reads it (agent-scope loads)
+// and forms each row as MatVecQ8 does (internal/num/quant.go:158-180): the
+// block terms float32(sum_b)·float32(ws_b·xs_b) into LDS by running sum
+// b mod 8, eight lanes a row adding their sum's terms in block order, the
+// sums combined ((0+1)+(2+3))+((4+5)+(6+7)) (DPP; addition commutes), then
+// the residual add x[r] = x[r] + row (model.go:596, not canonicalised).
+template <int C, int K>
+__device__ __forceinline__ void wo_after_values(const AttWoArgs &a, int wi) {
+    extern __shared__ __align__(16) float smem[];
+    constexpr int NS = K * C;
+    constexpr int k8p = wo_k8p(C), rs = 8 * k8p;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cols = a.cols, nb = cols >> 5, rows = a.rows;
+    const int R0 = wi * kWoRows + wave * K;  // the wave's first row
+    float *tbw = smem + wave * K * rs;
+    const int g = lane >> 3, L = lane & 7, gk = g < K ? g : K - 1;
+    const float ep0 = a.x[min(R0 + gk, rows - 1)];
+    __amdgpu_buffer_rsrc_t rw[K], rsc[K];
+#pragma unroll
+    for (int h = 0; h < K; h++) {
+        const int64_t r = min(R0 + h, rows - 1);
+        rw[h] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w + r * cols), 0, cols, kRsrcWord3);
+        rsc[h] = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.ws + r * nb), 0, nb * 4, kRsrcWord3);
+    }
+    // lane offsets: 16 code bytes and their block's scale; the last chunk's
+    // clamped into the row (lanes past it re-read its last piece, whose
+    // blocks are never summed)
+    const int wo = lane * 16, so = (lane >> 1) * 4;
+    const int wl = min((C - 1) * 1024 + wo, cols - 16), sl = min((C - 1) * 128 + so, nb * 4 - 4);
+    int4 wb[NS];
+    float sb[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int h = s / C, c = s % C;
+        const bool last = c == C - 1;
+        const rk_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rw[h], last ? wl : wo, last ? 0 : c * 1024, kAuxStream);
+        wb[s] = make_int4(v.x, v.y, v.z, v.w);
+        sb[s] = __builtin_bit_cast(float,
+                                   __builtin_amdgcn_raw_buffer_load_b32(rsc[h], last ? sl : so, last ? 0 : c * 128, 0));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    sync_wait_ready(a.sync, a.nw);
+
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(a.qx, 0, cols, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(a.xs, 0, nb * 4, kRsrcWord3);
+    int4 xq[C];
+    float xsr[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int o = c == C - 1 ? wl : c * 1024 + wo;
+        const rk_v4i v = __builtin_amdgcn_raw_buffer_load_b128(rq, o, 0, kAuxCoherent);
+        xq[c] = make_int4(v.x, v.y, v.z, v.w);
+        xsr[c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, (o >> 5) * 4, 0, kAuxCoherent));
+    }
+#pragma unroll
+    for (int s = 0; s < NS; s++) {
+        const int h = s / C, c = s % C;
+        const int sm = pair_sum(dot16(wb[s], xq[c], 0));
+        const float t = (float)sm * (sb[s] * xsr[c]);
+        const int b = c * 32 + (lane >> 1);
+        if ((lane & 1) == 0 && (c < C - 1 || b < nb)) tbw[h * rs + (b & 7) * k8p + (b >> 3)] = t;
+    }
+    float sum = 0.0f;
+    {
+        const float *p = tbw + gk * rs + L * k8p;
+        const int cnt = L < nb ? (nb - L + 7) >> 3 : 0;
+        int k = 0;
+        for (; k + 4 <= cnt; k += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(p + k);
+            sum += v.x;
+            sum += v.y;
+            sum += v.z;
+            sum += v.w;
+        }
+        for (; k < cnt; k++) sum += p[k];
+    }
+    sum = sum + dppf_x1(sum);
+    sum = sum + dppf_x2(sum);
+    sum = sum + __int_as_float(dpp_mirror8(__float_as_int(sum)));
+    const int l = R0 + g;
+    if (g < K && l < rows && L == 0) a.x[l] = ep0 + sum;
+}
+
+// Workgroups 0 .. na-1: the values (att_values_reg_kernel's work, the
+// producers); na .. na+nw-1: the Wo rows (waiting). The values workgroups
+// come first in the grid, so they are dispatched first: a waiting
+// workgroup never holds a place a producer still needs.
+template <int C>
+__global__ __launch_bounds__(kVrThreads) void att_values_wo_kernel(AttWoArgs a) {
+    if ((int)blockIdx.x < a.na) {
+        att_values_reg_body<true>(a.att, a.att_stride, a.vals, a.out, a.ctl, AttBatch{}, a.kv_mul, a.hs, a.kv_dim,
+                                  a.nsl, a.ctx_pad, a.qx, a.xs, a.xsum, blockIdx.x, 0, a.sync, a.na);
+        return;
+    }
+    wo_after_values<C, kWoRowsPerWave>(a, blockIdx.x - a.na);
+}
+
+bool launch_att_values_wo(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
+                          int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
+                          const uint8_t *wo_w, const float *wo_ws, int64_t wo_rows, int64_t wo_cols, float *x,
+                          unsigned long long *sync, hipStream_t s) {
+    if (!ctl || !qx || !sync || ctx <= kValShortCtx || ctx > kVrMaxCtx || hs % 32 != 0 || kv_dim % 4 != 0 ||
+        (reinterpret_cast<uintptr_t>(vals) & 15) != 0)
+        return false;
+    if (wo_cols != (int64_t)heads * hs || wo_cols <= 3072 || wo_cols > 4096 || wo_rows <= 0 || wo_rows % kWoRows)
+        return false;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute((const void *)att_values_wo_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)att_values_reg_lds(kVrMaxCtx));
+    });
+    AttWoArgs a{};
+    a.att = att;
+    a.vals = vals;
+    a.out = out;
+    a.ctl = ctl;
+    a.att_stride = att_stride;
+    a.kv_mul = heads / kv_heads;
+    a.hs = hs;
+    a.kv_dim = kv_dim;
+    a.nsl = hs / kValSlice;
+    a.ctx_pad = (ctx + 3) & ~3;
+    a.qx = qx;
+    a.xs = xs;
+    a.xsum = xsum;
+    a.w = wo_w;
+    a.ws = wo_ws;
+    a.x = x;
+    a.rows = (int)wo_rows;
+    a.cols = (int)wo_cols;
+    a.sync = sync;
+    a.na = heads * a.nsl;
+    a.nw = (int)(wo_rows / kWoRows);
+    const size_t lds = std::max(att_values_reg_lds(ctx), (size_t)kWoRows * 8 * wo_k8p(4) * 4);
+    RK_LAUNCH(att_values_wo_kernel<4>, dim3((unsigned)(a.na + a.nw)), dim3(kVrThreads), lds, s, a);
+    return true;
 }
 
 // QK-norm (internal/llm/model.go:551-558) and RoPE (:563-572) of one head

@@ -95,6 +95,8 @@ struct rk_stage {
     int moe_cap = 0;
     // the groupings' counters (MoeScratch::stat): experts selected, groupings
     unsigned long long *moe_stat = nullptr;
+    // the hand-off words of the values-and-Wo launch (kSyncWords)
+    unsigned long long *sync = nullptr;
 };
 
 namespace rk {
@@ -167,9 +169,12 @@ struct QkNorm {
     const float *k, *v, *q_norm, *k_norm;
 };
 
-static void enqueue_attention(rk_stage *s, hipStream_t st, const float *q, float *keys, float *vals, float *att,
+// wo (a decode step, qo given): the attention output's Wo product added
+// into the residual x in the values launch when launch_att_values_wo takes
+// the shapes; the return says whether it did.
+static bool enqueue_attention(rk_stage *s, hipStream_t st, const float *q, float *keys, float *vals, float *att,
                               float *out, const int32_t *ctl, const AttBatch &bt, const QScratch *qo,
-                              const QkNorm *qk = nullptr) {
+                              const QkNorm *qk = nullptr, const rk_matrix *wo = nullptr, float *x = nullptr) {
     rk_device *d = s->d;
     const rk_stage_config &c = s->c;
     int8_t *qx = qo ? qo->qx : nullptr;
@@ -196,9 +201,16 @@ static void enqueue_attention(rk_stage *s, hipStream_t st, const float *q, float
         ProfScope p(d, st, "att_scores");
         launch_att_scores(q, keys, att, c.ctx, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, c.inv_sqrt, st);
     }
+    if (wo && wo->kind == RK_Q8 && ctl && qo) {
+        ProfScope p(d, st, "att_values_wo");
+        if (launch_att_values_wo(att, c.ctx, vals, out, ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, qx, xs, xsum,
+                                 wo->w, wo->scales, wo->rows, wo->cols, x, s->sync, st))
+            return true;
+    }
     ProfScope p(d, st, "att_values");
     launch_att_values(att, c.ctx, vals, out, ctl, bt, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, qx, xs, xsum, st,
                       d->cu);
+    return false;
 }
 
 // The launches of one layer (Stage.Forward's body, model.go:530-611). The
@@ -256,10 +268,11 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
     // heads (head size a multiple of 32).
     const bool att_q = s->hs % 32 == 0;
     const QkNorm qk{s->k, s->v, D.q_norm, D.k_norm};
-    enqueue_attention(s, st, s->q, D.keys, D.vals, s->att, s->att_out, s->ctl, AttBatch{}, att_q ? &s->qa : nullptr,
-                      c.qk_norm ? &qk : nullptr);
+    const bool wo_done = enqueue_attention(s, st, s->q, D.keys, D.vals, s->att, s->att_out, s->ctl, AttBatch{},
+                                           att_q ? &s->qa : nullptr, c.qk_norm ? &qk : nullptr, L.wo, s->x);
     float *xo[1] = {s->x};
-    if ((rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, nullptr, &L.wo, 1, xo, kEpAdd, base)))
+    if (!wo_done &&
+        (rc = stage_product(s, st, "wo", att_q ? &s->qa : nullptr, s->att_out, nullptr, &L.wo, 1, xo, kEpAdd, base)))
         return rc;
     if (L.moe) {
         // a mixture of experts: its input RMSNorm_ffn(x) quantized into qb;
@@ -378,6 +391,16 @@ static int record(rk_stage *s, Rec which) {
         return hip_fail(d, e, "stage graph");
     }
     g = gr;
+    return RK_OK;
+}
+
+// After the stream is idle: whether a values-and-Wo launch gave up waiting
+// for its values (kSyncError; its Wo rows are then not the product).
+static int sync_check(rk_stage *s, const char *what) {
+    rk_device *d = s->d;
+    unsigned long long err = 0;
+    HIP_TRY(d, hipMemcpy(&err, s->sync + kSyncError, sizeof err, hipMemcpyDeviceToHost), what);
+    if (err) return fail(d, RK_ERR_HIP, "%s: a values-and-Wo launch timed out waiting for its values", what);
     return RK_OK;
 }
 
@@ -768,6 +791,7 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
     take((void **)&s->smp_temp, 4 * seqs);
     take((void **)&s->smp_state, 8 * seqs);
     take((void **)&s->smp_part, 4 * seqs * sample_parts());
+    take((void **)&s->sync, 8 * kSyncWords);
     // the MoE layers' shared scratch, for the largest batch the stage runs
     if (any_moe) {
         s->moe_cap = batch_cap(*c, seqs);
@@ -892,7 +916,7 @@ int rk_stage_forward(rk_stage *s, float *xs, int32_t pos, int32_t tokens) {
         HIP_TRY(d, hipStreamSynchronize(st), "stage submit");
         memcpy(xs + (int64_t)start * dim, s->h_x, (size_t)n * dim * 4);
     }
-    return RK_OK;
+    return tokens > 0 ? sync_check(s, "stage submit") : RK_OK;
 }
 
 int64_t rk_stage_bytes(const rk_stage *s) { return s ? s->bytes : -1; }
@@ -1047,7 +1071,7 @@ int rk_stage_generate_run(rk_stage *s, int32_t positions, float *logits) {
         }
     }
     HIP_TRY(d, hipStreamSynchronize(d->stream), "generate run");
-    return RK_OK;
+    return sync_check(s, "generate run");
 }
 
 int rk_stage_generate_tokens(rk_stage *s, int32_t from, int32_t n, int32_t *out) {
