@@ -165,12 +165,13 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
                        float *xs, int32_t *xsum, hipStream_t s, int cu = 0);
 // The values of a decode step (position in ctl) and the Wo product that
 // reads their Q8_0 form, x[r] += Wo_r·attn, in one launch: the values
-// workgroups as launch_att_values (contexts past 256 and up to 1024), then
-// workgroups of 32 Wo rows whose codes are requested at the launch's start
-// and wait for the last values workgroup through `sync` (kSyncWords words).
-// The results are those of the two launches, bit for bit. False (nothing
-// launched) when the shapes are not the ones it takes: a Q8_0 Wo of
-// 3073..4096 columns (heads·hs), rows a multiple of 32.
+// workgroups as launch_att_values (contexts up to 1024), then workgroups of
+// Wo rows (16 for contexts up to 256, else 32) whose codes are requested at
+// the launch's start and wait for the last values workgroup through `sync`
+// (kSyncWords words). The results are those of the two launches, bit for
+// bit. False (nothing launched) when the shapes are not the ones it takes:
+// a Q8_0 Wo of 3073..4096 columns (heads·hs, hs a multiple of 32), rows a
+// multiple of the workgroup's.
 bool launch_att_values_wo(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                           int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
                           const uint8_t *wo_w, const float *wo_ws, int64_t wo_rows, int64_t wo_cols, float *x,

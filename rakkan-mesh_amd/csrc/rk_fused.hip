@@ -798,6 +798,68 @@ bool launch_att_scores_qkn(const float *q_raw, const float *k_raw, const float *
 // product. The LDS can exceed 64 KiB (gfx950 gives a workgroup 160 KiB).
 // CH positions a chunk: 256, or 128 for contexts of up to 256 positions
 // (half the LDS: four workgroups a CU, for many short sequences at once).
+// A hand-off inside one launch, from the workgroups that produce an input
+// to those that wait for all of it (att_values_wo_kernel), through the
+// words of `sync` (kSync*; zero when the owner is made, never reset).
+// Launches of one stream run one after another, so a count that every
+// producer (na of them) or every waiting workgroup (nw) of a launch adds
+// one to tells the launch's number:
+//  * a producer stores its part with agent-scope stores (to the level where
+//    every XCD's loads of that scope look), waits until they are complete,
+//    then adds one to kSyncDone; the producer whose add completes a
+//    launch's count writes the launch's number into the flag words, one
+//    128-byte line per XCD, so that the waiting workgroups of each XCD poll
+//    their own line (measured: a hand-off in about 0.5 us where polls of
+//    one shared word took about 6);
+//  * a waiting workgroup adds one to kSyncArrive: the count before its add,
+//    over nw, plus one is this launch's number. It polls its flag
+//    (agent-scope loads) until the flag holds that number, then reads the
+//    part with agent-scope loads.
+// No fence is needed: the wait for the stores' completion orders them
+// before the count. The poll is bounded by the device's real-time clock
+// (kSyncTimeout); a workgroup that gives up sets kSyncError, which the
+// stage reads after the step.
+__device__ __forceinline__ void sync_signal_done(unsigned long long *sync, int na) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
+    if ((threadIdx.x & 63) == 0) {
+        const unsigned long long old =
+            __hip_atomic_fetch_add(sync + kSyncDone, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((old + 1) % (unsigned long long)na == 0) {
+            const unsigned long long n = (old + 1) / (unsigned long long)na;
+#pragma unroll
+            for (int xcd = 0; xcd < 8; xcd++)
+                __hip_atomic_store(sync + kSyncFlag + kSyncFlagStride * xcd, n, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// The waiting side, by the whole workgroup: thread 0 registers and polls,
+// then every wave passes a barrier (without a fence, so loads in flight are
+// not waited for).
+__device__ __forceinline__ void sync_wait_ready(unsigned long long *sync, int nw) {
+    if (threadIdx.x == 0) {
+        const unsigned long long want =
+            __hip_atomic_fetch_add(sync + kSyncArrive, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) /
+                (unsigned long long)nw +
+            1;
+        const unsigned long long *f = sync + kSyncFlag + kSyncFlagStride * (blockIdx.x & 7);
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        bool ok = false;
+        for (int i = 0; i < (1 << 24); i++) {
+            const unsigned long long v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((long long)(v - want) >= 0) {
+                ok = true;
+                break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        if (!ok) __hip_atomic_store(sync + kSyncError, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_barrier" ::: "memory");
+}
+
 constexpr int kValSlice = 32;
 constexpr int kValThreads = 256;
 constexpr int kValChunk = 256;
@@ -812,11 +874,14 @@ constexpr int kValQuads = kValThreads / (kValSlice / 4);             // position
 // VEC: head size and value-row stride are multiples of 4, so a thread's four
 // elements are one 16-byte load (a separate instance: a run-time choice would
 // be if-converted into four 4-byte loads for every shape).
-template <bool VEC, int CH>
-__global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *att, int32_t att_stride,
-                                                                 const float *vals, float *out, const int32_t *ctl,
-                                                                 AttBatch bt, int kv_mul, int hs, int kv_dim,
-                                                                 int ctx_pad, int8_t *qx, float *xs, int32_t *xsum) {
+//
+// The body for head bh, slice by and token z; SIG as att_values_reg_body's
+// (the Q8_0 block handed to the Wo workgroups of att_values_wo_kernel).
+template <bool VEC, int CH, bool SIG>
+__device__ __forceinline__ void att_values_body(const float *att, int32_t att_stride, const float *vals, float *out,
+                                                const int32_t *ctl, const AttBatch &bt, int kv_mul, int hs,
+                                                int kv_dim, int ctx_pad, int8_t *qx, float *xs, int32_t *xsum, int bh,
+                                                int by, int z, unsigned long long *sync, int na) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float s_red[kValThreads / 64];
     __shared__ float s_inv;
@@ -824,7 +889,6 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
     constexpr int kValPitch = val_pitch(CH), kValRounds = CH / (4 * kValQuads);
     static_assert(kValRounds >= 1, "a chunk is whole rounds");
     float *sp = smem + ctx_pad;  // [2][kValSlice][kValPitch] product tiles of two chunks
-    const int z = blockIdx.z;  // token of a batch (0 when the position comes from ctl)
     const int T = att_position(ctl, bt, z) + 1;
     att += (int64_t)z * bt.att_stride;
     out += (int64_t)z * bt.out_stride;
@@ -834,8 +898,8 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
         xs += (int64_t)z * (bt.out_stride >> 5);
         xsum += (int64_t)z * (bt.out_stride >> 5);
     }
-    const int h = blockIdx.x, g = h / kv_mul;
-    const int e0 = blockIdx.y * kValSlice;
+    const int h = bh, g = h / kv_mul;
+    const int e0 = by * kValSlice;
     const int ne = min(kValSlice, hs - e0);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *vbase = vals + (int64_t)g * hs + e0;
@@ -941,7 +1005,18 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
             int cs;
             const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
             const int64_t base = (int64_t)h * hs + e0;
-            if (lane < 8) {
+            if (SIG) {
+                // agent-scope stores, complete before the count
+                if (lane < 8) {
+                    __hip_atomic_store(reinterpret_cast<uint32_t *>(qx + base) + lane, pk, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0) {
+                        __hip_atomic_store(xs + (base >> 5), d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        xsum[base >> 5] = cs;
+                    }
+                }
+                sync_signal_done(sync, na);
+            } else if (lane < 8) {
                 reinterpret_cast<uint32_t *>(qx + base)[lane] = pk;
                 if (lane == 0) {
                     xs[base >> 5] = d;
@@ -950,6 +1025,15 @@ __global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *at
             }
         }
     }
+}
+
+template <bool VEC, int CH>
+__global__ __launch_bounds__(kValThreads) void att_values_kernel(const float *att, int32_t att_stride,
+                                                                 const float *vals, float *out, const int32_t *ctl,
+                                                                 AttBatch bt, int kv_mul, int hs, int kv_dim,
+                                                                 int ctx_pad, int8_t *qx, float *xs, int32_t *xsum) {
+    att_values_body<VEC, CH, false>(att, att_stride, vals, out, ctl, bt, kv_mul, hs, kv_dim, ctx_pad, qx, xs, xsum,
+                                    blockIdx.x, blockIdx.y, blockIdx.z, nullptr, 0);
 }
 
 // The same result for contexts up to kVrMaxCtx positions, with every
@@ -1015,68 +1099,6 @@ __device__ __forceinline__ float swz_chain_sum(const float *row, int n, int key,
         if (t + 3 < n) acc += v.w;
     }
     return acc;
-}
-
-// A hand-off inside one launch, from the workgroups that produce an input
-// to those that wait for all of it (att_values_wo_kernel), through the
-// words of `sync` (kSync*; zero when the owner is made, never reset).
-// Launches of one stream run one after another, so a count that every
-// producer (na of them) or every waiting workgroup (nw) of a launch adds
-// one to tells the launch's number:
-//  * a producer stores its part with agent-scope stores (to the level where
-//    every XCD's loads of that scope look), waits until they are complete,
-//    then adds one to kSyncDone; the producer whose add completes a
-//    launch's count writes the launch's number into the flag words, one
-//    128-byte line per XCD, so that the waiting workgroups of each XCD poll
-//    their own line (measured: a hand-off in about 0.5 us where polls of
-//    one shared word took about 6);
-//  * a waiting workgroup adds one to kSyncArrive: the count before its add,
-//    over nw, plus one is this launch's number. It polls its flag
-//    (agent-scope loads) until the flag holds that number, then reads the
-//    part with agent-scope loads.
-// No fence is needed: the wait for the stores' completion orders them
-// before the count. The poll is bounded by the device's real-time clock
-// (kSyncTimeout); a workgroup that gives up sets kSyncError, which the
-// stage reads after the step.
-__device__ __forceinline__ void sync_signal_done(unsigned long long *sync, int na) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
-    if ((threadIdx.x & 63) == 0) {
-        const unsigned long long old =
-            __hip_atomic_fetch_add(sync + kSyncDone, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((old + 1) % (unsigned long long)na == 0) {
-            const unsigned long long n = (old + 1) / (unsigned long long)na;
-#pragma unroll
-            for (int xcd = 0; xcd < 8; xcd++)
-                __hip_atomic_store(sync + kSyncFlag + kSyncFlagStride * xcd, n, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-}
-
-// The waiting side, by the whole workgroup: thread 0 registers and polls,
-// then every wave passes a barrier (without a fence, so loads in flight are
-// not waited for).
-__device__ __forceinline__ void sync_wait_ready(unsigned long long *sync, int nw) {
-    if (threadIdx.x == 0) {
-        const unsigned long long want =
-            __hip_atomic_fetch_add(sync + kSyncArrive, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) /
-                (unsigned long long)nw +
-            1;
-        const unsigned long long *f = sync + kSyncFlag + kSyncFlagStride * (blockIdx.x & 7);
-        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-        bool ok = false;
-        for (int i = 0; i < (1 << 24); i++) {
-            const unsigned long long v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if ((long long)(v - want) >= 0) {
-                ok = true;
-                break;
-            }
-            if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) break;
-            __builtin_amdgcn_s_sleep(2);
-        }
-        if (!ok) __hip_atomic_store(sync + kSyncError, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("s_barrier" ::: "memory");
 }
 
 // The body of att_values_reg_kernel for workgroup bx of token z. SIG: the
@@ -1310,12 +1332,12 @@ struct AttWoArgs {
     int na, nw;  // values workgroups (producers), Wo workgroups
 };
 
-// The values kernel holds about 200 VGPRs a lane (its value stripes), so a
-// CU takes one workgroup of this launch: 32 Wo rows a workgroup leave
-// 4096 / 32 = 128 of them beside the 128 values workgroups of a 32-head
-// model, one launch round on 256 CUs.
+// Wo rows a wave. With the register-held values (contexts past 256; about
+// 200 VGPRs a lane, so a CU takes one workgroup of the launch) a Wo
+// workgroup of 8 waves takes 32 rows: 4096 / 32 = 128 of them beside the
+// 128 values workgroups of a 32-head model, one launch round on 256 CUs.
+// With the short-context values (4 waves) it takes 16.
 constexpr int kWoRowsPerWave = 4;
-constexpr int kWoRows = (kVrThreads / 64) * kWoRowsPerWave;  // rows of a Wo workgroup
 
 // Floats of one row's term buffer: [running sum L][block / 8], the row's
 // C·32 blocks over 8 sums rounded up to 4 and padded by 4 (the writing
@@ -1330,14 +1352,14 @@ constexpr int wo_k8p(int c) { return ((c * 32 / 8 + 3) & ~3) + 4; }
 // b mod 8, eight lanes a row adding their sum's terms in block order, the
 // sums combined ((0+1)+(2+3))+((4+5)+(6+7)) (DPP; addition commutes), then
 // the residual add x[r] = x[r] + row (model.go:596, not canonicalised).
-template <int C, int K>
+template <int C, int K, int W>
 __device__ __forceinline__ void wo_after_values(const AttWoArgs &a, int wi) {
     extern __shared__ __align__(16) float smem[];
     constexpr int NS = K * C;
     constexpr int k8p = wo_k8p(C), rs = 8 * k8p;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cols = a.cols, nb = cols >> 5, rows = a.rows;
-    const int R0 = wi * kWoRows + wave * K;  // the wave's first row
+    const int R0 = wi * (W * K) + wave * K;  // the wave's first row
     float *tbw = smem + wave * K * rs;
     const int g = lane >> 3, L = lane & 7, gk = g < K ? g : K - 1;
     const float ep0 = a.x[min(R0 + gk, rows - 1)];
@@ -1408,33 +1430,42 @@ __device__ __forceinline__ void wo_after_values(const AttWoArgs &a, int wi) {
     if (g < K && l < rows && L == 0) a.x[l] = ep0 + sum;
 }
 
-// Workgroups 0 .. na-1: the values (att_values_reg_kernel's work, the
-// producers); na .. na+nw-1: the Wo rows (waiting). The values workgroups
-// come first in the grid, so they are dispatched first: a waiting
-// workgroup never holds a place a producer still needs.
-template <int C>
-__global__ __launch_bounds__(kVrThreads) void att_values_wo_kernel(AttWoArgs a) {
+// Workgroups 0 .. na-1: the values (the producers: workgroup b the
+// slice b mod nsl of head b / nsl, its Q8_0 block b); na .. na+nw-1: the Wo
+// rows (waiting). The values workgroups come first in the grid, so they
+// are dispatched first: a waiting workgroup never holds a place a producer
+// still needs. SHORT: contexts up to 256 (att_values_kernel's work, 4
+// waves), else att_values_reg_kernel's (8 waves).
+template <int C, bool SHORT>
+__global__ __launch_bounds__(SHORT ? kValThreads : kVrThreads) void att_values_wo_kernel(AttWoArgs a) {
     if ((int)blockIdx.x < a.na) {
-        att_values_reg_body<true>(a.att, a.att_stride, a.vals, a.out, a.ctl, AttBatch{}, a.kv_mul, a.hs, a.kv_dim,
-                                  a.nsl, a.ctx_pad, a.qx, a.xs, a.xsum, blockIdx.x, 0, a.sync, a.na);
+        if (SHORT)
+            att_values_body<true, kValShortChunk, true>(a.att, a.att_stride, a.vals, a.out, a.ctl, AttBatch{},
+                                                        a.kv_mul, a.hs, a.kv_dim, a.ctx_pad, a.qx, a.xs, a.xsum,
+                                                        blockIdx.x / a.nsl, blockIdx.x % a.nsl, 0, a.sync, a.na);
+        else
+            att_values_reg_body<true>(a.att, a.att_stride, a.vals, a.out, a.ctl, AttBatch{}, a.kv_mul, a.hs,
+                                      a.kv_dim, a.nsl, a.ctx_pad, a.qx, a.xs, a.xsum, blockIdx.x, 0, a.sync, a.na);
         return;
     }
-    wo_after_values<C, kWoRowsPerWave>(a, blockIdx.x - a.na);
+    wo_after_values<C, kWoRowsPerWave, (SHORT ? kValThreads : kVrThreads) / 64>(a, blockIdx.x - a.na);
 }
 
 bool launch_att_values_wo(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                           int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
                           const uint8_t *wo_w, const float *wo_ws, int64_t wo_rows, int64_t wo_cols, float *x,
                           unsigned long long *sync, hipStream_t s) {
-    if (!ctl || !qx || !sync || ctx <= kValShortCtx || ctx > kVrMaxCtx || hs % 32 != 0 || kv_dim % 4 != 0 ||
-        (reinterpret_cast<uintptr_t>(vals) & 15) != 0)
+    const bool shrt = ctx <= kValShortCtx;
+    const int wo_rows_wg = kWoRowsPerWave * (shrt ? kValThreads : kVrThreads) / 64;
+    if (!ctl || !qx || !sync || ctx > kVrMaxCtx || hs % 32 != 0 || kv_dim % 4 != 0 ||
+        (!shrt && (reinterpret_cast<uintptr_t>(vals) & 15) != 0))
         return false;
-    if (wo_cols != (int64_t)heads * hs || wo_cols <= 3072 || wo_cols > 4096 || wo_rows <= 0 || wo_rows % kWoRows)
+    if (wo_cols != (int64_t)heads * hs || wo_cols <= 3072 || wo_cols > 4096 || wo_rows <= 0 || wo_rows % wo_rows_wg)
         return false;
     static std::once_flag once;
     std::call_once(once, [] {
-        (void)hipFuncSetAttribute((const void *)att_values_wo_kernel<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)att_values_reg_lds(kVrMaxCtx));
+        (void)hipFuncSetAttribute((const void *)att_values_wo_kernel<4, false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)att_values_reg_lds(kVrMaxCtx));
     });
     AttWoArgs a{};
     a.att = att;
@@ -1457,9 +1488,18 @@ bool launch_att_values_wo(const float *att, int32_t att_stride, const float *val
     a.cols = (int)wo_cols;
     a.sync = sync;
     a.na = heads * a.nsl;
-    a.nw = (int)(wo_rows / kWoRows);
-    const size_t lds = std::max(att_values_reg_lds(ctx), (size_t)kWoRows * 8 * wo_k8p(4) * 4);
-    RK_LAUNCH(att_values_wo_kernel<4>, dim3((unsigned)(a.na + a.nw)), dim3(kVrThreads), lds, s, a);
+    a.nw = (int)(wo_rows / wo_rows_wg);
+    const size_t wo_lds = (size_t)wo_rows_wg * 8 * wo_k8p(4) * 4;
+    if (shrt) {
+        const int ctx_pad = (ctx + 3) & ~3;
+        const size_t lds = ctx <= kValShortChunk ? (size_t)(ctx_pad + kValSlice * val_pitch(kValShortChunk)) * 4
+                                                 : att_values_lds(ctx, kValShortChunk);
+        RK_LAUNCH((att_values_wo_kernel<4, true>), dim3((unsigned)(a.na + a.nw)), dim3(kValThreads),
+                  std::max(lds, wo_lds), s, a);
+    } else {
+        RK_LAUNCH((att_values_wo_kernel<4, false>), dim3((unsigned)(a.na + a.nw)), dim3(kVrThreads),
+                  std::max(att_values_reg_lds(ctx), wo_lds), s, a);
+    }
     return true;
 }
 

@@ -5,13 +5,16 @@ oracle's bits, as the two launches do (internal/llm/model.go:575-596: the
 attention output, its Q8_0 form, x += Wo·attn).
 
 The launch takes a Q8_0 Wo of 3073..4096 columns (heads x head size) and
-contexts of 257..1024 positions, so the models here have 32 heads of 128
+contexts of up to 1024 positions, so the models here have 32 heads of 128
 (q_dim 4096) over a narrow residual: small enough for the oracle, the
-shapes of config 3's attention. Covered: the Llama, Qwen2 (QKV bias) and
-Qwen3 (QK-norm) attention paths, decode positions on both sides of 256 and
-512 (one to three chunks of values), many launches of one stage (the
-launch counts carry over), two stages in turn (each its own words), the
-layers-only forward, and eager launches (the profiler's path)."""
+shapes of config 3's and config 5's attention. Covered: the Llama, Qwen2
+(QKV bias) and Qwen3 (QK-norm) attention paths with both values bodies
+(contexts up to 256: four waves, Wo workgroups of 16 rows; longer: the
+register-held values, Wo workgroups of 32 rows), decode positions on both
+sides of 128, 256 and 512 (one to three chunks of values), many launches
+of one stage (the launch counts carry over), two stages in turn (each its
+own words), the layers-only forward, and eager launches (the profiler's
+path)."""
 import numpy as np
 import pytest
 
@@ -44,6 +47,31 @@ def test_values_and_wo_in_one_launch_every_logit(dev, arch):
     # contexts from one chunk of 256 values to three
     prompt = [int(t) for t in np.random.default_rng(22).integers(0, c.vocab, 250)]
     check_generation(dev, m, prompt, 280, 640)
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen2", "qwen3"])
+def test_short_context_values_and_wo_every_logit(dev, arch):
+    """Contexts up to 256 (the short values kernel's work in the launch,
+    Wo workgroups of 16 rows): a 40-token prompt, then positions 40..169,
+    across the values' 128-position chunk edge; the launches counted."""
+    extra = {"qwen2": dict(qkv_bias=True, rope_theta=1e6, norm_eps=1e-6),
+             "qwen3": dict(qk_norm=True, rope_theta=1e6, norm_eps=1e-6)}.get(arch, {})
+    c = Config(seq_len=200, **{**BASE, "dim": 128}, **extra)  # Wo rows: a multiple of 16
+    m = coded_model(c, 28, 2e-5, 2e-4)
+    prompt = [int(t) for t in np.random.default_rng(29).integers(0, c.vocab, 40)]
+    check_generation(dev, m, prompt, 130, 200)
+    st, mats = make_stage(dev, m, 200)
+    emb = dev.upload(m.embed.kind, m.embed.rows, m.embed.cols, m.embed.q, m.embed.scales)
+    st.set_head(emb, emb, m.rms_final)
+    st.generate_start(prompt)
+    st.generate_run(len(prompt) - 1)
+    n_fused, n_wo = fused_launches(dev, lambda: st.generate_run(3))
+    assert n_fused == 3 * c.layers and n_wo == 0
+    st.free()
+    emb.free()
+    for mt in mats:
+        mt.free()
+    assert dev.used == 0
 
 
 def test_two_stages_in_turn_and_eager_launches(dev):
