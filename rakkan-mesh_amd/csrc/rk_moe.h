@@ -26,6 +26,12 @@ struct MoeScratch {
     // optional: each grouping of several tokens adds its selected experts'
     // count to stat[0] and 1 to stat[1]
     unsigned long long *stat = nullptr;
+    // optional: one token's feed-forward in one launch (moe_ffn1_kernel)
+    // takes moe_sync_words() hand-off words (zero when made, owned by one
+    // layer: every launch on them has the same shape and tags them with
+    // that layer's count) and the word a timed-out wait sets
+    unsigned long long *sync = nullptr;
+    unsigned long long *err = nullptr;
 };
 
 }  // namespace rk
@@ -52,6 +58,10 @@ struct rk_moe {
 };
 
 namespace rk {
+
+// 64-bit words of one layer's hand-off area for the one-token launch: two
+// sets of kSyncWords and the experts' tagged logits.
+int64_t moe_sync_words(const rk_moe *m);
 
 // Bytes of a MoeScratch for `cap` tokens of m; with mem, also lays it out
 // there (256-byte aligned pieces). A stage sizes one for the largest of its

@@ -35,6 +35,7 @@
 #include "rk_fused.h"
 #include "rk_mm.h"
 #include "rk_moe.h"
+#include "rk_sync.h"
 
 namespace rk {
 
@@ -725,7 +726,7 @@ __host__ __device__ inline Up1Lds up1_lds(int dim, int experts) {
     l.sxsum = l.sxs + 4 * nb;
     l.sp = (l.sxsum + 4 * nb + 15) & ~15;
     l.skey = l.sp + 4 * ep;
-    l.srank = l.skey + 8 * ep;
+    l.srank = l.skey + 8 * (ep > 128 ? ep : 128);  // (up to 128 experts: the ranks read 128 keys)
     l.sn = (l.srank + 4 * ep + 15) & ~15;
     l.stab = l.sn + 32 * ((((dim >> 5) + 3) & ~3) + 4) * 4;
     l.bytes = l.stab + 8 * 4 * experts;
@@ -1032,6 +1033,486 @@ __global__ __launch_bounds__(512) void moe_down1_kernel(const void *const *gptr,
     }
 }
 
+// ---------------------------------------------------------------------------
+// One token's whole feed-forward in one launch (a decode step): the router
+// product with the RMSNorm, the routing, each selected expert's W1/W3 rows
+// and W2 rows, and the ascending-order sum into the residual. The bits are
+// those of the router's launch (launch_fused with the norm prologue),
+// moe_up1_kernel and moe_down1_kernel. Workgroups of eight waves, in grid
+// order:
+//  * nr router workgroups of eight router rows (one a wave; lane b holds
+//    the row's block b, inputs up to 2048 wide): RMSNorm(x)'s Q8_0 input in
+//    LDS, each row's block terms float32(sum_b)·float32(ws_b·xs_b) in LDS by
+//    running sum b mod 8, eight lanes adding them in block order from +0,
+//    the tree ((0+1)+(2+3))+((4+5)+(6+7)) (MatVecQ8, quant.go:158-180).
+//    Workgroup 0 then collects the logits and routes the token
+//    (moe_up1_kernel's steps, spread over the workgroup).
+//  * nu up workgroups (place g, block hb of 32 hidden rows): the normed
+//    input, the wait for the selection, then the g-th selected expert's W1
+//    and W3 rows (four hidden rows a wave, eight lanes a row dot) and h as
+//    moe_up1_kernel's: one Q8_0 block, put at place g (ffn1_put_h).
+//  * nd down workgroups of R = 64/k output rows of every selected expert:
+//    the W2 rows requested once the selection is seen, every block of h
+//    collected into LDS (ffn1_get_h), the row dots, and lane r adding row
+//    r's k products by ascending expert from +0 into y; out = y or
+//    Canonical(out + y).
+// Every hand-off is a tagged word: 48 bits of data under the low 16 bits of
+// the launch's number, which each workgroup keeps for itself (its own
+// count word, read and written by it alone; launches of a stream run in
+// order). A reader polls, with agent-scope loads, until every word it needs
+// carries its launch's tag; no word is reset, no store waits for another,
+// and no atomic is involved (counts and flags on shared words measured
+// slower: atomics to one address serialise, and a store's acknowledgement
+// takes about a microsecond). The logits are one word each; the selection
+// is written by ascending expert index into every XCD's line (the experts
+// first, then their weights, which only the up rows' ends need); h's
+// 36-byte block is six words of six bytes. The words are the layer's own
+// (ffn1_sync_layout): tags count that layer's launches only.
+// A workgroup waits only for workgroups before it in the grid, which are
+// dispatched before it, so the launch always drains. Every wait is bounded
+// by the device clock (kSyncTimeout); one that gives up sets *err and goes
+// on with what memory holds, expert indices clamped into range.
+constexpr int kFfn1MaxK = 16;         // the selection's experts, then their weights, in an XCD's line
+constexpr int kFfn1LineWords = 2 * kFfn1MaxK;
+constexpr int kFfn1MaxExperts = 512;  // eight a lane of the collecting wave
+constexpr int kFfn1MaxCols = 2048;    // one input block a lane of a router row
+constexpr int kFfn1MaxHidden = 2048;  // eight W2 blocks a lane
+
+struct Ffn1Args {
+    const float *x, *norm_w;
+    float recip_n, eps;
+    const uint8_t *rw;  // the router [experts][dim] and its scales
+    const float *rws;
+    const uint8_t *const *w1;
+    const uint8_t *const *w3;
+    const uint8_t *const *w2;
+    const float *const *s1;
+    const float *const *s3;
+    const float *const *s2;
+    int experts, k, dim, hidden;
+    int32_t *sel;  // [k] the selection in selection order, and its weights
+    float *wsel;
+    float *out;
+    int residual;
+    // the layer's hand-off words (ffn1_sync_layout), zero when made
+    unsigned long long *lines;  // [8][kFfn1LineWords] the selection, a line per XCD
+    unsigned long long *lw;     // [experts] the tagged logits
+    unsigned long long *hw;     // [k][hidden/32][6] h's Q8_0 blocks as tagged words (ffn1_put_h)
+    unsigned long long *cnt;    // [nr + nu + nd] each workgroup's count of its launches
+    unsigned long long *err;
+    int nr, nu, nd;  // router, up and down workgroups
+};
+
+// The hand-off words of one layer: the selection lines, the tagged logits,
+// h's tagged blocks and every workgroup's launch count (each in whole
+// 128-byte lines).
+struct Ffn1Sync {
+    int64_t lines, lw, hw, cnt, words;
+};
+inline Ffn1Sync ffn1_sync_layout(int dim, int experts, int k, int hidden) {
+    auto al = [](int64_t w) { return (w + 15) & ~(int64_t)15; };
+    const int64_t nr = (experts + 7) / 8, nu = (int64_t)k * (hidden / 32), nd = (dim + 64 / k - 1) / (64 / k);
+    Ffn1Sync l;
+    l.lines = 0;
+    l.lw = 8 * kFfn1LineWords;
+    l.hw = l.lw + al(experts);
+    l.cnt = l.hw + al(6 * nu);
+    l.words = l.cnt + al(nr + nu + nd);
+    return l;
+}
+
+// LDS (bytes): the normed input's codes and scales and the norm's
+// transposed x, then each role's own: the router's terms [8][64], the
+// probabilities, keys and ranks [experts]; the up rows' pointer tables
+// [4][experts] and h [32]; the down rows' tables [2][experts], h
+// [k][hidden], its scales, and the row dots [64].
+struct Ffn1Lds {
+    int sxs, sn, role, sp, skey, srank, hq, hs, sv, bytes;
+};
+__host__ __device__ inline Ffn1Lds ffn1_lds(int dim, int experts, int k, int hidden) {
+    Ffn1Lds l;
+    const int nb = dim >> 5, pitch = ((nb + 3) & ~3) + 4, ep = (experts + 3) & ~3;
+    l.sxs = (dim + 15) & ~15;
+    l.sn = (l.sxs + 4 * nb + 15) & ~15;
+    l.role = (l.sn + 4 * 32 * pitch + 15) & ~15;
+    l.sp = l.role + 8 * 64 * 4;
+    l.skey = l.sp + 4 * ep;
+    l.srank = l.skey + 8 * ep;
+    const int router = l.srank + 4 * ep;
+    const int up = l.role + 8 * 4 * experts + 32 * 4;
+    l.hq = l.role + 8 * 2 * experts;
+    l.hs = l.hq + ((k * hidden + 15) & ~15);
+    l.sv = l.hs + ((4 * k * (hidden >> 5) + 15) & ~15);
+    const int down = l.sv + 64 * 4;
+    l.bytes = router > up ? (router > down ? router : down) : (up > down ? up : down);
+    return l;
+}
+
+// RMSNorm(x) (model.go:632-638) and its Q8_0 form (quant.go:34-53) into
+// LDS by a 512-thread workgroup, thread t holding x's and the weights'
+// group t (clamped): x transposed into sn, Dot32 by wave 0, then
+// quantize_group (moe_up1_kernel's steps). Ends with a barrier.
+__device__ __forceinline__ void ffn1_norm_quant(float4 xv, float4 wv, int dim, float recip_n, float eps, int8_t *sq,
+                                                float *sxs, float *sn, float *bcast) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int ng = dim >> 2, steps = dim >> 5, pitch = ((steps + 3) & ~3) + 4;
+    if (tid < ng) {
+        const int i = 4 * tid;
+        float *d = sn + (i & 31) * pitch + (i >> 5);
+        d[0] = xv.x;
+        d[pitch] = xv.y;
+        d[2 * pitch] = xv.z;
+        d[3 * pitch] = xv.w;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const float s = lane < 32 ? lds_dot32_self_t(sn, pitch, steps, lane) : 0.0f;
+        const float dot = dot32_reduce(s);
+        if (lane == 0) *bcast = rsqrt32((dot * recip_n) + eps);
+    }
+    __syncthreads();
+    const float r = *bcast;
+    float d;
+    int cs;
+    const uint32_t pk =
+        quantize_group(wv.x * (r * xv.x), wv.y * (r * xv.y), wv.z * (r * xv.z), wv.w * (r * xv.w), d, cs);
+    if (tid < ng) {
+        reinterpret_cast<uint32_t *>(sq)[tid] = pk;
+        if ((tid & 7) == 0) sxs[tid >> 3] = d;
+    }
+    __syncthreads();
+}
+
+
+// The routing of launch n by router workgroup 0 (every thread calls it):
+// wave 0 polls the tagged logits until all E carry the launch's tag, then
+// the softmax (up1_softmax: Go max, Exp32, one sequential sum, Recip32) and
+// each expert's key, the stable top-k as ranks (expert_ranks), the weights
+// p·Recip32(Σ p) with the sum in selection order from +0; sel/wsel in
+// selection order and the tagged words by ascending expert.
+template <int PER>
+__device__ void ffn1_route(const Ffn1Args &a, uint32_t tag, float *sp, unsigned long long *skey, int *srank,
+                           int *ssel) {
+    const int tid = threadIdx.x, lane = tid & 63, E = a.experts, k = a.k;
+    if (PER > 2)
+        for (int e = tid; e < E; e += 512) srank[e] = 0;
+    if (tid < 64) {
+        float lg[PER];
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        bool ok = false;
+        for (int i = 0; i < (1 << 24); i++) {
+            bool mine = true;
+#pragma unroll
+            for (int j = 0; j < PER; j++) {
+                if (64 * j < E) {  // uniform
+                    const unsigned long long v =
+                        __hip_atomic_load(a.lw + min(lane + 64 * j, E - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    lg[j] = u2f((uint32_t)v);
+                    mine = mine && (uint32_t)(v >> 48) == tag;
+                } else {
+                    lg[j] = 0.0f;
+                }
+            }
+            if (__all(mine)) {
+                ok = true;
+                break;
+            }
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (!ok && lane == 0) __hip_atomic_store(a.err, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        float m = lg[0];
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            if (lane + 64 * j < E) m = gomax(m, lg[j]);
+        m = wave_gomax(m);
+#pragma unroll
+        for (int j = 0; j < PER; j++)
+            if (lane + 64 * j < E) sp[lane + 64 * j] = exp32(lg[j] - m);
+        const float inv = recip32(lds_chain_sum(sp, E, 0.0f));
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int e = lane + 64 * j;
+            if (e < E) {
+                const float pv = sp[e] * inv;
+                sp[e] = pv;
+                skey[e] = route_key(pv, e);
+            }
+        }
+    }
+    __syncthreads();
+    if (PER == 2) {
+        // up to 128 experts: thread t counts the larger keys of expert t/4
+        // among key pairs 8q + 2(t mod 4), q < 16 (the quad's four reads
+        // of a step in distinct banks); the quad's counts summed by DPP
+        const int e = tid >> 2, part = tid & 3;
+        const unsigned long long ke = skey[min(e, E - 1)];
+        const ulonglong2 *p2 = reinterpret_cast<const ulonglong2 *>(skey) + part;
+        int c = 0;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const ulonglong2 v = p2[4 * q];
+            const int i0 = 8 * q + 2 * part;
+            c += ((i0 < E) & (v.x > ke)) + ((i0 + 1 < E) & (v.y > ke));
+        }
+        c += dpp_x1(c);
+        c += dpp_x2(c);
+        if (part == 0 && e < E && c < k) ssel[c] = e;
+    } else {
+        expert_ranks(skey, srank, E);
+        __syncthreads();
+        for (int e = tid; e < E; e += 512)
+            if (srank[e] < k) ssel[srank[e]] = e;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int mine = ssel[min(lane, k - 1)];
+        int place = 0;  // among the selection by ascending index (the experts are distinct)
+        for (int q = 0; q < k; q++) place += ssel[q] < mine ? 1 : 0;
+        // the experts first: the up and down workgroups request their rows
+        // on them; the weights are needed only after the up rows' dots
+        if (lane < k) {
+            const unsigned long long word = ((unsigned long long)tag << 48) | (unsigned long long)(mine & 0xFFFF);
+#pragma unroll
+            for (int xcd = 0; xcd < 8; xcd++)
+                __hip_atomic_store(a.lines + kFfn1LineWords * xcd + place, word, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+        const float ps = sp[mine];
+        float sum = 0.0f;
+        for (int r = 0; r < k; r++) sum += __shfl(ps, r);
+        const float wt = ps * recip32(sum);
+        if (lane < k) {
+            const unsigned long long word = ((unsigned long long)tag << 48) | (unsigned long long)f2u(wt);
+#pragma unroll
+            for (int xcd = 0; xcd < 8; xcd++)
+                __hip_atomic_store(a.lines + kFfn1LineWords * xcd + kFfn1MaxK + place, word, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            a.sel[lane] = mine;
+            a.wsel[lane] = wt;
+        }
+    }
+}
+
+// The waits for the selection of launch `tag`, by one wave (every lane
+// calls them): polls of its XCD's line until words off .. off+k-1 all carry
+// the tag; the experts (clamped) into s_e, or the weights into s_w.
+__device__ void ffn1_wait_line(const Ffn1Args &a, uint32_t tag, int off, int *s_e, float *s_w) {
+    const int lane = threadIdx.x & 63, k = a.k;
+    const unsigned long long *line = a.lines + kFfn1LineWords * (blockIdx.x & 7) + off;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long v = 0;
+    bool ok = false;
+    for (int i = 0; i < (1 << 24); i++) {
+        v = lane < k ? __hip_atomic_load(line + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : ((unsigned long long)tag << 48);
+        if (__all((uint32_t)(v >> 48) == tag)) {
+            ok = true;
+            break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok && lane == 0) __hip_atomic_store(a.err, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane < k) {
+        if (s_e) s_e[lane] = min((int)(v & 0xFFFF), a.experts - 1);
+        if (s_w) s_w[lane] = u2f((uint32_t)v);
+    }
+}
+
+// h's Q8_0 block (32 codes, then the scale: 36 bytes) as six words of six
+// bytes each under the launch's 16-bit tag, so a reader holding all six
+// words of its launch holds the block (no count, no wait for the stores).
+// By one wave: lanes 0-7 hold four codes each (pk), every lane the scale.
+__device__ __forceinline__ void ffn1_put_h(unsigned long long *hw, uint32_t pk, float d, uint32_t tag) {
+    const int lane = threadIdx.x & 63;
+    const int w = min(lane, 5), j0 = (6 * w) >> 2, o = (6 * w) & 3;  // bytes 6w.. from dword j0, byte o (0 or 2)
+    const uint32_t lo = __shfl(pk, j0), hi0 = __shfl(pk, min(j0 + 1, 7));
+    const uint32_t hi = j0 + 1 == 8 ? f2u(d) : hi0;
+    const unsigned long long bytes = (((unsigned long long)hi << 32) | lo) >> (8 * o);
+    if (lane < 6)
+        __hip_atomic_store(hw + lane, ((unsigned long long)tag << 48) | (bytes & 0xFFFFFFFFFFFFull), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The k·nhb blocks of h of launch `tag` into LDS (codes shq [block][32],
+// scales shs [block]), by the whole workgroup: polls of every block's last
+// word (two codes and the scale) until all carry the tag, then the other
+// five words until they do. A wait that gives up sets *err.
+__device__ void ffn1_get_h(const Ffn1Args &a, uint32_t tag, int nblk, int8_t *shq, float *shs, int *s_to) {
+    const int tid = threadIdx.x;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    if (tid == 0) *s_to = 0;
+    for (int pass = 0; pass < 2; pass++) {
+        const int per = pass == 0 ? 1 : 5;
+        for (int i = 0; i < (1 << 24); i++) {
+            int stale = 0;
+            for (int u = tid; u < nblk * per; u += 512) {
+                const int b = pass == 0 ? u : u / 5, wi = pass == 0 ? 5 : u - 5 * (u / 5);
+                const unsigned long long v =
+                    __hip_atomic_load(a.hw + 6 * b + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if ((uint32_t)(v >> 48) != tag) {
+                    stale = 1;
+                } else if (wi == 5) {
+                    *reinterpret_cast<uint16_t *>(shq + 32 * b + 30) = (uint16_t)v;
+                    shs[b] = u2f((uint32_t)(v >> 16));
+                } else {
+                    uint16_t *d = reinterpret_cast<uint16_t *>(shq + 32 * b + 6 * wi);
+                    d[0] = (uint16_t)v;
+                    d[1] = (uint16_t)(v >> 16);
+                    d[2] = (uint16_t)(v >> 32);
+                }
+            }
+            if (tid == 0 && __builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) *s_to = 1;
+            if (!__syncthreads_or(stale) || *s_to) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    if (tid == 0 && *s_to) __hip_atomic_store(a.err, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+}
+
+// This workgroup's launch number: its own count, one more (read and
+// written by this workgroup alone, launches of a stream being in order).
+__device__ __forceinline__ void ffn1_count(const Ffn1Args &a, unsigned long long *s_n) {
+    if (threadIdx.x == 0) {
+        const unsigned long long n = a.cnt[blockIdx.x] + 1;
+        a.cnt[blockIdx.x] = n;
+        *s_n = n;
+    }
+}
+
+template <int BU, int BD>
+__global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
+    extern __shared__ __align__(16) char flds[];
+    __shared__ float bcast;
+    __shared__ unsigned long long s_n;
+    __shared__ int s_e[kFfn1MaxK];
+    __shared__ float s_w[kFfn1MaxK];
+    __shared__ int s_to;
+    const int dim = a.dim, nb = dim >> 5, E = a.experts, k = a.k, H = a.hidden, nhb = H >> 5;
+    const Ffn1Lds L = ffn1_lds(dim, E, k, H);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bid = blockIdx.x;
+    int8_t *sq = reinterpret_cast<int8_t *>(flds);
+    float *sxs = reinterpret_cast<float *>(flds + L.sxs);
+    float *sn = reinterpret_cast<float *>(flds + L.sn);
+    const void **stab = reinterpret_cast<const void **>(flds + L.role);
+    ffn1_count(a, &s_n);
+
+    if (bid >= a.nr + a.nu) {
+        // ---- down: output rows R·di .. R·di+R-1 of every selected expert;
+        // group of eight lanes gi: place gi / R, row gi mod R ----
+        const int di = bid - a.nr - a.nu, R = 64 / k;
+        const int gi = tid >> 3, rl = tid & 7;
+        const int g = min(gi / R, k - 1), r = gi - (gi / R) * R;
+        const int64_t i = min(di * R + r, dim - 1);
+        int8_t *shq = reinterpret_cast<int8_t *>(flds + L.hq);
+        float *shs = reinterpret_cast<float *>(flds + L.hs);
+        float *sv = reinterpret_cast<float *>(flds + L.sv);
+        for (int t = tid; t < 2 * E; t += 512) stab[t] = t < E ? (const void *)a.w2[t] : (const void *)a.s2[t - E];
+        __syncthreads();
+        const uint32_t tag = (uint32_t)s_n & 0xFFFFu;
+        if (wave == 0) ffn1_wait_line(a, tag, 0, s_e, nullptr);
+        __syncthreads();
+        const int e = s_e[g];
+        int4 c0[BD], c1[BD];
+        float sw[BD];
+        lane_row_load<BD>(c0, c1, sw, static_cast<const uint8_t *>(stab[e]) + i * H,
+                          static_cast<const float *>(stab[E + e]) + i * nhb, nhb, rl);
+        ffn1_get_h(a, tag, k * nhb, shq, shs, &s_to);
+        const float v = tree8(lane_running_sum<BD>(c0, c1, sw, shq + g * H, shs + g * nhb, nhb, rl));
+        if (rl == 0 && gi < k * R) sv[gi] = v;
+        __syncthreads();
+        if (tid < R && di * R + tid < dim) {
+            float y = 0.0f;
+            for (int q = 0; q < k; q++) y += sv[q * R + tid];
+            float *dst = a.out + di * R + tid;
+            *dst = a.residual ? canonical(*dst + y) : y;
+        }
+        return;
+    }
+
+    // router and up workgroups: x and the norm weights, a group of four a thread
+    const int g4 = min(tid, (dim >> 2) - 1);
+    const float4 xv = reinterpret_cast<const float4 *>(a.x)[g4];
+    const float4 wv = reinterpret_cast<const float4 *>(a.norm_w)[g4];
+
+    if (bid < a.nr) {
+        // ---- router rows 8·bid + wave ----
+        const int row = bid * 8 + wave;
+        const int64_t rr = min(row, E - 1);
+        const int b = min(lane, nb - 1);
+        const uint8_t *rp = a.rw + rr * dim + 32 * b;
+        const int4 c0 = load_stream16_g(rp), c1 = load_stream16_g(rp + 16);
+        const float sw = loadf_g(a.rws + rr * nb + b);
+        ffn1_norm_quant(xv, wv, dim, a.recip_n, a.eps, sq, sxs, sn, &bcast);
+        const uint32_t tag = (uint32_t)s_n & 0xFFFFu;
+        const int4 *xp = reinterpret_cast<const int4 *>(sq + 32 * b);
+        const int sm = dot16(c1, xp[1], dot16(c0, xp[0], 0));
+        const float t = (float)sm * (sw * sxs[b]);
+        float *tw = reinterpret_cast<float *>(flds + L.role) + wave * 64;  // [running sum][b / 8]
+        if (lane < nb) tw[(lane & 7) * 8 + (lane >> 3)] = t;
+        __syncthreads();
+        float acc = 0.0f;
+        if (lane < 8) {
+            const float *p = tw + lane * 8;
+            const int cnt = lane < nb ? (nb - lane + 7) >> 3 : 0;
+            for (int m = 0; m < cnt; m++) acc += p[m];
+        }
+        acc = tree8(acc);
+        if (lane == 0 && row < E)
+            __hip_atomic_store(a.lw + row, ((unsigned long long)tag << 48) | (unsigned long long)f2u(acc),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (bid == 0) {
+            float *sp = reinterpret_cast<float *>(flds + L.sp);
+            unsigned long long *skey = reinterpret_cast<unsigned long long *>(flds + L.skey);
+            int *srank = reinterpret_cast<int *>(flds + L.srank);
+            if (E <= 128)
+                ffn1_route<2>(a, tag, sp, skey, srank, s_e);
+            else
+                ffn1_route<kFfn1MaxExperts / 64>(a, tag, sp, skey, srank, s_e);
+        }
+        return;
+    }
+
+    // ---- up: place g, hidden rows 32·hb .. 32·hb+31 (wave w rows 4w..4w+3:
+    // W1 of row q in lanes 16q..16q+7, W3 in 16q+8..16q+15) ----
+    const int ui = bid - a.nr, g = ui / nhb, hb = ui - g * nhb;
+    float *sh = reinterpret_cast<float *>(flds + L.role + 8 * 4 * E);
+    for (int t = tid; t < 4 * E; t += 512) {
+        const int tab = t / E, e = t - tab * E;
+        stab[t] = tab == 0 ? (const void *)a.w1[e] : tab == 1 ? (const void *)a.s1[e] : tab == 2 ? (const void *)a.w3[e]
+                                                                                            : (const void *)a.s3[e];
+    }
+    ffn1_norm_quant(xv, wv, dim, a.recip_n, a.eps, sq, sxs, sn, &bcast);
+    const uint32_t tag = (uint32_t)s_n & 0xFFFFu;
+    if (wave == 0) ffn1_wait_line(a, tag, 0, s_e, nullptr);
+    __syncthreads();
+    const int e = s_e[g];
+    const int rg = lane >> 3, rl = lane & 7, q = rg >> 1;
+    const int64_t j = hb * 32 + 4 * wave + q;
+    const bool w3row = rg & 1;
+    int4 c0[BU], c1[BU];
+    float sw[BU];
+    lane_row_load<BU>(c0, c1, sw, static_cast<const uint8_t *>(stab[(w3row ? 2 : 0) * E + e]) + j * dim,
+                      static_cast<const float *>(stab[(w3row ? 3 : 1) * E + e]) + j * nb, nb, rl);
+    const float v = tree8(lane_running_sum<BU>(c0, c1, sw, sq, sxs, nb, rl));
+    const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
+    if (wave == 0) ffn1_wait_line(a, tag, kFfn1MaxK, nullptr, s_w);
+    __syncthreads();
+    if ((lane & 15) == 0) sh[4 * wave + q] = s_w[g] * silu_mul(v, v3);
+    __syncthreads();
+    if (wave == 0) {
+        const float4 v4 = reinterpret_cast<const float4 *>(sh)[min(lane, 7)];
+        float d;
+        int cs;
+        const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
+        ffn1_put_h(a.hw + 6 * ((int64_t)g * nhb + hb), pk, d, tag);
+    }
+}
+
 // y_t = Σ o over the token's experts in ascending index, from +0; out_t = y_t,
 // or Canonical(out_t + y_t) (the layer's residual, model.go:608-610).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const int32_t *sel, int k, const float *o, int dim,
@@ -1103,6 +1584,8 @@ __global__ __launch_bounds__(kCnThreads) void moe_combine_norm_kernel(const int3
 }
 
 }  // namespace
+
+int64_t moe_sync_words(const rk_moe *m) { return ffn1_sync_layout(m->dim, m->experts, m->topk, m->hidden).words; }
 
 int64_t moe_scratch_layout(const rk_moe *m, int cap, char *mem, MoeScratch *sc) {
     const int64_t T = cap, K = m->topk, E = m->experts, D = m->dim, H = m->hidden;
@@ -1294,6 +1777,56 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
     if (tokens <= 0) return RK_OK;
     if (tokens > sc.cap) return fail(d, RK_ERR_ARGS, "moe: %d tokens beyond the scratch's %d", tokens, sc.cap);
     const int D = m->dim, E = m->experts, K = m->topk, H = m->hidden;
+    if (norm_w && tokens == 1 && !next && sc.sync && sc.err && D <= kFfn1MaxCols && E <= kFfn1MaxExperts &&
+        K <= kFfn1MaxK && H <= kFfn1MaxHidden) {
+        // one token, the whole feed-forward in one launch
+        Ffn1Args a{};
+        a.x = x;
+        a.norm_w = norm_w;
+        a.recip_n = recip_n;
+        a.eps = eps;
+        a.rw = m->router->w;
+        a.rws = m->router->scales;
+        a.w1 = m->w1;
+        a.w3 = m->w3;
+        a.w2 = m->w2;
+        a.s1 = m->s1;
+        a.s3 = m->s3;
+        a.s2 = m->s2;
+        a.experts = E;
+        a.k = K;
+        a.dim = D;
+        a.hidden = H;
+        const Ffn1Sync sy = ffn1_sync_layout(D, E, K, H);
+        a.lines = sc.sync + sy.lines;
+        a.lw = sc.sync + sy.lw;
+        a.hw = sc.sync + sy.hw;
+        a.cnt = sc.sync + sy.cnt;
+        a.sel = sc.sel;
+        a.wsel = sc.wsel;
+        a.out = out;
+        a.residual = residual ? 1 : 0;
+        a.err = sc.err;
+        a.nr = (E + 7) / 8;
+        a.nu = K * (H / 32);
+        a.nd = (D + 64 / K - 1) / (64 / K);
+        const size_t lds = (size_t)ffn1_lds(D, E, K, H).bytes;
+        const int bu = (D / 32 + 7) / 8, bd = (H / 32 + 7) / 8;
+        const dim3 grid((unsigned)(a.nr + a.nu + a.nd));
+        typedef void (*Ffn1Fn)(Ffn1Args);
+        static const Ffn1Fn fns[3][3] = {{moe_ffn1_kernel<2, 2>, moe_ffn1_kernel<2, 4>, moe_ffn1_kernel<2, 8>},
+                                         {moe_ffn1_kernel<4, 2>, moe_ffn1_kernel<4, 4>, moe_ffn1_kernel<4, 8>},
+                                         {moe_ffn1_kernel<8, 2>, moe_ffn1_kernel<8, 4>, moe_ffn1_kernel<8, 8>}};
+        const Ffn1Fn fn = fns[bu <= 2 ? 0 : bu <= 4 ? 1 : 2][bd <= 2 ? 0 : bd <= 4 ? 1 : 2];
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return hip_fail(d, e, "moe launch");
+        }
+        ProfScope p(d, s, "moe_ffn");
+        RK_LAUNCH(fn, grid, dim3(512), lds, s, a);
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? RK_OK : hip_fail(d, e, "moe launch");
+    }
     if (norm_w && tokens == 1 && D <= 2048 && E <= kUp1MaxExperts && K <= kMoeMaxK) {
         // one token: the router's product with the RMSNorm in its prologue,
         // then the W1/W3 rows with the routing and the norm folded in (the

@@ -95,8 +95,13 @@ struct rk_stage {
     int moe_cap = 0;
     // the groupings' counters (MoeScratch::stat): experts selected, groupings
     unsigned long long *moe_stat = nullptr;
-    // the hand-off words of the values-and-Wo launch (kSyncWords)
+    // the hand-off words of the values-and-Wo launch (kSyncWords; its
+    // kSyncError is also the MoE launches' error word)
     unsigned long long *sync = nullptr;
+    // each MoE layer's hand-off words for its one-token launch (a stride
+    // of moe_sync_stride words)
+    unsigned long long *moe_sync = nullptr;
+    int64_t moe_sync_stride = 0;
 };
 
 namespace rk {
@@ -280,6 +285,8 @@ static int enqueue_layer(rk_stage *s, int li, hipStream_t st, bool qb_ready) {
         MoeScratch sc;
         moe_scratch_layout(L.moe, s->moe_cap, s->moe_mem, &sc);
         sc.stat = s->moe_stat;
+        sc.sync = s->moe_sync + (int64_t)li * s->moe_sync_stride;
+        sc.err = s->sync + kSyncError;
         return enqueue_moe_x(L.moe, sc, s->x, D.rms_ffn, c.recip_dim, c.norm_eps, 1, s->qb.qx, s->qb.xs, s->qb.xsum,
                              s->x, true, st);
     }
@@ -394,13 +401,14 @@ static int record(rk_stage *s, Rec which) {
     return RK_OK;
 }
 
-// After the stream is idle: whether a values-and-Wo launch gave up waiting
-// for its values (kSyncError; its Wo rows are then not the product).
+// After the stream is idle: whether a launch with an in-launch hand-off
+// (values and Wo, a one-token MoE feed-forward) gave up waiting for its
+// input (kSyncError; its results are then not the product).
 static int sync_check(rk_stage *s, const char *what) {
     rk_device *d = s->d;
     unsigned long long err = 0;
     HIP_TRY(d, hipMemcpy(&err, s->sync + kSyncError, sizeof err, hipMemcpyDeviceToHost), what);
-    if (err) return fail(d, RK_ERR_HIP, "%s: a values-and-Wo launch timed out waiting for its values", what);
+    if (err) return fail(d, RK_ERR_HIP, "%s: a launch timed out waiting for a hand-off inside it", what);
     return RK_OK;
 }
 
@@ -800,6 +808,9 @@ int rk_stage_new(rk_device *d, const rk_stage_config *c, const rk_stage_layer *l
             if (layers[i].moe) mb = std::max(mb, moe_scratch_layout(layers[i].moe, s->moe_cap, nullptr, nullptr));
         take((void **)&s->moe_mem, mb);
         take((void **)&s->moe_stat, 16);
+        for (int i = 0; i < n_layers; i++)
+            if (layers[i].moe) s->moe_sync_stride = std::max(s->moe_sync_stride, moe_sync_words(layers[i].moe));
+        take((void **)&s->moe_sync, 8 * s->moe_sync_stride * n_layers);
     }
     s->ld.resize(n_layers);
     const int64_t bias_n = c->qkv_bias ? qdim + 2 * kvdim : 0;

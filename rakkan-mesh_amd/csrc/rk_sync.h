@@ -89,4 +89,20 @@ __device__ __forceinline__ bool sync_last_done(unsigned long long *count, int n,
     return *s_last != 0;
 }
 
+// The same, returning the launch's number (1, 2, ...) in every thread of
+// the workgroup whose add completes the launch's count, and 0 in every
+// other workgroup. s_n: a word of static LDS.
+__device__ __forceinline__ unsigned long long sync_last_number(unsigned long long *count, int n,
+                                                               unsigned long long *s_n) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned long long old =
+            __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_n = (old + 1) % (unsigned long long)n == 0 ? (old + 1) / (unsigned long long)n : 0ull;
+    }
+    __syncthreads();
+    return *s_n;
+}
+
 }  // namespace rk

@@ -181,6 +181,27 @@ def test_profiling_a_qk_norm_prompt(dev):
     assert dev.used == 0
 
 
+@pytest.mark.parametrize("dim,experts,ehidden,topk,lo,hi", [(2048, 16, 64, 16, 2e-4, 2e-3),
+                                                        (512, 32, 2048, 2, 5e-4, 5e-3),
+                                                        (64, 512, 32, 4, 1e-3, 1e-2)])
+def test_moe_stage_one_launch_limits(dev, dim, experts, ehidden, topk, lo, hi):
+    """A decode step's whole feed-forward in one launch at the edges of the
+    shapes it takes: inputs 2048 wide with 16 experts a token (four output
+    rows of each a down workgroup), an expert hidden width of 2048 (eight
+    W2 blocks a lane), and 512 experts (the routing's general ranks). One
+    generation each over two layers, every logit against the oracle."""
+    c = Config(dim=dim, hidden=64, layers=2, heads=4, kv_heads=2, vocab=50, seq_len=64, head_dim=32, qk_norm=True,
+               rope_theta=1e6, norm_eps=1e-6, dtype="q8_0")
+    m = moe_model(c, experts=experts, ehidden=ehidden, topk=topk, seed=9, lo=lo, hi=hi, router_scale=(1e-2, 5e-2))
+    g = GpuModel(dev, m)
+    try:
+        with oracle.matvec_threads(THREADS):
+            check_batch1(g, [3, 1, 4], 6, 64)
+    finally:
+        g.free()
+    assert dev.used == 0
+
+
 def test_moe_stage_many_experts(dev):
     """200 experts, top 8 (a lane of the routing holds up to 16 experts):
     one sequence, then three."""
