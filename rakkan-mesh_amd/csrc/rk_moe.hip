@@ -1335,38 +1335,53 @@ __device__ __forceinline__ void ffn1_put_h(unsigned long long *hw, uint32_t pk, 
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// One block's six words read (agent-scope) into LDS (codes shq, scale
+// shs) for those of them in `want` (bit i: word i) that carry the tag;
+// returns the bits of the words read.
+__device__ __forceinline__ int ffn1_h_words(const unsigned long long *hw, int b, int want, uint32_t tag, int8_t *shq,
+                                            float *shs) {
+    int got = 0;
+#pragma unroll
+    for (int wi = 0; wi < 6; wi++) {
+        if (!(want >> wi & 1)) continue;
+        const unsigned long long v = __hip_atomic_load(hw + 6 * b + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t)(v >> 48) != tag) continue;
+        got |= 1 << wi;
+        if (wi == 5) {
+            *reinterpret_cast<uint16_t *>(shq + 32 * b + 30) = (uint16_t)v;
+            shs[b] = u2f((uint32_t)(v >> 16));
+        } else {
+            uint16_t *d = reinterpret_cast<uint16_t *>(shq + 32 * b + 6 * wi);
+            d[0] = (uint16_t)v;
+            d[1] = (uint16_t)(v >> 16);
+            d[2] = (uint16_t)(v >> 32);
+        }
+    }
+    return got;
+}
+
 // The k·nhb blocks of h of launch `tag` into LDS (codes shq [block][32],
-// scales shs [block]), by the whole workgroup: polls of every block's last
-// word (two codes and the scale) until all carry the tag, then the other
-// five words until they do. A wait that gives up sets *err.
+// scales shs [block]), by the whole workgroup; thread t takes blocks t and
+// t + 512. While fewer than half the blocks are in, a round reads only a
+// block's last word (its scale: one word a block of polling); a block whose
+// last word is in reads the other five next round; once half are in, a
+// round reads all of a missing block's words (one round trip after its
+// stores land). A wait that gives up sets *err.
 __device__ void ffn1_get_h(const Ffn1Args &a, uint32_t tag, int nblk, int8_t *shq, float *shs, int *s_to) {
     const int tid = threadIdx.x;
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     if (tid == 0) *s_to = 0;
-    for (int pass = 0; pass < 2; pass++) {
-        const int per = pass == 0 ? 1 : 5;
-        for (int i = 0; i < (1 << 24); i++) {
-            int stale = 0;
-            for (int u = tid; u < nblk * per; u += 512) {
-                const int b = pass == 0 ? u : u / 5, wi = pass == 0 ? 5 : u - 5 * (u / 5);
-                const unsigned long long v =
-                    __hip_atomic_load(a.hw + 6 * b + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if ((uint32_t)(v >> 48) != tag) {
-                    stale = 1;
-                } else if (wi == 5) {
-                    *reinterpret_cast<uint16_t *>(shq + 32 * b + 30) = (uint16_t)v;
-                    shs[b] = u2f((uint32_t)(v >> 16));
-                } else {
-                    uint16_t *d = reinterpret_cast<uint16_t *>(shq + 32 * b + 6 * wi);
-                    d[0] = (uint16_t)v;
-                    d[1] = (uint16_t)(v >> 16);
-                    d[2] = (uint16_t)(v >> 32);
-                }
-            }
-            if (tid == 0 && __builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) *s_to = 1;
-            if (!__syncthreads_or(stale) || *s_to) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
+    int have0 = tid < nblk ? 0 : 63, have1 = tid + 512 < nblk ? 0 : 63;  // words in, per block
+    bool full = false;
+    for (int i = 0; i < (1 << 24); i++) {
+        if (have0 != 63)
+            have0 |= ffn1_h_words(a.hw, tid, full || (have0 & 32) ? 63 & ~have0 : 32, tag, shq, shs);
+        if (have1 != 63)
+            have1 |= ffn1_h_words(a.hw, tid + 512, full || (have1 & 32) ? 63 & ~have1 : 32, tag, shq, shs);
+        if (tid == 0 && __builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) *s_to = 1;
+        if (__syncthreads_count(have0 == 63 && have1 == 63) == 512 || *s_to) break;
+        full = full || 2 * __syncthreads_count((have0 & 32) != 0) >= nblk;
+        __builtin_amdgcn_s_sleep(1);
     }
     if (tid == 0 && *s_to) __hip_atomic_store(a.err, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();

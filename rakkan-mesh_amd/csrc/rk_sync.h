@@ -1,7 +1,6 @@
 // rk_sync.h — a hand-off between the workgroups of one launch, for gfx950:
 // producer workgroups store their part, waiting workgroups read it once all
-// producers of the launch are done (used by the values-and-Wo launch and by
-// the one-token MoE feed-forward).
+// producers of the launch are done (the values-and-Wo launch).
 #pragma once
 
 #include "rk_dev.h"
@@ -69,40 +68,6 @@ __device__ __forceinline__ void sync_wait_ready(unsigned long long *sync, int nw
         if (!ok) __hip_atomic_store(err, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     asm volatile("s_barrier" ::: "memory");
-}
-
-// The last-arrival form, for a launch whose parts are combined by one of its
-// own workgroups (no workgroup waits): every wave of a workgroup that has
-// stored its part with agent-scope stores calls it; the workgroup counts
-// itself done in `count` (n of them a launch), and the call returns true in
-// the one whose add completes the launch's count, all other parts then
-// being complete. One barrier; s_last: a word of static LDS.
-__device__ __forceinline__ bool sync_last_done(unsigned long long *count, int n, int *s_last) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned long long old =
-            __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *s_last = (old + 1) % (unsigned long long)n == 0;
-    }
-    __syncthreads();
-    return *s_last != 0;
-}
-
-// The same, returning the launch's number (1, 2, ...) in every thread of
-// the workgroup whose add completes the launch's count, and 0 in every
-// other workgroup. s_n: a word of static LDS.
-__device__ __forceinline__ unsigned long long sync_last_number(unsigned long long *count, int n,
-                                                               unsigned long long *s_n) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's stores are complete
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned long long old =
-            __hip_atomic_fetch_add(count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *s_n = (old + 1) % (unsigned long long)n == 0 ? (old + 1) / (unsigned long long)n : 0ull;
-    }
-    __syncthreads();
-    return *s_n;
 }
 
 }  // namespace rk
