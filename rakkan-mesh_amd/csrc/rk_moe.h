@@ -59,8 +59,8 @@ struct rk_moe {
 
 namespace rk {
 
-// 64-bit words of one layer's hand-off area for the one-token launch: two
-// sets of kSyncWords and the experts' tagged logits.
+// 64-bit words of one layer's hand-off area for the one-token launch (the
+// selection's lines, the tagged logits and h blocks, the count words).
 int64_t moe_sync_words(const rk_moe *m);
 
 // Bytes of a MoeScratch for `cap` tokens of m; with mem, also lays it out

@@ -1050,24 +1050,18 @@ __global__ __launch_bounds__(512) void moe_down1_kernel(const void *const *gptr,
 //  * nu up workgroups (place g, block hb of 32 hidden rows): the normed
 //    input, the wait for the selection, then the g-th selected expert's W1
 //    and W3 rows (four hidden rows a wave, eight lanes a row dot) and h as
-//    moe_up1_kernel's: one Q8_0 block, put at place g (ffn1_put_h).
+//    moe_up1_kernel's: one Q8_0 block, put at place g (tag_put_q8).
 //  * nd down workgroups of R = 64/k output rows of every selected expert:
 //    the W2 rows requested once the selection is seen, every block of h
-//    collected into LDS (ffn1_get_h), the row dots, and lane r adding row
+//    collected into LDS (tag_get_q8), the row dots, and lane r adding row
 //    r's k products by ascending expert from +0 into y; out = y or
 //    Canonical(out + y).
-// Every hand-off is a tagged word: 48 bits of data under the low 16 bits of
-// the launch's number, which each workgroup keeps for itself (its own
-// count word, read and written by it alone; launches of a stream run in
-// order). A reader polls, with agent-scope loads, until every word it needs
-// carries its launch's tag; no word is reset, no store waits for another,
-// and no atomic is involved (counts and flags on shared words measured
-// slower: atomics to one address serialise, and a store's acknowledgement
-// takes about a microsecond). The logits are one word each; the selection
-// is written by ascending expert index into every XCD's line (the experts
-// first, then their weights, which only the up rows' ends need); h's
-// 36-byte block is six words of six bytes. The words are the layer's own
-// (ffn1_sync_layout): tags count that layer's launches only.
+// Every hand-off is a tagged word (rk_sync.h), each workgroup keeping one
+// count word of its own (a layer's grid is fixed). The logits are one word
+// each; the selection is written by ascending expert index into every
+// XCD's line (the experts first, then their weights, which only the up
+// rows' ends need); h's blocks are tag_put_q8's six words. The words are
+// the layer's own (ffn1_sync_layout): tags count that layer's launches.
 // A workgroup waits only for workgroups before it in the grid, which are
 // dispatched before it, so the launch always drains. Every wait is bounded
 // by the device clock (kSyncTimeout); one that gives up sets *err and goes
@@ -1097,7 +1091,7 @@ struct Ffn1Args {
     // the layer's hand-off words (ffn1_sync_layout), zero when made
     unsigned long long *lines;  // [8][kFfn1LineWords] the selection, a line per XCD
     unsigned long long *lw;     // [experts] the tagged logits
-    unsigned long long *hw;     // [k][hidden/32][6] h's Q8_0 blocks as tagged words (ffn1_put_h)
+    unsigned long long *hw;     // [k][hidden/32][6] h's Q8_0 blocks as tagged words (tag_put_q8)
     unsigned long long *cnt;    // [nr + nu + nd] each workgroup's count of its launches
     unsigned long long *err;
     int nr, nu, nd;  // router, up and down workgroups
@@ -1320,88 +1314,10 @@ __device__ void ffn1_wait_line(const Ffn1Args &a, uint32_t tag, int off, int *s_
     }
 }
 
-// h's Q8_0 block (32 codes, then the scale: 36 bytes) as six words of six
-// bytes each under the launch's 16-bit tag, so a reader holding all six
-// words of its launch holds the block (no count, no wait for the stores).
-// By one wave: lanes 0-7 hold four codes each (pk), every lane the scale.
-__device__ __forceinline__ void ffn1_put_h(unsigned long long *hw, uint32_t pk, float d, uint32_t tag) {
-    const int lane = threadIdx.x & 63;
-    const int w = min(lane, 5), j0 = (6 * w) >> 2, o = (6 * w) & 3;  // bytes 6w.. from dword j0, byte o (0 or 2)
-    const uint32_t lo = __shfl(pk, j0), hi0 = __shfl(pk, min(j0 + 1, 7));
-    const uint32_t hi = j0 + 1 == 8 ? f2u(d) : hi0;
-    const unsigned long long bytes = (((unsigned long long)hi << 32) | lo) >> (8 * o);
-    if (lane < 6)
-        __hip_atomic_store(hw + lane, ((unsigned long long)tag << 48) | (bytes & 0xFFFFFFFFFFFFull), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// One block's six words read (agent-scope) into LDS (codes shq, scale
-// shs) for those of them in `want` (bit i: word i) that carry the tag;
-// returns the bits of the words read.
-__device__ __forceinline__ int ffn1_h_words(const unsigned long long *hw, int b, int want, uint32_t tag, int8_t *shq,
-                                            float *shs) {
-    int got = 0;
-#pragma unroll
-    for (int wi = 0; wi < 6; wi++) {
-        if (!(want >> wi & 1)) continue;
-        const unsigned long long v = __hip_atomic_load(hw + 6 * b + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if ((uint32_t)(v >> 48) != tag) continue;
-        got |= 1 << wi;
-        if (wi == 5) {
-            *reinterpret_cast<uint16_t *>(shq + 32 * b + 30) = (uint16_t)v;
-            shs[b] = u2f((uint32_t)(v >> 16));
-        } else {
-            uint16_t *d = reinterpret_cast<uint16_t *>(shq + 32 * b + 6 * wi);
-            d[0] = (uint16_t)v;
-            d[1] = (uint16_t)(v >> 16);
-            d[2] = (uint16_t)(v >> 32);
-        }
-    }
-    return got;
-}
-
-// The k·nhb blocks of h of launch `tag` into LDS (codes shq [block][32],
-// scales shs [block]), by the whole workgroup; thread t takes blocks t and
-// t + 512. While fewer than half the blocks are in, a round reads only a
-// block's last word (its scale: one word a block of polling); a block whose
-// last word is in reads the other five next round; once half are in, a
-// round reads all of a missing block's words (one round trip after its
-// stores land). A wait that gives up sets *err.
-__device__ void ffn1_get_h(const Ffn1Args &a, uint32_t tag, int nblk, int8_t *shq, float *shs, int *s_to) {
-    const int tid = threadIdx.x;
-    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-    if (tid == 0) *s_to = 0;
-    int have0 = tid < nblk ? 0 : 63, have1 = tid + 512 < nblk ? 0 : 63;  // words in, per block
-    bool full = false;
-    for (int i = 0; i < (1 << 24); i++) {
-        if (have0 != 63)
-            have0 |= ffn1_h_words(a.hw, tid, full || (have0 & 32) ? 63 & ~have0 : 32, tag, shq, shs);
-        if (have1 != 63)
-            have1 |= ffn1_h_words(a.hw, tid + 512, full || (have1 & 32) ? 63 & ~have1 : 32, tag, shq, shs);
-        if (tid == 0 && __builtin_amdgcn_s_memrealtime() - t0 > kSyncTimeout) *s_to = 1;
-        if (__syncthreads_count(have0 == 63 && have1 == 63) == 512 || *s_to) break;
-        full = full || 2 * __syncthreads_count((have0 & 32) != 0) >= nblk;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    if (tid == 0 && *s_to) __hip_atomic_store(a.err, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-}
-
-// This workgroup's launch number: its own count, one more (read and
-// written by this workgroup alone, launches of a stream being in order).
-__device__ __forceinline__ void ffn1_count(const Ffn1Args &a, unsigned long long *s_n) {
-    if (threadIdx.x == 0) {
-        const unsigned long long n = a.cnt[blockIdx.x] + 1;
-        a.cnt[blockIdx.x] = n;
-        *s_n = n;
-    }
-}
-
 template <int BU, int BD>
 __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
     extern __shared__ __align__(16) char flds[];
     __shared__ float bcast;
-    __shared__ unsigned long long s_n;
     __shared__ int s_e[kFfn1MaxK];
     __shared__ float s_w[kFfn1MaxK];
     __shared__ int s_to;
@@ -1414,7 +1330,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
     float *sxs = reinterpret_cast<float *>(flds + L.sxs);
     float *sn = reinterpret_cast<float *>(flds + L.sn);
     const void **stab = reinterpret_cast<const void **>(flds + L.role);
-    ffn1_count(a, &s_n);
+    const unsigned long long cnt0 = a.cnt[bid];  // this workgroup's own count (a layer's grid is fixed)
 
     if (bid >= a.nr + a.nu) {
         // ---- down: output rows R·di .. R·di+R-1 of every selected expert;
@@ -1428,7 +1344,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
         float *sv = reinterpret_cast<float *>(flds + L.sv);
         for (int t = tid; t < 2 * E; t += 512) stab[t] = t < E ? (const void *)a.w2[t] : (const void *)a.s2[t - E];
         __syncthreads();
-        const uint32_t tag = (uint32_t)s_n & 0xFFFFu;
+        const uint32_t tag = tag_of(tag_take(cnt0, a.cnt + bid, 1));
         if (wave == 0) ffn1_wait_line(a, tag, 0, s_e, nullptr);
         __syncthreads();
         const int e = s_e[g];
@@ -1436,7 +1352,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
         float sw[BD];
         lane_row_load<BD>(c0, c1, sw, static_cast<const uint8_t *>(stab[e]) + i * H,
                           static_cast<const float *>(stab[E + e]) + i * nhb, nhb, rl);
-        ffn1_get_h(a, tag, k * nhb, shq, shs, &s_to);
+        tag_get_q8<512>(a.hw, k * nhb, tag, shq, shs, a.err, &s_to);
         const float v = tree8(lane_running_sum<BD>(c0, c1, sw, shq + g * H, shs + g * nhb, nhb, rl));
         if (rl == 0 && gi < k * R) sv[gi] = v;
         __syncthreads();
@@ -1463,7 +1379,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
         const int4 c0 = load_stream16_g(rp), c1 = load_stream16_g(rp + 16);
         const float sw = loadf_g(a.rws + rr * nb + b);
         ffn1_norm_quant(xv, wv, dim, a.recip_n, a.eps, sq, sxs, sn, &bcast);
-        const uint32_t tag = (uint32_t)s_n & 0xFFFFu;
+        const uint32_t tag = tag_of(tag_take(cnt0, a.cnt + bid, 1));
         const int4 *xp = reinterpret_cast<const int4 *>(sq + 32 * b);
         const int sm = dot16(c1, xp[1], dot16(c0, xp[0], 0));
         const float t = (float)sm * (sw * sxs[b]);
@@ -1502,7 +1418,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
                                                                                             : (const void *)a.s3[e];
     }
     ffn1_norm_quant(xv, wv, dim, a.recip_n, a.eps, sq, sxs, sn, &bcast);
-    const uint32_t tag = (uint32_t)s_n & 0xFFFFu;
+    const uint32_t tag = tag_of(tag_take(cnt0, a.cnt + bid, 1));
     if (wave == 0) ffn1_wait_line(a, tag, 0, s_e, nullptr);
     __syncthreads();
     const int e = s_e[g];
@@ -1524,7 +1440,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
         float d;
         int cs;
         const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
-        ffn1_put_h(a.hw + 6 * ((int64_t)g * nhb + hb), pk, d, tag);
+        tag_put_q8(a.hw + 6 * ((int64_t)g * nhb + hb), pk, d, tag);
     }
 }
 
