@@ -561,11 +561,15 @@ def decode_bench(dev, rkhip, args):
     # xorshift64* state on the device (sample.go:26-43): the step ends with
     # the sampler's launches instead of the argmax's.
     st.sampler(0.8, 1234)
+    if args.eager:
+        dev.profile_start()
     st.generate_start(prompt)
     st.generate_run(prompt_len)
     t3 = time.perf_counter()
     st.generate_run(steps - 9)
     t4 = time.perf_counter()
+    if args.eager:
+        dev.profile_stop()
     dev.profile_start()
     st.generate_run(8)
     prof_s = dev.profile_stop()
@@ -777,14 +781,22 @@ def moe_bench(dev, rkhip, args):
         if args.eager:
             dev.profile_stop()
         ms_step = el / (steps - 1) * 1e3
+
+        def start_outside_profile():  # (batch 1's start runs the prompt: eager too under --eager)
+            if args.eager:
+                dev.profile_start()
+            start()
+            if args.eager:
+                dev.profile_stop()
+
         # per-kernel times: eager launches stamped one by one, after one
         # unstamped eager step (the first eager launches pay one-time host
         # work between a kernel's start event and its dispatch)
-        start()
+        start_outside_profile()
         dev.profile_start()
         run(1)
         dev.profile_stop()
-        start()
+        start_outside_profile()
         dev.profile_start()
         run(4)
         prof = dev.profile_stop()
