@@ -171,11 +171,19 @@ void launch_att_values(const float *att, int32_t att_stride, const float *vals, 
 // (kSyncWords words). The results are those of the two launches, bit for
 // bit. False (nothing launched) when the shapes are not the ones it takes:
 // a Q8_0 Wo of 3073..4096 columns (heads·hs, hs a multiple of 32), rows a
-// multiple of the workgroup's.
+// multiple of the workgroup's. With qk (a QK-norm layer's raw q, k and v,
+// contexts up to 256, hs = 128, else false) the launch also forms the
+// scores (launch_att_scores_qkn's work, the same bits), so it is the whole
+// attention of the step after the QKV product.
+struct QknIn {
+    const float *q_raw, *k_raw, *v_raw, *q_norm, *k_norm, *cos_t, *sin_t;
+    float *keys, *vals;  // the caches, where the position's k and v go
+    float recip_hs, eps, inv_sqrt;
+};
 bool launch_att_values_wo(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                           int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
                           const uint8_t *wo_w, const float *wo_ws, int64_t wo_rows, int64_t wo_cols, float *x,
-                          unsigned long long *sync, hipStream_t s);
+                          unsigned long long *sync, hipStream_t s, const QknIn *qk = nullptr);
 // QK-norm (Qwen3) and RoPE of raw q and k heads, k and v into the caches, at
 // the position in ctl (or, ctl null, for `tokens` rows at pos0, pos0+1, ...;
 // or, seq_pos set, row z at seq_pos[z] in caches cache_stride floats apart).

@@ -667,6 +667,42 @@ __device__ __forceinline__ void qk_norm_rope_wave(const float *x, const float *w
     }
 }
 
+// qk_norm_rope_wave's steps for hs = 128 on inputs loaded ahead into
+// registers (qk_row_load, issued before other loads so that the norm waits
+// only for its own): lane l < 32 keeps x_l, x_l+32, x_l+64, x_l+96 for the
+// Dot32 running sum l; lane p the pair (2p, 2p+1), its weights and table
+// entry p.
+struct QkRow {
+    float d[4], x0, x1, w0, w1, co, si;
+};
+
+__device__ __forceinline__ void qk_row_load(const float *x, const float *w, const float *cos_t, const float *sin_t,
+                                            int pos, QkRow &r) {
+    const int lane = threadIdx.x & 63, hl = lane & 31;
+#pragma unroll
+    for (int k = 0; k < 4; k++) r.d[k] = x[hl + 32 * k];
+    r.x0 = x[2 * lane];
+    r.x1 = x[2 * lane + 1];
+    r.w0 = w[2 * lane];
+    r.w1 = w[2 * lane + 1];
+    r.co = cos_t[(int64_t)pos * 64 + lane];
+    r.si = sin_t[(int64_t)pos * 64 + lane];
+}
+
+__device__ __forceinline__ void qk_row_norm_rope(const QkRow &r, float recip_hs, float eps, float *dst) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
+    if (lane < 32) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) s += r.d[k] * r.d[k];
+    }
+    const float dot = __shfl(dot32_reduce(s), 0);
+    const float rr = rsqrt32((dot * recip_hs) + eps);
+    const float v0 = r.w0 * (rr * r.x0), v1 = r.w1 * (rr * r.x1);
+    dst[2 * lane] = (v0 * r.co) - (v1 * r.si);
+    dst[2 * lane + 1] = (v0 * r.si) + (v1 * r.co);
+}
+
 // The scores of a decode step (or of independent sequences) with the
 // QK-norm and RoPE of the position's q and k folded in: wave 0 normalizes
 // the workgroup's q head into LDS, wave 1 (in the tile that holds the
@@ -816,11 +852,19 @@ constexpr int kValQuads = kValThreads / (kValSlice / 4);             // position
 //
 // The body for head bh, slice by and token z; SIG as att_values_reg_body's
 // (the Q8_0 block handed to the Wo workgroups of att_values_wo_kernel).
-template <bool VEC, int CH, bool SIG>
+// QKN (a decode step, hs = 128, contexts up to 256; qk given): the scores
+// are formed here from the raw q and k rows (att_scores_qkn_kernel's
+// steps: QK-norm and RoPE of q's head and of the position's key into LDS,
+// each cached key of the kv head read by a quad of lanes at the start),
+// one workgroup per kv head stores the position's k and v into the caches,
+// and the position's own value row is read from v_raw (no workgroup of
+// the launch reads the caches at the position).
+template <bool VEC, int CH, bool SIG, bool QKN = false>
 __device__ __forceinline__ void att_values_body(const float *att, int32_t att_stride, const float *vals, float *out,
                                                 const int32_t *ctl, const AttBatch &bt, int kv_mul, int hs,
                                                 int kv_dim, int ctx_pad, int8_t *qx, float *xs, int32_t *xsum, int bh,
-                                                int by, int z, unsigned long long *sync, int na) {
+                                                int by, int z, unsigned long long *sync, int na,
+                                                const QknIn *qk = nullptr) {
     extern __shared__ __align__(16) float smem[];
     __shared__ float s_red[kValThreads / 64];
     __shared__ float s_inv;
@@ -855,7 +899,8 @@ __device__ __forceinline__ void att_values_body(const float *att, int32_t att_st
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int t = min(c0 + 4 * (pq + kValQuads * r) + j, T - 1);
-                const float *row = vbase + (int64_t)t * kv_dim;
+                const float *row =
+                    QKN && t == T - 1 ? qk->v_raw + (int64_t)g * hs + e0 : vbase + (int64_t)t * kv_dim;
                 if (VEC) {
                     vr[r][j] = *reinterpret_cast<const float4 *>(row + min(4 * fq, ne - 4));
                 } else {
@@ -871,32 +916,134 @@ __device__ __forceinline__ void att_values_body(const float *att, int32_t att_st
     const float *ah = att + (int64_t)h * att_stride;
     constexpr int kScPer = 1024 / kValThreads;
     float sv[kScPer];
+    if (QKN) {
+        static_assert(!QKN || (CH == kValShortChunk && kValThreads == 256), "QKN: the short form");
+        __shared__ __align__(16) float sq[128], sk[128];
+        const int pos = T - 1, sub = tid & 3;
+        // waves 0 and 1: q's head and the position's key, requested first
+        QkRow qr;
+        if (wave == 0)
+            qk_row_load(qk->q_raw + (int64_t)h * 128, qk->q_norm, qk->cos_t, qk->sin_t, pos, qr);
+        else if (wave == 1)
+            qk_row_load(qk->k_raw + (int64_t)g * 128, qk->k_norm, qk->cos_t, qk->sin_t, pos, qr);
+        // lane sub of position t: elements 8·sub + 32·it + 0..7 of its key
+        auto load_key = [&](int t, float4 (&kr)[4][2]) {
+            const float *kg = qk->keys + (int64_t)(t < T ? t : 0) * kv_dim + (int64_t)g * 128 + 8 * sub;
 #pragma unroll
-    for (int k = 0; k < kScPer; k++) sv[k] = ah[min(tid + kValThreads * k, T - 1)];
-    load_chunk(0);
-
-    // softmax of the head's scores
-    float m = sv[0];
+            for (int it = 0; it < 4; it++) {
+                kr[it][0] = *reinterpret_cast<const float4 *>(kg + 32 * it);
+                kr[it][1] = *reinterpret_cast<const float4 *>(kg + 32 * it + 4);
+            }
+        };
+        // Dot32(q, k_t)·inv_sqrt on the held key (quad_dot32's steps; the
+        // position's own key from LDS), valid in the quad's lane 0
+        auto score = [&](int t, float4 (&kr)[4][2]) -> float {
+            if (t == pos) {
 #pragma unroll
-    for (int k = 0; k < kScPer; k++) {
-        if (tid + kValThreads * k < T) {
-            sa[tid + kValThreads * k] = sv[k];
-            m = gomax(m, sv[k]);
+                for (int it = 0; it < 4; it++) {
+                    kr[it][0] = *reinterpret_cast<const float4 *>(sk + 8 * sub + 32 * it);
+                    kr[it][1] = *reinterpret_cast<const float4 *>(sk + 8 * sub + 32 * it + 4);
+                }
+            }
+            float sacc[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) sacc[k] = 0.0f;
+#pragma unroll
+            for (int it = 0; it < 4; it++) {
+                const float4 q0 = *reinterpret_cast<const float4 *>(sq + 8 * sub + 32 * it);
+                const float4 q1 = *reinterpret_cast<const float4 *>(sq + 8 * sub + 32 * it + 4);
+                sacc[0] += q0.x * kr[it][0].x;
+                sacc[1] += q0.y * kr[it][0].y;
+                sacc[2] += q0.z * kr[it][0].z;
+                sacc[3] += q0.w * kr[it][0].w;
+                sacc[4] += q1.x * kr[it][1].x;
+                sacc[5] += q1.y * kr[it][1].y;
+                sacc[6] += q1.z * kr[it][1].z;
+                sacc[7] += q1.w * kr[it][1].w;
+            }
+            float e[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const float u = sacc[k] + dppf_x1(sacc[k]);
+                e[k] = u + dppf_x2(u);
+            }
+            return (((e[0] + e[1]) + (e[2] + e[3])) + ((e[4] + e[5]) + (e[6] + e[7]))) * qk->inv_sqrt;
+        };
+        // positions in rounds of 64 (a quad each): two rounds' keys in
+        // flight at the start, the rest (contexts past 128) after
+        const int t0 = tid >> 2;
+        float4 ka[4][2], kb[4][2];
+        load_key(t0, ka);
+        if (T > 64) load_key(t0 + 64, kb);  // uniform
+        load_chunk(0);
+        if (wave < 2) qk_row_norm_rope(qr, qk->recip_hs, qk->eps, wave == 0 ? sq : sk);
+        __syncthreads();
+        if (h % kv_mul == 0 && by == 0 && wave == 2) {
+            // the kv head's first workgroup: the position's k and v into
+            // the caches (read by the next launches)
+            float *kd = qk->keys + (int64_t)pos * kv_dim + (int64_t)g * 128;
+            float *vd = qk->vals + (int64_t)pos * kv_dim + (int64_t)g * 128;
+            const float *vs = qk->v_raw + (int64_t)g * 128;
+            for (int i = lane; i < 128; i += 64) {
+                kd[i] = sk[i];
+                vd[i] = vs[i];
+            }
         }
-    }
-    for (int t = tid + kValThreads * kScPer; t < T; t += kValThreads) {
-        const float v = ah[t];
-        sa[t] = v;
-        m = gomax(m, v);
-    }
-    m = wave_gomax(m);
-    if (lane == 0) s_red[wave] = m;
-    __syncthreads();
-    m = s_red[0];
+        // the scores in registers (quad lane 0: position t0 + 64r), their
+        // maximum (Go max, any order; -inf leaves it unchanged)
+        float dsc[4];
+        float m = -__builtin_huge_valf();
+        dsc[0] = score(t0, ka);
+        if (T > 64) dsc[1] = score(t0 + 64, kb);
+        if (T > 128) {  // uniform
+            load_key(t0 + 128, ka);
+            if (T > 192) load_key(t0 + 192, kb);
+            dsc[2] = score(t0 + 128, ka);
+            if (T > 192) dsc[3] = score(t0 + 192, kb);
+        }
 #pragma unroll
-    for (int w = 1; w < kValThreads / 64; w++) m = gomax(m, s_red[w]);
-    for (int t = tid; t < T; t += kValThreads) sa[t] = exp32(sa[t] - m);
-    __syncthreads();
+        for (int r = 0; r < 4; r++)
+            if (sub == 0 && t0 + 64 * r < T) m = gomax(m, dsc[r]);
+        m = wave_gomax(m);
+        if (lane == 0) s_red[wave] = m;
+        __syncthreads();
+        m = s_red[0];
+#pragma unroll
+        for (int w = 1; w < kValThreads / 64; w++) m = gomax(m, s_red[w]);
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+            if (sub == 0 && t0 + 64 * r < T) sa[t0 + 64 * r] = exp32(dsc[r] - m);
+        __syncthreads();
+    } else {
+#pragma unroll
+        for (int k = 0; k < kScPer; k++) sv[k] = ah[min(tid + kValThreads * k, T - 1)];
+        load_chunk(0);
+    }
+
+    if (!QKN) {
+        // softmax of the head's scores
+        float m = sv[0];
+#pragma unroll
+        for (int k = 0; k < kScPer; k++) {
+            if (tid + kValThreads * k < T) {
+                sa[tid + kValThreads * k] = sv[k];
+                m = gomax(m, sv[k]);
+            }
+        }
+        for (int t = tid + kValThreads * kScPer; t < T; t += kValThreads) {
+            const float v = ah[t];
+            sa[t] = v;
+            m = gomax(m, v);
+        }
+        m = wave_gomax(m);
+        if (lane == 0) s_red[wave] = m;
+        __syncthreads();
+        m = s_red[0];
+#pragma unroll
+        for (int w = 1; w < kValThreads / 64; w++) m = gomax(m, s_red[w]);
+        for (int t = tid; t < T; t += kValThreads) sa[t] = exp32(sa[t] - m);
+        __syncthreads();
+    }
     if (tid == 0) s_inv = recip32(lds_chain_sum(sa, T, 0.0f));
     __syncthreads();
     const float inv = s_inv;
@@ -1269,6 +1416,7 @@ struct AttWoArgs {
     int rows, cols;
     unsigned long long *sync;
     int na, nw;  // values workgroups (producers), Wo workgroups
+    QknIn qk;    // the QKN form's raw rows
 };
 
 // Wo rows a wave. With the register-held values (contexts past 256; about
@@ -1375,13 +1523,17 @@ __device__ __forceinline__ void wo_after_values(const AttWoArgs &a, int wi) {
 // are dispatched first: a waiting workgroup never holds a place a producer
 // still needs. SHORT: contexts up to 256 (att_values_kernel's work, 4
 // waves), else att_values_reg_kernel's (8 waves).
-template <int C, bool SHORT>
+// QKN: the short form with the scores formed in the values workgroups
+// (att_values_body's QKN).
+template <int C, bool SHORT, bool QKN = false>
 __global__ __launch_bounds__(SHORT ? kValThreads : kVrThreads) void att_values_wo_kernel(AttWoArgs a) {
+    static_assert(!QKN || SHORT, "QKN: the short form");
     if ((int)blockIdx.x < a.na) {
         if (SHORT)
-            att_values_body<true, kValShortChunk, true>(a.att, a.att_stride, a.vals, a.out, a.ctl, AttBatch{},
-                                                        a.kv_mul, a.hs, a.kv_dim, a.ctx_pad, a.qx, a.xs, a.xsum,
-                                                        blockIdx.x / a.nsl, blockIdx.x % a.nsl, 0, a.sync, a.na);
+            att_values_body<true, kValShortChunk, true, QKN>(a.att, a.att_stride, a.vals, a.out, a.ctl, AttBatch{},
+                                                             a.kv_mul, a.hs, a.kv_dim, a.ctx_pad, a.qx, a.xs, a.xsum,
+                                                             blockIdx.x / a.nsl, blockIdx.x % a.nsl, 0, a.sync, a.na,
+                                                             &a.qk);
         else
             att_values_reg_body<true>(a.att, a.att_stride, a.vals, a.out, a.ctl, AttBatch{}, a.kv_mul, a.hs,
                                       a.kv_dim, a.nsl, a.ctx_pad, a.qx, a.xs, a.xsum, blockIdx.x, 0, a.sync, a.na);
@@ -1393,8 +1545,9 @@ __global__ __launch_bounds__(SHORT ? kValThreads : kVrThreads) void att_values_w
 bool launch_att_values_wo(const float *att, int32_t att_stride, const float *vals, float *out, const int32_t *ctl,
                           int ctx, int heads, int kv_heads, int hs, int kv_dim, int8_t *qx, float *xs, int32_t *xsum,
                           const uint8_t *wo_w, const float *wo_ws, int64_t wo_rows, int64_t wo_cols, float *x,
-                          unsigned long long *sync, hipStream_t s) {
+                          unsigned long long *sync, hipStream_t s, const QknIn *qk) {
     const bool shrt = ctx <= kValShortCtx;
+    if (qk && (!shrt || hs != 128 || kv_dim != kv_heads * hs)) return false;
     const int wo_rows_wg = kWoRowsPerWave * (shrt ? kValThreads : kVrThreads) / 64;
     if (!ctl || !qx || !sync || ctx > kVrMaxCtx || hs % 32 != 0 || kv_dim % 4 != 0 ||
         (!shrt && (reinterpret_cast<uintptr_t>(vals) & 15) != 0))
@@ -1433,8 +1586,14 @@ bool launch_att_values_wo(const float *att, int32_t att_stride, const float *val
         const int ctx_pad = (ctx + 3) & ~3;
         const size_t lds = ctx <= kValShortChunk ? (size_t)(ctx_pad + kValSlice * val_pitch(kValShortChunk)) * 4
                                                  : att_values_lds(ctx, kValShortChunk);
-        RK_LAUNCH((att_values_wo_kernel<4, true>), dim3((unsigned)(a.na + a.nw)), dim3(kValThreads),
-                  std::max(lds, wo_lds), s, a);
+        if (qk) {
+            a.qk = *qk;
+            RK_LAUNCH((att_values_wo_kernel<4, true, true>), dim3((unsigned)(a.na + a.nw)), dim3(kValThreads),
+                      std::max(lds, wo_lds), s, a);
+        } else {
+            RK_LAUNCH((att_values_wo_kernel<4, true>), dim3((unsigned)(a.na + a.nw)), dim3(kValThreads),
+                      std::max(lds, wo_lds), s, a);
+        }
     } else {
         RK_LAUNCH((att_values_wo_kernel<4, false>), dim3((unsigned)(a.na + a.nw)), dim3(kVrThreads),
                   std::max(att_values_reg_lds(ctx), wo_lds), s, a);

@@ -186,6 +186,16 @@ static bool enqueue_attention(rk_stage *s, hipStream_t st, const float *q, float
     float *xs = qo ? qo->xs : nullptr;
     int32_t *xsum = qo ? qo->xsum : nullptr;
     bool scored = false;
+    if (qk && wo && wo->kind == RK_Q8 && ctl && qo) {
+        // a decode step of a QK-norm layer: the scores formed in the values
+        // launch (contexts up to 256)
+        const QknIn in{q,    qk->k, qk->v,        qk->q_norm, qk->k_norm, s->cos_t, s->sin_t,
+                       keys, vals,  c.recip_head, c.norm_eps, c.inv_sqrt};
+        ProfScope p(d, st, "att_values_wo");
+        if (launch_att_values_wo(att, c.ctx, vals, out, ctl, c.ctx, c.heads, c.kv_heads, s->hs, s->kvdim, qx, xs, xsum,
+                                 wo->w, wo->scales, wo->rows, wo->cols, x, s->sync, st, &in))
+            return true;
+    }
     if (qk) {
         {
             // a decode step or independent sequences: the norm folded into

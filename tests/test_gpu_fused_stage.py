@@ -227,6 +227,19 @@ def test_generation_real_shapes_one_layer(dev, name):
     check_generation(dev, m, [11, 7000, 123, 99], 12, 64)
 
 
+def test_generation_qk_norm_scores_in_the_values_launch_to_256(dev):
+    """A QK-norm layer's decode step with head size 128 at contexts up to 256
+    forms its scores inside the values-and-Wo launch (one quad of lanes a
+    cached key, in rounds of 64 positions; one workgroup per kv head storing
+    the position's k and v). Positions 99..255 reach every round, every logit
+    bitwise."""
+    c = Config(dim=256, hidden=128, layers=2, heads=32, kv_heads=4, vocab=64, seq_len=256, head_dim=128,
+               rope_theta=1000000.0, qk_norm=True, norm_eps=1e-6, dtype="q8_0")
+    m = coded_model(c, 12)
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, c.vocab, 100)]
+    check_generation(dev, m, prompt, 156, 256)
+
+
 @pytest.mark.parametrize("case", ["kv2_ctx1024", "kv2_ctx1100", "kv8_gqa_ctx1000"])
 def test_generation_long_context(dev, case):
     """Decode at positions up to the end of a long context, every logit
