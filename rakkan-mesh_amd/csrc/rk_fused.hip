@@ -868,6 +868,7 @@ __device__ __forceinline__ void att_values_body(const float *att, int32_t att_st
     extern __shared__ __align__(16) float smem[];
     __shared__ float s_red[kValThreads / 64];
     __shared__ float s_inv;
+    __shared__ __align__(16) float s_res[kValSlice];
     float *sa = smem;            // [ctx_pad] scores -> weights
     constexpr int kValPitch = val_pitch(CH), kValRounds = CH / (4 * kValQuads);
     static_assert(kValRounds >= 1, "a chunk is whole rounds");
@@ -1080,13 +1081,12 @@ __device__ __forceinline__ void att_values_body(const float *att, int32_t att_st
     if (wave == 0 && lane < ne) out[(int64_t)h * hs + e0 + lane] = acc;
     if (qx && ne == kValSlice) {
         // the slice is one Q8_0 block of the next input (e0 is a multiple
-        // of 32): lanes 0-7 take four values each
-        __syncthreads();  // every wave is past its last product write
-        if (wave == 0 && lane < kValSlice) sp[lane] = acc;
-        __syncthreads();
+        // of 32): lanes 0-7 of wave 0 take four values each, through a
+        // buffer only wave 0 touches (no barrier)
         if (wave == 0) {
+            if (lane < kValSlice) s_res[lane] = acc;
             const int q = min(lane, 7);
-            const float4 v4 = reinterpret_cast<const float4 *>(sp)[q];
+            const float4 v4 = reinterpret_cast<const float4 *>(s_res)[q];
             float d;
             int cs;
             const uint32_t pk = quantize_group(v4.x, v4.y, v4.z, v4.w, d, cs);
