@@ -368,6 +368,72 @@ __device__ __forceinline__ float tree8(float acc) {
     return acc + __int_as_float(dpp_mirror8(__float_as_int(acc)));
 }
 
+// ---- The same row dots with the row read in contiguous 16-byte pieces (a
+// 128-byte line per load instruction and row): at step k (k < 2·BPL) lane
+// rl holds half rl & 1 of block 4k + rl/2, so a lane pair holds a block
+// and pair_sum gives its exact sum in both lanes. Lane 2p keeps running sum
+// p (the even steps: blocks 8m + p) and lane 2p+1 running sum 4 + p (the
+// odd steps: blocks 8m + 4 + p), each in block order from +0; tree8_pair
+// forms the same tree. Measured on MI355X: 64 rows a workgroup read about
+// 15 % faster than as whole 32-byte blocks a lane; it holds more registers
+// where a row is summed against several inputs, so the kernels that run at
+// four waves a SIMD on the first form keep it. ----
+
+// The running sum a lane keeps (its m-th term is block L + 8m).
+__device__ __forceinline__ int pair_sum_index(int rl) { return (rl & 1) ? 4 + (rl >> 1) : rl >> 1; }
+
+// c0[m] at byte 256m + 16·rl, c1[m] at 256m + 128 + 16·rl (clamped into
+// the row: what lies past it is never summed), and the scales of the
+// lane's own blocks.
+template <int BPL, bool STREAM = true>
+__device__ __forceinline__ void lane_row_load_pair(int4 (&c0)[BPL], int4 (&c1)[BPL], float (&sw)[BPL],
+                                                   const uint8_t *row, const float *rs, int nb, int rl) {
+    const int last = 32 * nb - 16, L = pair_sum_index(rl);
+#pragma unroll
+    for (int m = 0; m < BPL; m++) {
+        const int o0 = min(256 * m + 16 * rl, last), o1 = min(256 * m + 128 + 16 * rl, last);
+        if (STREAM) {
+            c0[m] = load_stream16_g(row + o0);
+            c1[m] = load_stream16_g(row + o1);
+        } else {
+            c0[m] = load16_g(row + o0);
+            c1[m] = load16_g(row + o1);
+        }
+        sw[m] = loadf_g(rs + min(L + 8 * m, nb - 1));
+    }
+}
+
+// The lane's running sum of the row held by lane_row_load_pair with one
+// input, from +0. Every lane of the group calls it.
+template <int BPL>
+__device__ __forceinline__ float lane_running_sum_pair(const int4 (&c0)[BPL], const int4 (&c1)[BPL],
+                                                       const float (&sw)[BPL], const int8_t *xq, const float *xsc,
+                                                       int nb, int rl) {
+    const int last = 32 * nb - 16, L = pair_sum_index(rl);
+    const bool odd = rl & 1;
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < BPL; m++) {
+        const int o0 = min(256 * m + 16 * rl, last), o1 = min(256 * m + 128 + 16 * rl, last);
+        const int s0 = pair_sum(dot16(c0[m], *reinterpret_cast<const int4 *>(xq + o0), 0));
+        const int s1 = pair_sum(dot16(c1[m], *reinterpret_cast<const int4 *>(xq + o1), 0));
+        const int b = L + 8 * m;
+        if (b < nb) acc += (float)(odd ? s1 : s0) * (sw[m] * xsc[b]);
+    }
+    return acc;
+}
+
+// The tree over running sums held as lane_running_sum_pair leaves them
+// (lane 2p: s_p, lane 2p+1: s_4+p): lanes 2 apart give s0+s1, s2+s3,
+// s4+s5, s6+s7; lanes 4 apart (the half-row mirror, then the quad
+// reversed) the two halves; then the lane pair. Valid in all eight lanes.
+__device__ __forceinline__ float tree8_pair(float acc) {
+    acc = acc + dppf_x2(acc);
+    const int m8 = dpp_mirror8(__float_as_int(acc));
+    acc = acc + __int_as_float(__builtin_amdgcn_mov_dpp(m8, 0x1B, 0xF, 0xF, false));
+    return acc + dppf_x1(acc);
+}
+
 // RMSNorm (internal/llm/model.go:632-638: ss = Dot32(x,x)·recip_n + eps,
 // out_i = w_i·(Rsqrt32(ss)·x_i)) of x, then the Q8_0 quantization
 // (internal/num/quant.go:34-53) of the result into qx/xs/xsum: the input of

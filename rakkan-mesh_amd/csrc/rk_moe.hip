@@ -924,8 +924,8 @@ __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const floa
     const float *srow = static_cast<const float *>(stab[(w3row ? 3 : 1) * experts + e]);
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, wrow + (int64_t)j * dim, srow + (int64_t)j * nb, nb, rl);
-    const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq, sxs, nb, rl));
+    lane_row_load_pair<BPL>(c0, c1, sw, wrow + (int64_t)j * dim, srow + (int64_t)j * nb, nb, rl);
+    const float v = tree8_pair(lane_running_sum_pair<BPL>(c0, c1, sw, sq, sxs, nb, rl));
     const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
     if ((lane & 15) == 0) sh[4 * wave + q] = s_w * silu_mul(v, v3);
     __syncthreads();
@@ -972,7 +972,7 @@ __global__ __launch_bounds__(256) void moe_down8_kernel(const void *const *gptr,
     __builtin_amdgcn_sched_barrier(0);
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, w2 + (int64_t)min(i, dim - 1) * hidden, s2 + (int64_t)min(i, dim - 1) * nb, nb,
+    lane_row_load_pair<BPL>(c0, c1, sw, w2 + (int64_t)min(i, dim - 1) * hidden, s2 + (int64_t)min(i, dim - 1) * nb, nb,
                        rl);
     __builtin_amdgcn_sched_barrier(0);
     const int n16 = hidden >> 4;
@@ -991,7 +991,7 @@ __global__ __launch_bounds__(256) void moe_down8_kernel(const void *const *gptr,
         }
         __syncthreads();
         for (int pi = 0; pi < np; pi++) {
-            const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq + pi * hidden, sxs + pi * nb, nb, rl));
+            const float v = tree8_pair(lane_running_sum_pair<BPL>(c0, c1, sw, sq + pi * hidden, sxs + pi * nb, nb, rl));
             if (rl == 0 && i < dim) o[(int64_t)spair[pi] * dim + i] = v;
         }
         __syncthreads();
@@ -1021,8 +1021,8 @@ __global__ __launch_bounds__(512) void moe_down1_kernel(const void *const *gptr,
     const int p = grp[1 + 3 * gcap + g];
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, w2 + (int64_t)min(i, dim - 1) * hidden, s2 + (int64_t)min(i, dim - 1) * nb, nb, rl);
-    const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, hq + (int64_t)p * hidden, hs + (int64_t)p * nb, nb, rl));
+    lane_row_load_pair<BPL>(c0, c1, sw, w2 + (int64_t)min(i, dim - 1) * hidden, s2 + (int64_t)min(i, dim - 1) * nb, nb, rl);
+    const float v = tree8_pair(lane_running_sum_pair<BPL>(c0, c1, sw, hq + (int64_t)p * hidden, hs + (int64_t)p * nb, nb, rl));
     if (rl == 0 && gi < k * R) sv[gi] = v;
     __syncthreads();
     if (tid < R && blockIdx.x * R + tid < dim) {
@@ -1350,10 +1350,10 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
         const int e = s_e[g];
         int4 c0[BD], c1[BD];
         float sw[BD];
-        lane_row_load<BD>(c0, c1, sw, static_cast<const uint8_t *>(stab[e]) + i * H,
+        lane_row_load_pair<BD>(c0, c1, sw, static_cast<const uint8_t *>(stab[e]) + i * H,
                           static_cast<const float *>(stab[E + e]) + i * nhb, nhb, rl);
         tag_get_q8<512>(a.hw, k * nhb, tag, shq, shs, a.err, &s_to);
-        const float v = tree8(lane_running_sum<BD>(c0, c1, sw, shq + g * H, shs + g * nhb, nhb, rl));
+        const float v = tree8_pair(lane_running_sum_pair<BD>(c0, c1, sw, shq + g * H, shs + g * nhb, nhb, rl));
         if (rl == 0 && gi < k * R) sv[gi] = v;
         __syncthreads();
         if (tid < R && di * R + tid < dim) {
@@ -1427,9 +1427,9 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
     const bool w3row = rg & 1;
     int4 c0[BU], c1[BU];
     float sw[BU];
-    lane_row_load<BU>(c0, c1, sw, static_cast<const uint8_t *>(stab[(w3row ? 2 : 0) * E + e]) + j * dim,
+    lane_row_load_pair<BU>(c0, c1, sw, static_cast<const uint8_t *>(stab[(w3row ? 2 : 0) * E + e]) + j * dim,
                       static_cast<const float *>(stab[(w3row ? 3 : 1) * E + e]) + j * nb, nb, rl);
-    const float v = tree8(lane_running_sum<BU>(c0, c1, sw, sq, sxs, nb, rl));
+    const float v = tree8_pair(lane_running_sum_pair<BU>(c0, c1, sw, sq, sxs, nb, rl));
     const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
     if (wave == 0) ffn1_wait_line(a, tag, kFfn1MaxK, nullptr, s_w);
     __syncthreads();
