@@ -404,23 +404,35 @@ __device__ __forceinline__ void lane_row_load_pair(int4 (&c0)[BPL], int4 (&c1)[B
 }
 
 // The lane's running sum of the row held by lane_row_load_pair with one
-// input, from +0. Every lane of the group calls it.
-template <int BPL>
+// input, continued from acc. Every lane of the group calls it. EXACT: the row is
+// exactly 8·BPL blocks (nb is not read), so the input's offsets need no
+// clamp and fold into the reads' immediate offsets.
+template <int BPL, bool EXACT = false>
+__device__ __forceinline__ float lane_running_sum_pair_from(float acc, const int4 (&c0)[BPL], const int4 (&c1)[BPL],
+                                                            const float (&sw)[BPL], const int8_t *xq, const float *xsc,
+                                                            int nb, int rl) {
+    const int last = 32 * nb - 16, L = pair_sum_index(rl);
+    const bool odd = rl & 1;
+#pragma unroll
+    for (int m = 0; m < BPL; m++) {
+        const int o0 = EXACT ? 256 * m + 16 * rl : min(256 * m + 16 * rl, last);
+        const int o1 = EXACT ? 256 * m + 128 + 16 * rl : min(256 * m + 128 + 16 * rl, last);
+        const int d0 = dot16(c0[m], *reinterpret_cast<const int4 *>(xq + o0), 0);
+        const int d1 = dot16(c1[m], *reinterpret_cast<const int4 *>(xq + o1), 0);
+        // the block this lane keeps: its own half's dot plus the partner's
+        // (each lane sends the half its partner keeps)
+        const int sum = (odd ? d1 : d0) + __builtin_amdgcn_mov_dpp(odd ? d0 : d1, 0xB1, 0xF, 0xF, false);
+        const int b = L + 8 * m;
+        if (EXACT || b < nb) acc += (float)sum * (sw[m] * xsc[b]);
+    }
+    return acc;
+}
+
+template <int BPL, bool EXACT = false>
 __device__ __forceinline__ float lane_running_sum_pair(const int4 (&c0)[BPL], const int4 (&c1)[BPL],
                                                        const float (&sw)[BPL], const int8_t *xq, const float *xsc,
                                                        int nb, int rl) {
-    const int last = 32 * nb - 16, L = pair_sum_index(rl);
-    const bool odd = rl & 1;
-    float acc = 0.0f;
-#pragma unroll
-    for (int m = 0; m < BPL; m++) {
-        const int o0 = min(256 * m + 16 * rl, last), o1 = min(256 * m + 128 + 16 * rl, last);
-        const int s0 = pair_sum(dot16(c0[m], *reinterpret_cast<const int4 *>(xq + o0), 0));
-        const int s1 = pair_sum(dot16(c1[m], *reinterpret_cast<const int4 *>(xq + o1), 0));
-        const int b = L + 8 * m;
-        if (b < nb) acc += (float)(odd ? s1 : s0) * (sw[m] * xsc[b]);
-    }
-    return acc;
+    return lane_running_sum_pair_from<BPL, EXACT>(0.0f, c0, c1, sw, xq, xsc, nb, rl);
 }
 
 // The tree over running sums held as lane_running_sum_pair leaves them

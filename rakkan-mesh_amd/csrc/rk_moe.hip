@@ -609,9 +609,11 @@ __host__ __device__ constexpr int up8_lds(int dim) {
 
 // ALL: the call's tokens (at most kExpTok) are staged in LDS at the start,
 // every one of them, so the staging does not wait for the pair list; else
-// each pass stages its own pairs' inputs. The group's rows, count and list
-// are found with one load each (the grouping wrote the rows' addresses).
-template <int BPL, bool ALL>
+// each pass stages its own pairs' inputs. EX: the rows are exactly 8·BPL
+// blocks, read in contiguous pieces (lane_row_load_pair), else whole
+// blocks a lane. The group's rows, count and list are found with one load
+// each (the grouping wrote the rows' addresses).
+template <int BPL, bool ALL, bool EX>
 __global__ __launch_bounds__(512) void moe_up8_kernel(const void *const *gptr, const int32_t *grp, int gcap,
                                                       const float *gwt, int k, const int8_t *qx, const float *xs,
                                                       int tokens, int dim, int hidden, int8_t *hq, float *hs,
@@ -659,7 +661,12 @@ __global__ __launch_bounds__(512) void moe_up8_kernel(const void *const *gptr, c
     __builtin_amdgcn_sched_barrier(0);
     int4 c0[BPL], c1[BPL];
     float sw[BPL];
-    lane_row_load<BPL>(c0, c1, sw, (w3row ? w3 : w1) + (int64_t)j * dim, (w3row ? s3 : s1) + (int64_t)j * nb, nb, rl);
+    if (EX)
+        lane_row_load_pair<BPL>(c0, c1, sw, (w3row ? w3 : w1) + (int64_t)j * dim, (w3row ? s3 : s1) + (int64_t)j * nb,
+                                nb, rl);
+    else
+        lane_row_load<BPL>(c0, c1, sw, (w3row ? w3 : w1) + (int64_t)j * dim, (w3row ? s3 : s1) + (int64_t)j * nb, nb,
+                           rl);
     __builtin_amdgcn_sched_barrier(0);
     const int n16 = dim >> 4;
     for (int p0 = 0; p0 < count; p0 += kExpTok) {
@@ -688,7 +695,8 @@ __global__ __launch_bounds__(512) void moe_up8_kernel(const void *const *gptr, c
         }
         for (int pi = 0; pi < np; pi++) {
             const int u = ALL ? spair[pi] / k : pi;  // the input's place in LDS
-            const float v = tree8(lane_running_sum<BPL>(c0, c1, sw, sq + u * dim, sxs + u * nb, nb, rl));
+            const float v = EX ? tree8_pair(lane_running_sum_pair<BPL, true>(c0, c1, sw, sq + u * dim, sxs + u * nb, nb, rl))
+                               : tree8(lane_running_sum<BPL>(c0, c1, sw, sq + u * dim, sxs + u * nb, nb, rl));
             const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
             if ((lane & 15) == 0) sh[pi * 32 + 4 * wave + q] = swt[pi] * silu_mul(v, v3);
         }
@@ -1636,9 +1644,16 @@ static int enqueue_moe_experts(rk_moe *m, const MoeScratch &sc, const int8_t *qx
         const dim3 grid8((unsigned)(H / 32), (unsigned)groups), grid((unsigned)groups, (unsigned)(H / 32));
         const bool all = tokens <= kExpTok;
         const size_t lds = (size_t)up8_lds(D);
-#define RK_UP8(B, A)                                                                                                 \
-    RK_LAUNCH((moe_up8_kernel<B, A>), grid8, dim3(512), lds, s, sc.gptr, sc.grp, sc.gcap, sc.gwt, K, qx, xs, tokens, D, \
-              H, sc.hq, sc.hs, sc.hsum)
+        const bool ex = D / 32 == 8 * (bpl <= 2 ? 2 : bpl <= 4 ? 4 : 8);  // rows of exactly 8·B blocks
+#define RK_UP8(B, A)                                                                                                    \
+    do {                                                                                                                \
+        if (ex)                                                                                                         \
+            RK_LAUNCH((moe_up8_kernel<B, A, true>), grid8, dim3(512), lds, s, sc.gptr, sc.grp, sc.gcap, sc.gwt, K, qx,  \
+                      xs, tokens, D, H, sc.hq, sc.hs, sc.hsum);                                                         \
+        else                                                                                                            \
+            RK_LAUNCH((moe_up8_kernel<B, A, false>), grid8, dim3(512), lds, s, sc.gptr, sc.grp, sc.gcap, sc.gwt, K, qx, \
+                      xs, tokens, D, H, sc.hq, sc.hs, sc.hsum);                                                         \
+    } while (0)
         if (bpl <= 2) {
             if (all) RK_UP8(2, true);
             else RK_UP8(2, false);
