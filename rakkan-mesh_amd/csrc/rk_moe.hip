@@ -1322,7 +1322,9 @@ __device__ void ffn1_wait_line(const Ffn1Args &a, uint32_t tag, int off, int *s_
     }
 }
 
-template <int BU, int BD>
+// EX: the up rows are exactly 8·BU blocks and the down rows 8·BD (the
+// running sums' input offsets need no clamp).
+template <int BU, int BD, bool EX>
 __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
     extern __shared__ __align__(16) char flds[];
     __shared__ float bcast;
@@ -1361,7 +1363,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
         lane_row_load_pair<BD>(c0, c1, sw, static_cast<const uint8_t *>(stab[e]) + i * H,
                           static_cast<const float *>(stab[E + e]) + i * nhb, nhb, rl);
         tag_get_q8<512>(a.hw, k * nhb, tag, shq, shs, a.err, &s_to);
-        const float v = tree8_pair(lane_running_sum_pair<BD>(c0, c1, sw, shq + g * H, shs + g * nhb, nhb, rl));
+        const float v = tree8_pair(lane_running_sum_pair<BD, EX>(c0, c1, sw, shq + g * H, shs + g * nhb, nhb, rl));
         if (rl == 0 && gi < k * R) sv[gi] = v;
         __syncthreads();
         if (tid < R && di * R + tid < dim) {
@@ -1437,7 +1439,7 @@ __global__ __launch_bounds__(512) void moe_ffn1_kernel(Ffn1Args a) {
     float sw[BU];
     lane_row_load_pair<BU>(c0, c1, sw, static_cast<const uint8_t *>(stab[(w3row ? 2 : 0) * E + e]) + j * dim,
                       static_cast<const float *>(stab[(w3row ? 3 : 1) * E + e]) + j * nb, nb, rl);
-    const float v = tree8_pair(lane_running_sum_pair<BU>(c0, c1, sw, sq, sxs, nb, rl));
+    const float v = tree8_pair(lane_running_sum_pair<BU, EX>(c0, c1, sw, sq, sxs, nb, rl));
     const float v3 = row_shl8(v);  // lane 16q: the W3 dot of row q
     if (wave == 0) ffn1_wait_line(a, tag, kFfn1MaxK, nullptr, s_w);
     __syncthreads();
@@ -1760,10 +1762,15 @@ int enqueue_moe_x(rk_moe *m, const MoeScratch &sc, const float *x, const float *
         const int bu = (D / 32 + 7) / 8, bd = (H / 32 + 7) / 8;
         const dim3 grid((unsigned)(a.nr + a.nu + a.nd));
         typedef void (*Ffn1Fn)(Ffn1Args);
-        static const Ffn1Fn fns[3][3] = {{moe_ffn1_kernel<2, 2>, moe_ffn1_kernel<2, 4>, moe_ffn1_kernel<2, 8>},
-                                         {moe_ffn1_kernel<4, 2>, moe_ffn1_kernel<4, 4>, moe_ffn1_kernel<4, 8>},
-                                         {moe_ffn1_kernel<8, 2>, moe_ffn1_kernel<8, 4>, moe_ffn1_kernel<8, 8>}};
-        const Ffn1Fn fn = fns[bu <= 2 ? 0 : bu <= 4 ? 1 : 2][bd <= 2 ? 0 : bd <= 4 ? 1 : 2];
+#define RK_FFN1_ROW(U, X)                                                                                    \
+    {moe_ffn1_kernel<U, 2, X>, moe_ffn1_kernel<U, 3, X>, moe_ffn1_kernel<U, 4, X>, moe_ffn1_kernel<U, 8, X>}
+        static const Ffn1Fn fns[2][3][4] = {{RK_FFN1_ROW(2, false), RK_FFN1_ROW(4, false), RK_FFN1_ROW(8, false)},
+                                            {RK_FFN1_ROW(2, true), RK_FFN1_ROW(4, true), RK_FFN1_ROW(8, true)}};
+#undef RK_FFN1_ROW
+        const int iu = bu <= 2 ? 0 : bu <= 4 ? 1 : 2, id = bd <= 2 ? 0 : bd <= 3 ? 1 : bd <= 4 ? 2 : 3;
+        const int BUs[3] = {2, 4, 8}, BDs[4] = {2, 3, 4, 8};
+        const bool ex = D / 32 == 8 * BUs[iu] && H / 32 == 8 * BDs[id];  // rows of exactly 8·B blocks
+        const Ffn1Fn fn = fns[ex ? 1 : 0][iu][id];
         if (lds > 64 * 1024) {
             hipError_t e = hipFuncSetAttribute((const void *)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return hip_fail(d, e, "moe launch");
