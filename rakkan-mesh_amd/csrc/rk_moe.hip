@@ -953,7 +953,8 @@ __global__ __launch_bounds__(512) void moe_up1_kernel(const float *x, const floa
     }
 }
 
-template <int BPL>
+// EX: the W2 rows are exactly 8·BPL blocks (unclamped running sums).
+template <int BPL, bool EX>
 __global__ __launch_bounds__(256) void moe_down8_kernel(const void *const *gptr, const int32_t *grp, int gcap,
                                                         const int8_t *hq, const float *hs, int dim, int hidden,
                                                         float *o) {
@@ -999,7 +1000,8 @@ __global__ __launch_bounds__(256) void moe_down8_kernel(const void *const *gptr,
         }
         __syncthreads();
         for (int pi = 0; pi < np; pi++) {
-            const float v = tree8_pair(lane_running_sum_pair<BPL>(c0, c1, sw, sq + pi * hidden, sxs + pi * nb, nb, rl));
+            const float v =
+                tree8_pair(lane_running_sum_pair<BPL, EX>(c0, c1, sw, sq + pi * hidden, sxs + pi * nb, nb, rl));
             if (rl == 0 && i < dim) o[(int64_t)spair[pi] * dim + i] = v;
         }
         __syncthreads();
@@ -1686,18 +1688,25 @@ static int enqueue_moe_down(rk_moe *m, const MoeScratch &sc, int tokens, float *
         const int bpl = (H / 32 + 7) / 8;  // blocks of a W2 row per lane
         const size_t lds = (size_t)kExpTok * (H + (H / 32) * 4 + 4);
         const dim3 grid((unsigned)((D + 31) / 32), (unsigned)groups);
-        if (bpl <= 2)
-            RK_LAUNCH(moe_down8_kernel<2>, grid, dim3(256), lds, s, sc.gptr, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
-                      sc.o);
-        else if (bpl <= 4)
-            RK_LAUNCH(moe_down8_kernel<4>, grid, dim3(256), lds, s, sc.gptr, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
-                      sc.o);
-        else if (bpl <= 8)
-            RK_LAUNCH(moe_down8_kernel<8>, grid, dim3(256), lds, s, sc.gptr, sc.grp, sc.gcap, sc.hq, sc.hs, D, H,
-                      sc.o);
-        else
+#define RK_DOWN8(B, X)                                                                                       \
+    RK_LAUNCH((moe_down8_kernel<B, X>), grid, dim3(256), lds, s, sc.gptr, sc.grp, sc.gcap, sc.hq, sc.hs, D, H, sc.o)
+        const int nbh = H / 32;  // rows of exactly 8·B blocks take the unclamped form
+        if (bpl <= 2) {
+            if (nbh == 16) RK_DOWN8(2, true);
+            else RK_DOWN8(2, false);
+        } else if (bpl <= 3 && nbh == 24) {
+            RK_DOWN8(3, true);
+        } else if (bpl <= 4) {
+            if (nbh == 32) RK_DOWN8(4, true);
+            else RK_DOWN8(4, false);
+        } else if (bpl <= 8) {
+            if (nbh == 64) RK_DOWN8(8, true);
+            else RK_DOWN8(8, false);
+        } else {
             RK_LAUNCH(moe_down_kernel, dim3((unsigned)groups, (unsigned)((D + 15) / 16)), dim3(256), 0, s, m->w2,
                       m->s2, sc.grp, sc.gcap, sc.hq, sc.hs, D, H, sc.o);
+        }
+#undef RK_DOWN8
     }
     if (next && residual && D % 32 == 0 && D <= kMaxNormCols) {
         ProfScope p(d, s, "moe_combine");
