@@ -1047,9 +1047,7 @@ __device__ __forceinline__ void att_values_body(const float *att, int32_t att_st
     }
     if (tid == 0) s_inv = recip32(lds_chain_sum(sa, T, 0.0f));
     __syncthreads();
-    const float inv = s_inv;
-    for (int t = tid; t < T; t += kValThreads) sa[t] = sa[t] * inv;
-    __syncthreads();
+    const float inv = s_inv;  // a_t = e_t·inv, formed where the products read e_t
 
     // Chunk c: its products into tile c mod 2, chunk c+1's loads, a barrier,
     // then wave 0's sums over the tile. The tile was last read by wave 0's
@@ -1062,7 +1060,8 @@ __device__ __forceinline__ void att_values_body(const float *att, int32_t att_st
 #pragma unroll
         for (int r = 0; r < kValRounds; r++) {
             const int tt = 4 * (pq + kValQuads * r);
-            const float4 a4 = *reinterpret_cast<const float4 *>(sa + min(c0 + tt, ctx_pad - 4));
+            const float4 e4 = *reinterpret_cast<const float4 *>(sa + min(c0 + tt, ctx_pad - 4));
+            const float4 a4 = make_float4(e4.x * inv, e4.y * inv, e4.z * inv, e4.w * inv);
             float *dst = tile + (4 * fq) * kValPitch + tt;
             *reinterpret_cast<float4 *>(dst) =
                 make_float4(a4.x * vr[r][0].x, a4.y * vr[r][1].x, a4.z * vr[r][2].x, a4.w * vr[r][3].x);
@@ -1499,16 +1498,38 @@ __device__ __forceinline__ void wo_after_values(const AttWoArgs &a, int wi) {
     float sum = 0.0f;
     {
         const float *p = tbw + gk * rs + L * k8p;
-        const int cnt = L < nb ? (nb - L + 7) >> 3 : 0;
-        int k = 0;
-        for (; k + 4 <= cnt; k += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(p + k);
-            sum += v.x;
-            sum += v.y;
-            sum += v.z;
-            sum += v.w;
+        if (nb == 128) {
+            // (uniform: 4096 columns, sixteen terms a lane, read at once)
+            const float4 *p4 = reinterpret_cast<const float4 *>(p);
+            const float4 v0 = p4[0], v1 = p4[1], v2 = p4[2], v3 = p4[3];
+            sum += v0.x;
+            sum += v0.y;
+            sum += v0.z;
+            sum += v0.w;
+            sum += v1.x;
+            sum += v1.y;
+            sum += v1.z;
+            sum += v1.w;
+            sum += v2.x;
+            sum += v2.y;
+            sum += v2.z;
+            sum += v2.w;
+            sum += v3.x;
+            sum += v3.y;
+            sum += v3.z;
+            sum += v3.w;
+        } else {
+            const int cnt = L < nb ? (nb - L + 7) >> 3 : 0;
+            int k = 0;
+            for (; k + 4 <= cnt; k += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(p + k);
+                sum += v.x;
+                sum += v.y;
+                sum += v.z;
+                sum += v.w;
+            }
+            for (; k < cnt; k++) sum += p[k];
         }
-        for (; k < cnt; k++) sum += p[k];
     }
     sum = sum + dppf_x1(sum);
     sum = sum + dppf_x2(sum);
