@@ -721,9 +721,11 @@ bool launch_stream(int fmt, int pro, int epi, FusedArgs a, int cu, hipStream_t s
     };
     const StreamInst *inst = nullptr;
     int W = 0, nbatch = 0;
+    // (an entry below the instance's smallest workgroup is never taken: its
+    // prologue would leave part of the input unloaded)
     for (const StreamTune &t : kStreamTune)
         if (t.fmt == fmt && t.pro == pro && t.epi == epi && t.rows == a.rows && t.cols == cols && ncu == 256 &&
-            (inst = find(t.k, t.u))) {
+            t.w >= wmin && t.w <= 16 && (inst = find(t.k, t.u))) {
             W = t.w;
             nbatch = t.nbatch;
             break;
