@@ -370,14 +370,16 @@ __device__ __forceinline__ float tree8(float acc) {
 
 // ---- The same row dots with the row read in contiguous 16-byte pieces (a
 // 128-byte line per load instruction and row): at step k (k < 2·BPL) lane
-// rl holds half rl & 1 of block 4k + rl/2, so a lane pair holds a block
-// and pair_sum gives its exact sum in both lanes. Lane 2p keeps running sum
-// p (the even steps: blocks 8m + p) and lane 2p+1 running sum 4 + p (the
-// odd steps: blocks 8m + 4 + p), each in block order from +0; tree8_pair
-// forms the same tree. Measured on MI355X: 64 rows a workgroup read about
-// 15 % faster than as whole 32-byte blocks a lane; it holds more registers
-// where a row is summed against several inputs, so the kernels that run at
-// four waves a SIMD on the first form keep it. ----
+// rl holds half rl & 1 of block 4k + rl/2, so a lane pair holds a block.
+// Lane 2p keeps running sum p (the even steps: blocks 8m + p) and lane
+// 2p+1 running sum 4 + p (the odd steps: blocks 8m + 4 + p), each in block
+// order from +0, the block's exact sum formed from the pair's two dots by
+// one DPP exchange; tree8_pair forms the same tree. Measured on MI355X: 64
+// rows a workgroup read about 15 % faster than as whole 32-byte blocks a
+// lane. With the input offsets clamped (rows of any width) it holds more
+// registers where a row is summed against several inputs; at rows of
+// exactly 8·BPL blocks (EXACT) fewer. Kernels that would drop below four
+// waves a SIMD keep the first form. ----
 
 // The running sum a lane keeps (its m-th term is block L + 8m).
 __device__ __forceinline__ int pair_sum_index(int rl) { return (rl & 1) ? 4 + (rl >> 1) : rl >> 1; }
@@ -404,9 +406,9 @@ __device__ __forceinline__ void lane_row_load_pair(int4 (&c0)[BPL], int4 (&c1)[B
 }
 
 // The lane's running sum of the row held by lane_row_load_pair with one
-// input, continued from acc. Every lane of the group calls it. EXACT: the row is
-// exactly 8·BPL blocks (nb is not read), so the input's offsets need no
-// clamp and fold into the reads' immediate offsets.
+// input, continued from acc. Every lane of the group calls it. EXACT: the
+// row is exactly 8·BPL blocks (nb is not read), so the input's offsets
+// need no clamp and fold into the reads' immediate offsets.
 template <int BPL, bool EXACT = false>
 __device__ __forceinline__ float lane_running_sum_pair_from(float acc, const int4 (&c0)[BPL], const int4 (&c1)[BPL],
                                                             const float (&sw)[BPL], const int8_t *xq, const float *xsc,
